@@ -1,0 +1,229 @@
+/*
+ * sparseforge_amd — C ABI of the MI355X (gfx950) sparse-training hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and a
+ * hipStream_t passed as `void*` (NULL = the legacy default stream), enqueues
+ * its kernels on that stream and returns without synchronising.  Tensors are
+ * dense and row-major ([rows, cols] with row stride == cols) unless stated.
+ * Nothing here allocates device memory: entry points that need scratch
+ * take a `workspace` pointer whose minimum size the matching *_workspace_size
+ * function reports.  Return value: SF_OK or a negative SF_ERR_* code; the
+ * message of the most recent failure on the calling thread is returned by
+ * sf_last_error().
+ *
+ * The reference implementation is Python (liuhanzuo/SparseForge,
+ * legacy/sparse_modeling.py, legacy/utils.py, legacy/adamw.py,
+ * legacy/triton_block_sparse.py); each declaration names the reference lines
+ * whose behaviour it reproduces.  A ctypes binding of this header is
+ * sparseforge_amd/_lib.py.
+ */
+#ifndef SPARSEFORGE_AMD_H
+#define SPARSEFORGE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define SF_OK 0
+#define SF_ERR_INVALID (-1)     /* bad argument (shape, dtype, null pointer) */
+#define SF_ERR_UNSUPPORTED (-2) /* valid in the reference, not built on device */
+#define SF_ERR_HIP (-3)         /* HIP runtime / launch failure */
+
+/* ---- element types ----------------------------------------------------- */
+#define SF_DTYPE_F32 0
+#define SF_DTYPE_BF16 1
+
+/* ---- hard-mask projections (SparseLinear._hard_mask_from_soft) --------- */
+#define SF_HARD_NONE 0         /* all ones                       (:523-524)  */
+#define SF_HARD_THRESHOLD 1    /* soft > 0.5                     (:526-531)  */
+#define SF_HARD_NM_TAIL_KEEP 2 /* top-N of each M-group, tail columns = 1 (nm_2_4, :578-603) */
+#define SF_HARD_NM_STRICT 3    /* top-N of each M-group, cols % M == 0 required (structured, :720-735) */
+
+/* ---- importance metrics (compute_gate_target scores, :1041-1079) ------- */
+#define SF_METRIC_MAGNITUDE 0
+#define SF_METRIC_HESSIAN_OBD 1
+#define SF_METRIC_HESSIAN_RATIO 2
+#define SF_METRIC_HESSIAN 3
+#define SF_METRIC_WANDA 4
+#define SF_METRIC_MOVEMENT 5
+
+/* ---- gate-target forms ------------------------------------------------- */
+#define SF_GATE_UNSTRUCTURED 0 /* sigmoid((z - tau) / (T + 1e-8)), global tau  (:1097-1162) */
+#define SF_GATE_STRUCTURED 1   /* sigmoid((z - tau_g) / (T + 1e-8)), tau_g = N-th largest of group (:1164-1185) */
+#define SF_GATE_STRUCTURED_EXACT 2 /* top-N scatter of ones (:1176-1182) */
+
+/* ---- penalty pull applied to G inside update_mask (:1291-1573) ---------- */
+#define SF_PENALTY_NONE 0
+#define SF_PENALTY_MID 1            /* G -= c * (1 - 2 m)                 (:1567-1570) */
+#define SF_PENALTY_NM_2_4 2         /* G -= c * (m - top2(G)), tail target 1 (:1350-1393) */
+#define SF_PENALTY_STRUCTURED_TOPN 3 /* G -= c * (m - topN(G)), cols % M == 0 (:1531-1565) */
+
+const char* sf_last_error(void);
+int sf_version(void);
+
+/*
+ * Hard projection of a soft mask.  Replaces SparseLinear._hard_mask_from_soft
+ * (legacy/sparse_modeling.py:510-735) for hard types none / unstructured /
+ * nm_2_4 / structured.  Ties inside a group resolve exactly as torch.topk on
+ * the CPU does.  Device support: m_group == 4, 1 <= n_keep <= 3.
+ * soft: [rows, cols] (soft_dtype); hard: [rows, cols] (hard_dtype), values {0, 1}.
+ */
+int sf_hard_mask(const void* soft, int soft_dtype, void* hard, int hard_dtype, int64_t rows,
+                 int64_t cols, int kind, int n_keep, int m_group, void* stream);
+
+/*
+ * Parameters of one gate-target / mask-update call.  Host scalars are the
+ * values SparseLinear computes from its config and the step
+ * (legacy/sparse_modeling.py:932-985, :1242-1666).
+ */
+typedef struct sf_mask_params {
+  int64_t rows, cols;
+  int metric;          /* SF_METRIC_* */
+  int gate;            /* SF_GATE_* */
+  int n_keep, m_group; /* N, M of the structured gate and of topN penalties */
+  int hard_kind;       /* SF_HARD_* used for the flip count */
+  int hard_n, hard_m;  /* N, M of that hard projection */
+  int penalty;         /* SF_PENALTY_* (only when penalty_coef != 0) */
+  int has_frozen;      /* frozen_mask_flags is a full [rows, cols] tensor */
+  int snap_high;       /* step >= 2000: freeze_high snaps to 1 (:1632-1636) */
+  int score_dtype;     /* dtype the reference holds scores in (promotion of W, H) */
+  float temperature;   /* _temperature(step) */
+  float eps_metric;    /* 1e-8 */
+  float movement_temp; /* cfg.temperature (movement metric) */
+  float beta_struct;   /* _beta_structural(step) */
+  float mask_lr;       /* a of the EMA */
+  float penalty_coef;  /* mask_penalty_lr * lambda_mid */
+  float binarize;      /* mask_binarize_decay */
+  float freeze_low, freeze_high;
+  int apply_freeze;    /* freeze_low > 0 or freeze_high < 1 */
+} sf_mask_params;
+
+/*
+ * Workspace bytes needed by sf_score_stats / sf_gate_target / sf_update_mask
+ * for a [rows, cols] layer and a tau sample of `sample_size` elements.
+ */
+size_t sf_mask_workspace_size(int64_t rows, int64_t cols, int64_t sample_size);
+
+/*
+ * Global mean and population std (+1e-6) of the layer's scores
+ * (legacy/sparse_modeling.py:1083-1088).  stats_out: device float[2] = {mu, sigma}.
+ * W: weight, H: hessian_diag (or NULL), aux: scaler_row [cols] for wanda or
+ * grad_ema [rows, cols] for movement (or NULL).
+ */
+int sf_score_stats(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                   const void* aux, int aux_dtype, float* stats_out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/*
+ * Unstructured threshold tau = torch.quantile(z[sample_idx], q) with linear
+ * interpolation (legacy/sparse_modeling.py:987-1015).  sample_idx: device
+ * int64[sample_size] (NULL: use every element, sample_size must equal
+ * rows*cols).  stats: device {mu, sigma} from sf_score_stats.  tau_out: device float[1].
+ */
+int sf_tau_quantile(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                    const void* aux, int aux_dtype, const float* stats, const int64_t* sample_idx,
+                    int64_t sample_size, float q, float* tau_out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * Sample indices for the tau quantile: idx[i] uniform in [0, n) from the
+ * counter-based generator (seed, i).  Replaces torch.randint at :993.
+ */
+int sf_sample_indices(int64_t* idx, int64_t sample_size, int64_t n, uint64_t seed, void* stream);
+
+/*
+ * Gate target G (compute_gate_target, legacy/sparse_modeling.py:1018-1239):
+ * scores -> z-norm -> gate form -> beta structural mix -> frozen override.
+ * G: [rows, cols] in g_dtype.  stats / tau: device scalars from the calls above
+ * (tau unused for structured gates).  mask and frozen are read only for the
+ * frozen override.
+ */
+int sf_gate_target(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                   const void* aux, int aux_dtype, const void* mask, int mask_dtype,
+                   const void* frozen, int frozen_dtype, const float* stats, const float* tau, void* G,
+                   int g_dtype, void* stream);
+
+/*
+ * Fused periodic mask update (SparseLinear.update_mask body after the
+ * step gating, legacy/sparse_modeling.py:1288-1661): gate target, penalty
+ * pull + clamp, binarisation push, EMA mask <- clamp((1-a) m + a G), freeze
+ * snaps and flags, and the hard-mask flip count.  One read of W/H/mask, one
+ * write of mask.  flips: device int64[1], incremented (caller zeroes it).
+ */
+int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                   const void* aux, int aux_dtype, void* mask, int mask_dtype, void* frozen,
+                   int frozen_dtype, const float* stats, const float* tau, int64_t* flips,
+                   void* stream);
+
+/*
+ * Count of positions whose hard projection differs between two soft masks
+ * (legacy/sparse_modeling.py:1659-1661).  flips: device int64[1], incremented.
+ */
+int sf_hard_flip_count(const void* prev, const void* now, int dtype, int64_t rows, int64_t cols,
+                       int kind, int n_keep, int m_group, int64_t* flips, void* stream);
+
+/* ---- effective mask for the masked GEMMs (SparseLinear.forward, :759-771) */
+#define SF_EFF_SOFT 0 /* E = mask.to(weight dtype)                                  */
+#define SF_EFF_MIX 1  /* E = (hx * mask + (1 - hx) * hard(mask)).to(weight dtype)     */
+
+/*
+ * Effective mask E of a forward call, written in the weight dtype (the
+ * reference's `mask_cast`, legacy/sparse_modeling.py:72-73 and :759-771).
+ * mode SF_EFF_MIX uses the hard projection `hard_kind` (SF_HARD_*) with N:M =
+ * hard_n:hard_m; the arithmetic rounds in the mask dtype as the reference does.
+ */
+int sf_effective_mask(const void* mask, int mask_dtype, void* eff, int eff_dtype, int64_t rows, int64_t cols,
+                      int mode, float hx, int hard_kind, int hard_n, int hard_m, void* stream);
+
+/* ---- GEMM engine (FusedMaskedLinearSTE, :56-132, and the SLoRB F.linear pair, :790-794) */
+#define SF_LAYOUT_K 0  /* operand stored K-contiguous: X[row * ld + k]                        */
+#define SF_LAYOUT_MN 1 /* operand stored M/N-contiguous: X[k * ld + row] (a transposed view)  */
+
+typedef struct sf_gemm_desc {
+  int dtype;              /* element dtype of A1, A2, B1, B2, bmask, emask, dw            */
+  int a_layout, b_layout; /* SF_LAYOUT_*; (MN, K) is not built                            */
+  int64_t M, N, K1, K2;   /* K2 = 0: no second segment                                    */
+  const void* A1;
+  int64_t lda1;
+  const void* B1;
+  int64_t ldb1;
+  const void* A2;
+  int64_t lda2;
+  const void* B2;
+  int64_t ldb2;
+  const void* bmask; /* effective mask E applied to B1 (B1's layout and ld), or NULL  */
+  float bscale;      /* weight-scaling factor applied after E (1 = none)              */
+  void* C;           /* [M, N] row-major                                              */
+  int64_t ldc;
+  int c_dtype;
+  const void* bias; /* [N] added after rounding to c_dtype, or NULL                    */
+  int bias_dtype;
+  const void* emask; /* [M, N] (ld = ldc): C *= emask, or the test of the decay term   */
+  const void* dw;    /* [M, N] (ld = ldc): C += decay * dw * (emask < 0.5), or NULL   */
+  float decay;
+  int accumulate; /* C += result                                                        */
+} sf_gemm_desc;
+
+/*
+ * C = A1 . (B1 * E * s)^T + A2 . B2^T (+ bias), bf16 or f32 MFMA on gfx950.
+ * Replaces the cuBLAS matmuls of FusedMaskedLinearSTE.forward/backward
+ * (legacy/sparse_modeling.py:79-87, :113-125) with the mask applied inside
+ * the kernel, and folds the SLoRB term (:790-794) into the same accumulators.
+ */
+int sf_gemm(const sf_gemm_desc* d, void* stream);
+
+/*
+ * out[c] = sum_r A[r, c] for a row-major [rows, cols] matrix (bias gradient,
+ * legacy/sparse_modeling.py:127-129).  f32 accumulation, result in out_dtype.
+ */
+int sf_column_sum(const void* A, int a_dtype, int64_t rows, int64_t cols, void* out, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSEFORGE_AMD_H */

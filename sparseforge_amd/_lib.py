@@ -1,0 +1,227 @@
+"""ctypes binding of include/sparseforge_amd.h.
+
+The HIP library is loaded from the package directory (built in-tree by
+``sparseforge_amd.build``).  torch is imported first so that the library's
+``libamdhip64.so.7`` dependency resolves to the HIP runtime torch already
+loaded: device pointers and streams are then shared between the two.
+
+There is no fallback: if the library is missing, or a tensor handed to an
+op is not a contiguous tensor on a ROCm device, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsparseforge_amd.so")
+
+SF_OK = 0
+SF_ERR_INVALID = -1
+SF_ERR_UNSUPPORTED = -2
+SF_ERR_HIP = -3
+
+DT_F32 = 0
+DT_BF16 = 1
+
+HARD_NONE = 0
+HARD_THRESHOLD = 1
+HARD_NM_TAIL_KEEP = 2
+HARD_NM_STRICT = 3
+
+METRIC = {
+    "magnitude": 0,
+    "hessian_obd": 1,
+    "hessian_ratio": 2,
+    "hessian": 3,
+    "wanda": 4,
+    "movement": 5,
+}
+
+GATE_UNSTRUCTURED = 0
+GATE_STRUCTURED = 1
+GATE_STRUCTURED_EXACT = 2
+
+PENALTY_NONE = 0
+PENALTY_MID = 1
+PENALTY_NM_2_4 = 2
+PENALTY_STRUCTURED_TOPN = 3
+
+EFF_SOFT = 0
+EFF_MIX = 1
+
+LAYOUT_K = 0
+LAYOUT_MN = 1
+
+
+class MaskParams(ctypes.Structure):
+    """Mirror of ``sf_mask_params``."""
+
+    _fields_ = [
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("metric", ctypes.c_int),
+        ("gate", ctypes.c_int),
+        ("n_keep", ctypes.c_int),
+        ("m_group", ctypes.c_int),
+        ("hard_kind", ctypes.c_int),
+        ("hard_n", ctypes.c_int),
+        ("hard_m", ctypes.c_int),
+        ("penalty", ctypes.c_int),
+        ("has_frozen", ctypes.c_int),
+        ("snap_high", ctypes.c_int),
+        ("score_dtype", ctypes.c_int),
+        ("temperature", ctypes.c_float),
+        ("eps_metric", ctypes.c_float),
+        ("movement_temp", ctypes.c_float),
+        ("beta_struct", ctypes.c_float),
+        ("mask_lr", ctypes.c_float),
+        ("penalty_coef", ctypes.c_float),
+        ("binarize", ctypes.c_float),
+        ("freeze_low", ctypes.c_float),
+        ("freeze_high", ctypes.c_float),
+        ("apply_freeze", ctypes.c_int),
+    ]
+
+
+class GemmDesc(ctypes.Structure):
+    """Mirror of ``sf_gemm_desc``."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_int),
+        ("a_layout", ctypes.c_int),
+        ("b_layout", ctypes.c_int),
+        ("M", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("K1", ctypes.c_int64),
+        ("K2", ctypes.c_int64),
+        ("A1", ctypes.c_void_p),
+        ("lda1", ctypes.c_int64),
+        ("B1", ctypes.c_void_p),
+        ("ldb1", ctypes.c_int64),
+        ("A2", ctypes.c_void_p),
+        ("lda2", ctypes.c_int64),
+        ("B2", ctypes.c_void_p),
+        ("ldb2", ctypes.c_int64),
+        ("bmask", ctypes.c_void_p),
+        ("bscale", ctypes.c_float),
+        ("C", ctypes.c_void_p),
+        ("ldc", ctypes.c_int64),
+        ("c_dtype", ctypes.c_int),
+        ("bias", ctypes.c_void_p),
+        ("bias_dtype", ctypes.c_int),
+        ("emask", ctypes.c_void_p),
+        ("dw", ctypes.c_void_p),
+        ("decay", ctypes.c_float),
+        ("accumulate", ctypes.c_int),
+    ]
+
+
+byref = ctypes.byref
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+_MP = ctypes.POINTER(MaskParams)
+
+# name -> (restype, argtypes); one row per declaration of include/sparseforge_amd.h
+SIGNATURES = {
+    "sf_last_error": (ctypes.c_char_p, []),
+    "sf_version": (_I, []),
+    "sf_hard_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _I, _I, _P]),
+    "sf_mask_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "sf_score_stats": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _P, _SZ, _P]),
+    "sf_tau_quantile": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _P, _I64, _F, _P, _P, _SZ, _P]),
+    "sf_sample_indices": (_I, [_P, _I64, _I64, ctypes.c_uint64, _P]),
+    "sf_gate_target": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P]),
+    "sf_update_mask": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _P]),
+    "sf_hard_flip_count": (_I, [_P, _P, _I, _I64, _I64, _I, _I, _I, _P, _P]),
+    "sf_effective_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _F, _I, _I, _I, _P]),
+    "sf_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
+    "sf_column_sum": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the HIP library and bind every declared entry point (no GPU needed)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"sparseforge_amd: HIP library not found at {path}; build it with "
+                "`python -m sparseforge_amd.build` (there is no CPU fallback)"
+            )
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def lib() -> ctypes.CDLL:
+    return _lib if _lib is not None else load()
+
+
+def last_error() -> str:
+    msg = lib().sf_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the exception type the reference raises for the same condition."""
+    if rc == SF_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if rc == SF_ERR_INVALID:
+        raise ValueError(msg)
+    if rc == SF_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DT_F32
+    if t.dtype == torch.bfloat16:
+        return DT_BF16
+    raise TypeError(f"sparseforge_amd: unsupported dtype {t.dtype} (float32 / bfloat16 only)")
+
+
+def require_device(*tensors: torch.Tensor | None) -> torch.device:
+    """All given tensors must be contiguous ROCm tensors on one device."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"sparseforge_amd runs on the GPU only; got a tensor on {t.device} (no CPU path exists)"
+            )
+        if not t.is_contiguous():
+            raise ValueError("sparseforge_amd: tensors must be contiguous")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"sparseforge_amd: tensors on different devices ({dev} vs {t.device})")
+    if dev is None:
+        raise ValueError("sparseforge_amd: no tensor given")
+    return dev
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,160 @@
+// Shared device/host helpers for the sparseforge_amd HIP library (gfx950 / CDNA4).
+//
+// Everything here is header-only so that each translation unit of the library
+// inlines it; the C-ABI entry points live in the sf_*.hip files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/sparseforge_amd.h"
+
+namespace sf {
+
+// ---------------------------------------------------------------------------
+// Error plumbing: every entry point returns an SF_* status; the message of the
+// most recent failure on the calling host thread is kept for sf_last_error().
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+
+#define SF_CHECK_ARG(cond, ...)              \
+  do {                                       \
+    if (!(cond)) {                           \
+      ::sf::set_error(__VA_ARGS__);          \
+      return SF_ERR_INVALID;                 \
+    }                                        \
+  } while (0)
+
+#define SF_CHECK_HIP(expr)                                                   \
+  do {                                                                       \
+    hipError_t _e = (expr);                                                  \
+    if (_e != hipSuccess) {                                                  \
+      ::sf::set_error("%s failed: %s", #expr, hipGetErrorString(_e));        \
+      return SF_ERR_HIP;                                                     \
+    }                                                                        \
+  } while (0)
+
+// Status of the most recent launch on this thread (launch-configuration errors).
+inline int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e));
+    return SF_ERR_HIP;
+  }
+  return SF_OK;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 <-> f32, round-to-nearest-even (the rounding torch uses for .to(bf16)).
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  uint32_t u = static_cast<uint32_t>(h) << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Round an f32 to the nearest bf16 and return it as f32.
+__host__ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Load/store one element of a tensor whose dtype is a runtime SF_DTYPE_* code.
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dtype) {
+  return dtype == SF_DTYPE_F32 ? static_cast<const float*>(p)[i]
+                               : bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+__device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dtype, float v) {
+  if (dtype == SF_DTYPE_F32)
+    static_cast<float*>(p)[i] = v;
+  else
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+// ---------------------------------------------------------------------------
+// Total order used for top-N selection inside a group.  torch's CPU topk
+// compares with NaN greater than every number and NaN == NaN, and -0 == +0.
+// ordered_key maps a float to a uint32 with exactly that order.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ uint32_t ordered_key(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN: largest
+  if ((u & 0x7fffffffu) == 0u) u = 0u;                      // -0 == +0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ---------------------------------------------------------------------------
+// Tie table of torch.topk(k) over a group of 4 (CPU kernel of torch 2.10).
+// Index: key = sum_i lt_i << 2i with lt_i = #{j : v_j < v_i}; value: bit i set
+// when member i is kept.  The tables are data measured from torch.topk over
+// all 75 weak orderings of four values; unreachable keys hold 0.
+// ---------------------------------------------------------------------------
+__constant__ static const uint8_t kTopkTies4[3][256] = {
+    {4,0,0,1,0,0,0,0,0,0,2,1,2,0,2,0,0,0,0,0,0,2,0,1,0,0,2,1,0,2,2,0,0,0,1,1,0,0,1,1,2,2,0,0,2,2,0,0,4,0,4,0,0,4,4,0,4,4,0,0,0,0,0,0,
+     0,0,0,0,0,2,0,1,0,0,2,1,0,2,2,0,0,4,0,1,4,0,0,0,0,0,0,0,2,0,0,0,0,0,1,1,0,0,0,0,2,0,0,0,2,0,0,0,0,4,4,0,4,0,0,0,4,0,0,0,0,0,0,0,
+     0,0,8,1,0,0,1,1,2,2,0,0,2,2,0,0,0,0,8,1,0,0,0,0,2,0,0,0,2,0,0,0,4,4,0,0,4,0,0,0,0,0,0,0,0,0,0,0,4,4,0,0,4,0,0,0,0,0,0,0,0,0,0,0,
+     8,0,8,0,0,8,8,0,8,8,0,0,0,0,0,0,0,8,8,0,8,0,0,0,8,0,0,0,0,0,0,0,8,8,0,0,8,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0},
+    {12,0,0,5,0,0,0,0,0,0,3,3,10,0,3,0,0,0,0,0,0,6,0,3,0,0,3,3,0,6,3,0,0,0,5,5,0,0,5,5,6,6,0,0,6,6,0,0,12,0,5,0,0,6,5,0,6,6,0,0,0,0,0,0,
+     0,0,0,0,0,10,0,3,0,0,3,3,0,10,3,0,0,12,0,5,12,0,0,0,0,0,0,0,10,0,0,0,0,0,5,5,0,0,0,0,6,0,0,0,6,0,0,0,0,12,5,0,12,0,0,0,6,0,0,0,0,0,0,0,
+     0,0,9,9,0,0,9,9,10,10,0,0,10,10,0,0,0,0,9,9,0,0,0,0,10,0,0,0,10,0,0,0,12,12,0,0,12,0,0,0,0,0,0,0,0,0,0,0,12,12,0,0,12,0,0,0,0,0,0,0,0,0,0,0,
+     12,0,9,0,0,10,9,0,10,10,0,0,0,0,0,0,0,12,9,0,12,0,0,0,10,0,0,0,0,0,0,0,12,12,0,0,12,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0},
+    {13,0,0,13,0,0,0,0,0,0,11,11,11,0,11,0,0,0,0,0,0,7,0,7,0,0,7,7,0,7,7,0,0,0,13,13,0,0,7,7,7,7,0,0,7,7,0,0,13,0,13,0,0,7,7,0,7,7,0,0,0,0,0,0,
+     0,0,0,0,0,11,0,11,0,0,11,11,0,11,11,0,0,13,0,13,14,0,0,0,0,0,0,0,14,0,0,0,0,0,13,13,0,0,0,0,14,0,0,0,14,0,0,0,0,13,13,0,14,0,0,0,14,0,0,0,0,0,0,0,
+     0,0,13,13,0,0,11,11,14,11,0,0,14,11,0,0,0,0,13,13,0,0,0,0,14,0,0,0,14,0,0,0,13,13,0,0,14,0,0,0,0,0,0,0,0,0,0,0,14,13,0,0,14,0,0,0,0,0,0,0,0,0,0,0,
+     13,0,13,0,0,11,11,0,14,11,0,0,0,0,0,0,0,13,13,0,14,0,0,0,14,0,0,0,0,0,0,0,13,13,0,0,14,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0}};
+
+// Kept members (bitmask over 4) of torch.topk(k) on the group v[0..3].
+__device__ __forceinline__ uint32_t topk4_keep(const float v[4], int k) {
+  uint32_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) key[i] = ordered_key(v[i]);
+  uint32_t idx = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t lt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lt += key[j] < key[i] ? 1u : 0u;
+    idx |= lt << (2 * i);
+  }
+  return kTopkTies4[k - 1][idx];
+}
+
+// k-th largest value of the group (topk(k).values[..., -1]); NaN is largest.
+__device__ __forceinline__ float kth_largest4(const float v[4], int k) {
+  // rank_i = #{j : v_j > v_i} + #{j < i : v_j == v_i}; the member with rank k-1 is it.
+  uint32_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) key[i] = ordered_key(v[i]);
+  float out = v[0];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r += (key[j] > key[i]) || (j < i && key[j] == key[i]);
+    if (r == k - 1) out = v[i];
+  }
+  return out;
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Grid size for a grid-stride elementwise kernel: enough workgroups to fill
+// all 256 CUs several times over, never more than the work needs.
+inline int elementwise_grid(int64_t work_items, int block) {
+  int64_t g = ceil_div(work_items, block);
+  const int64_t cap = 256 * 16;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return static_cast<int>(g);
+}
+
+}  // namespace sf

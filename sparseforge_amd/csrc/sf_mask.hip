@@ -1,0 +1,963 @@
+// Mask construction on gfx950: hard N:M projection (K6), gate target (K7) and
+// the fused periodic mask update (K8) of SparseLinear, plus the score
+// statistics and the unstructured tau quantile they need.
+//
+// Work decomposition: one thread owns one 4-wide group along a row (the N:M
+// group of the 2:4 path), so top-N selection, penalty targets and flip counts
+// are register-local.  Rows with cols % 4 != 0 end in a partial "tail" group,
+// which the reference treats elementwise (nm_2_4 keeps tail columns at 1).
+// Grid-stride loops keep the launch at a fixed size; every kernel is
+// memory-bound and reads each tensor once.
+//
+// Arithmetic follows the reference's op order: each PyTorch op rounds to the
+// dtype of its result, reproduced with rnd(x, dtype); f32 division and sqrt
+// are IEEE correctly rounded in HIP (the default), as on the CPU.
+
+#include <initializer_list>
+#include <utility>
+
+#include "sf_common.hpp"
+#include "sf_rng.hpp"
+
+namespace sf {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float rnd(float x, int dtype) { return dtype == SF_DTYPE_BF16 ? round_bf16(x) : x; }
+__host__ __device__ __forceinline__ int promote(int a, int b) {
+  return (a == SF_DTYPE_F32 || b == SF_DTYPE_F32) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Load up to 4 consecutive elements [i, i + n) as f32; vector path when the
+// group is full and aligned.
+template <int DT>
+__device__ __forceinline__ void load4(const void* base, int64_t i, int n, bool vec, float out[4]) {
+  if (DT == SF_DTYPE_F32) {
+    const float* p = static_cast<const float*>(base) + i;
+    if (vec) {
+      float4 v = *reinterpret_cast<const float4*>(p);
+      out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[j] = j < n ? p[j] : 0.0f;
+    }
+  } else {
+    const uint16_t* p = static_cast<const uint16_t*>(base) + i;
+    if (vec) {
+      uint2 v = *reinterpret_cast<const uint2*>(p);
+      out[0] = bf16_to_f32(v.x & 0xffff); out[1] = bf16_to_f32(v.x >> 16);
+      out[2] = bf16_to_f32(v.y & 0xffff); out[3] = bf16_to_f32(v.y >> 16);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[j] = j < n ? bf16_to_f32(p[j]) : 0.0f;
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store4(void* base, int64_t i, int n, bool vec, const float v[4]) {
+  if (DT == SF_DTYPE_F32) {
+    float* p = static_cast<float*>(base) + i;
+    if (vec) {
+      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < n) p[j] = v[j];
+    }
+  } else {
+    uint16_t* p = static_cast<uint16_t*>(base) + i;
+    if (vec) {
+      uint2 o;
+      o.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+      o.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+      *reinterpret_cast<uint2*>(p) = o;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < n) p[j] = f32_to_bf16(v[j]);
+    }
+  }
+}
+
+// Runtime-dtype variant used for the rarely-used operands (aux, frozen flags).
+__device__ __forceinline__ void load4_any(const void* base, int dtype, int64_t i, int n, bool vec, float out[4]) {
+  if (dtype == SF_DTYPE_F32)
+    load4<SF_DTYPE_F32>(base, i, n, vec, out);
+  else
+    load4<SF_DTYPE_BF16>(base, i, n, vec, out);
+}
+
+// Group geometry: group g of the flattened [rows, ceil(cols/4)] grid.
+struct Group {
+  int64_t row, col, elem;  // first column / flat element of the group
+  int n;                   // valid members (4, or the tail width)
+  bool full;               // n == 4 (a complete N:M group)
+};
+
+__device__ __forceinline__ Group group_at(int64_t g, int64_t cols, int64_t gpr) {
+  Group G;
+  G.row = g / gpr;
+  int64_t gc = g - G.row * gpr;
+  G.col = gc * 4;
+  G.elem = G.row * cols + G.col;
+  int64_t rem = cols - G.col;
+  G.n = rem >= 4 ? 4 : static_cast<int>(rem);
+  G.full = G.n == 4;
+  return G;
+}
+
+// ---------------------------------------------------------------------------
+// Score of one element (legacy/sparse_modeling.py:1041-1079).  w, h, a are the
+// stored values (already widened to f32); each reference op rounds to its
+// result dtype.
+// ---------------------------------------------------------------------------
+struct ScoreSpec {
+  int metric, w_dtype, h_dtype, aux_dtype, score_dtype;
+  float eps, movement_temp;
+};
+
+__device__ __forceinline__ float score_of(const ScoreSpec& s, float w, float h, float a) {
+  switch (s.metric) {
+    case SF_METRIC_HESSIAN_OBD: {  // (H + eps) * (W * W)
+      float hp = rnd(h + s.eps, s.h_dtype);
+      float ww = rnd(w * w, s.w_dtype);
+      return rnd(hp * ww, promote(s.h_dtype, s.w_dtype));
+    }
+    case SF_METRIC_HESSIAN_RATIO: {  // |W| / sqrt(H + eps)
+      float hp = rnd(h + s.eps, s.h_dtype);
+      float sq = rnd(sqrtf(hp), s.h_dtype);
+      return rnd(fabsf(w) / sq, promote(s.h_dtype, s.w_dtype));
+    }
+    case SF_METRIC_HESSIAN:
+      return h;
+    case SF_METRIC_WANDA: {  // |W| * sqrt(scaler + eps)
+      float sp = rnd(a + s.eps, s.aux_dtype);
+      float sq = rnd(sqrtf(sp), s.aux_dtype);
+      return rnd(fabsf(w) * sq, promote(s.aux_dtype, s.w_dtype));
+    }
+    case SF_METRIC_MOVEMENT: {  // |W * g| / max(temperature, eps)
+      int pd = promote(s.w_dtype, s.aux_dtype);
+      float t = fabsf(rnd(w * a, pd));
+      return rnd(t / s.movement_temp, pd);
+    }
+    default:  // magnitude
+      return fabsf(w);
+  }
+}
+
+// Gather the operands of a group and compute the 4 scores.
+template <int WD, int HD>
+__device__ __forceinline__ void group_scores(const ScoreSpec& s, const void* W, const void* H, const void* aux,
+                                             const Group& g, bool vec, int64_t cols, float sc[4]) {
+  float w[4], h[4] = {0, 0, 0, 0}, a[4] = {0, 0, 0, 0};
+  load4<WD>(W, g.elem, g.n, vec, w);
+  if (H) load4<HD>(H, g.elem, g.n, vec, h);
+  if (aux) {
+    if (s.metric == SF_METRIC_WANDA)
+      load4_any(aux, s.aux_dtype, g.col, g.n, vec, a);  // scaler_row [cols]
+    else
+      load4_any(aux, s.aux_dtype, g.elem, g.n, vec, a);  // grad_ema [rows, cols]
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sc[j] = j < g.n ? score_of(s, w[j], h[j], a[j]) : 0.0f;
+}
+
+__device__ __forceinline__ float score_at(const ScoreSpec& s, const void* W, const void* H, const void* aux,
+                                          int64_t e, int64_t cols) {
+  float w = load_as_f32(W, e, s.w_dtype);
+  float h = H ? load_as_f32(H, e, s.h_dtype) : 0.0f;
+  float a = 0.0f;
+  if (aux) a = load_as_f32(aux, s.metric == SF_METRIC_WANDA ? e % cols : e, s.aux_dtype);
+  return score_of(s, w, h, a);
+}
+
+ScoreSpec make_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_dtype) {
+  ScoreSpec s;
+  s.metric = p->metric;
+  s.w_dtype = w_dtype;
+  s.h_dtype = h_dtype;
+  s.aux_dtype = aux_dtype;
+  s.score_dtype = p->score_dtype;
+  s.eps = p->eps_metric;
+  s.movement_temp = p->movement_temp;
+  return s;
+}
+
+// z-normalised score in the score dtype: ((s - mu) / sigma).to(score dtype)  (:1085-1088)
+__device__ __forceinline__ float znorm(float s, float mu, float sigma, int score_dtype) {
+  return rnd((s - mu) / sigma, score_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// K6: hard projection.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void hard_of_group(const float v[4], const Group& g, int kind, int n_keep, float out[4]) {
+  if (kind == SF_HARD_NONE) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = 1.0f;
+  } else if (kind == SF_HARD_THRESHOLD) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = v[j] > 0.5f ? 1.0f : 0.0f;
+  } else {  // N:M over groups of 4; a tail group keeps every column
+    uint32_t keep = g.full ? topk4_keep(v, n_keep) : 0xfu;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = ((keep >> j) & 1u) ? 1.0f : 0.0f;
+  }
+}
+
+template <int SD, int OD>
+__global__ void __launch_bounds__(kBlock) hard_mask_kernel(const void* __restrict__ soft, void* __restrict__ hard,
+                                                           int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                           int kind, int n_keep) {
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    float v[4], o[4];
+    load4<SD>(soft, g.elem, g.n, vec && g.full, v);
+    hard_of_group(v, g, kind, n_keep, o);
+    store4<OD>(hard, g.elem, g.n, vec && g.full, o);
+  }
+}
+
+// Sum of an int64 across the workgroup, then one atomic per workgroup.
+__device__ __forceinline__ void block_add_i64(int64_t v, int64_t* dst) {
+  __shared__ int64_t red[kBlock / 64];
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_down(v, off, 64);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t t = 0;
+    for (int i = 0; i < (int)(blockDim.x / 64); ++i) t += red[i];
+    if (t) atomicAdd(reinterpret_cast<unsigned long long*>(dst), static_cast<unsigned long long>(t));
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kBlock) flip_count_kernel(const void* __restrict__ prev, const void* __restrict__ now,
+                                                            int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                            int kind, int n_keep, int64_t* flips) {
+  int64_t cnt = 0;
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    float a[4], b[4], ha[4], hb[4];
+    load4<DT>(prev, g.elem, g.n, vec && g.full, a);
+    load4<DT>(now, g.elem, g.n, vec && g.full, b);
+    hard_of_group(a, g, kind, n_keep, ha);
+    hard_of_group(b, g, kind, n_keep, hb);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cnt += (j < g.n && ((ha[j] > 0.5f) != (hb[j] > 0.5f))) ? 1 : 0;
+  }
+  block_add_i64(cnt, flips);
+}
+
+// ---------------------------------------------------------------------------
+// Score statistics: per-workgroup f64 partial sums, then one workgroup folds
+// them in a fixed order (deterministic for a fixed grid).
+// ---------------------------------------------------------------------------
+constexpr int kStatsGrid = 1024;
+
+__device__ __forceinline__ void block_sum2_f64(double a, double b, double* out_a, double* out_b) {
+  __shared__ double ra[kBlock / 64], rb[kBlock / 64];
+  for (int off = 32; off > 0; off >>= 1) {
+    a += __shfl_down(a, off, 64);
+    b += __shfl_down(b, off, 64);
+  }
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) {
+    ra[wv] = a;
+    rb[wv] = b;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double ta = 0, tb = 0;
+    for (int i = 0; i < (int)(blockDim.x / 64); ++i) {
+      ta += ra[i];
+      tb += rb[i];
+    }
+    *out_a = ta;
+    *out_b = tb;
+  }
+}
+
+template <int WD, int HD>
+__global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, const void* __restrict__ W,
+                                                               const void* __restrict__ H, const void* __restrict__ aux,
+                                                               int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                               double* partial) {
+  double sum = 0.0, sq = 0.0;
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    float sc[4];
+    group_scores<WD, HD>(s, W, H, aux, g, vec && g.full, cols, sc);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < g.n) {
+        double d = sc[j];
+        sum += d;
+        sq += d * d;
+      }
+  }
+  block_sum2_f64(sum, sq, &partial[2 * blockIdx.x], &partial[2 * blockIdx.x + 1]);
+}
+
+__global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __restrict__ partial, int nparts,
+                                                             int64_t n, float* stats) {
+  double sum = 0.0, sq = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+    sum += partial[2 * i];
+    sq += partial[2 * i + 1];
+  }
+  __shared__ double tot[2];
+  block_sum2_f64(sum, sq, &tot[0], &tot[1]);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double mean = tot[0] / (double)n;
+    double var = tot[1] / (double)n - mean * mean;
+    if (var < 0.0) var = 0.0;
+    stats[0] = static_cast<float>(mean);
+    stats[1] = static_cast<float>(sqrt(var)) + 1e-6f;  // std(unbiased=False) + 1e-6 in f32
+  }
+}
+
+// ---------------------------------------------------------------------------
+// tau quantile: gather z at the sample indices as order-preserving uint32
+// keys, then a single-workgroup 4 x 8-bit radix select of the two order
+// statistics around rank q * (n - 1) and torch.lerp between them.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kBlock) tau_gather_kernel(ScoreSpec s, const void* __restrict__ W,
+                                                            const void* __restrict__ H, const void* __restrict__ aux,
+                                                            int64_t rows, int64_t cols, const float* __restrict__ stats,
+                                                            const int64_t* __restrict__ idx, int64_t m,
+                                                            uint32_t* __restrict__ keys) {
+  const float mu = stats[0], sigma = stats[1];
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t e = idx ? idx[i] : i;
+    const int64_t n = cols * rows;
+    e = e < 0 ? 0 : (e >= n ? n - 1 : e);  // indices outside the layer are clamped, never dereferenced
+    float z = znorm(score_at(s, W, H, aux, e, cols), mu, sigma, s.score_dtype);
+    keys[i] = ordered_key(z);
+  }
+}
+
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  if (k == 0xffffffffu) u = 0x7fc00000u;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+constexpr int kSelectBlock = 1024;
+
+__global__ void __launch_bounds__(kSelectBlock) tau_select_kernel(const uint32_t* __restrict__ keys, int64_t m,
+                                                                  float q, float* tau) {
+  __shared__ uint32_t hist[2][256];
+  __shared__ uint32_t sel[2];
+  __shared__ int64_t krem[2];
+  __shared__ int any_nan;
+  // torch.quantile: rank = q * (n - 1) in f32; NaN anywhere -> last index.
+  if (threadIdx.x == 0) any_nan = 0;
+  __syncthreads();
+  int local_nan = 0;
+  for (int64_t i = threadIdx.x; i < m; i += blockDim.x) local_nan |= keys[i] == 0xffffffffu;
+  if (local_nan) atomicOr(&any_nan, 1);
+  __syncthreads();
+  const int64_t last = m - 1;
+  float rank = q * static_cast<float>(last);
+  if (any_nan) rank = static_cast<float>(last);
+  const int64_t lo = static_cast<int64_t>(rank);
+  const int64_t hi = static_cast<int64_t>(ceilf(rank));
+  const float wgt = rank - static_cast<float>(lo);
+  if (threadIdx.x == 0) {
+    sel[0] = sel[1] = 0u;
+    krem[0] = lo;
+    krem[1] = hi;
+  }
+  uint32_t pmask = 0u;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = threadIdx.x; i < 512; i += blockDim.x) (&hist[0][0])[i] = 0u;
+    __syncthreads();
+    const uint32_t p0 = sel[0], p1 = sel[1];
+    for (int64_t i = threadIdx.x; i < m; i += blockDim.x) {
+      uint32_t k = keys[i];
+      uint32_t d = (k >> shift) & 0xffu;
+      if ((k & pmask) == p0) atomicAdd(&hist[0][d], 1u);
+      if ((k & pmask) == p1) atomicAdd(&hist[1][d], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+      const int t = threadIdx.x;
+      int64_t r = krem[t];
+      uint32_t d = 0;
+      for (; d < 256; ++d) {
+        if (r < (int64_t)hist[t][d]) break;
+        r -= hist[t][d];
+      }
+      krem[t] = r;
+      sel[t] |= d << shift;
+    }
+    pmask |= 0xffu << shift;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float a = key_to_float(sel[0]), b = key_to_float(sel[1]);
+    // torch lerp: small weight -> a + w (b - a); else b - (b - a)(1 - w)
+    float r = fabsf(wgt) < 0.5f ? a + wgt * (b - a) : b - (b - a) * (1.0f - wgt);
+    *tau = r;
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) sample_indices_kernel(int64_t* idx, int64_t m, uint64_t n, uint64_t seed) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m; i += (int64_t)gridDim.x * blockDim.x)
+    idx[i] = static_cast<int64_t>(uniform_below(counter_hash(seed, static_cast<uint64_t>(i)), n));
+}
+
+// ---------------------------------------------------------------------------
+// K7 / K8: gate target of one group, and the fused update.
+// ---------------------------------------------------------------------------
+struct GateSpec {
+  ScoreSpec s;
+  int gate, n_keep;
+  int has_frozen;
+  int mask_dtype, frozen_dtype;
+  float denom;        // T + 1e-8 in f32
+  float beta_struct;  // 0 disables the mix
+  float one_minus_beta;
+};
+
+// G of one group (compute_gate_target, :1083-1229).  mprev / frz: current mask
+// and frozen flags of the group (frz only read when has_frozen).
+__device__ __forceinline__ void gate_of_group(const GateSpec& gs, const float sc[4], const Group& g, float mu,
+                                              float sigma, float tau, const float mprev[4], const float frz[4],
+                                              float G[4]) {
+  const int sd = gs.s.score_dtype;
+  float z[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) z[j] = znorm(sc[j], mu, sigma, sd);
+  if (gs.gate == SF_GATE_UNSTRUCTURED) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) G[j] = rnd(sigmoidf_((z[j] - tau) / gs.denom), sd);
+  } else if (gs.gate == SF_GATE_STRUCTURED) {
+    float tg = kth_largest4(z, gs.n_keep);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) G[j] = rnd(sigmoidf_((z[j] - tg) / gs.denom), sd);
+  } else {  // structured exact
+    uint32_t keep = topk4_keep(z, gs.n_keep);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) G[j] = ((keep >> j) & 1u) ? 1.0f : 0.0f;
+  }
+  if (gs.beta_struct > 0.0f) {  // (:1199-1225): target = topN(z) on full groups, G itself on the tail
+    uint32_t keep = g.full ? topk4_keep(z, gs.n_keep) : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float t = g.full ? (((keep >> j) & 1u) ? 1.0f : 0.0f) : G[j];
+      G[j] = rnd(gs.one_minus_beta * G[j] + gs.beta_struct * t, sd);
+    }
+  }
+  if (gs.has_frozen) {  // G[frozen] = mask[frozen]  (:1227-1229)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (frz[j] != 0.0f) G[j] = rnd(mprev[j], sd);
+  }
+}
+
+template <int WD, int HD>
+__global__ void __launch_bounds__(kBlock) gate_target_kernel(GateSpec gs, const void* __restrict__ W,
+                                                             const void* __restrict__ H, const void* __restrict__ aux,
+                                                             const void* __restrict__ mask,
+                                                             const void* __restrict__ frozen,
+                                                             const float* __restrict__ stats,
+                                                             const float* __restrict__ tau_p, void* __restrict__ Gout,
+                                                             int g_dtype, int64_t cols, int64_t groups, int64_t gpr,
+                                                             bool vec) {
+  const float mu = stats[0], sigma = stats[1];
+  const float tau = tau_p ? *tau_p : 0.0f;
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    const bool v = vec && g.full;
+    float sc[4], mp[4] = {0, 0, 0, 0}, fz[4] = {0, 0, 0, 0}, G[4];
+    group_scores<WD, HD>(gs.s, W, H, aux, g, v, cols, sc);
+    if (gs.has_frozen) {
+      load4_any(frozen, gs.frozen_dtype, g.elem, g.n, v, fz);
+      load4_any(mask, gs.mask_dtype, g.elem, g.n, v, mp);
+    }
+    gate_of_group(gs, sc, g, mu, sigma, tau, mp, fz, G);
+    if (g_dtype == SF_DTYPE_F32)
+      store4<SF_DTYPE_F32>(Gout, g.elem, g.n, v, G);
+    else
+      store4<SF_DTYPE_BF16>(Gout, g.elem, g.n, v, G);
+  }
+}
+
+struct UpdateSpec {
+  GateSpec gs;
+  int penalty, pen_n;
+  float pen_coef;
+  float bin_lo, bin_hi;  // (1 - d), (1 + d) in f32; d == 0 disables
+  int binarize;
+  float keep_a, a;  // (1 - a), a
+  int apply_freeze, snap_high;
+  float freeze_low, freeze_high;
+  int hard_kind, hard_n;
+};
+
+template <int WD, int HD, int MD>
+__global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, const void* __restrict__ W,
+                                                             const void* __restrict__ H, const void* __restrict__ aux,
+                                                             void* __restrict__ mask, void* __restrict__ frozen,
+                                                             const float* __restrict__ stats,
+                                                             const float* __restrict__ tau_p, int64_t cols,
+                                                             int64_t groups, int64_t gpr, bool vec, int64_t* flips) {
+  const GateSpec& gs = us.gs;
+  const int sd = gs.s.score_dtype;
+  const float mu = stats[0], sigma = stats[1];
+  const float tau = tau_p ? *tau_p : 0.0f;
+  int64_t cnt = 0;
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    const bool v = vec && g.full;
+    float sc[4], mp[4], fz[4] = {0, 0, 0, 0}, G[4];
+    group_scores<WD, HD>(gs.s, W, H, aux, g, v, cols, sc);
+    load4<MD>(mask, g.elem, g.n, v, mp);
+    if (gs.has_frozen) load4_any(frozen, gs.frozen_dtype, g.elem, g.n, v, fz);
+    gate_of_group(gs, sc, g, mu, sigma, tau, mp, fz, G);
+
+    // penalty pull toward a target, then clamp (:1291-1573)
+    if (us.penalty != SF_PENALTY_NONE) {
+      if (us.penalty == SF_PENALTY_MID) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float pg = rnd(rnd(1.0f - 2.0f * mp[j], MD), sd);
+          G[j] = rnd(G[j] - rnd(us.pen_coef * pg, sd), sd);
+        }
+      } else {  // nm_2_4 / structured_topn: target = topN(G) on full groups, 1 on the tail
+        uint32_t keep = g.full ? topk4_keep(G, us.pen_n) : 0xfu;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float t = ((keep >> j) & 1u) ? 1.0f : 0.0f;
+          float delta = rnd(rnd(mp[j], sd) - t, sd);
+          G[j] = rnd(G[j] - rnd(us.pen_coef * delta, sd), sd);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) G[j] = fminf(fmaxf(G[j], 0.0f), 1.0f);
+    }
+    // multiplicative binarisation push (:1576-1590)
+    if (us.binarize) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (G[j] < 0.5f)
+          G[j] = rnd(G[j] * us.bin_lo, sd);
+        else if (G[j] > 0.5f)
+          G[j] = rnd(G[j] * us.bin_hi, sd);
+      }
+    }
+    // EMA: mask.mul_(1 - a).add_(G, alpha=a).clamp_(0, 1)  (:1593)
+    float mn[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float m1 = rnd(mp[j] * us.keep_a, MD);
+      float m2 = rnd(fmaf(G[j], us.a, m1), MD);
+      mn[j] = fminf(fmaxf(m2, 0.0f), 1.0f);
+    }
+    // freeze snaps and flags (:1621-1642)
+    if (us.apply_freeze) {
+      float fl[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        bool f0 = mn[j] <= us.freeze_low;
+        bool f1 = mn[j] >= us.freeze_high;
+        bool applied = f0;
+        if (f0) mn[j] = 0.0f;
+        if (us.snap_high) {
+          if (f1) mn[j] = 1.0f;
+          applied = applied || f1;
+        }
+        fl[j] = fmaxf(fz[j], applied ? 1.0f : 0.0f);
+      }
+      if (gs.has_frozen) {
+        if (gs.frozen_dtype == SF_DTYPE_F32)
+          store4<SF_DTYPE_F32>(frozen, g.elem, g.n, v, fl);
+        else
+          store4<SF_DTYPE_BF16>(frozen, g.elem, g.n, v, fl);
+      }
+    }
+    store4<MD>(mask, g.elem, g.n, v, mn);
+    // flips of the hard view (:1659-1661)
+    if (flips) {
+      float ha[4], hb[4];
+      hard_of_group(mp, g, us.hard_kind, us.hard_n, ha);
+      hard_of_group(mn, g, us.hard_kind, us.hard_n, hb);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cnt += (j < g.n && ((ha[j] > 0.5f) != (hb[j] > 0.5f))) ? 1 : 0;
+    }
+  }
+  if (flips) block_add_i64(cnt, flips);
+}
+
+// ---------------------------------------------------------------------------
+// host-side helpers
+// ---------------------------------------------------------------------------
+bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+bool dtype_ok(int d) { return d == SF_DTYPE_F32 || d == SF_DTYPE_BF16; }
+int esize(int d) { return d == SF_DTYPE_F32 ? 4 : 2; }
+
+// vector loads need cols % 4 == 0 and 4-element alignment of every operand
+bool vec_ok(int64_t cols, std::initializer_list<std::pair<const void*, int>> ops) {
+  if (cols % 4 != 0) return false;
+  for (auto& o : ops)
+    if (o.first && !aligned(o.first, 4 * esize(o.second))) return false;
+  return true;
+}
+
+int check_common(const sf_mask_params* p) {
+  SF_CHECK_ARG(p != nullptr, "null sf_mask_params");
+  SF_CHECK_ARG(p->rows >= 0 && p->cols >= 0, "negative shape [%lld, %lld]", (long long)p->rows, (long long)p->cols);
+  SF_CHECK_ARG(p->metric >= SF_METRIC_MAGNITUDE && p->metric <= SF_METRIC_MOVEMENT, "bad metric %d", p->metric);
+  SF_CHECK_ARG(dtype_ok(p->score_dtype), "bad score dtype %d", p->score_dtype);
+  return SF_OK;
+}
+
+int check_metric_operands(const sf_mask_params* p, const void* H, const void* aux) {
+  const int m = p->metric;
+  if (m == SF_METRIC_HESSIAN_OBD || m == SF_METRIC_HESSIAN_RATIO || m == SF_METRIC_HESSIAN)
+    SF_CHECK_ARG(H != nullptr, "metric %d needs hessian_diag", m);
+  if (m == SF_METRIC_WANDA || m == SF_METRIC_MOVEMENT) SF_CHECK_ARG(aux != nullptr, "metric %d needs aux tensor", m);
+  return SF_OK;
+}
+
+#define SF_DISPATCH_WH(wd, hd, ...)                                              \
+  do {                                                                           \
+    if ((wd) == SF_DTYPE_F32 && (hd) == SF_DTYPE_F32) {                          \
+      constexpr int WD_ = SF_DTYPE_F32, HD_ = SF_DTYPE_F32;                      \
+      __VA_ARGS__;                                                               \
+    } else if ((wd) == SF_DTYPE_F32) {                                           \
+      constexpr int WD_ = SF_DTYPE_F32, HD_ = SF_DTYPE_BF16;                     \
+      __VA_ARGS__;                                                               \
+    } else if ((hd) == SF_DTYPE_F32) {                                           \
+      constexpr int WD_ = SF_DTYPE_BF16, HD_ = SF_DTYPE_F32;                     \
+      __VA_ARGS__;                                                               \
+    } else {                                                                     \
+      constexpr int WD_ = SF_DTYPE_BF16, HD_ = SF_DTYPE_BF16;                    \
+      __VA_ARGS__;                                                               \
+    }                                                                            \
+  } while (0)
+
+}  // namespace
+}  // namespace sf
+
+using namespace sf;
+
+extern "C" int sf_hard_mask(const void* soft, int soft_dtype, void* hard, int hard_dtype, int64_t rows, int64_t cols,
+                            int kind, int n_keep, int m_group, void* stream) {
+  SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  SF_CHECK_ARG(dtype_ok(soft_dtype) && dtype_ok(hard_dtype), "bad dtype");
+  SF_CHECK_ARG(kind >= SF_HARD_NONE && kind <= SF_HARD_NM_STRICT, "bad hard kind %d", kind);
+  if (rows == 0 || cols == 0) return SF_OK;
+  SF_CHECK_ARG(soft && hard, "null tensor");
+  if (kind == SF_HARD_NM_TAIL_KEEP || kind == SF_HARD_NM_STRICT) {
+    if (m_group != 4 || n_keep < 1 || n_keep > 3) {
+      set_error("N:M hard mask with N=%d M=%d: only M=4, 1<=N<=3 is built on device", n_keep, m_group);
+      return SF_ERR_UNSUPPORTED;
+    }
+    SF_CHECK_ARG(kind != SF_HARD_NM_STRICT || cols % m_group == 0,
+                 "in_features (%lld) must be divisible by M (%d).", (long long)cols, m_group);
+  }
+  const int64_t gpr = ceil_div(cols, 4), groups = rows * gpr;
+  const bool vec = vec_ok(cols, {{soft, soft_dtype}, {hard, hard_dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+#define SF_LAUNCH_HARD(SDT, ODT) \
+  hard_mask_kernel<SDT, ODT><<<grid, kBlock, 0, st>>>(soft, hard, cols, groups, gpr, vec, kind, n_keep)
+  if (soft_dtype == SF_DTYPE_F32 && hard_dtype == SF_DTYPE_F32) SF_LAUNCH_HARD(SF_DTYPE_F32, SF_DTYPE_F32);
+  else if (soft_dtype == SF_DTYPE_F32) SF_LAUNCH_HARD(SF_DTYPE_F32, SF_DTYPE_BF16);
+  else if (hard_dtype == SF_DTYPE_F32) SF_LAUNCH_HARD(SF_DTYPE_BF16, SF_DTYPE_F32);
+  else SF_LAUNCH_HARD(SF_DTYPE_BF16, SF_DTYPE_BF16);
+#undef SF_LAUNCH_HARD
+  return launch_status("sf_hard_mask");
+}
+
+extern "C" int sf_hard_flip_count(const void* prev, const void* now, int dtype, int64_t rows, int64_t cols, int kind,
+                                  int n_keep, int m_group, int64_t* flips, void* stream) {
+  SF_CHECK_ARG(rows >= 0 && cols >= 0 && dtype_ok(dtype), "bad shape or dtype");
+  SF_CHECK_ARG(flips != nullptr, "null flips counter");
+  SF_CHECK_ARG(kind >= SF_HARD_NONE && kind <= SF_HARD_NM_STRICT, "bad hard kind %d", kind);
+  if (rows == 0 || cols == 0) return SF_OK;
+  SF_CHECK_ARG(prev && now, "null tensor");
+  if (kind >= SF_HARD_NM_TAIL_KEEP && (m_group != 4 || n_keep < 1 || n_keep > 3)) {
+    set_error("N:M flip count with N=%d M=%d: only M=4 is built on device", n_keep, m_group);
+    return SF_ERR_UNSUPPORTED;
+  }
+  const int64_t gpr = ceil_div(cols, 4), groups = rows * gpr;
+  const bool vec = vec_ok(cols, {{prev, dtype}, {now, dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  if (dtype == SF_DTYPE_F32)
+    flip_count_kernel<SF_DTYPE_F32><<<grid, kBlock, 0, st>>>(prev, now, cols, groups, gpr, vec, kind, n_keep, flips);
+  else
+    flip_count_kernel<SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(prev, now, cols, groups, gpr, vec, kind, n_keep, flips);
+  return launch_status("sf_hard_flip_count");
+}
+
+extern "C" size_t sf_mask_workspace_size(int64_t rows, int64_t cols, int64_t sample_size) {
+  (void)rows;
+  (void)cols;
+  size_t stats = sizeof(double) * 2 * kStatsGrid;
+  size_t keys = sizeof(uint32_t) * static_cast<size_t>(sample_size > 0 ? sample_size : 0);
+  return ((stats + 255) / 256) * 256 + keys;
+}
+
+extern "C" int sf_score_stats(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                              const void* aux, int aux_dtype, float* stats_out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (int rc = check_common(p)) return rc;
+  if (int rc = check_metric_operands(p, H, aux)) return rc;
+  SF_CHECK_ARG(dtype_ok(w_dtype) && (!H || dtype_ok(h_dtype)) && (!aux || dtype_ok(aux_dtype)), "bad dtype");
+  SF_CHECK_ARG(W && stats_out, "null tensor");
+  SF_CHECK_ARG(workspace && workspace_bytes >= sizeof(double) * 2 * kStatsGrid, "workspace too small");
+  const int64_t n = p->rows * p->cols;
+  SF_CHECK_ARG(n > 0, "empty score tensor");
+  if (!H) h_dtype = SF_DTYPE_F32;
+  ScoreSpec s = make_spec(p, w_dtype, h_dtype, aux_dtype);
+  const int64_t gpr = ceil_div(p->cols, 4), groups = p->rows * gpr;
+  const bool vec = vec_ok(p->cols, {{W, w_dtype}, {H, h_dtype}}) &&
+                   (!aux || p->metric != SF_METRIC_MOVEMENT || aligned(aux, 4 * esize(aux_dtype))) &&
+                   (!aux || p->metric != SF_METRIC_WANDA || aligned(aux, 4 * esize(aux_dtype)));
+  double* partial = static_cast<double*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  SF_DISPATCH_WH(w_dtype, h_dtype,
+                 stats_partial_kernel<WD_, HD_><<<kStatsGrid, kBlock, 0, st>>>(s, W, H, aux, p->cols, groups, gpr, vec,
+                                                                              partial));
+  stats_final_kernel<<<1, kBlock, 0, st>>>(partial, kStatsGrid, n, stats_out);
+  return launch_status("sf_score_stats");
+}
+
+extern "C" int sf_sample_indices(int64_t* idx, int64_t sample_size, int64_t n, uint64_t seed, void* stream) {
+  SF_CHECK_ARG(sample_size >= 0 && n > 0, "bad sample size %lld / n %lld", (long long)sample_size, (long long)n);
+  if (sample_size == 0) return SF_OK;
+  SF_CHECK_ARG(idx != nullptr, "null index tensor");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  sample_indices_kernel<<<elementwise_grid(sample_size, kBlock), kBlock, 0, st>>>(idx, sample_size,
+                                                                                   static_cast<uint64_t>(n), seed);
+  return launch_status("sf_sample_indices");
+}
+
+extern "C" int sf_tau_quantile(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                               const void* aux, int aux_dtype, const float* stats, const int64_t* sample_idx,
+                               int64_t sample_size, float q, float* tau_out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (int rc = check_common(p)) return rc;
+  if (int rc = check_metric_operands(p, H, aux)) return rc;
+  SF_CHECK_ARG(W && stats && tau_out, "null tensor");
+  SF_CHECK_ARG(sample_size > 0, "empty tau sample");
+  SF_CHECK_ARG(sample_idx || sample_size == p->rows * p->cols, "sample_size must equal numel without indices");
+  SF_CHECK_ARG(workspace && workspace_bytes >= sf_mask_workspace_size(p->rows, p->cols, sample_size),
+               "workspace too small");
+  if (!H) h_dtype = SF_DTYPE_F32;
+  ScoreSpec s = make_spec(p, w_dtype, h_dtype, aux_dtype);
+  size_t off = ((sizeof(double) * 2 * kStatsGrid + 255) / 256) * 256;
+  uint32_t* keys = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + off);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  tau_gather_kernel<<<elementwise_grid(sample_size, kBlock), kBlock, 0, st>>>(s, W, H, aux, p->rows, p->cols, stats,
+                                                                               sample_idx, sample_size, keys);
+  tau_select_kernel<<<1, kSelectBlock, 0, st>>>(keys, sample_size, q, tau_out);
+  return launch_status("sf_tau_quantile");
+}
+
+namespace sf {
+namespace {
+int make_gate_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_dtype, int mask_dtype, int frozen_dtype,
+                   GateSpec* gs) {
+  SF_CHECK_ARG(p->gate >= SF_GATE_UNSTRUCTURED && p->gate <= SF_GATE_STRUCTURED_EXACT, "bad gate %d", p->gate);
+  if (p->gate != SF_GATE_UNSTRUCTURED || p->beta_struct > 0.0f) {
+    if (p->m_group != 4 || p->n_keep < 1 || p->n_keep > 3) {
+      set_error("structured gate with N=%d M=%d: only M=4 is built on device", p->n_keep, p->m_group);
+      return SF_ERR_UNSUPPORTED;
+    }
+  }
+  if (p->gate != SF_GATE_UNSTRUCTURED)
+    SF_CHECK_ARG(p->cols % p->m_group == 0, "in_features (%lld) must be divisible by M (%d).", (long long)p->cols,
+                 p->m_group);
+  gs->s = make_spec(p, w_dtype, h_dtype, aux_dtype);
+  gs->gate = p->gate;
+  gs->n_keep = p->n_keep;
+  gs->has_frozen = p->has_frozen;
+  gs->mask_dtype = mask_dtype;
+  gs->frozen_dtype = frozen_dtype;
+  gs->denom = p->temperature + 1e-8f;
+  gs->beta_struct = p->beta_struct;
+  gs->one_minus_beta = static_cast<float>(1.0 - static_cast<double>(p->beta_struct));
+  return SF_OK;
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" int sf_gate_target(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                              const void* aux, int aux_dtype, const void* mask, int mask_dtype, const void* frozen,
+                              int frozen_dtype, const float* stats, const float* tau, void* G, int g_dtype,
+                              void* stream) {
+  if (int rc = check_common(p)) return rc;
+  if (int rc = check_metric_operands(p, H, aux)) return rc;
+  SF_CHECK_ARG(W && stats && G, "null tensor");
+  SF_CHECK_ARG(dtype_ok(w_dtype) && dtype_ok(g_dtype), "bad dtype");
+  SF_CHECK_ARG(p->gate != SF_GATE_UNSTRUCTURED || tau != nullptr, "unstructured gate needs tau");
+  SF_CHECK_ARG(!p->has_frozen || (frozen && mask), "frozen override needs mask and frozen flags");
+  if (!H) h_dtype = SF_DTYPE_F32;
+  GateSpec gs;
+  if (int rc = make_gate_spec(p, w_dtype, h_dtype, aux_dtype, mask_dtype, frozen_dtype, &gs)) return rc;
+  if (p->rows == 0 || p->cols == 0) return SF_OK;
+  const int64_t gpr = ceil_div(p->cols, 4), groups = p->rows * gpr;
+  const bool vec = vec_ok(p->cols, {{W, w_dtype}, {H, h_dtype}, {G, g_dtype}, {mask, mask_dtype},
+                                    {p->has_frozen ? frozen : nullptr, frozen_dtype}}) &&
+                   (!aux || aligned(aux, 4 * esize(aux_dtype)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  SF_DISPATCH_WH(w_dtype, h_dtype,
+                 gate_target_kernel<WD_, HD_><<<grid, kBlock, 0, st>>>(gs, W, H, aux, mask, frozen, stats, tau, G,
+                                                                      g_dtype, p->cols, groups, gpr, vec));
+  return launch_status("sf_gate_target");
+}
+
+extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                              const void* aux, int aux_dtype, void* mask, int mask_dtype, void* frozen,
+                              int frozen_dtype, const float* stats, const float* tau, int64_t* flips, void* stream) {
+  if (int rc = check_common(p)) return rc;
+  if (int rc = check_metric_operands(p, H, aux)) return rc;
+  SF_CHECK_ARG(W && stats && mask, "null tensor");
+  SF_CHECK_ARG(dtype_ok(w_dtype) && dtype_ok(mask_dtype), "bad dtype");
+  SF_CHECK_ARG(p->gate != SF_GATE_UNSTRUCTURED || tau != nullptr, "unstructured gate needs tau");
+  SF_CHECK_ARG(!p->has_frozen || frozen, "has_frozen without frozen flags");
+  SF_CHECK_ARG(p->penalty >= SF_PENALTY_NONE && p->penalty <= SF_PENALTY_STRUCTURED_TOPN, "bad penalty %d", p->penalty);
+  SF_CHECK_ARG(p->hard_kind >= SF_HARD_NONE && p->hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", p->hard_kind);
+  if (!H) h_dtype = SF_DTYPE_F32;
+  UpdateSpec us;
+  if (int rc = make_gate_spec(p, w_dtype, h_dtype, aux_dtype, mask_dtype, frozen_dtype, &us.gs)) return rc;
+  us.penalty = p->penalty_coef != 0.0f ? p->penalty : SF_PENALTY_NONE;
+  us.pen_n = p->n_keep;
+  if (us.penalty == SF_PENALTY_NM_2_4) us.pen_n = 2;
+  if (us.penalty == SF_PENALTY_NM_2_4 || us.penalty == SF_PENALTY_STRUCTURED_TOPN) {
+    if (us.penalty == SF_PENALTY_STRUCTURED_TOPN && (p->m_group != 4 || p->n_keep < 1 || p->n_keep > 3)) {
+      set_error("structured_topn penalty with N=%d M=%d: only M=4 is built on device", p->n_keep, p->m_group);
+      return SF_ERR_UNSUPPORTED;
+    }
+    SF_CHECK_ARG(us.penalty != SF_PENALTY_STRUCTURED_TOPN || p->cols % 4 == 0,
+                 "structured_topn penalty needs cols % M == 0 (the caller falls back to mid)");
+  }
+  us.pen_coef = p->penalty_coef;
+  us.binarize = p->binarize != 0.0f;
+  us.bin_lo = static_cast<float>(1.0 - static_cast<double>(p->binarize));
+  us.bin_hi = static_cast<float>(1.0 + static_cast<double>(p->binarize));
+  us.keep_a = static_cast<float>(1.0 - static_cast<double>(p->mask_lr));
+  // torch converts add_'s alpha to the op's dtype: bf16 when mask and G are both bf16
+  us.a = (mask_dtype == SF_DTYPE_BF16 && p->score_dtype == SF_DTYPE_BF16) ? round_bf16(p->mask_lr) : p->mask_lr;
+  us.apply_freeze = p->apply_freeze;
+  us.snap_high = p->snap_high;
+  us.freeze_low = p->freeze_low;
+  us.freeze_high = p->freeze_high;
+  us.hard_kind = p->hard_kind;
+  us.hard_n = p->hard_n;
+  if (p->hard_kind >= SF_HARD_NM_TAIL_KEEP && flips) {
+    if (p->hard_m != 4 || p->hard_n < 1 || p->hard_n > 3) {
+      set_error("flip count with N=%d M=%d: only M=4 is built on device", p->hard_n, p->hard_m);
+      return SF_ERR_UNSUPPORTED;
+    }
+    SF_CHECK_ARG(p->hard_kind != SF_HARD_NM_STRICT || p->cols % 4 == 0,
+                 "in_features (%lld) must be divisible by M (%d).", (long long)p->cols, p->hard_m);
+  }
+  if (p->rows == 0 || p->cols == 0) return SF_OK;
+  const int64_t gpr = ceil_div(p->cols, 4), groups = p->rows * gpr;
+  const bool vec = vec_ok(p->cols, {{W, w_dtype}, {H, h_dtype}, {mask, mask_dtype},
+                                    {p->has_frozen ? frozen : nullptr, frozen_dtype}}) &&
+                   (!aux || aligned(aux, 4 * esize(aux_dtype)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+#define SF_LAUNCH_UPD(MDT)                                                                                   \
+  SF_DISPATCH_WH(w_dtype, h_dtype,                                                                           \
+                 update_mask_kernel<WD_, HD_, MDT><<<grid, kBlock, 0, st>>>(us, W, H, aux, mask, frozen, stats, \
+                                                                            tau, p->cols, groups, gpr, vec, flips))
+  if (mask_dtype == SF_DTYPE_F32)
+    SF_LAUNCH_UPD(SF_DTYPE_F32);
+  else
+    SF_LAUNCH_UPD(SF_DTYPE_BF16);
+#undef SF_LAUNCH_UPD
+  return launch_status("sf_update_mask");
+}
+
+// ---------------------------------------------------------------------------
+// Effective mask of a forward call (SparseLinear.forward, :759-771 and
+// FusedMaskedLinearSTE.forward, :72-73): E = mask.to(weight dtype), or with
+// hardening E = (hx * mask + (1 - hx) * hard(mask)).to(weight dtype), each
+// product and the sum rounded in the mask dtype.
+// ---------------------------------------------------------------------------
+namespace sf {
+namespace {
+template <int MD, int ED>
+__global__ void __launch_bounds__(kBlock) effective_mask_kernel(const void* __restrict__ mask, void* __restrict__ eff,
+                                                                int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                                int mix, float hx, float one_minus_hx, int kind,
+                                                                int n_keep) {
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    const bool v = vec && g.full;
+    float m[4], e[4];
+    load4<MD>(mask, g.elem, g.n, v, m);
+    if (mix) {
+      float h[4];
+      hard_of_group(m, g, kind, n_keep, h);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] = rnd(rnd(hx * m[j], MD) + rnd(one_minus_hx * h[j], MD), MD);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] = m[j];
+    }
+    store4<ED>(eff, g.elem, g.n, v, e);
+  }
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, int eff_dtype, int64_t rows,
+                                 int64_t cols, int mode, float hx, int hard_kind, int hard_n, int hard_m,
+                                 void* stream) {
+  SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  SF_CHECK_ARG(dtype_ok(mask_dtype) && dtype_ok(eff_dtype), "bad dtype");
+  SF_CHECK_ARG(mode == SF_EFF_SOFT || mode == SF_EFF_MIX, "bad effective-mask mode %d", mode);
+  SF_CHECK_ARG(hard_kind >= SF_HARD_NONE && hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", hard_kind);
+  if (rows == 0 || cols == 0) return SF_OK;
+  SF_CHECK_ARG(mask && eff, "null tensor");
+  if (mode == SF_EFF_MIX && hard_kind >= SF_HARD_NM_TAIL_KEEP) {
+    if (hard_m != 4 || hard_n < 1 || hard_n > 3) {
+      set_error("N:M hard mask with N=%d M=%d: only M=4 is built on device", hard_n, hard_m);
+      return SF_ERR_UNSUPPORTED;
+    }
+    SF_CHECK_ARG(hard_kind != SF_HARD_NM_STRICT || cols % 4 == 0, "in_features (%lld) must be divisible by M (%d).",
+                 (long long)cols, hard_m);
+  }
+  const int64_t gpr = ceil_div(cols, 4), groups = rows * gpr;
+  const bool vec = vec_ok(cols, {{mask, mask_dtype}, {eff, eff_dtype}});
+  // (1 - hx) computed in double as in Python, then the f32 scalar of the op
+  const float omh = static_cast<float>(1.0 - static_cast<double>(hx));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  const int mix = mode == SF_EFF_MIX;
+#define SF_LAUNCH_EFF(MDT, EDT)                                                                              \
+  effective_mask_kernel<MDT, EDT><<<grid, kBlock, 0, st>>>(mask, eff, cols, groups, gpr, vec, mix, hx, omh, \
+                                                           hard_kind, hard_n)
+  if (mask_dtype == SF_DTYPE_F32 && eff_dtype == SF_DTYPE_F32) SF_LAUNCH_EFF(SF_DTYPE_F32, SF_DTYPE_F32);
+  else if (mask_dtype == SF_DTYPE_F32) SF_LAUNCH_EFF(SF_DTYPE_F32, SF_DTYPE_BF16);
+  else if (eff_dtype == SF_DTYPE_F32) SF_LAUNCH_EFF(SF_DTYPE_BF16, SF_DTYPE_F32);
+  else SF_LAUNCH_EFF(SF_DTYPE_BF16, SF_DTYPE_BF16);
+#undef SF_LAUNCH_EFF
+  return launch_status("sf_effective_mask");
+}

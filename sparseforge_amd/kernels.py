@@ -1,0 +1,154 @@
+"""torch-tensor wrappers over the C ABI (include/sparseforge_amd.h).
+
+Each function validates shapes/dtypes, takes raw device pointers from the
+tensors, launches on torch's current stream of the tensors' device and
+returns without synchronising.  Workspaces come from torch's caching
+allocator; the library itself never allocates.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib as L
+
+
+def _ws(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# hard projections (SparseLinear._hard_mask_from_soft, sparse_modeling.py:510-735)
+# ---------------------------------------------------------------------------
+def hard_mask(soft: torch.Tensor, kind: int, n_keep: int = 2, m_group: int = 4,
+              out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    dev = L.require_device(soft)
+    if soft.dim() != 2:
+        raise ValueError("hard_mask expects a 2-D soft mask")
+    if out is None:
+        out = torch.empty_like(soft, dtype=out_dtype or soft.dtype)
+    L.require_device(out)
+    rows, cols = soft.shape
+    L.check(
+        L.lib().sf_hard_mask(L.ptr(soft), L.dtype_code(soft), L.ptr(out), L.dtype_code(out), rows, cols,
+                             kind, n_keep, m_group, L.stream(dev)),
+        "sf_hard_mask",
+    )
+    return out
+
+
+def hard_flip_count(prev: torch.Tensor, now: torch.Tensor, kind: int, n_keep: int = 2, m_group: int = 4,
+                    counter: torch.Tensor | None = None) -> torch.Tensor:
+    """Device int64[1] count of positions where hard(prev) != hard(now)."""
+    dev = L.require_device(prev, now)
+    if prev.shape != now.shape or prev.dtype != now.dtype or prev.dim() != 2:
+        raise ValueError("hard_flip_count: prev/now must be 2-D with equal shape and dtype")
+    if counter is None:
+        counter = torch.zeros(1, dtype=torch.int64, device=dev)
+    rows, cols = prev.shape
+    L.check(
+        L.lib().sf_hard_flip_count(L.ptr(prev), L.ptr(now), L.dtype_code(prev), rows, cols, kind, n_keep,
+                                   m_group, L.ptr(counter), L.stream(dev)),
+        "sf_hard_flip_count",
+    )
+    return counter
+
+
+# ---------------------------------------------------------------------------
+# gate target and fused mask update (sparse_modeling.py:1018-1666)
+# ---------------------------------------------------------------------------
+@dataclass
+class MaskOperands:
+    """Device tensors of one layer's mask state."""
+
+    weight: torch.Tensor
+    mask: torch.Tensor
+    hessian: torch.Tensor | None = None   # hessian_diag [out, in] (None if placeholder)
+    aux: torch.Tensor | None = None       # scaler_row [in] (wanda) or grad_ema [out, in] (movement)
+    frozen: torch.Tensor | None = None    # frozen_mask_flags [out, in] (None if placeholder)
+
+    def device(self) -> torch.device:
+        dev = L.require_device(self.weight, self.mask, self.hessian, self.aux, self.frozen)
+        shape = tuple(self.weight.shape)
+        if self.weight.dim() != 2:
+            raise ValueError("mask ops expect a 2-D weight")
+        for name, t in (("mask", self.mask), ("hessian_diag", self.hessian), ("frozen_mask_flags", self.frozen)):
+            if t is not None and tuple(t.shape) != shape:
+                raise ValueError(f"{name} shape {tuple(t.shape)} != weight shape {shape}")
+        if self.aux is not None and tuple(self.aux.shape) not in (shape, (shape[1],)):
+            raise ValueError(f"aux shape {tuple(self.aux.shape)} fits neither {shape} nor ({shape[1]},)")
+        return dev
+
+    def dt(self, t: torch.Tensor | None) -> int:
+        return L.dtype_code(t) if t is not None else L.DT_F32
+
+
+def score_stats(p: L.MaskParams, ops: MaskOperands, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    dev = ops.device()
+    ws = workspace if workspace is not None else _ws(L.lib().sf_mask_workspace_size(p.rows, p.cols, 0), dev)
+    stats = torch.empty(2, dtype=torch.float32, device=dev)
+    L.check(
+        L.lib().sf_score_stats(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                               ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(stats), L.ptr(ws),
+                               ws.numel(), L.stream(dev)),
+        "sf_score_stats",
+    )
+    return stats
+
+
+def sample_indices(sample_size: int, n: int, seed: int, device: torch.device) -> torch.Tensor:
+    idx = torch.empty(sample_size, dtype=torch.int64, device=device)
+    L.check(L.lib().sf_sample_indices(L.ptr(idx), sample_size, n, seed & ((1 << 64) - 1), L.stream(device)),
+            "sf_sample_indices")
+    return idx
+
+
+def tau_quantile(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, q: float,
+                 sample_idx: torch.Tensor | None) -> torch.Tensor:
+    dev = ops.device()
+    if sample_idx is not None:
+        L.require_device(sample_idx)
+        if sample_idx.dim() != 1:
+            raise ValueError("sample indices must be 1-D")
+        if sample_idx.dtype != torch.int64:
+            raise TypeError("sample indices must be int64")
+        m = sample_idx.numel()
+    else:
+        m = p.rows * p.cols
+    ws = _ws(L.lib().sf_mask_workspace_size(p.rows, p.cols, m), dev)
+    tau = torch.empty(1, dtype=torch.float32, device=dev)
+    L.check(
+        L.lib().sf_tau_quantile(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                                ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(stats),
+                                L.ptr(sample_idx), m, float(q), L.ptr(tau), L.ptr(ws), ws.numel(), L.stream(dev)),
+        "sf_tau_quantile",
+    )
+    return tau
+
+
+def gate_target(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: torch.Tensor | None,
+                g_dtype: torch.dtype) -> torch.Tensor:
+    dev = ops.device()
+    G = torch.empty(p.rows, p.cols, dtype=g_dtype, device=dev)
+    L.check(
+        L.lib().sf_gate_target(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                               ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(ops.mask),
+                               ops.dt(ops.mask), L.ptr(ops.frozen), ops.dt(ops.frozen), L.ptr(stats), L.ptr(tau),
+                               L.ptr(G), L.dtype_code(G), L.stream(dev)),
+        "sf_gate_target",
+    )
+    return G
+
+
+def update_mask(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: torch.Tensor | None,
+                flips: torch.Tensor | None) -> None:
+    dev = ops.device()
+    L.check(
+        L.lib().sf_update_mask(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                               ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(ops.mask),
+                               ops.dt(ops.mask), L.ptr(ops.frozen), ops.dt(ops.frozen), L.ptr(stats), L.ptr(tau),
+                               L.ptr(flips), L.stream(dev)),
+        "sf_update_mask",
+    )

@@ -1,0 +1,326 @@
+"""Masked linear + SLoRB as autograd functions over the sf_gemm MFMA engine.
+
+Reference: legacy/sparse_modeling.py:56-132 (FusedMaskedLinearSTE) and
+:737-796 (SparseLinear.forward with the SLoRB pair of F.linear).
+
+    z  = x P^T                                    (SLoRB projection, [T, r])
+    y  = x (W.E.s)^T + z S^T + b                  (one GEMM: the z S^T term is a second K segment)
+    dz = dy S
+    dx = dy (W.E) + dz P                          (one GEMM, two K segments; no s, as in :113-115)
+    dW = dy^T x  (+ decay W [E < 0.5])            (STE: the mask does not enter dW, :120-125)
+    db = sum_t dy,  dS = dy^T z,  dP = dz^T x
+
+The backward is itself an autograd Function whose backward is written with
+the same kernels, so torch.autograd.grad(..., create_graph=True) and the
+Hutchinson Hessian-vector product (legacy/utils.py:772-795) work through it.
+SLoRB ranks that are not a multiple of the 16-byte vector width are padded
+with zero rows/columns of P and S, which leaves every product unchanged.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib as L
+from . import kernels as K
+
+
+# ---------------------------------------------------------------------------
+# GEMM front end
+# ---------------------------------------------------------------------------
+def _vec(dtype: torch.dtype) -> int:
+    return 8 if dtype == torch.bfloat16 else 4
+
+
+def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=None, bscale=1.0, bias=None,
+         emask=None, dw=None, decay=0.0, out=None, out_dtype=None, accumulate=False) -> torch.Tensor:
+    """C[M, N] = A1 . B1'^T (+ A2 . B2^T) on the device.
+
+    a_layout: L.LAYOUT_K (A1 is [M, K]) or L.LAYOUT_MN (A1 is [K, M]);
+    b_layout: L.LAYOUT_K (B1 is [N, K]) or L.LAYOUT_MN (B1 is [K, N]).
+    """
+    dev = L.require_device(A1, B1, A2, B2, bmask, bias, emask, dw, out)
+    dt = A1.dtype
+
+    def _shape(t, want, name):
+        if t is not None and tuple(t.shape) != tuple(want):
+            raise ValueError(f"gemm: {name} has shape {tuple(t.shape)}, expected {tuple(want)}")
+
+    def _op_shape(rows, k, layout):
+        return (rows, k) if layout == L.LAYOUT_K else (k, rows)
+
+    _shape(A1, _op_shape(M, K1, a_layout), "A1")
+    _shape(B1, _op_shape(N, K1, b_layout), "B1")
+    _shape(bmask, _op_shape(N, K1, b_layout), "bmask")
+    if K2:
+        if A2 is None or B2 is None:
+            raise ValueError("gemm: K2 > 0 needs A2 and B2")
+        _shape(A2, _op_shape(M, K2, a_layout), "A2")
+        _shape(B2, _op_shape(N, K2, b_layout), "B2")
+    _shape(bias, (N,), "bias")
+    _shape(emask, (M, N), "emask")
+    _shape(dw, (M, N), "dw")
+    _shape(out, (M, N), "out")
+    for t in (B1, A2, B2, bmask, emask, dw):
+        if t is not None and t.dtype != dt:
+            raise TypeError(f"gemm: operand dtype {t.dtype} != {dt}")
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype or dt, device=dev)
+    d = L.GemmDesc()
+    d.dtype = L.dtype_code(A1)
+    d.a_layout, d.b_layout = a_layout, b_layout
+    d.M, d.N, d.K1, d.K2 = M, N, K1, K2
+    d.A1, d.B1 = L.ptr(A1), L.ptr(B1)
+    d.lda1 = A1.shape[1]
+    d.ldb1 = B1.shape[1]
+    if K2:
+        d.A2, d.B2 = L.ptr(A2), L.ptr(B2)
+        d.lda2, d.ldb2 = A2.shape[1], B2.shape[1]
+    d.bmask = L.ptr(bmask)
+    d.bscale = float(bscale)
+    d.C, d.ldc, d.c_dtype = L.ptr(out), out.shape[1], L.dtype_code(out)
+    if bias is not None:
+        d.bias, d.bias_dtype = L.ptr(bias), L.dtype_code(bias)
+    d.emask, d.dw, d.decay = L.ptr(emask), L.ptr(dw), float(decay)
+    d.accumulate = int(bool(accumulate))
+    L.check(L.lib().sf_gemm(L.byref(d), L.stream(dev)), "sf_gemm")
+    return out
+
+
+def mm_nt(A, B, **kw):
+    """A [M, K] . B [N, K]^T"""
+    return gemm(A.shape[0], B.shape[0], A, B, A.shape[1], L.LAYOUT_K, L.LAYOUT_K, **kw)
+
+
+def mm_nn(A, B, **kw):
+    """A [M, K] . B [K, N]"""
+    return gemm(A.shape[0], B.shape[1], A, B, A.shape[1], L.LAYOUT_K, L.LAYOUT_MN, **kw)
+
+
+def mm_tn(A, B, **kw):
+    """A [K, M]^T . B [K, N]"""
+    return gemm(A.shape[1], B.shape[1], A, B, A.shape[0], L.LAYOUT_MN, L.LAYOUT_MN, **kw)
+
+
+def column_sum(A: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
+    dev = L.require_device(A)
+    out = torch.empty(A.shape[1], dtype=out_dtype, device=dev)
+    L.check(L.lib().sf_column_sum(L.ptr(A), L.dtype_code(A), A.shape[0], A.shape[1], L.ptr(out),
+                                  L.dtype_code(out), L.stream(dev)), "sf_column_sum")
+    return out
+
+
+def effective_mask(mask: torch.Tensor, dtype: torch.dtype, mode: str, hx: float, hard_kind: int, hard_n: int,
+                   hard_m: int = 4) -> torch.Tensor:
+    """E = mask.to(dtype) ('soft') or (hx*mask + (1-hx)*hard(mask)).to(dtype) ('mix')."""
+    dev = L.require_device(mask)
+    eff = torch.empty(mask.shape, dtype=dtype, device=dev)
+    m = L.EFF_MIX if mode == "mix" else L.EFF_SOFT
+    L.check(L.lib().sf_effective_mask(L.ptr(mask), L.dtype_code(mask), L.ptr(eff), L.dtype_code(eff),
+                                      mask.shape[0], mask.shape[1], m, float(hx), hard_kind, hard_n, hard_m,
+                                      L.stream(dev)), "sf_effective_mask")
+    return eff
+
+
+def _pad_rank(P: torch.Tensor, S: torch.Tensor):
+    """Zero-pad the SLoRB rank to a multiple of the vector width."""
+    r = P.shape[0]
+    v = _vec(P.dtype)
+    rp = (r + v - 1) // v * v
+    if rp == r:
+        return P.contiguous(), S.contiguous(), r
+    Pp = torch.zeros(rp, P.shape[1], dtype=P.dtype, device=P.device)
+    Pp[:r] = P
+    Sp = torch.zeros(S.shape[0], rp, dtype=S.dtype, device=S.device)
+    Sp[:, :r] = S
+    return Pp, Sp, r
+
+
+def _opt(t):
+    return t.contiguous() if t is not None else None
+
+
+# ---------------------------------------------------------------------------
+# autograd
+# ---------------------------------------------------------------------------
+class _MaskedLinearBackward(torch.autograd.Function):
+    """(gy, x, W, P, S, b?) -> (dx, dW, db, dP, dS); differentiable for the HVP."""
+
+    @staticmethod
+    def forward(ctx, gy, x, W, P, S, E, decay, has_bias):
+        has_slorb = P is not None
+        z = mm_nt(x, P) if has_slorb else None
+        dz = mm_nn(gy, S) if has_slorb else None
+        if has_slorb:
+            dx = mm_nn(gy, W, bmask=E, A2=dz, B2=P, K2=P.shape[0])
+        else:
+            dx = mm_nn(gy, W, bmask=E)
+        if decay != 0.0:
+            dW = mm_tn(gy, x, emask=E, dw=W, decay=decay)
+        else:
+            dW = mm_tn(gy, x)
+        db = column_sum(gy, W.dtype) if has_bias else None
+        dP = mm_tn(dz, x) if has_slorb else None
+        dS = mm_tn(gy, z) if has_slorb else None
+        ctx.save_for_backward(gy, x, W, P, S, E, z, dz)
+        ctx.decay = decay
+        ctx.has_slorb = has_slorb
+        return dx, dW, db, dP, dS
+
+    @staticmethod
+    def backward(ctx, g_dx, g_dW, g_db, g_dP, g_dS):
+        gy, x, W, P, S, E, z, dz = ctx.saved_tensors
+        if ctx.decay != 0.0 and g_dW is not None:
+            raise NotImplementedError("double backward of the SR-STE decay term")
+        T, out = gy.shape
+        dt = gy.dtype
+        g_dx, g_dW, g_db, g_dP, g_dS = (_opt(t) for t in (g_dx, g_dW, g_db, g_dP, g_dS))
+        if not ctx.has_slorb:
+            g_dP = g_dS = None
+        # d/d gy = gdx (W.E)^T + x gdW^T + [gdx P^T + x gdP^T] S^T + z gdS^T + gdb
+        ggy = None
+        if g_dx is not None and g_dW is not None:
+            ggy = mm_nt(g_dx, W, bmask=E, A2=x, B2=g_dW, K2=x.shape[1], bias=g_db)
+        elif g_dx is not None:
+            ggy = mm_nt(g_dx, W, bmask=E, bias=g_db)
+        elif g_dW is not None:
+            ggy = mm_nt(x, g_dW, bias=g_db)
+        u = None
+        if ctx.has_slorb:
+            if g_dx is not None and g_dP is not None:
+                u = mm_nt(g_dx, P, A2=x, B2=g_dP, K2=x.shape[1])
+            elif g_dx is not None:
+                u = mm_nt(g_dx, P)
+            elif g_dP is not None:
+                u = mm_nt(x, g_dP)
+            if u is not None or g_dS is not None:
+                if ggy is None:
+                    ggy = torch.zeros(T, out, dtype=dt, device=gy.device)
+                    if g_db is not None:
+                        ggy += g_db
+                if u is not None and g_dS is not None:
+                    mm_nt(u, S, A2=z, B2=g_dS, K2=z.shape[1], out=ggy, accumulate=True)
+                elif u is not None:
+                    mm_nt(u, S, out=ggy, accumulate=True)
+                else:
+                    mm_nt(z, g_dS, out=ggy, accumulate=True)
+        if ggy is None and g_db is not None:
+            ggy = g_db.expand(T, out).to(dt).contiguous()
+        # d/dx = gy gdW + (gy gdS) P + dz gdP
+        gx = None
+        if g_dW is not None:
+            gx = mm_nn(gy, g_dW)
+        if ctx.has_slorb and (g_dS is not None or g_dP is not None):
+            w = mm_nn(gy, g_dS) if g_dS is not None else None
+            if gx is None:
+                gx = torch.zeros_like(x)
+            if w is not None and g_dP is not None:
+                mm_nn(w, P, A2=dz, B2=g_dP, K2=dz.shape[1], out=gx, accumulate=True)
+            elif w is not None:
+                mm_nn(w, P, out=gx, accumulate=True)
+            else:
+                mm_nn(dz, g_dP, out=gx, accumulate=True)
+        else:
+            w = None
+        # d/dW = (gy^T gdx) . E
+        gW = mm_tn(gy, g_dx, emask=E) if g_dx is not None else None
+        # d/dP = dz^T gdx + (gy gdS)^T x ;  d/dS = gy^T (gdx P^T + x gdP^T)
+        gP = gS = None
+        if ctx.has_slorb:
+            if g_dx is not None and w is not None:
+                gP = gemm(P.shape[0], P.shape[1], dz, g_dx, T, L.LAYOUT_MN, L.LAYOUT_MN, A2=w, B2=x, K2=T)
+            elif g_dx is not None:
+                gP = mm_tn(dz, g_dx)
+            elif w is not None:
+                gP = mm_tn(w, x)
+            if u is not None:
+                gS = mm_tn(gy, u)
+        return ggy, gx, gW, gP, gS, None, None, None
+
+
+class _MaskedLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x2, W, bias, P, S, E, scale, decay):
+        if P is not None:
+            z = mm_nt(x2, P)
+            y = mm_nt(x2, W, bmask=E, bscale=scale, A2=z, B2=S, K2=P.shape[0], bias=bias)
+        else:
+            y = mm_nt(x2, W, bmask=E, bscale=scale, bias=bias)
+        ctx.save_for_backward(x2, W, P, S, E)
+        ctx.decay = decay
+        ctx.has_bias = bias is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2, W, P, S, E = ctx.saved_tensors
+        gy = gy.contiguous().to(W.dtype)
+        dx, dW, db, dP, dS = _MaskedLinearBackward.apply(gy, x2, W, P, S, E, ctx.decay, ctx.has_bias)
+        return dx, dW, db, dP, dS, None, None, None
+
+
+def _compute_dtype(x: torch.Tensor, W: torch.Tensor) -> torch.dtype:
+    if torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return W.dtype
+
+
+def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale, P=None, S=None, decay=0.0,
+                  eff=None):
+    """y = x (W.E.s)^T + (x P^T) S^T + b with STE gradients.
+
+    mask_mode: 'none' (E = 1), 'soft' (E = mask) or 'mix' (E = hx*mask + (1-hx)*hard(mask)).
+    eff: a precomputed E in the compute dtype (skips the mask pass).
+    """
+    L.require_device(x, weight, bias, mask, P, S)
+    dt = _compute_dtype(x, weight)
+    if dt not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"sparseforge_amd: unsupported compute dtype {dt}")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype != dt:
+        x2 = x2.to(dt)
+    x2 = x2.contiguous()
+    W = weight if weight.dtype == dt else weight.to(dt)
+    b = None if bias is None else (bias if bias.dtype == dt else bias.to(dt))
+    if eff is None and mask_mode != "none":
+        eff = effective_mask(mask, dt, mask_mode, hx, hard_kind, hard_n)
+    if mask_mode == "none":
+        eff = None
+    Pp = Sp = None
+    r = 0
+    if P is not None:
+        Pp, Sp, r = (P, S, P.shape[0]) if P.dtype == dt else (P.to(dt), S.to(dt), P.shape[0])
+        if Pp.shape[0] % _vec(dt):
+            Pp, Sp, r = _PadRank.apply(Pp, Sp)
+    y = _MaskedLinear.apply(x2, W, b, Pp, Sp, eff, float(scale), float(decay))
+    return y.view(*lead, y.shape[-1])
+
+
+class _PadRank(torch.autograd.Function):
+    """Zero-pad P [r, in] and S [out, r] to a rank multiple of the vector width (differentiable)."""
+
+    @staticmethod
+    def forward(ctx, P, S):
+        Pp, Sp, r = _pad_rank(P, S)
+        ctx.r = r
+        return Pp, Sp, r
+
+    @staticmethod
+    def backward(ctx, gPp, gSp, _):
+        r = ctx.r
+        gP = gPp[:r] if gPp is not None else None
+        gS = gSp[:, :r] if gSp is not None else None
+        return gP, gS
+
+
+class FusedMaskedLinearSTE(torch.autograd.Function):
+    """Drop-in of legacy/sparse_modeling.py:56-132: apply(x, weight, bias, mask, decay, scale_factor).
+
+    `mask` is the effective mask (any [out, in] float tensor); it is cast to the
+    weight dtype as the reference's `mask_cast` and applied inside the GEMMs.
+    """
+
+    @staticmethod
+    def apply(x, weight, bias, mask, decay: float, scale_factor: float = 1.0):  # noqa: D102
+        m = mask.detach().contiguous()
+        return masked_linear(x, weight, bias, m, "soft", 1.0, L.HARD_NONE, 2, scale_factor, decay=float(decay))

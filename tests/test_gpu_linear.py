@@ -1,0 +1,202 @@
+"""GPU parity of the masked linear GEMMs (K1-K5) against a float64 CPU reference.
+
+Bar: f32 within rtol 1e-5 (relative to the output scale), bf16 within rtol
+2e-2; gradients follow the reference's STE semantics (dW unmasked, no weight
+scale in dx, legacy/sparse_modeling.py:96-132).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+
+
+def _lin():
+    from sparseforge_amd import _lib as L
+    from sparseforge_amd import linear as lin
+
+    return L, lin
+
+
+def rel_err(got: torch.Tensor, ref: torch.Tensor) -> float:
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("shape", [(256, 512, 384), (300, 136, 72), (1024, 768, 3072), (64, 4096, 8)])
+def test_gemm_layouts(cuda_device, dtype, tol, shape):
+    L, lin = _lin()
+    M, K, N = shape
+    g = torch.Generator().manual_seed(M + K + N)
+    A = torch.randn(M, K, generator=g).to(dtype)
+    B = torch.randn(N, K, generator=g).to(dtype)
+    Bt = B.t().contiguous()
+    At = A.t().contiguous()
+    ref = A.double() @ B.double().t()
+    d = lambda t: t.to(cuda_device)
+    assert rel_err(lin.mm_nt(d(A), d(B)), ref) < tol
+    assert rel_err(lin.mm_nn(d(A), d(Bt)), ref) < tol
+    vec = 8 if dtype == torch.bfloat16 else 4
+    if M % vec:
+        # an M-contiguous operand needs M to be a multiple of the 16-byte vector: rejected on the host
+        with pytest.raises(ValueError, match="multiples"):
+            lin.mm_tn(d(At), d(Bt))
+    else:
+        assert rel_err(lin.mm_tn(d(At), d(Bt)), ref) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_gemm_mask_scale_bias_and_segment(cuda_device, dtype, tol):
+    L, lin = _lin()
+    g = torch.Generator().manual_seed(1)
+    T, IN, OUT, R = 320, 256, 200, 16
+    x = torch.randn(T, IN, generator=g).to(dtype)
+    W = torch.randn(OUT, IN, generator=g).to(dtype)
+    E = (torch.rand(OUT, IN, generator=g)).to(dtype)
+    z = torch.randn(T, R, generator=g).to(dtype)
+    S = torch.randn(OUT, R, generator=g).to(dtype)
+    b = torch.randn(OUT, generator=g).to(dtype)
+    d = lambda t: t.to(cuda_device)
+    got = lin.mm_nt(d(x), d(W), bmask=d(E), bscale=1.5, A2=d(z), B2=d(S), K2=R, bias=d(b))
+    Wm = (W.double() * E.double())
+    ref = x.double() @ (Wm * 1.5).t() + z.double() @ S.double().t() + b.double()
+    assert rel_err(got, ref) < tol
+    dx = lin.mm_nn(d(x[:, :OUT].contiguous()), d(W), bmask=d(E))
+    assert rel_err(dx, x[:, :OUT].double() @ Wm) < tol
+
+
+def _dense_reference(x, W, b, E, s, P, S, gy):
+    """float64 CPU restatement of FusedMaskedLinearSTE + SLoRB forward/backward."""
+    x = x.double().requires_grad_(True)
+    Wd, Ed = W.double(), E.double()
+    y = x @ (Wd * Ed * s).t()
+    if b is not None:
+        y = y + b.double()
+    if P is not None:
+        Pd = P.double().requires_grad_(True)
+        Sd = S.double().requires_grad_(True)
+        y = y + (x @ Pd.t()) @ Sd.t()
+    # STE: dW = gy^T x (unmasked), dx = gy (W.E) without s
+    gyd = gy.double()
+    dW = gyd.t() @ x.detach()
+    db = gyd.sum(0) if b is not None else None
+    dx = gyd @ (Wd * Ed)
+    out = dict(y=y.detach(), dW=dW, db=db)
+    if P is not None:
+        z = x.detach() @ Pd.detach().t()
+        dz = gyd @ Sd.detach()
+        dx = dx + dz @ Pd.detach()
+        out.update(dP=dz.t() @ x.detach(), dS=gyd.t() @ z)
+    out["dx"] = dx
+    return out
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("mode", ["soft", "mix", "none"])
+def test_sparse_linear_fwd_bwd(cuda_device, dtype, tol, mode):
+    from sparseforge_amd import sparse_modeling as sm
+    from oracle import masks as om
+
+    torch.manual_seed(0)
+    IN, OUT, T = 256, 192, 160
+    cfg = sm.SparseLinearConfig(mask_type="unstructured", hard_mask_type="nm_2_4", SLoRB=True, SLoRB_k=16,
+                                SLoRB_init_type="sum", trainable_projection=True, weight_scaling=True,
+                                mode="dense_forward" if mode == "none" else "sparse_forward")
+    layer = sm.SparseLinear(IN, OUT, sparselinear_config=cfg, bias=True).to(dtype).to(cuda_device)
+    g = torch.Generator().manual_seed(5)
+    W = (torch.randn(OUT, IN, generator=g) * 0.02).to(dtype)
+    b = (torch.randn(OUT, generator=g) * 0.1).to(dtype)
+    M = torch.rand(OUT, IN, generator=g).to(dtype)
+    with torch.no_grad():
+        layer.weight.copy_(W)
+        layer.bias.copy_(b)
+        layer.mask.copy_(M)
+        layer.init_SLoRB()
+        layer.SLoRB_Weight.copy_((torch.randn(OUT, IN // 16, generator=g) * 0.01).to(dtype))
+    hx = {"soft": 1.0, "mix": 0.3, "none": 1.0}[mode]
+    layer.hardening_x = hx
+    x = torch.randn(2, T // 2, IN, generator=g).to(dtype)
+    gy = torch.randn(2, T // 2, OUT, generator=g).to(dtype)
+    xd = x.to(cuda_device).requires_grad_(True)
+    y = layer(xd)
+    y.backward(gy.to(cuda_device))
+    if mode == "none":
+        E, s = torch.ones(OUT, IN), 1.0
+    elif mode == "soft":
+        E, s = M.float(), 1.0
+    else:
+        hard = torch.from_numpy(om.hard_mask_from_soft(M.float().numpy(), "nm_2_4"))
+        E = hx * M.float() + (1 - hx) * hard
+        s = 1.0 + (1.0 - hx) * (2.0 - 1.0)
+    ref = _dense_reference(x.reshape(T, IN), W, b, E.to(dtype), s, layer.x_proj.detach().cpu(),
+                           layer.SLoRB_Weight.detach().cpu(), gy.reshape(T, OUT))
+    assert rel_err(y.reshape(T, OUT), ref["y"]) < tol
+    assert rel_err(xd.grad.reshape(T, IN), ref["dx"]) < tol
+    assert rel_err(layer.weight.grad, ref["dW"]) < tol
+    assert rel_err(layer.bias.grad, ref["db"]) < tol
+    assert rel_err(layer.x_proj.grad, ref["dP"]) < tol
+    assert rel_err(layer.SLoRB_Weight.grad, ref["dS"]) < tol
+
+
+def test_sparse_linear_matches_reference_golden(cuda_device):
+    """FusedMaskedLinearSTE + SLoRB outputs/grads written by the reference code."""
+    from sparseforge_amd import sparse_modeling as sm
+
+    r = load_golden("linear_slorb_f32")
+    import ast
+
+    kw = ast.literal_eval(str(r["cfg"]))
+    cfg = sm.SparseLinearConfig(**kw)
+    layer = sm.SparseLinear(32, 20, sparselinear_config=cfg, bias=True).to(cuda_device)
+    with torch.no_grad():
+        layer.weight.copy_(torch.from_numpy(r["W"]))
+        layer.bias.copy_(torch.from_numpy(r["bias"]))
+        layer.mask.copy_(torch.from_numpy(r["mask"]))
+        layer.x_proj.copy_(torch.from_numpy(r["P"]))
+        layer.SLoRB_Weight.copy_(torch.from_numpy(r["S"]))
+    for j in range(3):
+        layer.hardening_x = float(r[f"hx{j}"])
+        x = torch.from_numpy(r[f"x{j}"]).to(cuda_device).requires_grad_(True)
+        y = layer(x)
+        y.backward(torch.from_numpy(r[f"gy{j}"]).to(cuda_device))
+        for name, got in (("y", y), ("dx", x.grad), ("dW", layer.weight.grad), ("db", layer.bias.grad),
+                          ("dP", layer.x_proj.grad), ("dS", layer.SLoRB_Weight.grad)):
+            ref = torch.from_numpy(r[f"{name}{j}"])
+            assert rel_err(got, ref) < 1e-5, (j, name, rel_err(got, ref))
+        layer.zero_grad(set_to_none=True)
+
+
+def test_double_backward_hvp_matches_reference(cuda_device):
+    """Hutchinson HVP through the custom backward equals the reference's (v X^T X, unmasked)."""
+    from sparseforge_amd import sparse_modeling as sm
+
+    r = load_golden("hutch_quadratic_f32")
+    cfg = sm.SparseLinearConfig(mask_type="unstructured", hard_mask_type="nm_2_4", mask_metric="hessian_ratio",
+                                beta=0.98)
+    layer = sm.SparseLinear(48, 24, sparselinear_config=cfg, bias=False).to(cuda_device)
+    with torch.no_grad():
+        layer.weight.copy_(torch.from_numpy(r["W"]))
+        layer.mask.copy_(torch.from_numpy(r["mask"]))
+    x = torch.from_numpy(r["x"]).to(cuda_device)
+    y = torch.from_numpy(r["y"]).to(cuda_device)
+    H = torch.from_numpy(r["init_H"]).double()
+    for j in range(3):
+        v = torch.from_numpy(r[f"v{j}"]).to(cuda_device)
+        loss = 0.5 * ((layer(x) - y) ** 2).sum()
+        (g,) = torch.autograd.grad(loss, [layer.weight], create_graph=True)
+        (hvp,) = torch.autograd.grad((g * v).sum(), [layer.weight])
+        est = (hvp * v).clamp_min(0).double().cpu()
+        H = 0.98 * H + 0.02 * est
+        assert rel_err(H, torch.from_numpy(r[f"H{j}"])) < 1e-5
+        H = torch.from_numpy(r[f"H{j}"]).double()
+
+
+def test_cpu_tensor_raises():
+    from sparseforge_amd import linear as lin
+
+    with pytest.raises(RuntimeError, match="GPU only"):
+        lin.mm_nt(torch.ones(8, 8), torch.ones(8, 8))

@@ -1,0 +1,62 @@
+"""The C-ABI library: every function include/sparseforge_amd.h declares is exported
+and bound, and the device tie table equals the torch.topk fixture (CPU only)."""
+import json
+import os
+import re
+
+import pytest
+
+from conftest import GOLDEN, REPO
+
+HEADER = os.path.join(REPO, "include", "sparseforge_amd.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(sf_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = header_functions()
+    assert "sf_gemm" in names and "sf_update_mask" in names and len(names) >= 10
+
+
+def test_library_exports_every_declared_symbol():
+    from sparseforge_amd import _lib as L
+
+    if not os.path.exists(L.LIB_PATH):
+        pytest.fail(f"HIP library not built at {L.LIB_PATH}")
+    lib = L.load()
+    names = header_functions()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(L.SIGNATURES) == names, "ctypes bindings differ from the header"
+    assert lib.sf_version() >= 100
+
+
+def test_error_path_without_gpu():
+    """An invalid call is rejected on the host before any device work."""
+    from sparseforge_amd import _lib as L
+
+    lib = L.load()
+    rc = lib.sf_hard_mask(None, 7, None, 0, 4, 4, 2, 2, 4, None)
+    assert rc == L.SF_ERR_INVALID
+    assert "dtype" in L.last_error()
+    d = L.GemmDesc()
+    d.dtype = 5
+    assert lib.sf_gemm(L.byref(d), None) == L.SF_ERR_INVALID
+
+
+def test_device_tie_table_matches_fixture():
+    src = open(os.path.join(REPO, "sparseforge_amd", "csrc", "sf_common.hpp")).read()
+    body = src[src.index("kTopkTies4[3][256] = {"):]
+    body = body[: body.index("};")]
+    rows = re.findall(r"\{([\d,\s]+)\}", body.split("=", 1)[1])
+    tables = [[int(v) for v in r.replace("\n", "").split(",") if v.strip()] for r in rows]
+    fx = json.load(open(os.path.join(GOLDEN, "topk_ties_m4.json")))["tables"]
+    for k in (1, 2, 3):
+        expect = [0] * 256
+        for key, row in fx[str(k)].items():
+            expect[int(key)] = row["keep"]
+        assert tables[k - 1] == expect, f"k={k}"

@@ -1,0 +1,149 @@
+"""Pins the mask oracle (oracle/masks.py) — CPU only.
+
+* top-N selection against torch.topk itself (the library the reference calls);
+* hard projections against torch.topk + scatter restated with torch;
+* quantile against torch.quantile;
+* gate target / update_mask / GLU joint update against golden vectors the
+  reference code wrote (tests/golden/make_reference_golden.py);
+* closed-form invariants of the structured gate.
+"""
+import ast
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from oracle import masks as om
+from oracle.numerics import BF16, F32, round_bf16
+
+
+def torch_keep(x: np.ndarray, k: int) -> np.ndarray:
+    t = torch.from_numpy(x)
+    idx = torch.topk(t, k, dim=-1).indices
+    return torch.zeros_like(t, dtype=torch.bool).scatter_(-1, idx, True).numpy()
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+def test_topk_all_weak_orderings(k):
+    pats = np.array(list(itertools.product(range(4), repeat=4)), dtype=np.float32)
+    assert (om.topk_keep(pats, k) == torch_keep(pats, k)).all()
+
+
+@pytest.mark.parametrize("k", [1, 2, 3])
+def test_topk_random_ties_nan_and_signed_zero(k):
+    rng = np.random.default_rng(k)
+    vals = np.array([0.0, -0.0, 1.0, -1.0, np.nan, np.inf, 0.5], dtype=np.float32)
+    x = vals[rng.integers(0, len(vals), size=(400, 37, 4))]
+    assert (om.topk_keep(x, k) == torch_keep(x, k)).all()
+    y = rng.integers(0, 3, size=(300, 50, 4)).astype(np.float32)
+    assert (om.topk_keep(y, k) == torch_keep(y, k)).all()
+
+
+def test_kth_largest_matches_topk_values():
+    rng = np.random.default_rng(3)
+    x = rng.integers(0, 4, size=(200, 30, 4)).astype(np.float32)
+    x[0, 0, 1] = np.nan
+    for k in (1, 2, 3):
+        ref = torch.topk(torch.from_numpy(x), k, dim=-1).values[..., -1].numpy()
+        got = om.kth_largest(x, k)
+        assert np.array_equal(ref, got, equal_nan=True)
+
+
+def test_all_ones_mask_keeps_columns_2_3():
+    hard = om.hard_mask_from_soft(np.ones((3, 8), np.float32), "nm_2_4")
+    assert (hard == np.tile([0, 0, 1, 1], (3, 2))).all()
+
+
+@pytest.mark.parametrize("cols", [4, 66, 7, 3])
+def test_nm_2_4_projection_matches_torch(cols):
+    rng = np.random.default_rng(cols)
+    soft = rng.integers(0, 5, size=(9, cols)).astype(np.float32) / 4
+    full = (cols // 4) * 4
+    ref = np.ones_like(soft)
+    if full:
+        ref[:, :full] = torch_keep(soft[:, :full].reshape(9, -1, 4), 2).reshape(9, full)
+    assert (om.hard_mask_from_soft(soft, "nm_2_4") == ref).all()
+    if full:
+        assert (ref[:, :full].reshape(9, -1, 4).sum(-1) == 2).all()
+
+
+def test_structured_requires_divisible_cols():
+    with pytest.raises(ValueError):
+        om.hard_mask_from_soft(np.ones((2, 6), np.float32), "structured")
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(100000) * 10.0 ** rng.integers(-8, 8, 100000)).astype(np.float32)
+    x[:4] = [np.nan, np.inf, -np.inf, -0.0]
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(round_bf16(x), ref, equal_nan=True)
+
+
+@pytest.mark.parametrize("q", [0.0, 0.3, 0.5, 0.777, 1.0])
+def test_quantile_matches_torch(q):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(4097).astype(np.float32)
+    assert om.quantile_linear(x, q) == torch.quantile(torch.from_numpy(x), q).item()
+
+
+def test_structured_gate_invariants():
+    rng = np.random.default_rng(5)
+    z = rng.standard_normal((16, 32)).astype(np.float32)
+    G = om.gate_target(z, F32, "structured", 0.5)
+    g = G.reshape(16, 8, 4)
+    zz = z.reshape(16, 8, 4)
+    second = om.kth_largest(zz, 2)
+    at_second = np.take_along_axis(g, np.argmax(zz == second[..., None], -1)[..., None], -1)
+    assert (at_second == 0.5).all()
+    assert ((g > 0) & (g < 1)).all()
+    assert ((g >= 0.5).sum(-1) >= 2).all()
+
+
+def _dt(name):
+    return BF16 if "bfloat16" in str(name) else F32
+
+
+def _cfg(rec):
+    return om.full_config(**ast.literal_eval(str(rec["cfg"])))
+
+
+@pytest.mark.parametrize("case", ["gate_unstr_ratio_f32", "gate_unstr_beta_f32", "gate_unstr_frozen_f32",
+                                  "gate_struct_f32", "gate_struct_exact_f32", "gate_unstr_ratio_bf16",
+                                  "gate_struct_bf16"])
+def test_gate_target_matches_reference_golden(case):
+    r = load_golden(case)
+    c = _cfg(r)
+    dt = _dt(r["dtype"])
+    step = int(r["step"])
+    sch = om.layer_schedule(c, step)
+    assert sch["T"] == float(r["T"]) and sch["sparsity"] == float(r["sparsity"]) and sch["beta_s"] == float(r["beta_s"])
+    frozen = r["frozen"] if r["frozen"].shape == r["W"].shape else None
+    G = om.layer_gate_target(c, step, r["W"], r["H"], r["mask"], frozen, r["idx"], dt, dt, dt)
+    tol = 1e-6 if dt == F32 else 2 ** -8
+    np.testing.assert_allclose(G, r["G"], rtol=0, atol=tol)
+
+
+@pytest.mark.parametrize("case", ["update_paper_f32", "update_mid_bin_f32", "update_struct_topn_f32",
+                                  "update_freeze_f32", "update_paper_bf16"])
+def test_update_mask_matches_reference_golden(case):
+    r = load_golden(case)
+    c = _cfg(r)
+    dt = _dt(r["dtype"])
+    mask = r["init_mask"].copy()
+    frozen = r["init_frozen"].copy() if r["init_frozen"].shape == r["W"].shape else None
+    for j, step in enumerate(r["steps"]):
+        out = om.layer_update_mask(c, int(step), r["W"], r["H"], mask, frozen, r[f"idx{j}"], float(r["lam"]), dt, dt, dt)
+        assert out is not None
+        mask, nf, flips, hx = out
+        if nf is not None:
+            frozen = nf
+        tol = 1e-6 if dt == F32 else 2 ** -8
+        np.testing.assert_allclose(mask, r[f"mask{j}"], rtol=0, atol=tol)
+        if frozen is not None:
+            assert (frozen == r[f"frozen{j}"]).all()
+        assert flips == int(r[f"flips{j}"])
+        assert hx == float(r[f"hx{j}"])
+        mask = r[f"mask{j}"].copy()  # continue from the reference state
