@@ -36,6 +36,7 @@ extern "C" {
 /* ---- element types ----------------------------------------------------- */
 #define SF_DTYPE_F32 0
 #define SF_DTYPE_BF16 1
+#define SF_DTYPE_U8 2 /* byte and-mask (0x00 / 0xFF per element); sf_effective_mask output only */
 
 /* ---- hard-mask projections (SparseLinear._hard_mask_from_soft) --------- */
 #define SF_HARD_NONE 0         /* all ones                       (:523-524)  */
@@ -169,6 +170,8 @@ int sf_hard_flip_count(const void* prev, const void* now, int dtype, int64_t row
 /* ---- effective mask for the masked GEMMs (SparseLinear.forward, :759-771) */
 #define SF_EFF_SOFT 0 /* E = mask.to(weight dtype)                                  */
 #define SF_EFF_MIX 1  /* E = (hx * mask + (1 - hx) * hard(mask)).to(weight dtype)     */
+#define SF_EFF_HARD 2 /* E = hard(mask) (the hx = 0 case of MIX), any eff dtype; with
+                         eff_dtype SF_DTYPE_U8 it is written as a byte and-mask        */
 
 /*
  * Effective mask E of a forward call, written in the weight dtype (the
@@ -206,6 +209,8 @@ typedef struct sf_gemm_desc {
   const void* dw;    /* [M, N] (ld = ldc): C += decay * dw * (emask < 0.5), or NULL   */
   float decay;
   int accumulate; /* C += result                                                        */
+  int bmask_bytes; /* bmask is a byte and-mask (SF_EFF_HARD with SF_DTYPE_U8): B1 elements
+                      are kept or zeroed; requires bscale == 1                          */
 } sf_gemm_desc;
 
 /*

@@ -25,6 +25,7 @@ SF_ERR_HIP = -3
 
 DT_F32 = 0
 DT_BF16 = 1
+DT_U8 = 2
 
 HARD_NONE = 0
 HARD_THRESHOLD = 1
@@ -51,6 +52,7 @@ PENALTY_STRUCTURED_TOPN = 3
 
 EFF_SOFT = 0
 EFF_MIX = 1
+EFF_HARD = 2
 
 LAYOUT_K = 0
 LAYOUT_MN = 1
@@ -116,6 +118,7 @@ class GemmDesc(ctypes.Structure):
         ("dw", ctypes.c_void_p),
         ("decay", ctypes.c_float),
         ("accumulate", ctypes.c_int),
+        ("bmask_bytes", ctypes.c_int),
     ]
 
 

@@ -6,20 +6,30 @@
 // A is stored K-contiguous (A[m * lda + k]) or M-contiguous (A[k * lda + m]);
 // B is stored K-contiguous (B[n * ldb + k]) or N-contiguous (B[k * ldb + n]).
 // The three products of a masked linear map onto it as
-//   forward   y  = x (W.E)^T   : A K-contig (x [T, in]),   B K-contig (W [out, in])
-//   input grad dx = dy (W.E)   : A K-contig (dy [T, out]), B N-contig (W [out, in])
-//   weight grad dW = dy^T x    : A M-contig (dy [T, out]), B N-contig (x [T, in])
+//   forward    y  = x (W.E)^T : A K-contig (x [T, in]),   B K-contig (W [out, in])
+//   input grad dx = dy (W.E)  : A K-contig (dy [T, out]), B N-contig (W [out, in])
+//   weight grad dW = dy^T x   : A M-contig (dy [T, out]), B N-contig (x [T, in])
 // The second K segment concatenates the SLoRB low-rank term into the same
 // accumulators ([x | z] . [W.E | S]^T) instead of a separate GEMM + add.
 //
 // Tiling: 256 threads = 4 waves in a 2 x 2 grid; a workgroup owns a 256 x 256
-// tile of C, each wave 128 x 128 as 4 x 4 MFMA 32x32 blocks.  A and B tiles of
-// BK k-values are staged through double-buffered LDS with k contiguous per
-// row, so an MFMA operand fragment is one 16-byte LDS read per lane.
-// M/N-contiguous operands are transposed in registers (8 x 8 blocks) on their
-// way into LDS.  The mask multiply happens in registers between the global
-// load and the LDS store: no masked copy of W is ever written to memory.
-// Global loads of step k+1 are issued before the MFMAs of step k.
+// tile of C, each wave 128 x 128 as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16
+// (256 fp32 accumulators per lane, held in AGPRs).  One k-stage (64 bf16) of
+// the A and B tiles is staged through double-buffered LDS with k contiguous
+// per row and a 144-byte row pitch, so a fragment is one conflict-free 16-byte
+// LDS read per lane.
+//
+// Pipeline: the global loads of stage s+2 are issued right after stage s+1 is
+// written to LDS, so a whole stage of MFMAs covers their latency; the raw
+// words sit in registers until the LDS write, where the mask multiply (B only)
+// and, for M/N-contiguous operands, an 8 x 8 register transpose happen.  No
+// masked copy of W is ever written to memory.  Inside a stage the LDS reads of
+// k-step kk+1 are issued before the MFMAs of kk.
+//
+// Tile order: dispatch ids are spread round-robin over the 8 XCDs; they are
+// remapped so each XCD walks a contiguous range of tiles, ordered in bands of
+// 8 M-tiles, which keeps the A and B k-slices of the concurrently resident
+// tiles of one XCD in that XCD's L2.
 
 #include "sf_common.hpp"
 
@@ -27,6 +37,7 @@ namespace sf {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
@@ -36,6 +47,9 @@ constexpr int kWaveM = 128;
 constexpr int kWaveN = 128;
 constexpr int kFragM = kWaveM / 32;  // 4
 constexpr int kFragN = kWaveN / 32;  // 4
+constexpr int kGroupM = 8;           // M-tiles per L2 band
+constexpr int kXcds = 8;
+constexpr int kEpiPitch = 132;     // f32 row pitch of the epilogue staging (64 rows x 128 cols per wave)
 
 struct GemmArgs {
   int64_t M, N, K1, K2;
@@ -59,7 +73,8 @@ struct GemmArgs {
   const void* dw;     // [M, N]: C += decay * dw * (emask < 0.5)
   float decay;
   int accumulate;  // C += result
-  int64_t tiles_n;
+  int c_aligned;   // C is 16-byte aligned
+  int64_t tiles_m, tiles_n;
 };
 
 // Element traits.  bf16 uses v_mfma_f32_32x32x16_bf16 (8 k-values per lane),
@@ -69,10 +84,10 @@ struct Tr;
 
 template <>
 struct Tr<uint16_t> {
-  static constexpr int VEC = 8;      // elements per 16-byte vector
-  static constexpr int BK = 64;      // k per LDS stage
-  static constexpr int PITCH = 72;   // LDS row pitch (elements): 144 B keeps 16 B lane reads conflict-free
-  static constexpr int MK = 16;      // k per MFMA
+  static constexpr int VEC = 8;     // elements per 16-byte vector
+  static constexpr int BK = 64;     // k per LDS stage
+  static constexpr int PITCH = 72;  // LDS row pitch (elements): 144 B keeps 16 B lane reads conflict-free
+  static constexpr int MK = 16;     // k per MFMA
   static constexpr int DT = SF_DTYPE_BF16;
 };
 
@@ -93,7 +108,10 @@ struct V4 {
 __device__ __forceinline__ V4 ld16(const void* p) {
   uint4 v = *reinterpret_cast<const uint4*>(p);
   V4 r;
-  r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  r.w[0] = v.x;
+  r.w[1] = v.y;
+  r.w[2] = v.z;
+  r.w[3] = v.w;
   return r;
 }
 __device__ __forceinline__ V4 zero16() {
@@ -102,46 +120,89 @@ __device__ __forceinline__ V4 zero16() {
   return r;
 }
 
-// Apply mask (and scale) to a vector of B elements, with the reference's
-// rounding: w = round(W * E) then round(w * s).
-template <typename T>
-__device__ __forceinline__ V4 apply_mask(V4 w, V4 e, bool has_scale, float s) {
-  V4 o;
-  if constexpr (sizeof(T) == 2) {
+// How B1 is masked while it is staged: not at all, by a multiplicative
+// effective mask in the element dtype (rounded as the reference does), or by
+// a byte and-mask (0x00 / 0xFF per element) for masks whose values are 0 or 1.
+constexpr int kMaskNone = 0, kMaskMul = 1, kMaskByte = 2;
+
+// Mask words that accompany one 16-byte operand vector.
+template <typename T, int MK>
+struct MaskWords {
+  static constexpr int N = MK == kMaskMul ? 4 : (MK == kMaskByte ? (int)(16 / sizeof(T)) / 4 : 1);
+};
+
+// bf16 halves of a dword as f32, and the hardware round-to-nearest-even pack
+// (v_cvt_pk_bf16_f32) back to two bf16.
+__device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  bf16x2_t v;
+  v[0] = static_cast<__bf16>(lo);
+  v[1] = static_cast<__bf16>(hi);
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float hround(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
+__device__ __forceinline__ uint16_t hbits(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
+
+// Masked B vector.  Multiplicative mask, with the reference's rounding:
+// w = round(W * E), then round(w * s) when a weight-scaling factor is set.
+// Byte and-mask: each element is kept or zeroed (exactly W * E for E in {0, 1});
+// v_perm widens mask bytes (b0, b1) to the dword (b0, b0, b1, b1).
+template <typename T, int MK>
+__device__ __forceinline__ V4 apply_mask(const V4& w, const uint32_t (&e)[MaskWords<T, MK>::N], bool has_scale,
+                                         float s) {
+  if constexpr (MK == kMaskNone) {
+    return w;
+  } else if constexpr (MK == kMaskByte) {
+    V4 o;
+    if constexpr (sizeof(T) == 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float lo = bf16_to_f32(w.w[i] & 0xffffu) * bf16_to_f32(e.w[i] & 0xffffu);
-      float hi = bf16_to_f32(w.w[i] >> 16) * bf16_to_f32(e.w[i] >> 16);
-      if (has_scale) {
-        lo = round_bf16(lo) * s;
-        hi = round_bf16(hi) * s;
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t m = e[i >> 1];
+        o.w[i] = w.w[i] & __builtin_amdgcn_perm(m, m, (i & 1) ? 0x03030202u : 0x01010000u);
       }
-      o.w[i] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float v = __uint_as_float(w.w[i]) * __uint_as_float(e.w[i]);
-      if (has_scale) v = v * s;
-      o.w[i] = __float_as_uint(v);
+      for (int i = 0; i < 4; ++i) o.w[i] = w.w[i] & __builtin_amdgcn_perm(e[0], e[0], 0x01010101u * i);
     }
+    return o;
+  } else {
+    V4 o;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float lo = lo_f(w.w[i]) * lo_f(e[i]);
+        float hi = hi_f(w.w[i]) * hi_f(e[i]);
+        if (has_scale) {
+          lo = hround(lo) * s;
+          hi = hround(hi) * s;
+        }
+        o.w[i] = pack2(lo, hi);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = __uint_as_float(w.w[i]) * __uint_as_float(e[i]);
+        if (has_scale) v = v * s;
+        o.w[i] = __float_as_uint(v);
+      }
+    }
+    return o;
   }
-  return o;
 }
 
 // Transpose a VEC x VEC block held as VEC row vectors (row = k, lanes of the
 // vector = m) into VEC vectors of k-values, one per m.
 template <typename T>
-__device__ __forceinline__ void transpose_block(V4 v[], V4 out[]) {
+__device__ __forceinline__ void transpose_block(const V4* v, V4* out) {
   if constexpr (sizeof(T) == 2) {
     // out[m].dword[j] = (in[2j][m], in[2j+1][m]) packed lo/hi
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t a = v[2 * j].w[m >> 1], b = v[2 * j + 1].w[m >> 1];
-        // select the 16-bit half m & 1 of a (low result half) and of b (high result half)
-        uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t a = v[2 * j].w[m >> 1], b = v[2 * j + 1].w[m >> 1];
+        const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
         out[m].w[j] = __builtin_amdgcn_perm(b, a, sel);
       }
     }
@@ -153,79 +214,155 @@ __device__ __forceinline__ void transpose_block(V4 v[], V4 out[]) {
   }
 }
 
-// Per-thread staging of one operand tile (8 vectors of 16 bytes).
+// Per-thread share of one operand tile: 8 raw 16-byte vectors (+ their mask words).
+template <typename T, int MK>
 struct Stage {
   V4 v[8];
+  uint32_t e[MK == kMaskNone ? 1 : 8][MaskWords<T, MK>::N];
 };
 
-// Load the thread's share of a [256 rows x BK] tile of a K-contiguous operand.
-// rows: the tile's first row; K limit k_end; mask optional.
-template <typename T>
-__device__ __forceinline__ void load_kc(Stage& st, const T* base, int64_t ld, int64_t row0, int64_t rows_total,
-                                        int64_t k0, int64_t k_end, const T* mask, bool has_scale, float s) {
-  constexpr int VEC = Tr<T>::VEC, BK = Tr<T>::BK, CPR = BK / VEC;  // chunks per row (8)
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int v = t + kThreads * i;
-    const int r = v / CPR, c = v % CPR;
-    const int64_t row = row0 + r, k = k0 + c * VEC;
-    if (row < rows_total && k < k_end) {
-      st.v[i] = ld16(base + row * ld + k);
-      if (mask) st.v[i] = apply_mask<T>(st.v[i], ld16(mask + row * ld + k), has_scale, s);
-    } else {
-      st.v[i] = zero16();
-    }
-  }
+// Raw buffer loads: an SGPR resource holds the tensor base and its byte
+// extent; a lane offset at or past the extent reads zeros without touching
+// memory, which is how rows past M/N and k past K are padded.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr uint32_t kOob = 0x80000000u;  // a lane offset past every operand's extent (extents are < 2^31 bytes)
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ V4 bload(Rsrc r, uint32_t voff, uint32_t soff) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  V4 o;
+  o.w[0] = x[0];
+  o.w[1] = x[1];
+  o.w[2] = x[2];
+  o.w[3] = x[3];
+  return o;
 }
 
-template <typename T>
-__device__ __forceinline__ void store_kc(const Stage& st, T* lds) {
+// Per-thread load state of one operand for one tile and one K segment.
+//   K-contiguous (L == 0), element (r, k) at base[r * ld + k]: vector i of the
+//   thread is row t / CPR + 32 i, k-chunk t % CPR; one lane offset per vector
+//   (rows past the operand get an out-of-range offset), and the stage's k0 in
+//   the scalar offset, which only ever moves in-range lanes to in-range bytes.
+//   A wave reads 8 rows x 128 B per instruction.
+//   Row-contiguous (L == 1), element (r, k) at base[k * ld + r]: the thread
+//   owns VEC x VEC blocks (k-block t % KB, row-block t / KB [+ 32 for the second
+//   f32 block]); one lane offset per loaded k-row, advanced by BK rows a stage.
+template <typename T, int L>
+struct Loader {
+  static constexpr int VEC = Tr<T>::VEC, BK = Tr<T>::BK, CPR = BK / VEC;
+  Rsrc rs, re;     // operand and (B1 only) its effective mask
+  uint32_t off[8];  // lane byte offset of each of the thread's 8 vectors (kOob: padding)
+  uint32_t k_step;  // row-contig: bytes one stage advances (BK rows)
+  int kchunk;       // K-contig: first k of the thread's chunk within a stage
+  int64_t k_end;
+
+  __device__ __forceinline__ void init(const void* base, const void* emask, int64_t ld, int64_t row0,
+                                       int64_t rows_total, int64_t kend, bool emask_bytes = false) {
+    const int t = threadIdx.x;
+    k_end = kend;
+    if constexpr (L == 0) {
+      const int64_t bytes = rows_total * ld * (int64_t)sizeof(T);
+      rs = make_rsrc(base, bytes);
+      re = make_rsrc(emask ? emask : base, emask ? (emask_bytes ? bytes / (int64_t)sizeof(T) : bytes) : 0);
+      kchunk = (t % CPR) * VEC;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t row = row0 + t / CPR + 32 * i;
+        off[i] = row < rows_total ? (uint32_t)((row * ld + kchunk) * (int64_t)sizeof(T)) : kOob;
+      }
+      k_step = 0;
+    } else {
+      const int64_t bytes = kend * ld * (int64_t)sizeof(T);
+      rs = make_rsrc(base, bytes);
+      re = make_rsrc(emask ? emask : base, emask ? (emask_bytes ? bytes / (int64_t)sizeof(T) : bytes) : 0);
+      constexpr int KB = BK / VEC;
+#pragma unroll
+      for (int q = 0; q < 8 / VEC; ++q) {
+        const int b = t + kThreads * q;
+        const int kb = b % KB, rb = b / KB;
+        const int64_t r = row0 + rb * VEC;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j)
+          off[q * VEC + j] = r < rows_total ? (uint32_t)(((kb * VEC + j) * ld + r) * (int64_t)sizeof(T)) : kOob;
+      }
+      k_step = (uint32_t)(BK * ld * (int64_t)sizeof(T));
+      kchunk = 0;
+    }
+  }
+
+  // Issue the loads of the stage starting at k0 (k0 advances by BK per call).
+  // Mask words of the vector at operand byte offset o (scalar offset so):
+  // the element-dtype mask shares the operand's offsets, the byte mask
+  // takes them divided by the element size (kOob stays past its extent).
+  template <int MK>
+  __device__ __forceinline__ void load_mask(uint32_t (&e)[MaskWords<T, MK>::N], uint32_t o, uint32_t so) {
+    if constexpr (MK == kMaskMul) {
+      const V4 x = bload(re, o, so);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) e[w] = x.w[w];
+    } else if constexpr (MK == kMaskByte) {
+      constexpr int sh = sizeof(T) == 2 ? 1 : 2;
+      if constexpr (sizeof(T) == 2) {
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(re, (int)(o >> sh), (int)(so >> sh), 0);
+        e[0] = x[0];
+        e[1] = x[1];
+      } else {
+        e[0] = __builtin_amdgcn_raw_buffer_load_b32(re, (int)(o >> sh), (int)(so >> sh), 0);
+      }
+    }
+  }
+
+  template <int MK>
+  __device__ __forceinline__ void load(Stage<T, MK>& st, int64_t k0) {
+    if constexpr (L == 0) {
+      const bool k_ok = k0 + kchunk < k_end;  // the k-tail chunk of the last stage reads zeros
+      const uint32_t kb = (uint32_t)(k0 * (int64_t)sizeof(T));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t o = k_ok ? off[i] : kOob;
+        st.v[i] = bload(rs, o, kb);
+        if constexpr (MK != kMaskNone) load_mask<MK>(st.e[i], o, kb);
+      }
+    } else {
+      // k rows past K fall past the resource extent; lane offsets move by a stage afterwards
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        st.v[i] = bload(rs, off[i], 0);
+        if constexpr (MK != kMaskNone) load_mask<MK>(st.e[i], off[i], 0);
+        off[i] = off[i] >= kOob ? kOob : off[i] + k_step;
+      }
+    }
+  }
+};
+
+template <typename T, int MK>
+__device__ __forceinline__ void store_kc(const Stage<T, MK>& st, T* lds, bool has_scale, float s) {
   constexpr int VEC = Tr<T>::VEC, BK = Tr<T>::BK, CPR = BK / VEC, P = Tr<T>::PITCH;
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int v = t + kThreads * i;
-    const int r = v / CPR, c = v % CPR;
-    T* dst = lds + r * P + c * VEC;
+    V4 x = st.v[i];
+    if constexpr (MK != kMaskNone) x = apply_mask<T, MK>(x, st.e[i], has_scale, s);
+    T* dst = lds + (v / CPR) * P + (v % CPR) * VEC;
     if constexpr (sizeof(T) == 2) {
-      *reinterpret_cast<uint4*>(dst) = make_uint4(st.v[i].w[0], st.v[i].w[1], st.v[i].w[2], st.v[i].w[3]);
+      *reinterpret_cast<uint4*>(dst) = make_uint4(x.w[0], x.w[1], x.w[2], x.w[3]);
     } else {
       uint32_t* d = reinterpret_cast<uint32_t*>(dst);
-      d[0] = st.v[i].w[0]; d[1] = st.v[i].w[1]; d[2] = st.v[i].w[2]; d[3] = st.v[i].w[3];
+      d[0] = x.w[0];
+      d[1] = x.w[1];
+      d[2] = x.w[2];
+      d[3] = x.w[3];
     }
   }
 }
 
-// Row-contiguous ("M/N-contiguous") operand: element (r, k) at base[k * ld + r].
-// The tile is cut into VEC x VEC blocks; block b: kb = b % (BK/VEC), rb = b / (BK/VEC).
-template <typename T>
-__device__ __forceinline__ void load_rc(Stage& st, const T* base, int64_t ld, int64_t row0, int64_t rows_total,
-                                        int64_t k0, int64_t k_end, const T* mask, bool has_scale, float s) {
-  constexpr int VEC = Tr<T>::VEC, BK = Tr<T>::BK, KB = BK / VEC;
-  constexpr int BLOCKS_PER_THREAD = 8 / VEC;  // 1 (bf16) or 2 (f32)
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int q = 0; q < BLOCKS_PER_THREAD; ++q) {
-    const int b = t + kThreads * q;
-    const int kb = b % KB, rb = b / KB;
-    const int64_t r = row0 + rb * VEC;
-#pragma unroll
-    for (int j = 0; j < VEC; ++j) {
-      const int64_t k = k0 + kb * VEC + j;
-      V4& dst = st.v[q * VEC + j];
-      if (r < rows_total && k < k_end) {
-        dst = ld16(base + k * ld + r);
-        if (mask) dst = apply_mask<T>(dst, ld16(mask + k * ld + r), has_scale, s);
-      } else {
-        dst = zero16();
-      }
-    }
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void store_rc(const Stage& st, T* lds) {
+template <typename T, int MK>
+__device__ __forceinline__ void store_rc(const Stage<T, MK>& st, T* lds, bool has_scale, float s) {
   constexpr int VEC = Tr<T>::VEC, BK = Tr<T>::BK, KB = BK / VEC, P = Tr<T>::PITCH;
   constexpr int BLOCKS_PER_THREAD = 8 / VEC;
   const int t = threadIdx.x;
@@ -235,7 +372,10 @@ __device__ __forceinline__ void store_rc(const Stage& st, T* lds) {
     const int kb = b % KB, rb = b / KB;
     V4 in[VEC], out[VEC];
 #pragma unroll
-    for (int j = 0; j < VEC; ++j) in[j] = st.v[q * VEC + j];
+    for (int j = 0; j < VEC; ++j) {
+      in[j] = st.v[q * VEC + j];
+      if constexpr (MK != kMaskNone) in[j] = apply_mask<T, MK>(in[j], st.e[q * VEC + j], has_scale, s);
+    }
     transpose_block<T>(in, out);
 #pragma unroll
     for (int i = 0; i < VEC; ++i) {
@@ -244,92 +384,107 @@ __device__ __forceinline__ void store_rc(const Stage& st, T* lds) {
         *reinterpret_cast<uint4*>(dst) = make_uint4(out[i].w[0], out[i].w[1], out[i].w[2], out[i].w[3]);
       } else {
         uint32_t* d = reinterpret_cast<uint32_t*>(dst);
-        d[0] = out[i].w[0]; d[1] = out[i].w[1]; d[2] = out[i].w[2]; d[3] = out[i].w[3];
+        d[0] = out[i].w[0];
+        d[1] = out[i].w[1];
+        d[2] = out[i].w[2];
+        d[3] = out[i].w[3];
       }
     }
   }
 }
 
+// Tile coordinates of workgroup `pid` (XCD-contiguous ranges, bands of kGroupM M-tiles).
+__device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) {
+  const int64_t total = tiles_m * tiles_n;
+  if (total % kXcds == 0) pid = (pid % kXcds) * (total / kXcds) + pid / kXcds;
+  const int64_t band = kGroupM * tiles_n;
+  const int64_t first_m = (pid / band) * kGroupM;
+  const int64_t gm = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  const int64_t r = pid % band;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
+
 __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) { return load_as_f32(p, i, dtype); }
 
-template <typename T, int AL, int BL>
+template <typename T, int AL, int BL, int MASK>
 __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
-  constexpr int BK = Tr<T>::BK, P = Tr<T>::PITCH, MK = Tr<T>::MK;
+  constexpr int BK = Tr<T>::BK, P = Tr<T>::PITCH, MK = Tr<T>::MK, KSTEPS = BK / MK;
   extern __shared__ __align__(16) unsigned char smem[];
-  T* As = reinterpret_cast<T*>(smem);                   // [2][256][P]
-  T* Bs = As + 2 * kTileM * P;                          // [2][256][P]
+  T* As = reinterpret_cast<T*>(smem);  // [2][256][P]
+  T* Bs = As + 2 * kTileM * P;         // [2][256][P]
 
-  // Tile order: consecutive workgroups walk N fastest within a band of rows so
-  // that concurrently resident tiles share A rows and B columns in L2.
-  const int64_t tile = blockIdx.x;
-  const int64_t tm = tile / g.tiles_n, tn = tile % g.tiles_n;
+  int64_t tm, tn;
+  tile_coords(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int64_t m0 = tm * kTileM, n0 = tn * kTileN;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int64_t nk1 = ceil_div(g.K1, BK), nk2 = g.A2 ? ceil_div(g.K2, BK) : 0, nk = nk1 + nk2;
+  const int64_t nk1 = ceil_div(g.K1, BK), nk2 = g.A2 ? ceil_div(g.K2, BK) : 0;
+  const bool has_scale = g.has_scale != 0;
+  const float bscale = g.bscale;
 
-  f32x16_t acc[kFragM][kFragN];
+  f32x16_t acc[kFragM * kFragN];
 #pragma unroll
-  for (int i = 0; i < kFragM; ++i)
-#pragma unroll
-    for (int j = 0; j < kFragN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  for (int i = 0; i < kFragM * kFragN; ++i) acc[i] = f32x16_t{};
 
-  Stage sa, sb;
-  auto load_step = [&](int64_t s) {
-    const bool seg2 = s >= nk1;
-    const T* A = static_cast<const T*>(seg2 ? g.A2 : g.A1);
-    const T* B = static_cast<const T*>(seg2 ? g.B2 : g.B1);
-    const int64_t lda = seg2 ? g.lda2 : g.lda1, ldb = seg2 ? g.ldb2 : g.ldb1;
-    const int64_t k0 = (seg2 ? s - nk1 : s) * BK, kend = seg2 ? g.K2 : g.K1;
-    const T* msk = seg2 ? nullptr : static_cast<const T*>(g.bmask);
-    const bool hs = !seg2 && g.has_scale;
-    if (AL == 0)
-      load_kc<T>(sa, A, lda, m0, g.M, k0, kend, nullptr, false, 1.0f);
-    else
-      load_rc<T>(sa, A, lda, m0, g.M, k0, kend, nullptr, false, 1.0f);
-    if (BL == 0)
-      load_kc<T>(sb, B, ldb, n0, g.N, k0, kend, msk, hs, g.bscale);
-    else
-      load_rc<T>(sb, B, ldb, n0, g.N, k0, kend, msk, hs, g.bscale);
-  };
-  auto store_step = [&](int buf) {
+  // Segment 1 (A1 . (B1.E.s)^T) runs through the pipelined loop below.
+  Loader<T, AL> la;
+  Loader<T, BL> lb;
+  la.init(g.A1, nullptr, g.lda1, m0, g.M, g.K1);
+  lb.init(g.B1, MASK != kMaskNone ? g.bmask : nullptr, g.ldb1, n0, g.N, g.K1, MASK == kMaskByte);
+  Stage<T, kMaskNone> sa;
+  Stage<T, MASK> sb;
+
+  auto store_a = [&](const Stage<T, kMaskNone>& st, int buf) {
     T* a = As + buf * kTileM * P;
+    if (AL == 0)
+      store_kc<T, kMaskNone>(st, a, false, 1.0f);
+    else
+      store_rc<T, kMaskNone>(st, a, false, 1.0f);
+  };
+  auto store_b = [&](int buf) {
     T* b = Bs + buf * kTileN * P;
-    if (AL == 0) store_kc<T>(sa, a); else store_rc<T>(sa, a);
-    if (BL == 0) store_kc<T>(sb, b); else store_rc<T>(sb, b);
+    if (BL == 0)
+      store_kc<T, MASK>(sb, b, has_scale, bscale);
+    else
+      store_rc<T, MASK>(sb, b, has_scale, bscale);
   };
 
-  if (nk > 0) {
-    load_step(0);
-    store_step(0);
-  }
-  __syncthreads();
-
-  for (int64_t s = 0; s < nk; ++s) {
-    const int buf = static_cast<int>(s & 1);
-    if (s + 1 < nk) load_step(s + 1);
+  // MFMAs of one LDS stage; hook(kk) runs after the MFMAs of k-step kk are issued.
+  auto mfma_stage = [&](int buf, auto&& hook) {
     const T* a = As + buf * kTileM * P + (wm * kWaveM + (lane & 31)) * P;
     const T* b = Bs + buf * kTileN * P + (wn * kWaveN + (lane & 31)) * P;
+    if constexpr (sizeof(T) == 2) {
+      bf16x8_t fa[2][kFragM], fb[2][kFragN];
+      const int kl = (lane >> 5) * 8;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += MK) {
-      if constexpr (sizeof(T) == 2) {
-        const int ko = kk + (lane >> 5) * 8;
-        bf16x8_t fa[kFragM], fb[kFragN];
+      for (int i = 0; i < kFragM; ++i) fa[0][i] = *reinterpret_cast<const bf16x8_t*>(a + i * 32 * P + kl);
 #pragma unroll
-        for (int i = 0; i < kFragM; ++i) fa[i] = *reinterpret_cast<const bf16x8_t*>(a + i * 32 * P + ko);
+      for (int j = 0; j < kFragN; ++j) fb[0][j] = *reinterpret_cast<const bf16x8_t*>(b + j * 32 * P + kl);
 #pragma unroll
-        for (int j = 0; j < kFragN; ++j) fb[j] = *reinterpret_cast<const bf16x8_t*>(b + j * 32 * P + ko);
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        const int cur = kk & 1;
+        if (kk + 1 < KSTEPS) {
+          const int ko = (kk + 1) * MK + kl;
+#pragma unroll
+          for (int i = 0; i < kFragM; ++i) fa[cur ^ 1][i] = *reinterpret_cast<const bf16x8_t*>(a + i * 32 * P + ko);
+#pragma unroll
+          for (int j = 0; j < kFragN; ++j) fb[cur ^ 1][j] = *reinterpret_cast<const bf16x8_t*>(b + j * 32 * P + ko);
+        }
 #pragma unroll
         for (int i = 0; i < kFragM; ++i)
 #pragma unroll
           for (int j = 0; j < kFragN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-      } else {
-        const int ko = kk + (lane >> 5);
+            acc[i * kFragN + j] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i * kFragN + j], 0, 0, 0);
+        hook(kk * 4 / KSTEPS);
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        const int ko = kk * MK + (lane >> 5);
         float fa[kFragM], fb[kFragN];
 #pragma unroll
         for (int i = 0; i < kFragM; ++i) fa[i] = a[i * 32 * P + ko];
@@ -339,49 +494,144 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
         for (int i = 0; i < kFragM; ++i)
 #pragma unroll
           for (int j = 0; j < kFragN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            acc[i * kFragN + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i * kFragN + j], 0, 0, 0);
+        if (kk % (KSTEPS / 4) == 0) hook(kk * 4 / KSTEPS);
       }
     }
-    if (s + 1 < nk) store_step(buf ^ 1);
+  };
+
+  if (nk1 > 0) {
+    la.load(sa, 0);
+    lb.load(sb, 0);
+    store_a(sa, 0);
+    store_b(0);
+  }
+  if (nk1 > 1) {
+    la.load(sa, BK);
+    lb.load(sb, BK);
+  }
+  __syncthreads();
+
+  // Stage s: MFMAs over LDS buffer s & 1.  Interleaved with them (one quarter
+  // of the stage each): the raw registers of stage s+1 go to the other buffer
+  // (A, then B, with the mask applied), and the loads of stage s+2 are issued
+  // into the freed registers (A, then B).  The other buffer was last read in
+  // stage s-1, which every wave finished at the barrier.
+  for (int64_t s = 0; s < nk1; ++s) {
+    const int buf = static_cast<int>(s & 1);
+    const bool do_store = s + 1 < nk1, do_load = s + 2 < nk1;
+    const int64_t k_next = (s + 2) * BK;
+    mfma_stage(buf, [&](int q) {
+      if (q == 0 && do_store) store_a(sa, buf ^ 1);
+      if (q == 1 && do_store) store_b(buf ^ 1);
+      if (q == 2 && do_load) la.load(sa, k_next);
+      if (q == 3 && do_load) lb.load(sb, k_next);
+    });
     __syncthreads();
   }
 
+  // Segment 2 (the SLoRB term A2 . B2^T, a few stages, never masked): plain
+  // load -> LDS -> MFMA steps through buffer 0.
+  if (nk2 > 0) {
+    Loader<T, AL> la2;
+    Loader<T, BL> lb2;
+    la2.init(g.A2, nullptr, g.lda2, m0, g.M, g.K2);
+    lb2.init(g.B2, nullptr, g.ldb2, n0, g.N, g.K2);
+    for (int64_t s2 = 0; s2 < nk2; ++s2) {
+      Stage<T, kMaskNone> ta, tb;
+      la2.load(ta, s2 * BK);
+      lb2.load(tb, s2 * BK);
+      store_a(ta, 0);
+      if (BL == 0)
+        store_kc<T, kMaskNone>(tb, Bs, false, 1.0f);
+      else
+        store_rc<T, kMaskNone>(tb, Bs, false, 1.0f);
+      __syncthreads();
+      mfma_stage(0, [](int) {});
+      __syncthreads();
+    }
+  }
+
   // Epilogue.  32x32 accumulator layout: lane holds column (lane % 32) and
-  // rows (e / 4) * 8 + (lane / 32) * 4 + e % 4, e = 0..15.
-  const int cdt = g.c_dtype;
-  const int edt = Tr<T>::DT;
+  // rows (e / 4) * 8 + (lane / 32) * 4 + e % 4, e = 0..15.  The accumulators
+  // go through LDS in two halves of 64 rows per wave (the operand buffers are
+  // free now); each lane then owns 8 consecutive columns of a row, so C is
+  // read and written with 16-byte accesses and the optional epilogue operands
+  // (bias, mask product, decay term, accumulation) are read coalesced.
+  float* ep = reinterpret_cast<float*>(smem) + wave * (64 * kEpiPitch);
+  const int64_t wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
+  const bool cbf = g.c_dtype == SF_DTYPE_BF16;
+  const bool plain = !g.emask && !g.accumulate;
 #pragma unroll
-  for (int i = 0; i < kFragM; ++i) {
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kFragN; ++j) {
-      const int64_t col = n0 + wn * kWaveN + j * 32 + (lane & 31);
-      if (col >= g.N) continue;
-      const float bv = g.bias ? load_elem(g.bias, col, g.bias_dtype) : 0.0f;
+    for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wm * kWaveM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (row >= g.M) continue;
-        const int64_t off = row * g.ldc + col;
-        // result of the matmul in the output dtype, then the reference's follow-up ops
-        float v = cdt == SF_DTYPE_BF16 ? round_bf16(acc[i][j][e]) : acc[i][j][e];
-        if (g.bias) v = cdt == SF_DTYPE_BF16 ? round_bf16(v + bv) : v + bv;
-        if (g.emask) {
-          const float em = load_elem(g.emask, off, edt);
-          if (g.dw) {
-            if (em < 0.5f) {
-              float d = g.decay * load_elem(g.dw, off, edt);
-              if (cdt == SF_DTYPE_BF16) d = round_bf16(d);
-              v = cdt == SF_DTYPE_BF16 ? round_bf16(v + d) : v + d;
-            }
-          } else {
-            v = cdt == SF_DTYPE_BF16 ? round_bf16(v * em) : v * em;
+      for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = ii * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          ep[r * kEpiPitch + j * 32 + (lane & 31)] = acc[(2 * h + ii) * kFragN + j][e];
+        }
+    __syncthreads();
+    for (int it = 0; it < 16; ++it) {
+      const int flat = it * 64 + lane;
+      const int r = flat >> 4, c = (flat & 15) * 8;
+      const int64_t row = wrow0 + h * 64 + r, col = wcol0 + c;
+      if (row >= g.M || col >= g.N) continue;
+      float v[8];
+      const float4 p0 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c);
+      const float4 p1 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c + 4);
+      v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+      v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+      const int64_t off = row * g.ldc + col;
+      const bool vec = g.c_aligned && col + 8 <= g.N && (off & 7) == 0;
+      if (plain && vec) {
+        // result of the matmul in the output dtype, then + bias (rounded again)
+        if (g.bias) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float b = load_elem(g.bias, col + q, g.bias_dtype);
+            v[q] = cbf ? hround(v[q]) + b : v[q] + b;
           }
         }
-        if (g.accumulate) {
-          float o = load_elem(g.C, off, cdt);
-          v = o + v;
+        if (cbf) {
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.C) + off) =
+              make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+        } else {
+          float* cp = static_cast<float*>(g.C) + off;
+          *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<float4*>(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
         }
-        store_from_f32(g.C, off, cdt, v);
+        continue;
+      }
+      const int edt = Tr<T>::DT;
+      for (int q = 0; q < 8; ++q) {
+        if (col + q >= g.N) break;
+        const int64_t o = off + q;
+        float x = cbf ? hround(v[q]) : v[q];
+        if (g.bias) {
+          const float b = load_elem(g.bias, col + q, g.bias_dtype);
+          x = cbf ? hround(x + b) : x + b;
+        }
+        if (g.emask) {
+          const float em = load_elem(g.emask, o, edt);
+          if (g.dw) {
+            if (em < 0.5f) {
+              float d = g.decay * load_elem(g.dw, o, edt);
+              if (cbf) d = hround(d);
+              x = cbf ? hround(x + d) : x + d;
+            }
+          } else {
+            x = cbf ? hround(x * em) : x * em;
+          }
+        }
+        if (g.accumulate) x = load_elem(g.C, o, g.c_dtype) + x;
+        if (cbf)
+          static_cast<uint16_t*>(g.C)[o] = hbits(x);
+        else
+          static_cast<float*>(g.C)[o] = x;
       }
     }
   }
@@ -392,21 +642,28 @@ constexpr size_t smem_bytes() {
   return sizeof(T) * 2ull * (kTileM + kTileN) * Tr<T>::PITCH;
 }
 
-template <typename T, int AL, int BL>
+template <typename T, int AL, int BL, int MASK>
 int launch_gemm(const GemmArgs& g, hipStream_t st) {
   static bool attr_set = false;  // per instantiation; host code runs the attribute call once
-  auto kern = gemm_kernel<T, AL, BL>;
+  auto kern = gemm_kernel<T, AL, BL, MASK>;
   const size_t smem = smem_bytes<T>();
   if (!attr_set) {
-    SF_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));
+    SF_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(smem)));
     attr_set = true;
   }
-  const int64_t tiles = ceil_div(g.M, kTileM) * g.tiles_n;
+  const int64_t tiles = g.tiles_m * g.tiles_n;
   if (tiles == 0) return SF_OK;
   SF_CHECK_ARG(tiles < (1ll << 31), "GEMM grid too large");
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), smem, st, g);
   return launch_status("sf_gemm");
+}
+
+template <typename T, int MASK>
+int dispatch_layouts(const sf_gemm_desc* d, const GemmArgs& g, hipStream_t st) {
+  if (d->a_layout == SF_LAYOUT_K && d->b_layout == SF_LAYOUT_K) return launch_gemm<T, 0, 0, MASK>(g, st);
+  if (d->a_layout == SF_LAYOUT_K) return launch_gemm<T, 0, 1, MASK>(g, st);
+  return launch_gemm<T, 1, 1, MASK>(g, st);
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -422,7 +679,8 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   SF_CHECK_ARG(d->c_dtype == SF_DTYPE_BF16 || d->c_dtype == SF_DTYPE_F32, "bad output dtype %d", d->c_dtype);
   SF_CHECK_ARG(d->a_layout == SF_LAYOUT_K || d->a_layout == SF_LAYOUT_MN, "bad A layout");
   SF_CHECK_ARG(d->b_layout == SF_LAYOUT_K || d->b_layout == SF_LAYOUT_MN, "bad B layout");
-  SF_CHECK_ARG(!(d->a_layout == SF_LAYOUT_MN && d->b_layout == SF_LAYOUT_K), "A M-contiguous with B K-contiguous is not built");
+  SF_CHECK_ARG(!(d->a_layout == SF_LAYOUT_MN && d->b_layout == SF_LAYOUT_K),
+               "A M-contiguous with B K-contiguous is not built");
   SF_CHECK_ARG(d->M >= 0 && d->N >= 0 && d->K1 >= 0 && d->K2 >= 0, "negative GEMM size");
   if (d->M == 0 || d->N == 0) return SF_OK;
   SF_CHECK_ARG(d->C, "null C");
@@ -441,31 +699,63 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                    chk_operand(d->A2, d->lda2, d->a_layout, d->M, d->K2) &&
                    chk_operand(d->B1, d->ldb1, d->b_layout, d->N, d->K1) &&
                    chk_operand(d->B2, d->ldb2, d->b_layout, d->N, d->K2) &&
-                   chk_operand(d->bmask, d->ldb1, d->b_layout, d->N, d->K1),
+                   (d->bmask_bytes ? (!d->bmask || (reinterpret_cast<uintptr_t>(d->bmask) % vec == 0))
+                               : chk_operand(d->bmask, d->ldb1, d->b_layout, d->N, d->K1)),
                "GEMM operands must be 16-byte aligned with contiguous extents and leading dims that are multiples "
                "of %d elements (M=%lld N=%lld K1=%lld K2=%lld)",
                vec, (long long)d->M, (long long)d->N, (long long)d->K1, (long long)d->K2);
   SF_CHECK_ARG(d->ldc >= d->N, "ldc < N");
+  // operands are addressed with 32-bit buffer offsets; kOob must lie past every extent
+  const int64_t es = d->dtype == SF_DTYPE_BF16 ? 2 : 4;
+  auto extent = [&](const void* p, int64_t ld, int layout, int64_t rows, int64_t K) -> int64_t {
+    if (!p || K == 0) return 0;
+    return (layout == SF_LAYOUT_K ? rows : K) * ld * es;
+  };
+  const int64_t lim = int64_t(1) << 31;
+  if (extent(d->A1, d->lda1, d->a_layout, d->M, d->K1) >= lim || extent(d->A2, d->lda2, d->a_layout, d->M, d->K2) >= lim ||
+      extent(d->B1, d->ldb1, d->b_layout, d->N, d->K1) >= lim || extent(d->B2, d->ldb2, d->b_layout, d->N, d->K2) >= lim) {
+    set_error("sf_gemm: operands of 2 GiB or more are not supported (M=%lld N=%lld K1=%lld)", (long long)d->M,
+              (long long)d->N, (long long)d->K1);
+    return SF_ERR_UNSUPPORTED;
+  }
   SF_CHECK_ARG(!d->dw || d->emask, "the decay epilogue needs the effective mask");
   GemmArgs g;
-  g.M = d->M; g.N = d->N; g.K1 = d->K1; g.K2 = d->K2;
-  g.A1 = d->A1; g.lda1 = d->lda1; g.A2 = d->K2 ? d->A2 : nullptr; g.lda2 = d->lda2;
-  g.B1 = d->B1; g.ldb1 = d->ldb1; g.B2 = d->B2; g.ldb2 = d->ldb2;
-  g.bmask = d->bmask;
+  g.M = d->M;
+  g.N = d->N;
+  g.K1 = d->K1;
+  g.K2 = d->K2;
+  g.A1 = d->A1;
+  g.lda1 = d->lda1;
+  g.A2 = d->K2 ? d->A2 : nullptr;
+  g.lda2 = d->lda2;
+  g.B1 = d->B1;
+  g.ldb1 = d->ldb1;
+  g.B2 = d->B2;
+  g.ldb2 = d->ldb2;
+  g.bmask = d->K1 ? d->bmask : nullptr;
   g.bscale = d->bscale;
   g.has_scale = d->bscale != 1.0f;
-  g.C = d->C; g.ldc = d->ldc; g.c_dtype = d->c_dtype;
-  g.bias = d->bias; g.bias_dtype = d->bias_dtype;
-  g.emask = d->emask; g.dw = d->dw; g.decay = d->decay;
+  g.C = d->C;
+  g.ldc = d->ldc;
+  g.c_dtype = d->c_dtype;
+  g.bias = d->bias;
+  g.bias_dtype = d->bias_dtype;
+  g.emask = d->emask;
+  g.dw = d->dw;
+  g.decay = d->decay;
   g.accumulate = d->accumulate;
+  g.c_aligned = al16(d->C);
+  g.tiles_m = ceil_div(d->M, kTileM);
   g.tiles_n = ceil_div(d->N, kTileN);
+  // the weight-scaling factor is applied together with a multiplicative mask
+  SF_CHECK_ARG(!g.has_scale || (g.bmask && !d->bmask_bytes), "bscale != 1 needs a multiplicative effective mask");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool bf = d->dtype == SF_DTYPE_BF16;
-  if (d->a_layout == SF_LAYOUT_K && d->b_layout == SF_LAYOUT_K)
-    return bf ? launch_gemm<uint16_t, 0, 0>(g, st) : launch_gemm<float, 0, 0>(g, st);
-  if (d->a_layout == SF_LAYOUT_K)
-    return bf ? launch_gemm<uint16_t, 0, 1>(g, st) : launch_gemm<float, 0, 1>(g, st);
-  return bf ? launch_gemm<uint16_t, 1, 1>(g, st) : launch_gemm<float, 1, 1>(g, st);
+  if (g.bmask && d->bmask_bytes)
+    return bf ? dispatch_layouts<uint16_t, kMaskByte>(d, g, st) : dispatch_layouts<float, kMaskByte>(d, g, st);
+  if (g.bmask)
+    return bf ? dispatch_layouts<uint16_t, kMaskMul>(d, g, st) : dispatch_layouts<float, kMaskMul>(d, g, st);
+  return bf ? dispatch_layouts<uint16_t, kMaskNone>(d, g, st) : dispatch_layouts<float, kMaskNone>(d, g, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -484,7 +774,8 @@ __global__ void __launch_bounds__(256) column_sum_kernel(const void* __restrict_
     for (int64_t r = rg; r < rows; r += 4) s += load_as_f32(A, r * cols + col, a_dtype);
   part[rg][c] = s;
   __syncthreads();
-  if (rg == 0 && col < cols) store_from_f32(out, col, out_dtype, ((part[0][c] + part[1][c]) + part[2][c]) + part[3][c]);
+  if (rg == 0 && col < cols)
+    store_from_f32(out, col, out_dtype, ((part[0][c] + part[1][c]) + part[2][c]) + part[3][c]);
 }
 }  // namespace
 }  // namespace sf

@@ -924,6 +924,30 @@ __global__ void __launch_bounds__(kBlock) effective_mask_kernel(const void* __re
     store4<ED>(eff, g.elem, g.n, v, e);
   }
 }
+// Hard projection as a byte and-mask: 0xFF where the element is kept, 0x00 where it is pruned.
+template <int MD>
+__global__ void __launch_bounds__(kBlock) hard_bytes_kernel(const void* __restrict__ mask, uint8_t* __restrict__ out,
+                                                            int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                            int kind, int n_keep) {
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    const bool v = vec && g.full;
+    float m[4], h[4];
+    load4<MD>(mask, g.elem, g.n, v, m);
+    hard_of_group(m, g, kind, n_keep, h);
+    if (v) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w |= (h[j] > 0.5f ? 0xffu : 0u) << (8 * j);
+      *reinterpret_cast<uint32_t*>(out + g.elem) = w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j < g.n) out[g.elem + j] = h[j] > 0.5f ? 0xff : 0;
+    }
+  }
+}
 }  // namespace
 }  // namespace sf
 
@@ -931,8 +955,13 @@ extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, in
                                  int64_t cols, int mode, float hx, int hard_kind, int hard_n, int hard_m,
                                  void* stream) {
   SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
-  SF_CHECK_ARG(dtype_ok(mask_dtype) && dtype_ok(eff_dtype), "bad dtype");
-  SF_CHECK_ARG(mode == SF_EFF_SOFT || mode == SF_EFF_MIX, "bad effective-mask mode %d", mode);
+  SF_CHECK_ARG(mode == SF_EFF_SOFT || mode == SF_EFF_MIX || mode == SF_EFF_HARD, "bad effective-mask mode %d", mode);
+  SF_CHECK_ARG(dtype_ok(mask_dtype) && (dtype_ok(eff_dtype) || (mode == SF_EFF_HARD && eff_dtype == SF_DTYPE_U8)),
+               "bad dtype");
+  if (mode == SF_EFF_HARD) {  // hx = 0: E = hard(mask)
+    mode = SF_EFF_MIX;
+    hx = 0.0f;
+  }
   SF_CHECK_ARG(hard_kind >= SF_HARD_NONE && hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", hard_kind);
   if (rows == 0 || cols == 0) return SF_OK;
   SF_CHECK_ARG(mask && eff, "null tensor");
@@ -945,6 +974,18 @@ extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, in
                  (long long)cols, hard_m);
   }
   const int64_t gpr = ceil_div(cols, 4), groups = rows * gpr;
+  if (eff_dtype == SF_DTYPE_U8) {
+    const bool vb = vec_ok(cols, {{mask, mask_dtype}}) && aligned(eff, 4);
+    hipStream_t sb = static_cast<hipStream_t>(stream);
+    const int gb = elementwise_grid(groups, kBlock);
+    if (mask_dtype == SF_DTYPE_F32)
+      hard_bytes_kernel<SF_DTYPE_F32><<<gb, kBlock, 0, sb>>>(mask, static_cast<uint8_t*>(eff), cols, groups, gpr, vb,
+                                                             hard_kind, hard_n);
+    else
+      hard_bytes_kernel<SF_DTYPE_BF16><<<gb, kBlock, 0, sb>>>(mask, static_cast<uint8_t*>(eff), cols, groups, gpr, vb,
+                                                              hard_kind, hard_n);
+    return launch_status("sf_effective_mask");
+  }
   const bool vec = vec_ok(cols, {{mask, mask_dtype}, {eff, eff_dtype}});
   // (1 - hx) computed in double as in Python, then the f32 scalar of the op
   const float omh = static_cast<float>(1.0 - static_cast<double>(hx));

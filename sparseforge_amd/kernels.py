@@ -13,6 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib as L
+from . import profiling as _prof
 
 
 def _ws(nbytes: int, device: torch.device) -> torch.Tensor:
@@ -31,11 +32,12 @@ def hard_mask(soft: torch.Tensor, kind: int, n_keep: int = 2, m_group: int = 4,
         out = torch.empty_like(soft, dtype=out_dtype or soft.dtype)
     L.require_device(out)
     rows, cols = soft.shape
-    L.check(
-        L.lib().sf_hard_mask(L.ptr(soft), L.dtype_code(soft), L.ptr(out), L.dtype_code(out), rows, cols,
-                             kind, n_keep, m_group, L.stream(dev)),
-        "sf_hard_mask",
-    )
+    with _prof.region("sf_hard_mask", soft.numel() * (soft.element_size() + out.element_size()), "B", dev):
+        L.check(
+            L.lib().sf_hard_mask(L.ptr(soft), L.dtype_code(soft), L.ptr(out), L.dtype_code(out), rows, cols,
+                                 kind, n_keep, m_group, L.stream(dev)),
+            "sf_hard_mask",
+        )
     return out
 
 
@@ -84,17 +86,22 @@ class MaskOperands:
     def dt(self, t: torch.Tensor | None) -> int:
         return L.dtype_code(t) if t is not None else L.DT_F32
 
+    def score_bytes(self) -> int:
+        """Bytes of the score operands (W, H, aux), each read once."""
+        return sum(t.numel() * t.element_size() for t in (self.weight, self.hessian, self.aux) if t is not None)
+
 
 def score_stats(p: L.MaskParams, ops: MaskOperands, workspace: torch.Tensor | None = None) -> torch.Tensor:
     dev = ops.device()
     ws = workspace if workspace is not None else _ws(L.lib().sf_mask_workspace_size(p.rows, p.cols, 0), dev)
     stats = torch.empty(2, dtype=torch.float32, device=dev)
-    L.check(
-        L.lib().sf_score_stats(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
-                               ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(stats), L.ptr(ws),
-                               ws.numel(), L.stream(dev)),
-        "sf_score_stats",
-    )
+    with _prof.region("sf_score_stats", ops.score_bytes(), "B", dev):
+        L.check(
+            L.lib().sf_score_stats(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                                   ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(stats), L.ptr(ws),
+                                   ws.numel(), L.stream(dev)),
+            "sf_score_stats",
+        )
     return stats
 
 
@@ -119,12 +126,14 @@ def tau_quantile(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, q: flo
         m = p.rows * p.cols
     ws = _ws(L.lib().sf_mask_workspace_size(p.rows, p.cols, m), dev)
     tau = torch.empty(1, dtype=torch.float32, device=dev)
-    L.check(
-        L.lib().sf_tau_quantile(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
-                                ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(stats),
-                                L.ptr(sample_idx), m, float(q), L.ptr(tau), L.ptr(ws), ws.numel(), L.stream(dev)),
-        "sf_tau_quantile",
-    )
+    with _prof.region("sf_tau_quantile", m * 8, "B", dev):
+        L.check(
+            L.lib().sf_tau_quantile(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                                    ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(stats),
+                                    L.ptr(sample_idx), m, float(q), L.ptr(tau), L.ptr(ws), ws.numel(),
+                                    L.stream(dev)),
+            "sf_tau_quantile",
+        )
     return tau
 
 
@@ -145,10 +154,15 @@ def gate_target(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: to
 def update_mask(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: torch.Tensor | None,
                 flips: torch.Tensor | None) -> None:
     dev = ops.device()
-    L.check(
-        L.lib().sf_update_mask(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
-                               ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(ops.mask),
-                               ops.dt(ops.mask), L.ptr(ops.frozen), ops.dt(ops.frozen), L.ptr(stats), L.ptr(tau),
-                               L.ptr(flips), L.stream(dev)),
-        "sf_update_mask",
-    )
+    # W, H, aux read once; mask read and written; frozen flags read and written when freezing
+    nbytes = ops.score_bytes() + 2 * ops.mask.numel() * ops.mask.element_size()
+    if ops.frozen is not None and p.apply_freeze:
+        nbytes += 2 * ops.frozen.numel() * ops.frozen.element_size()
+    with _prof.region("sf_update_mask", nbytes, "B", dev):
+        L.check(
+            L.lib().sf_update_mask(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                                   ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(ops.mask),
+                                   ops.dt(ops.mask), L.ptr(ops.frozen), ops.dt(ops.frozen), L.ptr(stats),
+                                   L.ptr(tau), L.ptr(flips), L.stream(dev)),
+            "sf_update_mask",
+        )

@@ -22,6 +22,7 @@ import torch
 
 from . import _lib as L
 from . import kernels as K
+from . import profiling as _prof
 
 
 # ---------------------------------------------------------------------------
@@ -37,6 +38,8 @@ def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=
 
     a_layout: L.LAYOUT_K (A1 is [M, K]) or L.LAYOUT_MN (A1 is [K, M]);
     b_layout: L.LAYOUT_K (B1 is [N, K]) or L.LAYOUT_MN (B1 is [K, N]).
+    bmask: effective mask of B1 in B1's dtype (multiplied in), or a uint8
+    and-mask (0x00 / 0xFF per element) for a 0/1 mask.
     """
     dev = L.require_device(A1, B1, A2, B2, bmask, bias, emask, dw, out)
     dt = A1.dtype
@@ -60,9 +63,12 @@ def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=
     _shape(emask, (M, N), "emask")
     _shape(dw, (M, N), "dw")
     _shape(out, (M, N), "out")
-    for t in (B1, A2, B2, bmask, emask, dw):
+    bmask_bytes = bmask is not None and bmask.dtype == torch.uint8
+    for t in (B1, A2, B2, None if bmask_bytes else bmask, emask, dw):
         if t is not None and t.dtype != dt:
             raise TypeError(f"gemm: operand dtype {t.dtype} != {dt}")
+    if bmask_bytes and bscale != 1.0:
+        raise ValueError("gemm: a byte and-mask cannot carry a weight-scaling factor")
     if out is None:
         out = torch.empty(M, N, dtype=out_dtype or dt, device=dev)
     d = L.GemmDesc()
@@ -76,13 +82,15 @@ def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=
         d.A2, d.B2 = L.ptr(A2), L.ptr(B2)
         d.lda2, d.ldb2 = A2.shape[1], B2.shape[1]
     d.bmask = L.ptr(bmask)
+    d.bmask_bytes = int(bmask_bytes)
     d.bscale = float(bscale)
     d.C, d.ldc, d.c_dtype = L.ptr(out), out.shape[1], L.dtype_code(out)
     if bias is not None:
         d.bias, d.bias_dtype = L.ptr(bias), L.dtype_code(bias)
     d.emask, d.dw, d.decay = L.ptr(emask), L.ptr(dw), float(decay)
     d.accumulate = int(bool(accumulate))
-    L.check(L.lib().sf_gemm(L.byref(d), L.stream(dev)), "sf_gemm")
+    with _prof.region("sf_gemm", 2.0 * M * N * (K1 + K2), "FLOP", dev):
+        L.check(L.lib().sf_gemm(L.byref(d), L.stream(dev)), "sf_gemm")
     return out
 
 
@@ -111,14 +119,28 @@ def column_sum(A: torch.Tensor, out_dtype: torch.dtype) -> torch.Tensor:
 
 def effective_mask(mask: torch.Tensor, dtype: torch.dtype, mode: str, hx: float, hard_kind: int, hard_n: int,
                    hard_m: int = 4) -> torch.Tensor:
-    """E = mask.to(dtype) ('soft') or (hx*mask + (1-hx)*hard(mask)).to(dtype) ('mix')."""
+    """E = mask.to(dtype) ('soft'), (hx*mask + (1-hx)*hard(mask)).to(dtype) ('mix') or hard(mask) ('hard').
+
+    With mode 'hard' and dtype torch.uint8 the result is a byte and-mask
+    (0xFF kept, 0x00 pruned) that the GEMMs apply while staging W.
+    """
     dev = L.require_device(mask)
     eff = torch.empty(mask.shape, dtype=dtype, device=dev)
-    m = L.EFF_MIX if mode == "mix" else L.EFF_SOFT
-    L.check(L.lib().sf_effective_mask(L.ptr(mask), L.dtype_code(mask), L.ptr(eff), L.dtype_code(eff),
-                                      mask.shape[0], mask.shape[1], m, float(hx), hard_kind, hard_n, hard_m,
-                                      L.stream(dev)), "sf_effective_mask")
+    m = {"mix": L.EFF_MIX, "hard": L.EFF_HARD}.get(mode, L.EFF_SOFT)
+    code = L.DT_U8 if dtype == torch.uint8 else L.dtype_code(eff)
+    nbytes = mask.numel() * (mask.element_size() + eff.element_size())
+    with _prof.region("sf_effective_mask", nbytes, "B", dev):
+        L.check(L.lib().sf_effective_mask(L.ptr(mask), L.dtype_code(mask), L.ptr(eff), code,
+                                          mask.shape[0], mask.shape[1], m, float(hx), hard_kind, hard_n, hard_m,
+                                          L.stream(dev)), "sf_effective_mask")
     return eff
+
+
+def _as_values(E: torch.Tensor | None, dt: torch.dtype) -> torch.Tensor | None:
+    """A byte and-mask as 0/1 values of dtype dt (for epilogue products); other masks unchanged."""
+    if E is not None and E.dtype == torch.uint8:
+        return (E != 0).to(dt)
+    return E
 
 
 def _pad_rank(P: torch.Tensor, S: torch.Tensor):
@@ -146,16 +168,18 @@ class _MaskedLinearBackward(torch.autograd.Function):
     """(gy, x, W, P, S, b?) -> (dx, dW, db, dP, dS); differentiable for the HVP."""
 
     @staticmethod
-    def forward(ctx, gy, x, W, P, S, E, decay, has_bias):
+    def forward(ctx, gy, x, W, P, S, E, decay, has_bias, z_fwd=None):
         has_slorb = P is not None
-        z = mm_nt(x, P) if has_slorb else None
+        # z = x P^T is kept from the forward; its dependence on x and P is
+        # written out explicitly in backward(), so the cached copy is detached.
+        z = (z_fwd if z_fwd is not None else mm_nt(x, P)) if has_slorb else None
         dz = mm_nn(gy, S) if has_slorb else None
         if has_slorb:
             dx = mm_nn(gy, W, bmask=E, A2=dz, B2=P, K2=P.shape[0])
         else:
             dx = mm_nn(gy, W, bmask=E)
         if decay != 0.0:
-            dW = mm_tn(gy, x, emask=E, dw=W, decay=decay)
+            dW = mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay)
         else:
             dW = mm_tn(gy, x)
         db = column_sum(gy, W.dtype) if has_bias else None
@@ -222,7 +246,7 @@ class _MaskedLinearBackward(torch.autograd.Function):
         else:
             w = None
         # d/dW = (gy^T gdx) . E
-        gW = mm_tn(gy, g_dx, emask=E) if g_dx is not None else None
+        gW = mm_tn(gy, g_dx, emask=_as_values(E, W.dtype)) if g_dx is not None else None
         # d/dP = dz^T gdx + (gy gdS)^T x ;  d/dS = gy^T (gdx P^T + x gdP^T)
         gP = gS = None
         if ctx.has_slorb:
@@ -234,27 +258,28 @@ class _MaskedLinearBackward(torch.autograd.Function):
                 gP = mm_tn(w, x)
             if u is not None:
                 gS = mm_tn(gy, u)
-        return ggy, gx, gW, gP, gS, None, None, None
+        return ggy, gx, gW, gP, gS, None, None, None, None
 
 
 class _MaskedLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x2, W, bias, P, S, E, scale, decay):
+        z = None
         if P is not None:
             z = mm_nt(x2, P)
             y = mm_nt(x2, W, bmask=E, bscale=scale, A2=z, B2=S, K2=P.shape[0], bias=bias)
         else:
             y = mm_nt(x2, W, bmask=E, bscale=scale, bias=bias)
-        ctx.save_for_backward(x2, W, P, S, E)
+        ctx.save_for_backward(x2, W, P, S, E, z)
         ctx.decay = decay
         ctx.has_bias = bias is not None
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        x2, W, P, S, E = ctx.saved_tensors
+        x2, W, P, S, E, z = ctx.saved_tensors
         gy = gy.contiguous().to(W.dtype)
-        dx, dW, db, dP, dS = _MaskedLinearBackward.apply(gy, x2, W, P, S, E, ctx.decay, ctx.has_bias)
+        dx, dW, db, dP, dS = _MaskedLinearBackward.apply(gy, x2, W, P, S, E, ctx.decay, ctx.has_bias, z)
         return dx, dW, db, dP, dS, None, None, None
 
 
@@ -283,7 +308,11 @@ def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale
     W = weight if weight.dtype == dt else weight.to(dt)
     b = None if bias is None else (bias if bias.dtype == dt else bias.to(dt))
     if eff is None and mask_mode != "none":
-        eff = effective_mask(mask, dt, mask_mode, hx, hard_kind, hard_n)
+        if mask_mode == "mix" and hx <= 0.0 and scale == 1.0:
+            # E = hard(mask) exactly: staged as a byte and-mask (W * 1 = W, W * 0 = 0)
+            eff = effective_mask(mask, torch.uint8, "hard", 0.0, hard_kind, hard_n)
+        else:
+            eff = effective_mask(mask, dt, mask_mode, hx, hard_kind, hard_n)
     if mask_mode == "none":
         eff = None
     Pp = Sp = None

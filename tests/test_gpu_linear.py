@@ -69,6 +69,43 @@ def test_gemm_mask_scale_bias_and_segment(cuda_device, dtype, tol):
     assert rel_err(dx, x[:, :OUT].double() @ Wm) < tol
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("shape", [(256, 512, 384), (300, 136, 72), (1024, 768, 3072)])
+def test_gemm_byte_and_mask(cuda_device, dtype, tol, shape):
+    """A uint8 and-mask (0xFF keep / 0x00 prune) equals multiplying by the 0/1 mask, in both B layouts."""
+    L, lin = _lin()
+    M, K, N = shape
+    g = torch.Generator().manual_seed(11 + M)
+    A = torch.randn(M, K, generator=g).to(dtype)
+    B = torch.randn(N, K, generator=g).to(dtype)
+    keep = torch.rand(N, K, generator=g) < 0.5
+    E8 = (keep.to(torch.uint8) * 255)
+    ref = A.double() @ (B.double() * keep.double()).t()
+    d = lambda t: t.to(cuda_device)
+    got = lin.mm_nt(d(A), d(B), bmask=d(E8))
+    assert rel_err(got, ref) < tol
+    # input-grad layout: C = G . (B.E) with B [N, K] read N-contiguous
+    G = torch.randn(M, N, generator=g).to(dtype)
+    got2 = lin.mm_nn(d(G), d(B), bmask=d(E8))
+    ref2 = G.double() @ (B.double() * keep.double())
+    assert rel_err(got2, ref2) < tol
+
+
+@pytest.mark.parametrize("mdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("cols", [64, 66, 4096])
+def test_effective_mask_hard_bytes_bit_exact(cuda_device, mdt, cols):
+    """sf_effective_mask(SF_EFF_HARD, uint8) is 0xFF exactly where the oracle's 2:4 projection keeps."""
+    L, lin = _lin()
+    from oracle import masks as om
+
+    g = torch.Generator().manual_seed(cols)
+    soft = torch.rand(37, cols, generator=g).to(mdt)
+    soft[3, :8] = 1.0  # all-tie groups keep columns 2, 3
+    got = lin.effective_mask(soft.to(cuda_device), torch.uint8, "hard", 0.0, L.HARD_NM_TAIL_KEEP, 2).cpu()
+    ref = om.hard_mask_from_soft(soft.float().numpy(), "nm_2_4")
+    assert torch.equal(got, torch.from_numpy((ref > 0.5).astype(np.uint8) * 255))
+
+
 def _dense_reference(x, W, b, E, s, P, S, gy):
     """float64 CPU restatement of FusedMaskedLinearSTE + SLoRB forward/backward."""
     x = x.double().requires_grad_(True)
@@ -96,7 +133,7 @@ def _dense_reference(x, W, b, E, s, P, S, gy):
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-@pytest.mark.parametrize("mode", ["soft", "mix", "none"])
+@pytest.mark.parametrize("mode", ["soft", "mix", "hard", "none"])
 def test_sparse_linear_fwd_bwd(cuda_device, dtype, tol, mode):
     from sparseforge_amd import sparse_modeling as sm
     from oracle import masks as om
@@ -117,7 +154,9 @@ def test_sparse_linear_fwd_bwd(cuda_device, dtype, tol, mode):
         layer.mask.copy_(M)
         layer.init_SLoRB()
         layer.SLoRB_Weight.copy_((torch.randn(OUT, IN // 16, generator=g) * 0.01).to(dtype))
-    hx = {"soft": 1.0, "mix": 0.3, "none": 1.0}[mode]
+    hx = {"soft": 1.0, "mix": 0.3, "hard": 0.0, "none": 1.0}[mode]
+    if mode == "hard":
+        cfg.weight_scaling = False  # hx = 0 without scaling: the byte and-mask path
     layer.hardening_x = hx
     x = torch.randn(2, T // 2, IN, generator=g).to(dtype)
     gy = torch.randn(2, T // 2, OUT, generator=g).to(dtype)
@@ -131,7 +170,7 @@ def test_sparse_linear_fwd_bwd(cuda_device, dtype, tol, mode):
     else:
         hard = torch.from_numpy(om.hard_mask_from_soft(M.float().numpy(), "nm_2_4"))
         E = hx * M.float() + (1 - hx) * hard
-        s = 1.0 + (1.0 - hx) * (2.0 - 1.0)
+        s = 1.0 + (1.0 - hx) * (2.0 - 1.0) if cfg.weight_scaling else 1.0
     ref = _dense_reference(x.reshape(T, IN), W, b, E.to(dtype), s, layer.x_proj.detach().cpu(),
                            layer.SLoRB_Weight.detach().cpu(), gy.reshape(T, OUT))
     assert rel_err(y.reshape(T, OUT), ref["y"]) < tol
