@@ -211,6 +211,10 @@ typedef struct sf_gemm_desc {
   int accumulate; /* C += result                                                        */
   int bmask_bytes; /* bmask is a byte and-mask (SF_EFF_HARD with SF_DTYPE_U8): B1 elements
                       are kept or zeroed; requires bscale == 1                          */
+  void* workspace; /* optional scratch of sf_gemm_workspace_size(desc) bytes, 16-byte
+                      aligned: lets a GEMM with few output tiles split K (f32 partial
+                      sums reduced in a fixed order); NULL runs it unsplit             */
+  size_t workspace_bytes;
 } sf_gemm_desc;
 
 /*
@@ -220,6 +224,12 @@ typedef struct sf_gemm_desc {
  * the kernel, and folds the SLoRB term (:790-794) into the same accumulators.
  */
 int sf_gemm(const sf_gemm_desc* d, void* stream);
+
+/*
+ * Scratch bytes sf_gemm would use for this descriptor's split-K (0: no split).
+ * Depends only on dtype, M, N and K1.
+ */
+size_t sf_gemm_workspace_size(const sf_gemm_desc* d);
 
 /*
  * out[c] = sum_r A[r, c] for a row-major [rows, cols] matrix (bias gradient,

@@ -119,6 +119,8 @@ class GemmDesc(ctypes.Structure):
         ("decay", ctypes.c_float),
         ("accumulate", ctypes.c_int),
         ("bmask_bytes", ctypes.c_int),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -145,6 +147,7 @@ SIGNATURES = {
     "sf_hard_flip_count": (_I, [_P, _P, _I, _I64, _I64, _I, _I, _I, _P, _P]),
     "sf_effective_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _F, _I, _I, _I, _P]),
     "sf_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
+    "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "sf_column_sum": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
 }
 

@@ -26,7 +26,9 @@ LIB_NAME = "libsparseforge_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = os.environ.get("SF_OFFLOAD_ARCH", "gfx950")
 
-# Packed-FP32 VALU forms are disabled for every HIP translation unit.
+# Packed-FP32 VALU forms are disabled for every HIP translation unit, and no
+# multiply-add is fused implicitly: the kernels reproduce the reference's
+# per-op f32 rounding and call fmaf() where the reference itself fuses.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -34,6 +36,7 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-function",
+    "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
 ]

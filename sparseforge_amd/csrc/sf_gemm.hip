@@ -75,6 +75,9 @@ struct GemmArgs {
   int accumulate;  // C += result
   int c_aligned;   // C is 16-byte aligned
   int64_t tiles_m, tiles_n;
+  int splits;            // K splits (1: the kernel writes C itself)
+  int64_t split_stages;  // segment-1 stages per split
+  float* partial;        // splits > 1: [splits][M][N] f32 partial sums
 };
 
 // Element traits.  bf16 uses v_mfma_f32_32x32x16_bf16 (8 k-values per lane),
@@ -259,8 +262,11 @@ struct Loader {
   int kchunk;       // K-contig: first k of the thread's chunk within a stage
   int64_t k_end;
 
+  // kstart: first k of the first stage this workgroup loads (row-contiguous
+  // offsets advance from there; K-contiguous loads take k0 per call).
   __device__ __forceinline__ void init(const void* base, const void* emask, int64_t ld, int64_t row0,
-                                       int64_t rows_total, int64_t kend, bool emask_bytes = false) {
+                                       int64_t rows_total, int64_t kend, bool emask_bytes = false,
+                                       int64_t kstart = 0) {
     const int t = threadIdx.x;
     k_end = kend;
     if constexpr (L == 0) {
@@ -286,7 +292,8 @@ struct Loader {
         const int64_t r = row0 + rb * VEC;
 #pragma unroll
         for (int j = 0; j < VEC; ++j)
-          off[q * VEC + j] = r < rows_total ? (uint32_t)(((kb * VEC + j) * ld + r) * (int64_t)sizeof(T)) : kOob;
+          off[q * VEC + j] =
+              r < rows_total ? (uint32_t)(((kstart + kb * VEC + j) * ld + r) * (int64_t)sizeof(T)) : kOob;
       }
       k_step = (uint32_t)(BK * ld * (int64_t)sizeof(T));
       kchunk = 0;
@@ -414,14 +421,23 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   T* As = reinterpret_cast<T*>(smem);  // [2][256][P]
   T* Bs = As + 2 * kTileM * P;         // [2][256][P]
 
+  // Split-K: workgroups [kz * tiles, (kz + 1) * tiles) take segment-1 stages
+  // [kz * split_stages, (kz + 1) * split_stages); the last split also runs segment 2.
+  const int64_t tiles = g.tiles_m * g.tiles_n;
+  const int64_t kz = blockIdx.x / tiles;
   int64_t tm, tn;
-  tile_coords(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(blockIdx.x - kz * tiles, g.tiles_m, g.tiles_n, tm, tn);
   const int64_t m0 = tm * kTileM, n0 = tn * kTileN;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int64_t nk1 = ceil_div(g.K1, BK), nk2 = g.A2 ? ceil_div(g.K2, BK) : 0;
+  const int64_t nk1_all = ceil_div(g.K1, BK);
+  const int64_t s_begin = kz * g.split_stages;
+  const int64_t s_end = (s_begin + g.split_stages < nk1_all) ? s_begin + g.split_stages : nk1_all;
+  const int64_t nk1 = s_end > s_begin ? s_end - s_begin : 0;  // segment-1 stages of this workgroup
+  const int64_t nk2 = (g.A2 && kz == g.splits - 1) ? ceil_div(g.K2, BK) : 0;
+  const int64_t kbase = s_begin * BK;
   const bool has_scale = g.has_scale != 0;
   const float bscale = g.bscale;
 
@@ -432,8 +448,8 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   // Segment 1 (A1 . (B1.E.s)^T) runs through the pipelined loop below.
   Loader<T, AL> la;
   Loader<T, BL> lb;
-  la.init(g.A1, nullptr, g.lda1, m0, g.M, g.K1);
-  lb.init(g.B1, MASK != kMaskNone ? g.bmask : nullptr, g.ldb1, n0, g.N, g.K1, MASK == kMaskByte);
+  la.init(g.A1, nullptr, g.lda1, m0, g.M, g.K1, false, kbase);
+  lb.init(g.B1, MASK != kMaskNone ? g.bmask : nullptr, g.ldb1, n0, g.N, g.K1, MASK == kMaskByte, kbase);
   Stage<T, kMaskNone> sa;
   Stage<T, MASK> sb;
 
@@ -501,14 +517,14 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   };
 
   if (nk1 > 0) {
-    la.load(sa, 0);
-    lb.load(sb, 0);
+    la.load(sa, kbase);
+    lb.load(sb, kbase);
     store_a(sa, 0);
     store_b(0);
   }
   if (nk1 > 1) {
-    la.load(sa, BK);
-    lb.load(sb, BK);
+    la.load(sa, kbase + BK);
+    lb.load(sb, kbase + BK);
   }
   __syncthreads();
 
@@ -520,7 +536,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   for (int64_t s = 0; s < nk1; ++s) {
     const int buf = static_cast<int>(s & 1);
     const bool do_store = s + 1 < nk1, do_load = s + 2 < nk1;
-    const int64_t k_next = (s + 2) * BK;
+    const int64_t k_next = kbase + (s + 2) * BK;
     mfma_stage(buf, [&](int q) {
       if (q == 0 && do_store) store_a(sa, buf ^ 1);
       if (q == 1 && do_store) store_b(buf ^ 1);
@@ -585,6 +601,17 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
       const float4 p1 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c + 4);
       v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
       v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+      if (g.splits > 1) {
+        // split-K: raw f32 partial sums; sf_gemm's reduce kernel applies the epilogue
+        float* pp = g.partial + (kz * g.M + row) * g.N + col;
+        if (col + 8 <= g.N && (g.N & 3) == 0) {
+          *reinterpret_cast<float4*>(pp) = make_float4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<float4*>(pp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+          for (int q = 0; q < 8 && col + q < g.N; ++q) pp[q] = v[q];
+        }
+        continue;
+      }
       const int64_t off = row * g.ldc + col;
       const bool vec = g.c_aligned && col + 8 <= g.N && (off & 7) == 0;
       if (plain && vec) {
@@ -637,6 +664,44 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   }
 }
 
+// Split-K reduction: C = epilogue(sum over splits of the f32 partials), the
+// splits summed in index order (deterministic), then the same output
+// rounding, bias, mask product / decay term and accumulation as the GEMM
+// epilogue.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int elem_dtype) {
+  const int64_t total = g.M * g.N;
+  const bool cbf = g.c_dtype == SF_DTYPE_BF16;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = idx / g.N, col = idx - row * g.N;
+    float x = 0.0f;
+    for (int z = 0; z < g.splits; ++z) x += g.partial[z * total + idx];
+    const int64_t o = row * g.ldc + col;
+    if (cbf) x = hround(x);
+    if (g.bias) {
+      const float b = load_elem(g.bias, col, g.bias_dtype);
+      x = cbf ? hround(x + b) : x + b;
+    }
+    if (g.emask) {
+      const float em = load_elem(g.emask, o, elem_dtype);
+      if (g.dw) {
+        if (em < 0.5f) {
+          float d = g.decay * load_elem(g.dw, o, elem_dtype);
+          if (cbf) d = hround(d);
+          x = cbf ? hround(x + d) : x + d;
+        }
+      } else {
+        x = cbf ? hround(x * em) : x * em;
+      }
+    }
+    if (g.accumulate) x = load_elem(g.C, o, g.c_dtype) + x;
+    if (cbf)
+      static_cast<uint16_t*>(g.C)[o] = hbits(x);
+    else
+      static_cast<float*>(g.C)[o] = x;
+  }
+}
+
 template <typename T>
 constexpr size_t smem_bytes() {
   return sizeof(T) * 2ull * (kTileM + kTileN) * Tr<T>::PITCH;
@@ -654,9 +719,15 @@ int launch_gemm(const GemmArgs& g, hipStream_t st) {
   }
   const int64_t tiles = g.tiles_m * g.tiles_n;
   if (tiles == 0) return SF_OK;
-  SF_CHECK_ARG(tiles < (1ll << 31), "GEMM grid too large");
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), smem, st, g);
-  return launch_status("sf_gemm");
+  SF_CHECK_ARG(tiles * g.splits < (1ll << 31), "GEMM grid too large");
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles * g.splits)), dim3(kThreads), smem, st, g);
+  if (int rc = launch_status("sf_gemm")) return rc;
+  if (g.splits > 1) {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>(elementwise_grid(g.M * g.N, 256))),
+                       dim3(256), 0, st, g, Tr<T>::DT);
+    return launch_status("sf_gemm (split-K reduce)");
+  }
+  return SF_OK;
 }
 
 template <typename T, int MASK>
@@ -668,10 +739,31 @@ int dispatch_layouts(const sf_gemm_desc* d, const GemmArgs& g, hipStream_t st) {
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// K splits for a GEMM whose tile grid would leave most of the 256 CUs idle:
+// enough splits to give about one workgroup per CU, each split keeping at
+// least 8 stages of K, at most 16 splits.
+int choose_splits(const sf_gemm_desc* d) {
+  const int64_t tiles = ceil_div(d->M, kTileM) * ceil_div(d->N, kTileN);
+  const int bk = d->dtype == SF_DTYPE_BF16 ? Tr<uint16_t>::BK : Tr<float>::BK;
+  const int64_t stages = ceil_div(d->K1, bk);
+  if (tiles >= 128 || stages < 16) return 1;
+  int64_t sp = ceil_div(256, tiles);
+  if (sp > stages / 8) sp = stages / 8;
+  if (sp > 16) sp = 16;
+  return sp < 2 ? 1 : static_cast<int>(sp);
+}
+
 }  // namespace
 }  // namespace sf
 
 using namespace sf;
+
+extern "C" size_t sf_gemm_workspace_size(const sf_gemm_desc* d) {
+  if (!d || d->M <= 0 || d->N <= 0 || d->K1 <= 0) return 0;
+  if (d->dtype != SF_DTYPE_BF16 && d->dtype != SF_DTYPE_F32) return 0;
+  const int sp = choose_splits(d);
+  return sp > 1 ? static_cast<size_t>(sp) * d->M * d->N * sizeof(float) : 0;
+}
 
 extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   SF_CHECK_ARG(d != nullptr, "null sf_gemm_desc");
@@ -747,6 +839,18 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   g.c_aligned = al16(d->C);
   g.tiles_m = ceil_div(d->M, kTileM);
   g.tiles_n = ceil_div(d->N, kTileN);
+  g.splits = 1;
+  g.split_stages = ceil_div(d->K1, d->dtype == SF_DTYPE_BF16 ? Tr<uint16_t>::BK : Tr<float>::BK);
+  g.partial = nullptr;
+  {
+    const int sp = choose_splits(d);
+    const size_t need = static_cast<size_t>(sp) * d->M * d->N * sizeof(float);
+    if (sp > 1 && d->workspace && d->workspace_bytes >= need && al16(d->workspace)) {
+      g.splits = sp;
+      g.split_stages = ceil_div(g.split_stages, sp);
+      g.partial = static_cast<float*>(d->workspace);
+    }
+  }
   // the weight-scaling factor is applied together with a multiplicative mask
   SF_CHECK_ARG(!g.has_scale || (g.bmask && !d->bmask_bytes), "bscale != 1 needs a multiplicative effective mask");
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -327,9 +327,14 @@ __global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __res
 }
 
 // ---------------------------------------------------------------------------
-// tau quantile: gather z at the sample indices as order-preserving uint32
-// keys, then a single-workgroup 4 x 8-bit radix select of the two order
-// statistics around rank q * (n - 1) and torch.lerp between them.
+// tau quantile: z at the sample indices as order-preserving uint32 keys
+// (a wide gather kernel: the reads are random), then one 1024-thread
+// workgroup runs a 4 x 8-bit radix select of the two order statistics around
+// rank q * (n - 1) and torch.lerp between them.  Each pass histograms the
+// current digit of the keys that match each statistic's prefix into 16
+// per-wave LDS histograms (z-scores crowd into a few exponent bins, so
+// per-wave copies keep atomic contention low), reading keys 16 bytes at a
+// time; pass 0 also flags NaN (torch.quantile then takes the last rank).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(kBlock) tau_gather_kernel(ScoreSpec s, const void* __restrict__ W,
                                                             const void* __restrict__ H, const void* __restrict__ aux,
@@ -337,12 +342,11 @@ __global__ void __launch_bounds__(kBlock) tau_gather_kernel(ScoreSpec s, const v
                                                             const int64_t* __restrict__ idx, int64_t m,
                                                             uint32_t* __restrict__ keys) {
   const float mu = stats[0], sigma = stats[1];
+  const int64_t n = cols * rows;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m; i += (int64_t)gridDim.x * blockDim.x) {
     int64_t e = idx ? idx[i] : i;
-    const int64_t n = cols * rows;
     e = e < 0 ? 0 : (e >= n ? n - 1 : e);  // indices outside the layer are clamped, never dereferenced
-    float z = znorm(score_at(s, W, H, aux, e, cols), mu, sigma, s.score_dtype);
-    keys[i] = ordered_key(z);
+    keys[i] = ordered_key(znorm(score_at(s, W, H, aux, e, cols), mu, sigma, s.score_dtype));
   }
 }
 
@@ -354,64 +358,147 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return f;
 }
 
-constexpr int kSelectBlock = 1024;
+constexpr int kSelGrid = 32;             // workgroups of a radix pass
+constexpr int kSelStride = 2 * 256 + 1;  // partial histogram words per workgroup (+ NaN flag)
 
-__global__ void __launch_bounds__(kSelectBlock) tau_select_kernel(const uint32_t* __restrict__ keys, int64_t m,
-                                                                  float q, float* tau) {
-  __shared__ uint32_t hist[2][256];
-  __shared__ uint32_t sel[2];
-  __shared__ int64_t krem[2];
-  __shared__ int any_nan;
-  // torch.quantile: rank = q * (n - 1) in f32; NaN anywhere -> last index.
-  if (threadIdx.x == 0) any_nan = 0;
+// Select state after fixing the digits of passes 0..p.
+struct SelState {
+  uint32_t prefix[2];  // digits fixed so far of the lo / hi order statistic
+  int64_t krem[2];     // rank still to skip inside the current prefix
+  float wgt;           // lerp weight
+  int any_nan;
+};
+
+// Fix the digit of pass `pass` in `st` from that pass's partial histograms
+// (run by a whole workgroup; `st` is in LDS).  Pass 0 also derives the
+// ranks: rank = q * (n - 1) in f32 as torch.quantile does, the last rank
+// when any key is NaN.
+__device__ void advance_state(SelState& st, const uint32_t* __restrict__ partial, int nparts, int pass, int64_t m,
+                              float q) {
+  __shared__ uint32_t tot[2][256];
+  __shared__ int nan_any;
+  const int t = threadIdx.x;
+  if (t == 0) nan_any = 0;
   __syncthreads();
+  for (int i = t; i < 2 * 256; i += blockDim.x) {
+    uint32_t c = 0;
+#pragma unroll 8
+    for (int p = 0; p < nparts; ++p) c += partial[(int64_t)p * kSelStride + i];
+    (&tot[0][0])[i] = c;
+  }
+  if (pass == 0 && t < nparts && partial[(int64_t)t * kSelStride + 2 * 256]) atomicOr(&nan_any, 1);
+  __syncthreads();
+  if (t == 0 && pass == 0) {
+    const int64_t last = m - 1;
+    float rank = q * static_cast<float>(last);
+    if (nan_any) rank = static_cast<float>(last);
+    const int64_t lo = static_cast<int64_t>(rank);
+    st.krem[0] = lo;
+    st.krem[1] = static_cast<int64_t>(ceilf(rank));
+    st.wgt = rank - static_cast<float>(lo);
+    st.any_nan = nan_any;
+    st.prefix[0] = st.prefix[1] = 0u;
+  }
+  __syncthreads();
+  // inclusive prefix sums of both histograms (Hillis-Steele over 256 bins;
+  // pass 0 histograms every key once, in tot[0], for both statistics)
+  __shared__ uint32_t inc[2][256];
+  const int b = t;  // blockDim.x == 256: one bin per thread, both statistics
+  const uint32_t h0 = tot[0][b], h1 = pass == 0 ? tot[0][b] : tot[1][b];
+  uint32_t v0 = h0, v1 = h1;
+  for (int off = 1; off < 256; off <<= 1) {
+    inc[0][b] = v0;
+    inc[1][b] = v1;
+    __syncthreads();
+    if (b >= off) {
+      v0 += inc[0][b - off];
+      v1 += inc[1][b - off];
+    }
+    __syncthreads();
+  }
+  // the digit of statistic k is the one bin whose [exclusive, inclusive)
+  // prefix range holds its remaining rank (the last bin if the rank is past
+  // the total, which a consistent histogram never produces)
+  const int shift = 24 - 8 * pass;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t incl = k == 0 ? v0 : v1;
+    const uint32_t excl = incl - (k == 0 ? h0 : h1);
+    const int64_t r = st.krem[k];
+    if ((r >= (int64_t)excl && r < (int64_t)incl) || (b == 255 && r >= (int64_t)incl)) {
+      inc[k][0] = static_cast<uint32_t>(b);
+      inc[k][1] = static_cast<uint32_t>(r - (int64_t)excl);
+    }
+  }
+  __syncthreads();
+  if (t < 2) {
+    st.prefix[t] |= inc[t][0] << shift;
+    st.krem[t] = inc[t][1];
+  }
+  __syncthreads();
+}
+
+// Radix pass `pass` over kSelGrid workgroups.  Every workgroup first brings
+// the state up to date with the previous pass (redundantly, so no workgroup
+// waits for another), then histograms the current digit of the keys that
+// match each statistic's prefix into per-wave LDS histograms and publishes
+// the sum.  Workgroup 0 publishes the state the next pass starts from.
+__global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __restrict__ keys, int64_t m, int pass, float q,
+                                                          const SelState* __restrict__ state_in,
+                                                          SelState* __restrict__ state_out,
+                                                          const uint32_t* __restrict__ partial_in,
+                                                          uint32_t* __restrict__ partial_out) {
+  constexpr int kWaves = kBlock / 64;
+  __shared__ uint32_t hist[kWaves][2][256];
+  __shared__ SelState st;
+  __shared__ int nan;
+  const int t = threadIdx.x;
+  if (pass >= 2 && t == 0) st = *state_in;
+  if (t == 0) nan = 0;
+  __syncthreads();
+  if (pass >= 1) advance_state(st, partial_in, gridDim.x, pass - 1, m, q);
+  if (pass >= 1 && blockIdx.x == 0 && t == 0) *state_out = st;
+  for (int i = t; i < kWaves * 2 * 256; i += kBlock) (&hist[0][0][0])[i] = 0u;
+  __syncthreads();
+  const int wv = t >> 6;
+  const int shift = 24 - 8 * pass;
+  const uint32_t pmask = pass == 0 ? 0u : ~0u << (shift + 8);
+  const uint32_t p0 = pass == 0 ? 0u : st.prefix[0], p1 = pass == 0 ? 0u : st.prefix[1];
   int local_nan = 0;
-  for (int64_t i = threadIdx.x; i < m; i += blockDim.x) local_nan |= keys[i] == 0xffffffffu;
-  if (local_nan) atomicOr(&any_nan, 1);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + t; i < m; i += (int64_t)gridDim.x * blockDim.x) {
+    const uint32_t k = keys[i];
+    const uint32_t d = (k >> shift) & 0xffu;
+    local_nan |= k == 0xffffffffu;
+    if ((k & pmask) == p0) atomicAdd(&hist[wv][0][d], 1u);
+    if (pass > 0 && (k & pmask) == p1) atomicAdd(&hist[wv][1][d], 1u);
+  }
+  if (local_nan) atomicOr(&nan, 1);
   __syncthreads();
-  const int64_t last = m - 1;
-  float rank = q * static_cast<float>(last);
-  if (any_nan) rank = static_cast<float>(last);
-  const int64_t lo = static_cast<int64_t>(rank);
-  const int64_t hi = static_cast<int64_t>(ceilf(rank));
-  const float wgt = rank - static_cast<float>(lo);
-  if (threadIdx.x == 0) {
-    sel[0] = sel[1] = 0u;
-    krem[0] = lo;
-    krem[1] = hi;
+  uint32_t* out = partial_out + (int64_t)blockIdx.x * kSelStride;
+  for (int i = t; i < 2 * 256; i += kBlock) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) c += (&hist[w][0][0])[i];
+    out[i] = c;
   }
-  uint32_t pmask = 0u;
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    for (int i = threadIdx.x; i < 512; i += blockDim.x) (&hist[0][0])[i] = 0u;
-    __syncthreads();
-    const uint32_t p0 = sel[0], p1 = sel[1];
-    for (int64_t i = threadIdx.x; i < m; i += blockDim.x) {
-      uint32_t k = keys[i];
-      uint32_t d = (k >> shift) & 0xffu;
-      if ((k & pmask) == p0) atomicAdd(&hist[0][d], 1u);
-      if ((k & pmask) == p1) atomicAdd(&hist[1][d], 1u);
-    }
-    __syncthreads();
-    if (threadIdx.x < 2) {
-      const int t = threadIdx.x;
-      int64_t r = krem[t];
-      uint32_t d = 0;
-      for (; d < 256; ++d) {
-        if (r < (int64_t)hist[t][d]) break;
-        r -= hist[t][d];
-      }
-      krem[t] = r;
-      sel[t] |= d << shift;
-    }
-    pmask |= 0xffu << shift;
-    __syncthreads();
-  }
+  if (t == 0) out[2 * 256] = nan;
+}
+
+// After pass 3: fix its digit and lerp the two order statistics (torch.lerp:
+// small weight -> a + w (b - a), else b - (b - a)(1 - w), each op rounded).
+__global__ void __launch_bounds__(kBlock) tau_final_kernel(int64_t m, float q, int nparts,
+                                                           const SelState* __restrict__ state_in,
+                                                           const uint32_t* __restrict__ partial_in,
+                                                           float* __restrict__ tau) {
+  __shared__ SelState st;
+  if (threadIdx.x == 0) st = *state_in;
+  __syncthreads();
+  advance_state(st, partial_in, nparts, 3, m, q);
   if (threadIdx.x == 0) {
-    float a = key_to_float(sel[0]), b = key_to_float(sel[1]);
-    // torch lerp: small weight -> a + w (b - a); else b - (b - a)(1 - w)
-    float r = fabsf(wgt) < 0.5f ? a + wgt * (b - a) : b - (b - a) * (1.0f - wgt);
-    *tau = r;
+    const float lo = key_to_float(st.prefix[0]), hi = key_to_float(st.prefix[1]);
+    const float w = st.wgt;
+    const float dlt = __fsub_rn(hi, lo);
+    *tau = fabsf(w) < 0.5f ? __fadd_rn(lo, __fmul_rn(w, dlt)) : __fsub_rn(hi, __fmul_rn(dlt, __fsub_rn(1.0f, w)));
   }
 }
 
@@ -709,12 +796,23 @@ extern "C" int sf_hard_flip_count(const void* prev, const void* now, int dtype, 
   return launch_status("sf_hard_flip_count");
 }
 
+namespace sf {
+namespace {
+// Workspace layout: [stats partials | 2 select states | 2 x partial histograms | keys], 256-byte aligned parts.
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+size_t ws_stats_bytes() { return align256(sizeof(double) * 2 * kStatsGrid); }
+size_t ws_state_off() { return ws_stats_bytes(); }
+size_t ws_partial_off() { return ws_state_off() + align256(2 * sizeof(SelState)); }
+size_t ws_partial_bytes() { return align256(sizeof(uint32_t) * kSelStride * kSelGrid); }
+size_t ws_keys_off() { return ws_partial_off() + 2 * ws_partial_bytes(); }
+}  // namespace
+}  // namespace sf
+
 extern "C" size_t sf_mask_workspace_size(int64_t rows, int64_t cols, int64_t sample_size) {
   (void)rows;
   (void)cols;
-  size_t stats = sizeof(double) * 2 * kStatsGrid;
-  size_t keys = sizeof(uint32_t) * static_cast<size_t>(sample_size > 0 ? sample_size : 0);
-  return ((stats + 255) / 256) * 256 + keys;
+  if (sample_size <= 0) return ws_stats_bytes();
+  return ws_keys_off() + sizeof(uint32_t) * static_cast<size_t>(sample_size);
 }
 
 extern "C" int sf_score_stats(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
@@ -765,12 +863,20 @@ extern "C" int sf_tau_quantile(const sf_mask_params* p, const void* W, int w_dty
                "workspace too small");
   if (!H) h_dtype = SF_DTYPE_F32;
   ScoreSpec s = make_spec(p, w_dtype, h_dtype, aux_dtype);
-  size_t off = ((sizeof(double) * 2 * kStatsGrid + 255) / 256) * 256;
-  uint32_t* keys = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + off);
+  char* ws = static_cast<char*>(workspace);
+  uint32_t* keys = reinterpret_cast<uint32_t*>(ws + ws_keys_off());
+  SelState* states = reinterpret_cast<SelState*>(ws + ws_state_off());
+  uint32_t* parts[2] = {reinterpret_cast<uint32_t*>(ws + ws_partial_off()),
+                        reinterpret_cast<uint32_t*>(ws + ws_partial_off() + ws_partial_bytes())};
   hipStream_t st = static_cast<hipStream_t>(stream);
   tau_gather_kernel<<<elementwise_grid(sample_size, kBlock), kBlock, 0, st>>>(s, W, H, aux, p->rows, p->cols, stats,
                                                                                sample_idx, sample_size, keys);
-  tau_select_kernel<<<1, kSelectBlock, 0, st>>>(keys, sample_size, q, tau_out);
+  // pass p reads state p-2 (slot p & 1) and partials p-1, writes state p-1 (slot (p + 1) & 1) and partials p
+  const int grid = static_cast<int>(ceil_div(sample_size, kBlock) < kSelGrid ? ceil_div(sample_size, kBlock) : kSelGrid);
+  for (int pass = 0; pass < 4; ++pass)
+    tau_pass_kernel<<<grid, kBlock, 0, st>>>(keys, sample_size, pass, q, &states[pass & 1], &states[(pass + 1) & 1],
+                                             parts[(pass + 1) & 1], parts[pass & 1]);
+  tau_final_kernel<<<1, kBlock, 0, st>>>(sample_size, q, grid, &states[0], parts[1], tau_out);
   return launch_status("sf_tau_quantile");
 }
 

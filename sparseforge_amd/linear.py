@@ -89,6 +89,11 @@ def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=
         d.bias, d.bias_dtype = L.ptr(bias), L.dtype_code(bias)
     d.emask, d.dw, d.decay = L.ptr(emask), L.ptr(dw), float(decay)
     d.accumulate = int(bool(accumulate))
+    ws_bytes = L.lib().sf_gemm_workspace_size(L.byref(d))
+    ws = None
+    if ws_bytes:  # split-K scratch from torch's caching allocator; the library never allocates
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        d.workspace, d.workspace_bytes = ws.data_ptr(), ws_bytes
     with _prof.region("sf_gemm", 2.0 * M * N * (K1 + K2), "FLOP", dev):
         L.check(L.lib().sf_gemm(L.byref(d), L.stream(dev)), "sf_gemm")
     return out

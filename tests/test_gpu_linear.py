@@ -239,3 +239,45 @@ def test_cpu_tensor_raises():
 
     with pytest.raises(RuntimeError, match="GPU only"):
         lin.mm_nt(torch.ones(8, 8), torch.ones(8, 8))
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_gemm_split_k_skinny(cuda_device, dtype, tol):
+    """GEMMs with few output tiles and long K split K over f32 partials; the
+    reduce applies bias / accumulation, and the second K segment runs once."""
+    L, lin = _lin()
+    g = torch.Generator().manual_seed(23)
+    d = lambda t: t.to(cuda_device)
+    # SLoRB-shaped products: z = x P^T (N = 64), dP = dz^T x (M = 64, K = T)
+    T, IN, R, OUT = 4096, 1024, 64, 320
+    x = torch.randn(T, IN, generator=g).to(dtype)
+    P = torch.randn(R, IN, generator=g).to(dtype)
+    dz = torch.randn(T, R, generator=g).to(dtype)
+    desc = L.GemmDesc()
+    desc.dtype, desc.M, desc.N, desc.K1 = L.dtype_code(x), T, R, IN
+    assert L.lib().sf_gemm_workspace_size(L.byref(desc)) > 0  # this shape splits
+    assert rel_err(lin.mm_nt(d(x), d(P)), x.double() @ P.double().t()) < tol
+    assert rel_err(lin.mm_tn(d(dz), d(x)), dz.double().t() @ x.double()) < tol
+    # second segment + bias on the last split, then accumulate into an existing C
+    W = torch.randn(OUT, IN, generator=g).to(dtype)
+    S = torch.randn(OUT, R, generator=g).to(dtype)
+    z = torch.randn(256, R, generator=g).to(dtype)
+    xa = x[:256].contiguous()
+    b = torch.randn(OUT, generator=g).to(dtype)
+    ref = xa.double() @ W.double().t() + z.double() @ S.double().t() + b.double()
+    got = lin.mm_nt(d(xa), d(W), A2=d(z), B2=d(S), K2=R, bias=d(b))
+    assert rel_err(got, ref) < tol
+    base = torch.randn(256, OUT, generator=g).to(dtype)
+    acc = d(base.clone())
+    lin.mm_nt(d(xa), d(W), out=acc, accumulate=True)
+    assert rel_err(acc, base.double() + xa.double() @ W.double().t()) < tol
+
+
+def test_gemm_split_k_deterministic(cuda_device):
+    L, lin = _lin()
+    g = torch.Generator().manual_seed(29)
+    x = torch.randn(8192, 64, generator=g).bfloat16().to(cuda_device)
+    y = torch.randn(8192, 512, generator=g).bfloat16().to(cuda_device)
+    r1 = lin.mm_tn(x, y)
+    r2 = lin.mm_tn(x, y)
+    assert torch.equal(r1, r2)

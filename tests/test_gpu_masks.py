@@ -198,3 +198,27 @@ def test_tau_quantile_matches_torch(cuda_device):
     for q in (0.0, 0.37, 0.5, 1.0):
         t2 = layer2._tau_unstructured(scores.to(cuda_device), q)
         assert t2.item() == torch.quantile(scores, q).item()
+
+
+@pytest.mark.parametrize("case", ["gauss", "ties", "nan", "tiny"])
+def test_tau_quantile_radix_select_large(cuda_device, case):
+    """The multi-workgroup radix select equals torch.quantile over 262144 keys (ties, NaN, tiny inputs)."""
+    sm = _sm()
+    cfg = sm.SparseLinearConfig(mask_type="unstructured", tau_sample_size=10 ** 7)
+    layer = sm.SparseLinear(64, 32, sparselinear_config=cfg, bias=False).to(cuda_device)
+    g = torch.Generator().manual_seed(17)
+    if case == "tiny":
+        scores = torch.randn(1, 3, generator=g)
+    else:
+        scores = torch.randn(512, 512, generator=g)
+    if case == "ties":
+        scores = (scores * 4).round() / 4  # a handful of distinct values, huge tie runs
+    if case == "nan":
+        scores[7, 9] = float("nan")
+    for q in (0.0, 0.25, 0.5, 0.9, 1.0):
+        got = layer._tau_unstructured(scores.to(cuda_device), q).item()
+        ref = torch.quantile(scores, q).item()
+        if case == "nan":
+            assert got != got and ref != ref
+        else:
+            assert got == ref, (case, q, got, ref)
