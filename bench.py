@@ -17,6 +17,9 @@ Metric (BASELINE.json): SparseLinear fwd+bwd TFLOP/s at LLaMA-2-7B shapes;
   temperature taken from a 1.0 -> 0.01 geometric schedule over 10 steps.
   GB/s counts 20 B per parameter (stats pass: W 2 + H 4; update pass: W 2 +
   H 4 + mask read 4 + mask write 4).
+* ``adamw`` -- one step = the fused mask-aware AdamW update of every masked
+  linear of the 7B model (f32 master weight, bf16 gradient, f32 moments and
+  soft mask, bf16 working copy written back): 32 B per parameter.
 * ``roofline`` -- the dominant kernel (the sf_gemm MFMA GEMM): algorithmic
   FLOPs of the step over the summed device time of its sf_gemm launches,
   timed with HIP events on the launch stream inside the timed region.
@@ -47,10 +50,30 @@ LINEARS = [("q_proj", HIDDEN, HIDDEN), ("k_proj", HIDDEN, HIDDEN), ("v_proj", HI
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 MASK_BYTES_PER_PARAM = 20   # stats pass 6 B + update pass 14 B
+ADAMW_BYTES_PER_PARAM = 32  # master r/w 8, grad 2, m r/w 8, v r/w 8, mask 4, bf16 copy 2
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+TRAFFIC_SUMMARY = os.path.join("profiles", "hbm_traffic_7b_layer.md")
+
+
+def profiled_traffic() -> dict:
+    """Per-launch HBM bytes measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (copy-calibrated) recorded in the committed traffic summary; {} when absent."""
+    out = {}
+    try:
+        with open(os.path.join(REPO, TRAFFIC_SUMMARY)) as f:
+            for line in f:
+                if line.startswith("bench-traffic:"):
+                    for kv in line.split(":", 1)[1].split():
+                        k, v = kv.split("=")
+                        out[k] = int(v)
+    except OSError:
+        pass
+    return out
 
 
 def step_flops(tokens: int) -> float:
@@ -181,6 +204,28 @@ def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
                       f"tokens (full shapes, SLoRB rank {RANK}), {reps} reps in {el:.1f} s"}
 
 
+def cpu_adamw_baseline(budget_s: float = 6.0) -> dict:
+    import numpy as np
+
+    from oracle import adamw as oa
+
+    rng = np.random.default_rng(2)
+    n = 1 << 22  # 4 M params
+    p = (rng.standard_normal(n, dtype=np.float32) * 0.02)
+    g = (rng.standard_normal(n, dtype=np.float32) * 1e-3)
+    mask = rng.random(n, dtype=np.float32)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        p, m, v, _ = oa.step(p, g, m, v, None, mask, reps + 1, 1e-4, (0.9, 0.95), 1e-8, 0.1, decay=6e-5)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 20:
+            break
+    return {"value": round(ADAMW_BYTES_PER_PARAM * n * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port", "sample": f"numpy oracle (oracle/adamw.py) on {n} params, {reps} steps in {el:.1f} s"}
+
+
 def cpu_mask_baseline(budget_s: float = 8.0) -> dict:
     import numpy as np
 
@@ -216,7 +261,10 @@ def main(argv=None) -> int:
     ap.add_argument("--tokens", type=int, default=TOKENS)
     ap.add_argument("--mask-layers", type=int, default=LAYERS, help="decoder layers in the mask-update arena")
     ap.add_argument("--mask-steps", type=int, default=10)
+    ap.add_argument("--adamw-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--calib", action="store_true",
+                    help="first run one plain 256 MiB device copy (a known-size reference for HBM byte counters)")
     a = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -237,6 +285,12 @@ def main(argv=None) -> int:
     L.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if a.calib:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # reads 256 MiB, writes 256 MiB
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---- SparseLinear leg ---------------------------------------------------
     log(f"building decoder layer (T={a.tokens}, bf16, SLoRB rank {RANK})")
@@ -292,9 +346,40 @@ def main(argv=None) -> int:
     st_gbs = ms_["sf_score_stats"].rate / 1e9
     log(f"mask update: {mel * 1e3 / a.mask_steps:.2f} ms/update of the arena, {mask_gbs:.0f} GB/s; "
         f"sf_update_mask {up_gbs:.0f} GB/s, sf_score_stats {st_gbs:.0f} GB/s")
-    del arena
+    # ---- mask-aware AdamW leg (same arena: W is the bf16 copy, M the mask) ---
+    from sparseforge_amd.adamw import adamw_step_
+
+    log("building AdamW state (f32 master, bf16 grad, f32 m / v)")
+    gen = torch.Generator(device=dev).manual_seed(2)
+    opt_state = []
+    arena = [(W, M) for W, _H, M in arena]  # the Hutchinson accumulator is not an AdamW operand: free it
+    for W, M in arena:
+        master = W.float()
+        grad = (torch.randn(W.shape, generator=gen, device=dev) * 1e-3).to(torch.bfloat16)
+        opt_state.append((master, grad, torch.zeros_like(master), torch.zeros_like(master), M, W))
+    torch.cuda.synchronize()
+
+    def adamw_leg_step(k):
+        for master, grad, m, v, M, W in opt_state:
+            adamw_step_(master, grad, m, v, None, M, k, 1e-4, (0.9, 0.95), 1e-8, 0.1, decay=6e-5, bf16_copy=W)
+
+    adamw_leg_step(1)  # warmup
+    torch.cuda.synchronize()
+    with prof.kernel_timer() as at:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(a.adamw_steps):
+            adamw_leg_step(k + 2)
+        torch.cuda.synchronize()
+        ael = time.perf_counter() - t0
+    as_ = at.summary()["sf_adamw_step"]
+    adamw_gbs = ADAMW_BYTES_PER_PARAM * n_params * a.adamw_steps / ael / 1e9
+    log(f"adamw: {ael * 1e3 / a.adamw_steps:.2f} ms/step of the arena, {adamw_gbs:.0f} GB/s; "
+        f"sf_adamw_step {as_.rate / 1e9:.0f} GB/s over kernel time")
+    del arena, opt_state
     torch.cuda.empty_cache()
 
+    traffic = profiled_traffic()
     out = {
         "metric": "SparseLinear fwd+bwd TFLOP/s @7B shapes; 2:4 mask-update HBM GB/s",
         "value": round(tflops, 3),
@@ -312,7 +397,9 @@ def main(argv=None) -> int:
                                "11008x4096, down 4096x11008), hard 2:4 mask (hardening_x=0), SLoRB rank 64",
                    "tokens": a.tokens, "linears": len(LINEARS), "flops_per_step": flops},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tflops, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic.get("sf_gemm_bytes_per_launch"), "traffic_unit": "B/launch",
+                     "traffic_source": TRAFFIC_SUMMARY,
                      "kernel": "sf_gemm (gemm_kernel<bf16>)", "launches": g.launches,
                      "avg_launch_ms": round(g.avg_ms, 4)},
         "kernels": other,
@@ -321,16 +408,26 @@ def main(argv=None) -> int:
             "ms_per_update": round(mel * 1e3 / a.mask_steps, 3), "bytes_per_param": MASK_BYTES_PER_PARAM,
             "roofline": {"bound": "hbm", "kernel": "sf_update_mask", "achieved": round(up_gbs, 2),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(up_gbs / PEAK_HBM_GBS, 4),
-                         "traffic": None, "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4)},
+                         "traffic": traffic.get("sf_update_mask_bytes_per_launch"), "traffic_unit": "B/launch",
+                         "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4)},
             "score_stats_gbs": round(st_gbs, 2),
             "kernels": {n: {"launches": s.launches, "avg_ms": round(s.avg_ms, 4), "total_ms": round(s.total_ms, 3)}
                         for n, s in ms_.items()},
         },
     }
+    out["adamw"] = {
+        "value": round(adamw_gbs, 2), "unit": "GB/s", "params": n_params, "steps": a.adamw_steps,
+        "ms_per_step": round(ael * 1e3 / a.adamw_steps, 3), "bytes_per_param": ADAMW_BYTES_PER_PARAM,
+        "roofline": {"bound": "hbm", "kernel": "sf_adamw_step", "achieved": round(as_.rate / 1e9, 2),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(as_.rate / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": traffic.get("sf_adamw_step_bytes_per_launch"), "traffic_unit": "B/launch",
+                     "avg_launch_ms": round(as_.avg_ms, 4)},
+    }
     if not a.no_cpu:
         log("timing CPU baseline (numpy oracle)")
         out["cpu_baseline"] = cpu_baseline()
         out["mask_update"]["cpu_baseline"] = cpu_mask_baseline()
+        out["adamw"]["cpu_baseline"] = cpu_adamw_baseline()
     print(json.dumps(out), flush=True)
     return 0
 

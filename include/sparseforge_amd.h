@@ -237,6 +237,29 @@ size_t sf_gemm_workspace_size(const sf_gemm_desc* d);
  */
 int sf_column_sum(const void* A, int a_dtype, int64_t rows, int64_t cols, void* out, int out_dtype, void* stream);
 
+/* ---- mask-aware AdamW (AdamW.step, legacy/adamw.py:65-176) ------------- */
+typedef struct sf_adamw_params {
+  double lr, weight_decay, beta1, beta2, eps;
+  double decay; /* SR-STE masked-decay strength: the optimizer's `decay` (:51, :76-77, :101) */
+  double l1;    /* adaptive_l1_decay (:56)                                                   */
+  int amsgrad;
+  int apply_l1; /* the parameter is >= 2-D (the l1 term also needs a mask, :171-172)        */
+  int64_t step; /* state['step'] after this step's increment (:146)                         */
+} sf_adamw_params;
+
+/*
+ * One AdamW step of one parameter tensor of n elements, in place: param,
+ * exp_avg, exp_avg_sq (and max_exp_avg_sq when amsgrad), replacing the
+ * per-parameter body of AdamW.step (legacy/adamw.py:84-174) with one fused
+ * pass.  mask (the parameter's `mask` attribute, :99) may be NULL: no
+ * masked decay and no L1 term.  param_bf16_copy (may be NULL) receives the
+ * updated parameter rounded to bf16 (an f32 master parameter with its bf16
+ * working copy).  Scalars follow the reference's Python doubles.
+ */
+int sf_adamw_step(void* param, int param_dtype, const void* grad, int grad_dtype, void* exp_avg, void* exp_avg_sq,
+                  void* max_exp_avg_sq, int state_dtype, const void* mask, int mask_dtype, void* param_bf16_copy,
+                  int64_t n, const sf_adamw_params* hp, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -124,6 +124,23 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+class AdamwParams(ctypes.Structure):
+    """Mirror of ``sf_adamw_params``."""
+
+    _fields_ = [
+        ("lr", ctypes.c_double),
+        ("weight_decay", ctypes.c_double),
+        ("beta1", ctypes.c_double),
+        ("beta2", ctypes.c_double),
+        ("eps", ctypes.c_double),
+        ("decay", ctypes.c_double),
+        ("l1", ctypes.c_double),
+        ("amsgrad", ctypes.c_int),
+        ("apply_l1", ctypes.c_int),
+        ("step", ctypes.c_int64),
+    ]
+
+
 byref = ctypes.byref
 
 _P = ctypes.c_void_p
@@ -149,6 +166,7 @@ SIGNATURES = {
     "sf_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
     "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "sf_column_sum": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
+    "sf_adamw_step": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _P, _I64, ctypes.POINTER(AdamwParams), _P]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,209 @@
+// Fused mask-aware AdamW step (K10) on gfx950.
+//
+// One memory-bound pass per parameter tensor replaces the ~10 PyTorch ops
+// per parameter of AdamW.step (legacy/adamw.py:79-174).  Per element, in the
+// reference's op order and f32 arithmetic (each tensor op rounds to its
+// result dtype; torch's add(alpha=) and addcmul are fused multiply-adds on
+// the CPU, addcdiv is w + (value * y) / z with separate roundings):
+//
+//   p  <- p * (1 - lr wd)                                   (:85)
+//   g  <- g + decay * (p * (1 - mask))        if mask       (:98-109)
+//   m  <- m b1 + (1 - b1) g                                  (:151)
+//   v  <- v b2 + ((1 - b2) g) g                              (:152)
+//   vmax <- max(vmax, v)                      if amsgrad     (:153-155)
+//   d  <- sqrt(v or vmax) / sqrt(bc2) + eps                  (:157-159)
+//   p  <- p + (-lr / bc1) m / d                              (:161-163)
+//   p  <- p - lr * (l1 sign(p) / d)           if l1 > 0, mask, 2-D (:171-174)
+//
+// Optionally the updated parameter is also written as a bf16 copy (an f32
+// master parameter with the bf16 weight the GEMMs read).  Each thread owns
+// 4 consecutive elements; 16-byte loads when every operand allows them.
+
+#include "sf_common.hpp"
+
+namespace sf {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float rnd(float x, int dtype) { return dtype == SF_DTYPE_BF16 ? round_bf16(x) : x; }
+
+struct AdamArgs {
+  void* p;
+  const void* g;
+  void* m;
+  void* v;
+  void* vmax;
+  const void* mask;
+  void* pcopy;
+  int64_t n;
+  int p_dt, g_dt, s_dt, m_dt;
+  float c_wd;       // 1 - lr * wd
+  float decay;      // SR-STE masked decay
+  float b1, omb1;   // beta1, 1 - beta1
+  float b2, omb2;   // beta2, 1 - beta2
+  float sqrt_bc2;   // sqrt(1 - beta2^step)
+  float eps;
+  float neg_ss;     // -lr / (1 - beta1^step)
+  float l1;         // adaptive L1 strength (0: off)
+  float neg_lr;     // -lr
+  int amsgrad;
+};
+
+__device__ __forceinline__ int promote(int a, int b) {
+  return (a == SF_DTYPE_F32 || b == SF_DTYPE_F32) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
+}
+
+template <int PD, int SD>
+__device__ __forceinline__ void adam_element(const AdamArgs& a, float& p, float g, float& m, float& v, float& vmax,
+                                             float mask, bool has_mask) {
+  p = rnd(p * a.c_wd, PD);
+  if (has_mask) {
+    const int tdt = promote(PD, a.m_dt);  // dtype of p * (1 - mask)
+    const float t = rnd(p * rnd(1.0f - mask, a.m_dt), tdt);
+    g = rnd(fmaf(t, a.decay, g), promote(a.g_dt, tdt));
+  }
+  m = rnd(m * a.b1, SD);
+  m = rnd(fmaf(g, a.omb1, m), SD);
+  v = rnd(v * a.b2, SD);
+  v = rnd(fmaf(a.omb2 * g, g, v), SD);
+  float vv = v;
+  if (a.amsgrad) {
+    vmax = fmaxf(vmax, v);
+    vv = vmax;
+  }
+  const float d = rnd(rnd(rnd(sqrtf(vv), SD) / a.sqrt_bc2, SD) + a.eps, SD);
+  p = rnd(p + (a.neg_ss * m) / d, PD);
+  if (a.l1 > 0.0f && has_mask) {
+    const float sg = p > 0.0f ? 1.0f : (p < 0.0f ? -1.0f : p);  // torch.sign (NaN stays NaN)
+    const float lt = rnd(rnd(a.l1 * sg, PD) / d, PD);
+    p = rnd(fmaf(lt, a.neg_lr, p), PD);
+  }
+}
+
+// 4 consecutive elements as f32: one 16-byte (f32) or 8-byte (bf16) access
+// when `vec`, element by element (cnt of them) otherwise.
+__device__ __forceinline__ void ld4(const void* b, int64_t i0, int dt, bool vec, int cnt, float o[4]) {
+  if (vec) {
+    if (dt == SF_DTYPE_F32) {
+      const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(b) + i0);
+      o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
+    } else {
+      const uint2 x = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(b) + i0);
+      o[0] = bf16_to_f32(x.x & 0xffffu); o[1] = bf16_to_f32(x.x >> 16);
+      o[2] = bf16_to_f32(x.y & 0xffffu); o[3] = bf16_to_f32(x.y >> 16);
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o[j] = j < cnt ? load_as_f32(b, i0 + j, dt) : 0.0f;
+}
+
+__device__ __forceinline__ void st4(void* b, int64_t i0, int dt, bool vec, int cnt, const float v[4]) {
+  if (vec) {
+    if (dt == SF_DTYPE_F32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(b) + i0) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint2 x;
+      x.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+      x.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(b) + i0) = x;
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (j < cnt) store_from_f32(b, i0 + j, dt, v[j]);
+}
+
+template <int PD, int SD>
+__global__ void __launch_bounds__(kBlock) adamw_kernel(AdamArgs a, bool aligned) {
+  const int64_t nvec = (a.n + 3) / 4;
+  const bool has_mask = a.mask != nullptr;
+  for (int64_t iv = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; iv < nvec;
+       iv += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i0 = iv * 4;
+    const int cnt = a.n - i0 >= 4 ? 4 : static_cast<int>(a.n - i0);
+    const bool vec = aligned && cnt == 4;
+    float p[4], g[4], m[4], v[4], x[4] = {0, 0, 0, 0}, mk[4] = {0, 0, 0, 0};
+    ld4(a.p, i0, PD, vec, cnt, p);
+    ld4(a.g, i0, a.g_dt, vec, cnt, g);
+    ld4(a.m, i0, SD, vec, cnt, m);
+    ld4(a.v, i0, SD, vec, cnt, v);
+    if (a.amsgrad) ld4(a.vmax, i0, SD, vec, cnt, x);
+    if (has_mask) ld4(a.mask, i0, a.m_dt, vec, cnt, mk);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) adam_element<PD, SD>(a, p[j], g[j], m[j], v[j], x[j], mk[j], has_mask);
+    st4(a.p, i0, PD, vec, cnt, p);
+    st4(a.m, i0, SD, vec, cnt, m);
+    st4(a.v, i0, SD, vec, cnt, v);
+    if (a.amsgrad) st4(a.vmax, i0, SD, vec, cnt, x);
+    if (a.pcopy) st4(a.pcopy, i0, SF_DTYPE_BF16, vec, cnt, p);
+  }
+}
+
+bool dt_ok(int d) { return d == SF_DTYPE_F32 || d == SF_DTYPE_BF16; }
+
+}  // namespace
+}  // namespace sf
+
+using namespace sf;
+
+extern "C" int sf_adamw_step(void* param, int param_dtype, const void* grad, int grad_dtype, void* exp_avg,
+                             void* exp_avg_sq, void* max_exp_avg_sq, int state_dtype, const void* mask, int mask_dtype,
+                             void* param_bf16_copy, int64_t n, const sf_adamw_params* hp, void* stream) {
+  SF_CHECK_ARG(hp != nullptr, "null sf_adamw_params");
+  SF_CHECK_ARG(n >= 0, "negative element count");
+  SF_CHECK_ARG(dt_ok(param_dtype) && dt_ok(grad_dtype) && dt_ok(state_dtype) && (!mask || dt_ok(mask_dtype)),
+               "bad dtype");
+  SF_CHECK_ARG(hp->step >= 1, "step must be >= 1 (the count after this step)");
+  SF_CHECK_ARG(hp->lr >= 0.0 && hp->eps >= 0.0, "Invalid learning rate or epsilon value");
+  SF_CHECK_ARG(hp->beta1 >= 0.0 && hp->beta1 < 1.0 && hp->beta2 >= 0.0 && hp->beta2 < 1.0,
+               "Invalid beta parameter");
+  if (n == 0) return SF_OK;
+  SF_CHECK_ARG(param && grad && exp_avg && exp_avg_sq, "null tensor");
+  SF_CHECK_ARG(!hp->amsgrad || max_exp_avg_sq, "amsgrad needs max_exp_avg_sq");
+  AdamArgs a;
+  a.p = param;
+  a.g = grad;
+  a.m = exp_avg;
+  a.v = exp_avg_sq;
+  a.vmax = hp->amsgrad ? max_exp_avg_sq : nullptr;
+  a.mask = mask;
+  a.pcopy = param_bf16_copy;
+  a.n = n;
+  a.p_dt = param_dtype;
+  a.g_dt = grad_dtype;
+  a.s_dt = state_dtype;
+  a.m_dt = mask ? mask_dtype : SF_DTYPE_F32;
+  // Python-side scalars in double, then the f32 scalar operand of each tensor op
+  a.c_wd = static_cast<float>(1.0 - hp->lr * hp->weight_decay);
+  a.decay = static_cast<float>(hp->decay);
+  a.b1 = static_cast<float>(hp->beta1);
+  a.omb1 = static_cast<float>(1.0 - hp->beta1);
+  a.b2 = static_cast<float>(hp->beta2);
+  a.omb2 = static_cast<float>(1.0 - hp->beta2);
+  const double bc1 = 1.0 - pow(hp->beta1, static_cast<double>(hp->step));
+  const double bc2 = 1.0 - pow(hp->beta2, static_cast<double>(hp->step));
+  a.sqrt_bc2 = static_cast<float>(sqrt(bc2));
+  a.eps = static_cast<float>(hp->eps);
+  a.neg_ss = static_cast<float>(-(hp->lr / bc1));
+  a.l1 = mask && hp->apply_l1 ? static_cast<float>(hp->l1) : 0.0f;
+  a.neg_lr = static_cast<float>(-hp->lr);
+  a.amsgrad = hp->amsgrad;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid((n + 3) / 4, kBlock);
+  auto al = [](const void* q, int dt) { return !q || (reinterpret_cast<uintptr_t>(q) % (dt == SF_DTYPE_F32 ? 16 : 8)) == 0; };
+  const bool aligned = al(param, param_dtype) && al(grad, grad_dtype) && al(exp_avg, state_dtype) &&
+                       al(exp_avg_sq, state_dtype) && al(a.vmax, state_dtype) && al(mask, a.m_dt) &&
+                       al(param_bf16_copy, SF_DTYPE_BF16);
+  if (param_dtype == SF_DTYPE_F32 && state_dtype == SF_DTYPE_F32)
+    adamw_kernel<SF_DTYPE_F32, SF_DTYPE_F32><<<grid, kBlock, 0, st>>>(a, aligned);
+  else if (param_dtype == SF_DTYPE_F32)
+    adamw_kernel<SF_DTYPE_F32, SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(a, aligned);
+  else if (state_dtype == SF_DTYPE_F32)
+    adamw_kernel<SF_DTYPE_BF16, SF_DTYPE_F32><<<grid, kBlock, 0, st>>>(a, aligned);
+  else
+    adamw_kernel<SF_DTYPE_BF16, SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(a, aligned);
+  return launch_status("sf_adamw_step");
+}
