@@ -260,6 +260,33 @@ int sf_adamw_step(void* param, int param_dtype, const void* grad, int grad_dtype
                   void* max_exp_avg_sq, int state_dtype, const void* mask, int mask_dtype, void* param_bf16_copy,
                   int64_t n, const sf_adamw_params* hp, void* stream);
 
+/* ---- Hutchinson Hessian diagonal (update_hessian_hutchinson, legacy/utils.py:710-869) ----
+ * Probe v(seed, i) = +-1 from bit i % 64 of output i / 64 of the SplitMix64
+ * stream seeded with `seed`: a pure function, regenerated wherever needed.  It
+ * replaces the torch.randint draw of _rademacher_like (:710-711). */
+
+/* v[0..n) = v(seed, i) in dtype (the tensor the backward of the probe dot needs). */
+int sf_rademacher(void* v, int dtype, int64_t n, uint64_t seed, void* stream);
+
+/* Scratch bytes of sf_rademacher_dot. */
+size_t sf_rademacher_dot_workspace_size(void);
+
+/*
+ * out (device float[1]) = sum_i g[i] * v_i, the per-weight term of the probe
+ * dot (legacy/utils.py:781-788); v from (seed, i), or from `v` when not NULL.
+ * f64 partial sums in a fixed order (deterministic).
+ */
+int sf_rademacher_dot(const void* g, int g_dtype, const void* v, int v_dtype, int64_t n, uint64_t seed, float* out,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * H <- beta * H + (1 - beta) * clamp(hvp * v, min=0), in place, one pass
+ * (legacy/utils.py:806-868 single-GPU branch).  v from (seed, i), or from `v`
+ * when not NULL (the reference's own probes in parity tests).
+ */
+int sf_hutchinson_update(void* H, int h_dtype, const void* hvp, int hvp_dtype, const void* v, int v_dtype, int64_t n,
+                         uint64_t seed, double beta, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

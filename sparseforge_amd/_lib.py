@@ -167,6 +167,10 @@ SIGNATURES = {
     "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "sf_column_sum": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
     "sf_adamw_step": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _P, _I64, ctypes.POINTER(AdamwParams), _P]),
+    "sf_rademacher": (_I, [_P, _I, _I64, ctypes.c_uint64, _P]),
+    "sf_rademacher_dot_workspace_size": (_SZ, []),
+    "sf_rademacher_dot": (_I, [_P, _I, _P, _I, _I64, ctypes.c_uint64, _P, _P, _SZ, _P]),
+    "sf_hutchinson_update": (_I, [_P, _I, _P, _I, _P, _I, _I64, ctypes.c_uint64, ctypes.c_double, _P]),
 }
 
 _lock = threading.Lock()

@@ -1,0 +1,134 @@
+// Hutchinson Hessian-diagonal estimation (K9) on gfx950.
+//
+// update_hessian_hutchinson (legacy/utils.py:714-869) draws a Rademacher
+// probe v per SparseLinear weight, forms dot = sum_W sum(g_W * v_W) from the
+// first-order gradients (create_graph=True), takes hvp = d dot / d W through
+// the double backward, and folds est = clamp(hvp * v, 0) into the layer's
+// hessian_diag by an EMA.  Here:
+//
+//   sf_rademacher          v materialised (the backward of the dot needs it)
+//   sf_rademacher_dot      sum(g * v) with v regenerated on the fly
+//   sf_hutchinson_update   H <- beta H + (1 - beta) clamp(hvp * v, 0): one pass,
+//                          v regenerated from (seed, index) -- 0 bytes of HBM --
+//                          or read from an explicit tensor (parity tests feed
+//                          the reference's own probes).
+//
+// v(seed, i) = +1 / -1 from bit i % 64 of SplitMix64 output i / 64 of the
+// stream seeded with `seed` (sf_rng.hpp): a pure function of (seed, i), so
+// the dot, the backward and the update agree on v without storing it.
+
+#include "sf_common.hpp"
+#include "sf_rng.hpp"
+
+namespace sf {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kDotGrid = 1024;
+
+__device__ __forceinline__ float rnd(float x, int dtype) { return dtype == SF_DTYPE_BF16 ? round_bf16(x) : x; }
+
+__device__ __forceinline__ float probe(const void* v, int v_dtype, uint64_t seed, int64_t i) {
+  return v ? load_as_f32(v, i, v_dtype) : rademacher(seed, static_cast<uint64_t>(i));
+}
+
+__global__ void __launch_bounds__(kBlock) rademacher_kernel(void* v, int dtype, int64_t n, uint64_t seed) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    store_from_f32(v, i, dtype, rademacher(seed, static_cast<uint64_t>(i)));
+}
+
+// Per-workgroup f64 partial sums of g * v (fixed grid: deterministic), then one
+// workgroup folds them in index order.
+__global__ void __launch_bounds__(kBlock) rademacher_dot_partial(const void* __restrict__ g, int g_dtype,
+                                                                 const void* __restrict__ v, int v_dtype, int64_t n,
+                                                                 uint64_t seed, double* __restrict__ partial) {
+  double s = 0.0;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    s += static_cast<double>(load_as_f32(g, i, g_dtype)) * probe(v, v_dtype, seed, i);
+  __shared__ double red[kBlock / 64];
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_down(s, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < kBlock / 64; ++w) t += red[w];
+    partial[blockIdx.x] = t;
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) rademacher_dot_final(const double* __restrict__ partial, int nparts,
+                                                               float* __restrict__ out) {
+  __shared__ double red[kBlock];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += kBlock) s += partial[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int off = kBlock / 2; off > 0; off >>= 1) {
+    if (threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = static_cast<float>(red[0]);
+}
+
+// H <- H * beta + (1 - beta) * clamp(hvp * v, 0), in the reference's op order:
+// est = (hvp * v) in the promoted dtype, clamp_min(0), H.mul_(beta) then
+// add_(est, alpha=1 - beta) (a fused multiply-add in torch's CPU kernel).
+template <int HD>
+__global__ void __launch_bounds__(kBlock) hutch_update_kernel(void* __restrict__ H, const void* __restrict__ hvp,
+                                                              int hvp_dtype, const void* __restrict__ v, int v_dtype,
+                                                              int est_dtype, int64_t n, uint64_t seed, float beta,
+                                                              float omb) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    float est = rnd(load_as_f32(hvp, i, hvp_dtype) * probe(v, v_dtype, seed, i), est_dtype);
+    est = est < 0.0f ? 0.0f : est;  // clamp(min=0); NaN passes through as in torch.clamp
+    const float h = rnd(load_as_f32(H, i, HD) * beta, HD);
+    store_from_f32(H, i, HD, rnd(fmaf(est, omb, h), HD));
+  }
+}
+
+bool dt_ok(int d) { return d == SF_DTYPE_F32 || d == SF_DTYPE_BF16; }
+
+}  // namespace
+}  // namespace sf
+
+using namespace sf;
+
+extern "C" int sf_rademacher(void* v, int dtype, int64_t n, uint64_t seed, void* stream) {
+  SF_CHECK_ARG(n >= 0 && dt_ok(dtype), "bad size or dtype");
+  if (n == 0) return SF_OK;
+  SF_CHECK_ARG(v, "null tensor");
+  rademacher_kernel<<<elementwise_grid(n, kBlock), kBlock, 0, static_cast<hipStream_t>(stream)>>>(v, dtype, n, seed);
+  return launch_status("sf_rademacher");
+}
+
+extern "C" size_t sf_rademacher_dot_workspace_size(void) { return sizeof(double) * kDotGrid; }
+
+extern "C" int sf_rademacher_dot(const void* g, int g_dtype, const void* v, int v_dtype, int64_t n, uint64_t seed,
+                                 float* out, void* workspace, size_t workspace_bytes, void* stream) {
+  SF_CHECK_ARG(n >= 0 && dt_ok(g_dtype) && (!v || dt_ok(v_dtype)), "bad size or dtype");
+  SF_CHECK_ARG(out && (n == 0 || g), "null tensor");
+  SF_CHECK_ARG(workspace && workspace_bytes >= sf_rademacher_dot_workspace_size(), "workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  double* partial = static_cast<double*>(workspace);
+  rademacher_dot_partial<<<kDotGrid, kBlock, 0, st>>>(g, g_dtype, v, v_dtype, n, seed, partial);
+  rademacher_dot_final<<<1, kBlock, 0, st>>>(partial, kDotGrid, out);
+  return launch_status("sf_rademacher_dot");
+}
+
+extern "C" int sf_hutchinson_update(void* H, int h_dtype, const void* hvp, int hvp_dtype, const void* v, int v_dtype,
+                                    int64_t n, uint64_t seed, double beta, void* stream) {
+  SF_CHECK_ARG(n >= 0 && dt_ok(h_dtype) && dt_ok(hvp_dtype) && (!v || dt_ok(v_dtype)), "bad size or dtype");
+  if (n == 0) return SF_OK;
+  SF_CHECK_ARG(H && hvp, "null tensor");
+  // (hvp * v) takes the promoted dtype of the two (v is in the weight dtype in the reference)
+  const int est_dtype = (hvp_dtype == SF_DTYPE_F32 || (v && v_dtype == SF_DTYPE_F32)) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
+  const float b = static_cast<float>(beta), omb = static_cast<float>(1.0 - beta);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(n, kBlock);
+  if (h_dtype == SF_DTYPE_F32)
+    hutch_update_kernel<SF_DTYPE_F32><<<grid, kBlock, 0, st>>>(H, hvp, hvp_dtype, v, v_dtype, est_dtype, n, seed, b, omb);
+  else
+    hutch_update_kernel<SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(H, hvp, hvp_dtype, v, v_dtype, est_dtype, n, seed, b,
+                                                                omb);
+  return launch_status("sf_hutchinson_update");
+}
