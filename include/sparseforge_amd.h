@@ -215,7 +215,22 @@ typedef struct sf_gemm_desc {
                       aligned: lets a GEMM with few output tiles split K (f32 partial
                       sums reduced in a fixed order); NULL runs it unsplit             */
   size_t workspace_bytes;
+  /* Block-sparse-16 operands (the compressed layout of convert_to_block_sparse,
+     legacy/triton_block_sparse.py:46-103, plus its block map from sf_bsr_*): */
+  int b_format;           /* SF_BFMT_*.  BSR16: B1 is the blocks array [nnz][16][16] of a
+                             weight W; b_layout SF_LAYOUT_K gives B = W (forward, W is
+                             [N, K1]), SF_LAYOUT_MN gives B = W^T (input gradient, W is
+                             [K1, N]); pruned blocks are skipped, no bmask / K2     */
+  const int32_t* b_map;   /* [b_map_rows][b_map_cols] block indices of W, -1 = pruned   */
+  int64_t b_map_rows, b_map_cols;
+  void* c_blocks;         /* non-NULL: C is written only at the blocks c_map lists, into
+                             c_blocks [nnz][16][16] (the SDDMM weight gradient)        */
+  const int32_t* c_map;   /* [M/16][N/16] block indices of C, -1 = not stored            */
+  int64_t c_map_rows, c_map_cols;
 } sf_gemm_desc;
+
+#define SF_BFMT_DENSE 0
+#define SF_BFMT_BSR16 1
 
 /*
  * C = A1 . (B1 * E * s)^T + A2 . B2^T (+ bias), bf16 or f32 MFMA on gfx950.
@@ -236,6 +251,29 @@ size_t sf_gemm_workspace_size(const sf_gemm_desc* d);
  * legacy/sparse_modeling.py:127-129).  f32 accumulation, result in out_dtype.
  */
 int sf_column_sum(const void* A, int a_dtype, int64_t rows, int64_t cols, void* out, int out_dtype, void* stream);
+
+/* ---- block-sparse-16 index (convert_to_block_sparse, legacy/triton_block_sparse.py:46-103) ----
+ * A block is kept iff sum(|W * mask|) over it is > 0 (a block holding a NaN is
+ * dropped, as the reference's sum > 0 test does).  Building a layout:
+ * sf_bsr_count -> sf_bsr_scan -> (read row_ptr[nbr] = nnz, allocate) -> sf_bsr_fill. */
+
+/* flags [nbr * nbc] (1 = kept) and counts [nbr] of kept blocks per block row. */
+int sf_bsr_count(const void* W, int w_dtype, const void* mask, int mask_dtype, int64_t rows, int64_t cols,
+                 int block_size, uint8_t* flags, int32_t* counts, void* stream);
+
+/* row_ptr [nbr + 1] = exclusive scan of counts (row_ptr[0] = 0). */
+int sf_bsr_scan(const int32_t* counts, int64_t nbr, int32_t* row_ptr, void* stream);
+
+/* col_idx [nnz] (ascending per block row), blocks [nnz][bs][bs] = W * mask in
+ * blocks_dtype, and optionally block_map [nbr][nbc] (index or -1). */
+int sf_bsr_fill(const void* W, int w_dtype, const void* mask, int mask_dtype, int64_t rows, int64_t cols,
+                int block_size, const uint8_t* flags, const int32_t* row_ptr, int32_t* col_idx, void* blocks,
+                int blocks_dtype, int32_t* block_map, void* stream);
+
+/* block_map [nbr][nbc] from any CSR block index (row_ptr must be a valid scan
+ * over col_idx; out-of-range columns are ignored). */
+int sf_bsr_block_map(const int32_t* row_ptr, const int32_t* col_idx, int64_t nbr, int64_t nbc, int32_t* block_map,
+                     void* stream);
 
 /* ---- mask-aware AdamW (AdamW.step, legacy/adamw.py:65-176) ------------- */
 typedef struct sf_adamw_params {

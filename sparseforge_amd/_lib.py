@@ -57,6 +57,9 @@ EFF_HARD = 2
 LAYOUT_K = 0
 LAYOUT_MN = 1
 
+BFMT_DENSE = 0
+BFMT_BSR16 = 1
+
 
 class MaskParams(ctypes.Structure):
     """Mirror of ``sf_mask_params``."""
@@ -121,6 +124,14 @@ class GemmDesc(ctypes.Structure):
         ("bmask_bytes", ctypes.c_int),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("b_format", ctypes.c_int),
+        ("b_map", ctypes.c_void_p),
+        ("b_map_rows", ctypes.c_int64),
+        ("b_map_cols", ctypes.c_int64),
+        ("c_blocks", ctypes.c_void_p),
+        ("c_map", ctypes.c_void_p),
+        ("c_map_rows", ctypes.c_int64),
+        ("c_map_cols", ctypes.c_int64),
     ]
 
 
@@ -167,6 +178,10 @@ SIGNATURES = {
     "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "sf_column_sum": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
     "sf_adamw_step": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _P, _I64, ctypes.POINTER(AdamwParams), _P]),
+    "sf_bsr_count": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _P, _P, _P]),
+    "sf_bsr_scan": (_I, [_P, _I64, _P, _P]),
+    "sf_bsr_fill": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _P, _P, _P, _P, _I, _P, _P]),
+    "sf_bsr_block_map": (_I, [_P, _P, _I64, _I64, _P, _P]),
     "sf_rademacher": (_I, [_P, _I, _I64, ctypes.c_uint64, _P]),
     "sf_rademacher_dot_workspace_size": (_SZ, []),
     "sf_rademacher_dot": (_I, [_P, _I, _P, _I, _I64, ctypes.c_uint64, _P, _P, _SZ, _P]),

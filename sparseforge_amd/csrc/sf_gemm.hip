@@ -78,6 +78,13 @@ struct GemmArgs {
   int splits;            // K splits (1: the kernel writes C itself)
   int64_t split_stages;  // segment-1 stages per split
   float* partial;        // splits > 1: [splits][M][N] f32 partial sums
+  // block-sparse-16 B1 (B layouts 2 / 3): B1 is the blocks array, b_map its block map
+  const int32_t* b_map;
+  int64_t b_map_rows, b_map_cols;
+  // block-sparse-16 C: the epilogue writes only the blocks c_map lists, into c_blocks
+  void* c_blocks;
+  const int32_t* c_map;
+  int64_t c_map_rows, c_map_cols;
 };
 
 // Element traits.  bf16 uses v_mfma_f32_32x32x16_bf16 (8 k-values per lane),
@@ -400,6 +407,102 @@ __device__ __forceinline__ void store_rc(const Stage<T, MK>& st, T* lds, bool ha
   }
 }
 
+// B operand gathered from a block-sparse-16 weight W: 16 x 16 blocks stored
+// row-major in `blocks`, located through a block map [rows][cols] of block
+// indices (-1: the block is pruned and reads as zeros).  TRANS = 0 (B layout
+// 2): B(n, k) = W(n, k), the forward y = x W^T.  TRANS = 1 (B layout 3):
+// B(n, k) = W(k, n), the input gradient dx = dy W.  Thread t owns 8
+// consecutive 16-byte vectors of one block of the stage's tile (16 blocks
+// along n x BK/16 along k), so a block's data is read as contiguous 128-byte
+// runs; its map entry is fetched one stage ahead.
+template <typename T, int TRANS>
+struct BsrLoader {
+  static constexpr int VEC = Tr<T>::VEC, BK = Tr<T>::BK, KBLK = BK / 16;
+  static constexpr int VPB = 256 / VEC;     // vectors per block
+  static constexpr int VPR = 16 / VEC;      // vectors per block row
+  const T* blocks;
+  const int32_t* map;
+  int64_t nbr, nbc;  // block-map extent
+  int64_t nb0;       // first block along n of the tile
+  int bn, bk, w0;    // the thread's block (along n, along k within a stage) and first vector in it
+  int32_t idx_next;  // map entry of the thread's block in the next stage to load
+
+  __device__ __forceinline__ void init(const void* blk, const int32_t* m, int64_t rows, int64_t cols, int64_t n0,
+                                       int64_t kstart) {
+    blocks = static_cast<const T*>(blk);
+    map = m;
+    nbr = rows;
+    nbc = cols;
+    nb0 = n0 / 16;
+    const int b = (threadIdx.x * 8) / VPB;
+    bn = b / KBLK;
+    bk = b % KBLK;
+    w0 = (threadIdx.x * 8) % VPB;
+    idx_next = lookup(kstart);
+  }
+  __device__ __forceinline__ int32_t lookup(int64_t k0) const {
+    const int64_t kb = k0 / 16 + bk, n_b = nb0 + bn;
+    const int64_t r = TRANS ? kb : n_b, c = TRANS ? n_b : kb;
+    if (r >= nbr || c >= nbc) return -1;
+    return map[r * nbc + c];
+  }
+  // Load the stage at k0 (its map entry was fetched by the previous call) and
+  // prefetch the map entry of the stage after it.  Returns the block index.
+  __device__ __forceinline__ int32_t load(Stage<T, kMaskNone>& st, int64_t k0) {
+    const int32_t idx = idx_next;
+    idx_next = lookup(k0 + BK);
+    const T* src = blocks + (int64_t)(idx < 0 ? 0 : idx) * 256 + w0 * VEC;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.v[i] = idx >= 0 ? ld16(src + i * VEC) : zero16();
+    return idx;
+  }
+  // Write the staged vectors to the B tile of LDS ([n][k], pitch P), and the
+  // block's presence flag (by the thread holding the block's first vectors).
+  __device__ __forceinline__ void store(const Stage<T, kMaskNone>& st, int32_t idx, T* lds, uint8_t* pres) const {
+    constexpr int P = Tr<T>::PITCH;
+    if (w0 == 0) pres[bn * KBLK + bk] = idx >= 0 ? 1 : 0;
+    if constexpr (TRANS == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int w = w0 + i, row = w / VPR, ch = w % VPR;
+        T* dst = lds + (bn * 16 + row) * P + bk * 16 + ch * VEC;
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<uint4*>(dst) = make_uint4(st.v[i].w[0], st.v[i].w[1], st.v[i].w[2], st.v[i].w[3]);
+        } else {
+          uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+          d[0] = st.v[i].w[0];
+          d[1] = st.v[i].w[1];
+          d[2] = st.v[i].w[2];
+          d[3] = st.v[i].w[3];
+        }
+      }
+    } else {
+      // the thread holds KR consecutive block rows (= k) x 16 columns (= n):
+      // write, for each n, its KR k-values contiguously
+      constexpr int KR = 8 / VPR;  // 4 (bf16) or 2 (f32)
+      const int k_row0 = w0 / VPR;
+#pragma unroll
+      for (int n = 0; n < 16; ++n) {
+        const int ch = n / VEC, e = n % VEC;
+        T* dst = lds + (bn * 16 + n) * P + bk * 16 + k_row0;
+        if constexpr (sizeof(T) == 2) {
+          uint32_t h[KR];
+#pragma unroll
+          for (int r = 0; r < KR; ++r) {
+            const uint32_t wd = st.v[r * VPR + ch].w[e >> 1];
+            h[r] = (e & 1) ? (wd >> 16) : (wd & 0xffffu);
+          }
+          *reinterpret_cast<uint2*>(dst) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+        } else {
+          uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+#pragma unroll
+          for (int r = 0; r < KR; ++r) d[r] = st.v[r * VPR + ch].w[e];
+        }
+      }
+    }
+  }
+};
+
 // Tile coordinates of workgroup `pid` (XCD-contiguous ranges, bands of kGroupM M-tiles).
 __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_t tiles_n, int64_t& tm, int64_t& tn) {
   const int64_t total = tiles_m * tiles_n;
@@ -446,12 +549,26 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   for (int i = 0; i < kFragM * kFragN; ++i) acc[i] = f32x16_t{};
 
   // Segment 1 (A1 . (B1.E.s)^T) runs through the pipelined loop below.
+  constexpr bool kBsr = BL >= 2;  // B1 is a block-sparse-16 weight (layouts 2 / 3)
+  constexpr int kBlkK = BK / 16;  // block columns of a stage along k
+  uint8_t* pres = smem + 2 * (kTileM + kTileN) * P * sizeof(T);  // [2][16][kBlkK] presence of B blocks
   Loader<T, AL> la;
-  Loader<T, BL> lb;
+  Loader<T, (BL >= 2 ? 0 : BL)> lb;
+  BsrLoader<T, (BL == 3 ? 1 : 0)> lbs;
   la.init(g.A1, nullptr, g.lda1, m0, g.M, g.K1, false, kbase);
-  lb.init(g.B1, MASK != kMaskNone ? g.bmask : nullptr, g.ldb1, n0, g.N, g.K1, MASK == kMaskByte, kbase);
+  if constexpr (kBsr)
+    lbs.init(g.B1, g.b_map, g.b_map_rows, g.b_map_cols, n0, kbase);
+  else
+    lb.init(g.B1, MASK != kMaskNone ? g.bmask : nullptr, g.ldb1, n0, g.N, g.K1, MASK == kMaskByte, kbase);
   Stage<T, kMaskNone> sa;
   Stage<T, MASK> sb;
+  int32_t sb_idx = -1;  // block index of the staged B block (block-sparse B)
+  auto load_b = [&](int64_t k0) {
+    if constexpr (kBsr)
+      sb_idx = lbs.load(sb, k0);
+    else
+      lb.load(sb, k0);
+  };
 
   auto store_a = [&](const Stage<T, kMaskNone>& st, int buf) {
     T* a = As + buf * kTileM * P;
@@ -462,10 +579,22 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   };
   auto store_b = [&](int buf) {
     T* b = Bs + buf * kTileN * P;
-    if (BL == 0)
+    if constexpr (kBsr)
+      lbs.store(sb, sb_idx, b, pres + buf * 16 * kBlkK);
+    else if (BL == 0)
       store_kc<T, MASK>(sb, b, has_scale, bscale);
     else
       store_rc<T, MASK>(sb, b, has_scale, bscale);
+  };
+  // block-sparse B: does N-fragment j of this wave meet a kept block at k-step kk?
+  auto frag_live = [&](int buf, int j, int kk) -> bool {
+    if constexpr (!kBsr) {
+      return true;
+    } else {
+      const uint8_t* pr = pres + buf * 16 * kBlkK;
+      const int nb = (wn * kWaveN + j * 32) / 16, kb = (kk * MK) / 16;
+      return (pr[nb * kBlkK + kb] | pr[(nb + 1) * kBlkK + kb]) != 0;
+    }
   };
 
   // MFMAs of one LDS stage; hook(kk) runs after the MFMAs of k-step kk are issued.
@@ -490,11 +619,13 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
           for (int j = 0; j < kFragN; ++j) fb[cur ^ 1][j] = *reinterpret_cast<const bf16x8_t*>(b + j * 32 * P + ko);
         }
 #pragma unroll
-        for (int i = 0; i < kFragM; ++i)
+        for (int j = 0; j < kFragN; ++j) {
+          if (!frag_live(buf, j, kk)) continue;  // both 16-row blocks of the fragment pruned
 #pragma unroll
-          for (int j = 0; j < kFragN; ++j)
+          for (int i = 0; i < kFragM; ++i)
             acc[i * kFragN + j] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i * kFragN + j], 0, 0, 0);
+        }
         hook(kk * 4 / KSTEPS);
       }
     } else {
@@ -507,10 +638,12 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < kFragN; ++j) fb[j] = b[j * 32 * P + ko];
 #pragma unroll
-        for (int i = 0; i < kFragM; ++i)
+        for (int j = 0; j < kFragN; ++j) {
+          if (!frag_live(buf, j, kk)) continue;
 #pragma unroll
-          for (int j = 0; j < kFragN; ++j)
+          for (int i = 0; i < kFragM; ++i)
             acc[i * kFragN + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i * kFragN + j], 0, 0, 0);
+        }
         if (kk % (KSTEPS / 4) == 0) hook(kk * 4 / KSTEPS);
       }
     }
@@ -518,13 +651,13 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
 
   if (nk1 > 0) {
     la.load(sa, kbase);
-    lb.load(sb, kbase);
+    load_b(kbase);
     store_a(sa, 0);
     store_b(0);
   }
   if (nk1 > 1) {
     la.load(sa, kbase + BK);
-    lb.load(sb, kbase + BK);
+    load_b(kbase + BK);
   }
   __syncthreads();
 
@@ -541,7 +674,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
       if (q == 0 && do_store) store_a(sa, buf ^ 1);
       if (q == 1 && do_store) store_b(buf ^ 1);
       if (q == 2 && do_load) la.load(sa, k_next);
-      if (q == 3 && do_load) lb.load(sb, k_next);
+      if (q == 3 && do_load) load_b(k_next);
     });
     __syncthreads();
   }
@@ -550,7 +683,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
   // load -> LDS -> MFMA steps through buffer 0.
   if (nk2 > 0) {
     Loader<T, AL> la2;
-    Loader<T, BL> lb2;
+    Loader<T, (BL >= 2 ? 0 : BL)> lb2;
     la2.init(g.A2, nullptr, g.lda2, m0, g.M, g.K2);
     lb2.init(g.B2, nullptr, g.ldb2, n0, g.N, g.K2);
     for (int64_t s2 = 0; s2 < nk2; ++s2) {
@@ -601,6 +734,24 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
       const float4 p1 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c + 4);
       v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
       v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+      if (g.c_blocks) {
+        // block-sparse C (the SDDMM weight gradient): only kept 16 x 16 blocks are written,
+        // row (row % 16) of block c_map[row / 16][col / 16], 8 columns at a time
+        const int64_t bi = (row / 16 < g.c_map_rows && col / 16 < g.c_map_cols)
+                               ? g.c_map[(row / 16) * g.c_map_cols + col / 16] : -1;
+        if (bi >= 0) {
+          const int64_t o = bi * 256 + (row % 16) * 16 + (col % 16);
+          if (g.c_dtype == SF_DTYPE_BF16) {
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c_blocks) + o) =
+                make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+          } else {
+            float* cp = static_cast<float*>(g.c_blocks) + o;
+            *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4*>(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+          }
+        }
+        continue;
+      }
       if (g.splits > 1) {
         // split-K: raw f32 partial sums; sf_gemm's reduce kernel applies the epilogue
         float* pp = g.partial + (kz * g.M + row) * g.N + col;
@@ -704,7 +855,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int elem
 
 template <typename T>
 constexpr size_t smem_bytes() {
-  return sizeof(T) * 2ull * (kTileM + kTileN) * Tr<T>::PITCH;
+  return sizeof(T) * 2ull * (kTileM + kTileN) * Tr<T>::PITCH + 2 * 16 * (Tr<T>::BK / 16);
 }
 
 template <typename T, int AL, int BL, int MASK>
@@ -732,6 +883,10 @@ int launch_gemm(const GemmArgs& g, hipStream_t st) {
 
 template <typename T, int MASK>
 int dispatch_layouts(const sf_gemm_desc* d, const GemmArgs& g, hipStream_t st) {
+  if constexpr (MASK == kMaskNone) {
+    if (d->b_format == SF_BFMT_BSR16)
+      return d->b_layout == SF_LAYOUT_K ? launch_gemm<T, 0, 2, MASK>(g, st) : launch_gemm<T, 0, 3, MASK>(g, st);
+  }
   if (d->a_layout == SF_LAYOUT_K && d->b_layout == SF_LAYOUT_K) return launch_gemm<T, 0, 0, MASK>(g, st);
   if (d->a_layout == SF_LAYOUT_K) return launch_gemm<T, 0, 1, MASK>(g, st);
   return launch_gemm<T, 1, 1, MASK>(g, st);
@@ -775,7 +930,7 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
                "A M-contiguous with B K-contiguous is not built");
   SF_CHECK_ARG(d->M >= 0 && d->N >= 0 && d->K1 >= 0 && d->K2 >= 0, "negative GEMM size");
   if (d->M == 0 || d->N == 0) return SF_OK;
-  SF_CHECK_ARG(d->C, "null C");
+  SF_CHECK_ARG(d->C || d->c_blocks, "null C");
   SF_CHECK_ARG(d->K1 == 0 || (d->A1 && d->B1), "null A1/B1");
   SF_CHECK_ARG(d->K2 == 0 || (d->A2 && d->B2), "null A2/B2");
   const int vec = d->dtype == SF_DTYPE_BF16 ? 8 : 4;
@@ -787,9 +942,23 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     if (layout == SF_LAYOUT_K) return K % vec == 0 && ld >= K;
     return rows % vec == 0 && ld >= rows;
   };
+  const bool bsr_b = d->b_format == SF_BFMT_BSR16;
+  SF_CHECK_ARG(d->b_format == SF_BFMT_DENSE || bsr_b, "bad B format %d", d->b_format);
+  if (bsr_b) {
+    SF_CHECK_ARG(d->a_layout == SF_LAYOUT_K, "a block-sparse B needs a K-contiguous A");
+    SF_CHECK_ARG(d->b_map && d->b_map_rows >= 0 && d->b_map_cols >= 0, "block-sparse B needs its block map");
+    SF_CHECK_ARG(!d->bmask && d->K2 == 0, "block-sparse B takes no effective mask and no second K segment");
+    SF_CHECK_ARG(d->K1 % 16 == 0, "block-sparse B: K (%lld) must be a multiple of 16", (long long)d->K1);
+    SF_CHECK_ARG(d->K1 == 0 || (d->B1 && al16(d->B1)), "block-sparse B: blocks must be 16-byte aligned");
+  }
+  if (d->c_blocks) {
+    SF_CHECK_ARG(d->c_map && d->M % 16 == 0 && d->N % 16 == 0 && al16(d->c_blocks),
+                 "block-sparse C needs its block map, M and N multiples of 16 and 16-byte aligned blocks");
+    SF_CHECK_ARG(!d->bias && !d->emask && !d->accumulate, "block-sparse C takes no bias, mask product or accumulation");
+  }
   SF_CHECK_ARG(chk_operand(d->A1, d->lda1, d->a_layout, d->M, d->K1) &&
                    chk_operand(d->A2, d->lda2, d->a_layout, d->M, d->K2) &&
-                   chk_operand(d->B1, d->ldb1, d->b_layout, d->N, d->K1) &&
+                   (bsr_b || chk_operand(d->B1, d->ldb1, d->b_layout, d->N, d->K1)) &&
                    chk_operand(d->B2, d->ldb2, d->b_layout, d->N, d->K2) &&
                    (d->bmask_bytes ? (!d->bmask || (reinterpret_cast<uintptr_t>(d->bmask) % vec == 0))
                                : chk_operand(d->bmask, d->ldb1, d->b_layout, d->N, d->K1)),
@@ -805,7 +974,8 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   };
   const int64_t lim = int64_t(1) << 31;
   if (extent(d->A1, d->lda1, d->a_layout, d->M, d->K1) >= lim || extent(d->A2, d->lda2, d->a_layout, d->M, d->K2) >= lim ||
-      extent(d->B1, d->ldb1, d->b_layout, d->N, d->K1) >= lim || extent(d->B2, d->ldb2, d->b_layout, d->N, d->K2) >= lim) {
+      (!bsr_b && extent(d->B1, d->ldb1, d->b_layout, d->N, d->K1) >= lim) ||
+      extent(d->B2, d->ldb2, d->b_layout, d->N, d->K2) >= lim) {
     set_error("sf_gemm: operands of 2 GiB or more are not supported (M=%lld N=%lld K1=%lld)", (long long)d->M,
               (long long)d->N, (long long)d->K1);
     return SF_ERR_UNSUPPORTED;
@@ -837,6 +1007,13 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   g.decay = d->decay;
   g.accumulate = d->accumulate;
   g.c_aligned = al16(d->C);
+  g.b_map = bsr_b ? d->b_map : nullptr;
+  g.b_map_rows = d->b_map_rows;
+  g.b_map_cols = d->b_map_cols;
+  g.c_blocks = d->c_blocks;
+  g.c_map = d->c_map;
+  g.c_map_rows = d->c_map_rows;
+  g.c_map_cols = d->c_map_cols;
   g.tiles_m = ceil_div(d->M, kTileM);
   g.tiles_n = ceil_div(d->N, kTileN);
   g.splits = 1;
@@ -845,7 +1022,7 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   {
     const int sp = choose_splits(d);
     const size_t need = static_cast<size_t>(sp) * d->M * d->N * sizeof(float);
-    if (sp > 1 && d->workspace && d->workspace_bytes >= need && al16(d->workspace)) {
+    if (sp > 1 && !d->c_blocks && d->workspace && d->workspace_bytes >= need && al16(d->workspace)) {
       g.splits = sp;
       g.split_stages = ceil_div(g.split_stages, sp);
       g.partial = static_cast<float*>(d->workspace);
