@@ -165,6 +165,62 @@ def mask_step(torch, L, K, arena, step: int, flips, sample_idx):
 # ---------------------------------------------------------------------------
 # CPU baseline: the numpy oracle on a bounded token sample
 # ---------------------------------------------------------------------------
+BSR_SHAPE = (11008, 4096)  # gate/up projection of LLaMA-2-7B, 688 x 256 blocks of 16 x 16
+
+
+def bsr_leg(torch, dev, tokens: int, density: float, steps: int, warmup: int) -> dict:
+    """Block-sparse-16 linear at the gate/up shape: build the index, then fwd + dx + SDDMM dW per step."""
+    from sparseforge_amd import block_sparse as bs
+    from sparseforge_amd import profiling as prof
+
+    out_f, in_f = BSR_SHAPE
+    bm = torch.rand(out_f // 16, in_f // 16, generator=torch.Generator().manual_seed(1)) < density
+    gen = torch.Generator(device=dev).manual_seed(3)
+    W = (torch.randn(out_f, in_f, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    M = bm.to(dev).repeat_interleave(16, 0).repeat_interleave(16, 1).to(torch.bfloat16)
+    x = torch.randn(tokens, in_f, generator=gen, device=dev).to(torch.bfloat16)
+    gy = torch.randn(tokens, out_f, generator=gen, device=dev).to(torch.bfloat16)
+    bs.convert_to_block_sparse(W, M, return_block_map=True)  # warmup
+    torch.cuda.synchronize()
+    with prof.kernel_timer() as bt:
+        t0 = time.perf_counter()
+        blocks, rp, ci, bmap = bs.convert_to_block_sparse(W, M, return_block_map=True)
+        torch.cuda.synchronize()
+        build_ms = (time.perf_counter() - t0) * 1e3
+    nnz = ci.numel()
+
+    def step():
+        bs._bsr_gemm(x, blocks, bmap, out_f, False, torch.bfloat16)
+        bs._bsr_gemm(gy, blocks, bmap, in_f, True, torch.bfloat16)
+        bs.bsr_sddmm(gy, x, bmap, nnz, torch.bfloat16)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with prof.kernel_timer() as kt:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+    flops = 3 * 2.0 * tokens * nnz * 256  # kept blocks only
+    gk = kt.summary()["sf_gemm_bsr"]
+    kernel_tflops = flops * steps / (gk.total_ms * 1e-3) / 1e12
+    build_bytes = W.numel() * 4 + nnz * 256 * 2  # read W and M (bf16), write the kept blocks
+    res = {"density": density, "nnz_blocks": nnz, "total_blocks": bm.numel(), "tokens": tokens,
+           "value": round(flops * steps / el / 1e12, 3), "unit": "TFLOP/s (kept blocks, fwd + dx + SDDMM dW)",
+           "ms_per_step": round(el * 1e3 / steps, 4),
+           "roofline": {"bound": "mfma", "kernel": "sf_gemm (block-sparse modes)", "achieved": round(kernel_tflops, 3),
+                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4), "launches": gk.launches,
+                        "avg_launch_ms": round(gk.avg_ms, 4)},
+           "build": {"ms": round(build_ms, 3), "GB/s": round(build_bytes / (build_ms * 1e-3) / 1e9, 2),
+                     "kernel_ms": round(bt.summary()["sf_bsr_build"].total_ms, 3)}}
+    log(f"bsr d={density}: nnz {nnz}/{bm.numel()}, {res['value']:.1f} TFLOP/s, kernels {kernel_tflops:.1f} TFLOP/s; "
+        f"build {build_ms:.2f} ms")
+    return res
+
+
 def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
     import numpy as np
 
@@ -262,6 +318,7 @@ def main(argv=None) -> int:
     ap.add_argument("--mask-layers", type=int, default=LAYERS, help="decoder layers in the mask-update arena")
     ap.add_argument("--mask-steps", type=int, default=10)
     ap.add_argument("--adamw-steps", type=int, default=5)
+    ap.add_argument("--bsr-steps", type=int, default=5, help="steps of the block-sparse leg (0 skips it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--calib", action="store_true",
                     help="first run one plain 256 MiB device copy (a known-size reference for HBM byte counters)")
@@ -379,6 +436,10 @@ def main(argv=None) -> int:
     del arena, opt_state
     torch.cuda.empty_cache()
 
+    # ---- block-sparse-16 leg (gate/up shape, block densities 0.5 and 0.25) ----
+    bsr = [bsr_leg(torch, dev, a.tokens, d, a.bsr_steps, 2) for d in (0.5, 0.25)] if a.bsr_steps > 0 else []
+    torch.cuda.empty_cache()
+
     traffic = profiled_traffic()
     out = {
         "metric": "SparseLinear fwd+bwd TFLOP/s @7B shapes; 2:4 mask-update HBM GB/s",
@@ -423,6 +484,8 @@ def main(argv=None) -> int:
                      "traffic": traffic.get("sf_adamw_step_bytes_per_launch"), "traffic_unit": "B/launch",
                      "avg_launch_ms": round(as_.avg_ms, 4)},
     }
+    if bsr:
+        out["block_sparse"] = bsr
     if not a.no_cpu:
         log("timing CPU baseline (numpy oracle)")
         out["cpu_baseline"] = cpu_baseline()

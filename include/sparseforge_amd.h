@@ -167,6 +167,35 @@ int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtype, const vo
 int sf_hard_flip_count(const void* prev, const void* now, int dtype, int64_t rows, int64_t cols,
                        int kind, int n_keep, int m_group, int64_t* flips, void* stream);
 
+/*
+ * Joint importance score of a GLU gate/up pair: S = score(gate) + score(up),
+ * each from its own layer's metric, eps and operands
+ * (_compute_importance_scores, legacy/utils.py:480-533, summed at :415-420),
+ * the sum rounded in s_dtype (the promotion of the two score dtypes).  Both
+ * layers share the operand dtypes.  S: [rows, cols], written.
+ */
+int sf_joint_scores(const sf_mask_params* gate_p, const void* gate_W, const void* gate_H,
+                    const void* gate_aux, const sf_mask_params* up_p, const void* up_W, const void* up_H,
+                    const void* up_aux, int w_dtype, int h_dtype, int aux_dtype, void* S, int s_dtype,
+                    void* stream);
+
+/*
+ * Joint mask update of a GLU gate/up pair (legacy/utils.py:422-479 with
+ * _compute_joint_gate_target :536-613 and _apply_mid_penalty_to_gate
+ * :615-643): one pass computes G from the joint score S (z-scored with
+ * `stats` of S and rounded in the mask dtype, so p->score_dtype must equal
+ * mask_dtype), the gate layer's frozen flags and mask, the penalty against
+ * the gate mask (SF_PENALTY_MID or SF_PENALTY_STRUCTURED_TOPN), the
+ * binarisation push, then the EMA of BOTH masks with that G.  No freeze step
+ * (the reference's joint path has none).  Flip counts use p->hard_kind /
+ * hard_n for the gate and up_hard_kind / up_hard_n for the up layer; each
+ * counter is device int64[1], incremented (NULL skips it).
+ */
+int sf_glu_update_masks(const sf_mask_params* p, const void* S, int s_dtype, void* gate_mask,
+                        void* up_mask, int mask_dtype, const void* gate_frozen, int frozen_dtype,
+                        const float* stats, const float* tau, int up_hard_kind, int up_hard_n,
+                        int64_t* gate_flips, int64_t* up_flips, void* stream);
+
 /* ---- effective mask for the masked GEMMs (SparseLinear.forward, :759-771) */
 #define SF_EFF_SOFT 0 /* E = mask.to(weight dtype)                                  */
 #define SF_EFF_MIX 1  /* E = (hx * mask + (1 - hx) * hard(mask)).to(weight dtype)     */

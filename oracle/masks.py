@@ -238,6 +238,29 @@ def gate_target(z: np.ndarray, sdt: str, mask_type: str, T: float, tau=None, N: 
 # ---------------------------------------------------------------------------
 # update_mask after the step gating (sparse_modeling.py:1288-1661)
 # ---------------------------------------------------------------------------
+def binarize_push(G: np.ndarray, d: float, sdt: str) -> np.ndarray:
+    """Multiplicative push away from 0.5 (sparse_modeling.py:1576-1590; utils.py:437-446)."""
+    if d == 0.0:
+        return G
+    lt, gt = G < 0.5, G > 0.5
+    G = G.copy()
+    G[lt] = rnd(G[lt] * np.float32(1.0 - d), sdt)
+    G[gt] = rnd(G[gt] * np.float32(1.0 + d), sdt)
+    return G
+
+
+def ema(prev: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: float) -> np.ndarray:
+    """mask.mul_(1 - a).add_(G, alpha=a).clamp_(0, 1) (sparse_modeling.py:1593; utils.py:448-449).
+
+    add_ with alpha is a fused multiply-add; torch converts alpha to the op's
+    dtype, so it is a bf16 alpha when mask and G are both bf16."""
+    prev = np.asarray(prev, dtype=np.float32)
+    alpha = np.float32(mask_lr) if F32 in (mdt, sdt) else round_bf16(np.float32(mask_lr))
+    m1 = rnd(prev * np.float32(1.0 - mask_lr), mdt)
+    m2 = rnd((np.asarray(G, np.float64) * np.float64(alpha) + m1.astype(np.float64)).astype(np.float32), mdt)
+    return np.clip(m2, 0.0, 1.0).astype(np.float32)
+
+
 def update_mask(mask: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: float, penalty_mode: str = "none",
                 penalty_coef: float = 0.0, N: int = 2, M: int = 4, binarize: float = 0.0, freeze_low: float = 0.0,
                 freeze_high: float = 1.0, step: int = 0, frozen=None, hard_type: str = "nm_2_4"):
@@ -264,17 +287,8 @@ def update_mask(mask: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: fl
             pg = rnd(rnd(np.float32(1.0) - np.float32(2.0) * prev, mdt), sdt)
             G = rnd(G - rnd(c * pg, sdt), sdt)
         G = np.clip(G, 0.0, 1.0).astype(np.float32)
-    if binarize != 0.0:  # :1576-1590
-        lt, gt = G < 0.5, G > 0.5
-        G = G.copy()
-        G[lt] = rnd(G[lt] * np.float32(1.0 - binarize), sdt)
-        G[gt] = rnd(G[gt] * np.float32(1.0 + binarize), sdt)
-    # EMA (:1593): mask.mul_(1 - a).add_(G, alpha=a).clamp_(0, 1); add with alpha is a fused multiply-add
-    # torch converts add_'s alpha to the op's dtype: a bf16 alpha when mask and G are both bf16
-    alpha = np.float32(mask_lr) if F32 in (mdt, sdt) else round_bf16(np.float32(mask_lr))
-    m1 = rnd(prev * np.float32(1.0 - mask_lr), mdt)
-    m2 = rnd((G.astype(np.float64) * np.float64(alpha) + m1.astype(np.float64)).astype(np.float32), mdt)
-    new = np.clip(m2, 0.0, 1.0).astype(np.float32)
+    G = binarize_push(G, binarize, sdt)
+    new = ema(prev, G, sdt, mdt, mask_lr)
     new_frozen = None
     if freeze_low > 0.0 or freeze_high < 1.0:  # :1621-1642
         f0 = new <= np.float32(freeze_low)
@@ -386,3 +400,64 @@ def layer_update_mask(c: dict, step: int, W, H, mask, frozen, sample_idx, lambda
         frozen, effective_hard_type(c))
     hx = layer_schedule(c, step)["hx"]
     return new, new_frozen, flips, hx
+
+
+def glu_joint_update(c: dict, step: int, Wg, Hg, Mg, Wu, Hu, Mu, frozen_g, sample_idx, lambda_mid: float,
+                     w_dt=F32, h_dt=F32, m_dt=F32, aux_g=None, aux_u=None, aux_dt=F32):
+    """_update_glu_joint_mask (utils.py:363-479) for one gate/up pair sharing config c (the gate's).
+
+    Joint score S = score(gate) + score(up) in the score dtype (:415-420); z and G
+    in the mask dtype (_compute_joint_gate_target, :536-613; a mask_type other than
+    structured behaves as unstructured); the penalty compares G with the GATE mask
+    (_apply_mid_penalty_to_gate, :615-643: structured_topn when cols % M == 0,
+    else mid; any other mode only clamps); binarisation; the same G EMA'd into
+    both masks; no freeze.  Returns (gate_mask, up_mask, flips_gate, flips_up,
+    hardening_x) or None when the step is gated off.
+    """
+    if (not c["change_mask"]) or c["mask_type"] == "none":
+        return None
+    if step < int(c["sparsity_warmup_steps"]):
+        return None
+    K = max(1, _period(c, step))
+    if step % K != 0:
+        return None
+    metric = c["mask_metric"]
+    sdt = score_dtype(metric, w_dt, h_dt, aux_dt)
+    sg = scores(Wg, Hg, aux_g, metric, w_dt, h_dt, aux_dt, temperature=c["temperature"])
+    su = scores(Wu, Hu, aux_u, metric, w_dt, h_dt, aux_dt, temperature=c["temperature"])
+    S = rnd(sg + su, sdt)
+    mu, sigma = score_stats(S)
+    z = znorm(S, mu, sigma, m_dt)
+    sch = layer_schedule(c, step)
+    mtype = "structured" if c["mask_type"] == "structured" else "unstructured"
+    N, M = int(c["N"]), int(c["M"])
+    tau = None
+    if mtype == "unstructured":
+        flat = z.ravel()
+        sample = flat[np.asarray(sample_idx)] if sample_idx is not None else flat
+        tau = quantile_linear(sample, sch["sparsity"])
+    G = gate_target(z, m_dt, mtype, sch["T"], tau, N, M, bool(c["structured_exact"]), sch["beta_s"], Mg, frozen_g)
+    Mg = np.asarray(Mg, np.float32)
+    rows, cols = Mg.shape
+    lam = float(lambda_mid or 0.0)
+    if lam != 0.0:
+        pen_lr = float(c["mask_penalty_lr"]) if c["mask_penalty_lr"] is not None else float(c["mask_lr"])
+        coef = np.float32(pen_lr * lam)
+        mode = c["mask_penalty_mode"] or "mid"
+        if mode == "structured_topn" and cols % M != 0:
+            mode = "mid"
+        if mode == "structured_topn":
+            target = topk_keep(G.reshape(rows, cols // M, M), N).astype(np.float32).reshape(rows, cols)
+            G = rnd(G - rnd(coef * rnd(rnd(Mg, m_dt) - target, m_dt), m_dt), m_dt)
+        elif mode == "mid":
+            pg = rnd(rnd(np.float32(1.0) - np.float32(2.0) * Mg, m_dt), m_dt)
+            G = rnd(G - rnd(coef * pg, m_dt), m_dt)
+        G = np.clip(G, 0.0, 1.0).astype(np.float32)
+    G = binarize_push(G, float(c["mask_binarize_decay"] or 0.0), m_dt)
+    new_g = ema(Mg, G, m_dt, m_dt, float(c["mask_lr"]))
+    new_u = ema(Mu, G, m_dt, m_dt, float(c["mask_lr"]))
+    ht = effective_hard_type(c)
+    fg = int(((hard_mask_from_soft(Mg, ht, N, M) > 0.5) ^ (hard_mask_from_soft(new_g, ht, N, M) > 0.5)).sum())
+    fu = int(((hard_mask_from_soft(np.asarray(Mu, np.float32), ht, N, M) > 0.5)
+              ^ (hard_mask_from_soft(new_u, ht, N, M) > 0.5)).sum())
+    return new_g, new_u, fg, fu, sch["hx"]

@@ -173,6 +173,8 @@ SIGNATURES = {
     "sf_gate_target": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P]),
     "sf_update_mask": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _P]),
     "sf_hard_flip_count": (_I, [_P, _P, _I, _I64, _I64, _I, _I, _I, _P, _P]),
+    "sf_joint_scores": (_I, [_MP, _P, _P, _P, _MP, _P, _P, _P, _I, _I, _I, _P, _I, _P]),
+    "sf_glu_update_masks": (_I, [_MP, _P, _I, _P, _P, _I, _P, _I, _P, _P, _I, _I, _P, _P, _P]),
     "sf_effective_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _F, _I, _I, _I, _P]),
     "sf_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
     "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),

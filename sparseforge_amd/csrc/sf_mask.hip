@@ -597,6 +597,64 @@ struct UpdateSpec {
   int hard_kind, hard_n;
 };
 
+// Penalty pull toward a target, then clamp (:1291-1573), and the
+// multiplicative binarisation push (:1576-1590).  mp: the mask the penalty
+// compares against; sd: dtype of G.
+template <int MD>
+__device__ __forceinline__ void pull_and_push(const UpdateSpec& us, int sd, const Group& g, const float mp[4],
+                                              float G[4]) {
+  if (us.penalty != SF_PENALTY_NONE) {
+    if (us.penalty == SF_PENALTY_MID) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float pg = rnd(rnd(1.0f - 2.0f * mp[j], MD), sd);
+        G[j] = rnd(G[j] - rnd(us.pen_coef * pg, sd), sd);
+      }
+    } else {  // nm_2_4 / structured_topn: target = topN(G) on full groups, 1 on the tail
+      uint32_t keep = g.full ? topk4_keep(G, us.pen_n) : 0xfu;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float t = ((keep >> j) & 1u) ? 1.0f : 0.0f;
+        float delta = rnd(rnd(mp[j], sd) - t, sd);
+        G[j] = rnd(G[j] - rnd(us.pen_coef * delta, sd), sd);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) G[j] = fminf(fmaxf(G[j], 0.0f), 1.0f);
+  }
+  if (us.binarize) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (G[j] < 0.5f)
+        G[j] = rnd(G[j] * us.bin_lo, sd);
+      else if (G[j] > 0.5f)
+        G[j] = rnd(G[j] * us.bin_hi, sd);
+    }
+  }
+}
+
+// EMA: mask.mul_(1 - a).add_(G, alpha=a).clamp_(0, 1)  (:1593)
+template <int MD>
+__device__ __forceinline__ void ema_of(const UpdateSpec& us, const float mp[4], const float G[4], float mn[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float m1 = rnd(mp[j] * us.keep_a, MD);
+    float m2 = rnd(fmaf(G[j], us.a, m1), MD);
+    mn[j] = fminf(fmaxf(m2, 0.0f), 1.0f);
+  }
+}
+
+// Positions of a group where the hard views of a and b differ (:1659-1661).
+__device__ __forceinline__ int flips_of(const float a[4], const float b[4], const Group& g, int kind, int n) {
+  float ha[4], hb[4];
+  hard_of_group(a, g, kind, n, ha);
+  hard_of_group(b, g, kind, n, hb);
+  int c = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c += (j < g.n && ((ha[j] > 0.5f) != (hb[j] > 0.5f))) ? 1 : 0;
+  return c;
+}
+
 template <int WD, int HD, int MD>
 __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, const void* __restrict__ W,
                                                              const void* __restrict__ H, const void* __restrict__ aux,
@@ -618,45 +676,9 @@ __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, cons
     load4<MD>(mask, g.elem, g.n, v, mp);
     if (gs.has_frozen) load4_any(frozen, gs.frozen_dtype, g.elem, g.n, v, fz);
     gate_of_group(gs, sc, g, mu, sigma, tau, mp, fz, G);
-
-    // penalty pull toward a target, then clamp (:1291-1573)
-    if (us.penalty != SF_PENALTY_NONE) {
-      if (us.penalty == SF_PENALTY_MID) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float pg = rnd(rnd(1.0f - 2.0f * mp[j], MD), sd);
-          G[j] = rnd(G[j] - rnd(us.pen_coef * pg, sd), sd);
-        }
-      } else {  // nm_2_4 / structured_topn: target = topN(G) on full groups, 1 on the tail
-        uint32_t keep = g.full ? topk4_keep(G, us.pen_n) : 0xfu;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float t = ((keep >> j) & 1u) ? 1.0f : 0.0f;
-          float delta = rnd(rnd(mp[j], sd) - t, sd);
-          G[j] = rnd(G[j] - rnd(us.pen_coef * delta, sd), sd);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) G[j] = fminf(fmaxf(G[j], 0.0f), 1.0f);
-    }
-    // multiplicative binarisation push (:1576-1590)
-    if (us.binarize) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (G[j] < 0.5f)
-          G[j] = rnd(G[j] * us.bin_lo, sd);
-        else if (G[j] > 0.5f)
-          G[j] = rnd(G[j] * us.bin_hi, sd);
-      }
-    }
-    // EMA: mask.mul_(1 - a).add_(G, alpha=a).clamp_(0, 1)  (:1593)
+    pull_and_push<MD>(us, sd, g, mp, G);
     float mn[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float m1 = rnd(mp[j] * us.keep_a, MD);
-      float m2 = rnd(fmaf(G[j], us.a, m1), MD);
-      mn[j] = fminf(fmaxf(m2, 0.0f), 1.0f);
-    }
+    ema_of<MD>(us, mp, G, mn);
     // freeze snaps and flags (:1621-1642)
     if (us.apply_freeze) {
       float fl[4];
@@ -680,16 +702,74 @@ __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, cons
       }
     }
     store4<MD>(mask, g.elem, g.n, v, mn);
-    // flips of the hard view (:1659-1661)
-    if (flips) {
-      float ha[4], hb[4];
-      hard_of_group(mp, g, us.hard_kind, us.hard_n, ha);
-      hard_of_group(mn, g, us.hard_kind, us.hard_n, hb);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) cnt += (j < g.n && ((ha[j] > 0.5f) != (hb[j] > 0.5f))) ? 1 : 0;
-    }
+    if (flips) cnt += flips_of(mp, mn, g, us.hard_kind, us.hard_n);
   }
   if (flips) block_add_i64(cnt, flips);
+}
+
+// ---------------------------------------------------------------------------
+// GLU gate/up joint update (legacy/utils.py:363-643).  The joint score
+// S = score(gate) + score(up) is written once (its statistics, tau sample and
+// the update all read it), then one pass computes G from S with the gate
+// layer's mask and frozen flags and applies the same G to both masks.
+// ---------------------------------------------------------------------------
+template <int WD, int HD>
+__global__ void __launch_bounds__(kBlock) joint_scores_kernel(ScoreSpec sg, const void* __restrict__ Wg,
+                                                              const void* __restrict__ Hg, const void* __restrict__ ag,
+                                                              ScoreSpec su, const void* __restrict__ Wu,
+                                                              const void* __restrict__ Hu, const void* __restrict__ au,
+                                                              void* __restrict__ S, int s_dtype, int64_t cols,
+                                                              int64_t groups, int64_t gpr, bool vec) {
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    const bool v = vec && g.full;
+    float a[4], b[4], o[4];
+    group_scores<WD, HD>(sg, Wg, Hg, ag, g, v, cols, a);
+    group_scores<WD, HD>(su, Wu, Hu, au, g, v, cols, b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = rnd(a[j] + b[j], s_dtype);
+    if (s_dtype == SF_DTYPE_F32)
+      store4<SF_DTYPE_F32>(S, g.elem, g.n, v, o);
+    else
+      store4<SF_DTYPE_BF16>(S, g.elem, g.n, v, o);
+  }
+}
+
+template <int SD, int MD>
+__global__ void __launch_bounds__(kBlock) glu_update_kernel(UpdateSpec us, const void* __restrict__ S,
+                                                            void* __restrict__ mask_g, void* __restrict__ mask_u,
+                                                            const void* __restrict__ frozen_g,
+                                                            const float* __restrict__ stats,
+                                                            const float* __restrict__ tau_p, int up_kind, int up_n,
+                                                            int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                            int64_t* flips_g, int64_t* flips_u) {
+  const GateSpec& gs = us.gs;
+  const int sd = gs.s.score_dtype;  // the mask dtype: z and G live in it (:541-545)
+  const float mu = stats[0], sigma = stats[1];
+  const float tau = tau_p ? *tau_p : 0.0f;
+  int64_t cg = 0, cu = 0;
+  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    Group g = group_at(gi, cols, gpr);
+    const bool v = vec && g.full;
+    float sc[4], pg[4], pu[4], fz[4] = {0, 0, 0, 0}, G[4], ng[4], nu[4];
+    load4<SD>(S, g.elem, g.n, v, sc);
+    load4<MD>(mask_g, g.elem, g.n, v, pg);
+    load4<MD>(mask_u, g.elem, g.n, v, pu);
+    if (gs.has_frozen) load4_any(frozen_g, gs.frozen_dtype, g.elem, g.n, v, fz);
+    gate_of_group(gs, sc, g, mu, sigma, tau, pg, fz, G);
+    pull_and_push<MD>(us, sd, g, pg, G);  // the penalty compares against the gate mask (:615-641)
+    ema_of<MD>(us, pg, G, ng);
+    ema_of<MD>(us, pu, G, nu);
+    store4<MD>(mask_g, g.elem, g.n, v, ng);
+    store4<MD>(mask_u, g.elem, g.n, v, nu);
+    if (flips_g) cg += flips_of(pg, ng, g, us.hard_kind, us.hard_n);
+    if (flips_u) cu += flips_of(pu, nu, g, up_kind, up_n);
+  }
+  if (flips_g) block_add_i64(cg, flips_g);
+  __syncthreads();  // both sums share the workgroup's reduction array
+  if (flips_u) block_add_i64(cu, flips_u);
 }
 
 // ---------------------------------------------------------------------------
@@ -905,6 +985,44 @@ int make_gate_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_dt
   gs->one_minus_beta = static_cast<float>(1.0 - static_cast<double>(p->beta_struct));
   return SF_OK;
 }
+// Scalars of the fused update (penalty, binarisation, EMA, freeze, flip view) from the host params.
+int make_update_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_dtype, int mask_dtype,
+                     int frozen_dtype, bool want_flips, UpdateSpec* us) {
+  if (int rc = make_gate_spec(p, w_dtype, h_dtype, aux_dtype, mask_dtype, frozen_dtype, &us->gs)) return rc;
+  us->penalty = p->penalty_coef != 0.0f ? p->penalty : SF_PENALTY_NONE;
+  us->pen_n = p->n_keep;
+  if (us->penalty == SF_PENALTY_NM_2_4) us->pen_n = 2;
+  if (us->penalty == SF_PENALTY_NM_2_4 || us->penalty == SF_PENALTY_STRUCTURED_TOPN) {
+    if (us->penalty == SF_PENALTY_STRUCTURED_TOPN && (p->m_group != 4 || p->n_keep < 1 || p->n_keep > 3)) {
+      set_error("structured_topn penalty with N=%d M=%d: only M=4 is built on device", p->n_keep, p->m_group);
+      return SF_ERR_UNSUPPORTED;
+    }
+    SF_CHECK_ARG(us->penalty != SF_PENALTY_STRUCTURED_TOPN || p->cols % 4 == 0,
+                 "structured_topn penalty needs cols % M == 0 (the caller falls back to mid)");
+  }
+  us->pen_coef = p->penalty_coef;
+  us->binarize = p->binarize != 0.0f;
+  us->bin_lo = static_cast<float>(1.0 - static_cast<double>(p->binarize));
+  us->bin_hi = static_cast<float>(1.0 + static_cast<double>(p->binarize));
+  us->keep_a = static_cast<float>(1.0 - static_cast<double>(p->mask_lr));
+  // torch converts add_'s alpha to the op's dtype: bf16 when mask and G are both bf16
+  us->a = (mask_dtype == SF_DTYPE_BF16 && p->score_dtype == SF_DTYPE_BF16) ? round_bf16(p->mask_lr) : p->mask_lr;
+  us->apply_freeze = p->apply_freeze;
+  us->snap_high = p->snap_high;
+  us->freeze_low = p->freeze_low;
+  us->freeze_high = p->freeze_high;
+  us->hard_kind = p->hard_kind;
+  us->hard_n = p->hard_n;
+  if (p->hard_kind >= SF_HARD_NM_TAIL_KEEP && want_flips) {
+    if (p->hard_m != 4 || p->hard_n < 1 || p->hard_n > 3) {
+      set_error("flip count with N=%d M=%d: only M=4 is built on device", p->hard_n, p->hard_m);
+      return SF_ERR_UNSUPPORTED;
+    }
+    SF_CHECK_ARG(p->hard_kind != SF_HARD_NM_STRICT || p->cols % 4 == 0,
+                 "in_features (%lld) must be divisible by M (%d).", (long long)p->cols, p->hard_m);
+  }
+  return SF_OK;
+}
 }  // namespace
 }  // namespace sf
 
@@ -947,39 +1065,8 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
   SF_CHECK_ARG(p->hard_kind >= SF_HARD_NONE && p->hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", p->hard_kind);
   if (!H) h_dtype = SF_DTYPE_F32;
   UpdateSpec us;
-  if (int rc = make_gate_spec(p, w_dtype, h_dtype, aux_dtype, mask_dtype, frozen_dtype, &us.gs)) return rc;
-  us.penalty = p->penalty_coef != 0.0f ? p->penalty : SF_PENALTY_NONE;
-  us.pen_n = p->n_keep;
-  if (us.penalty == SF_PENALTY_NM_2_4) us.pen_n = 2;
-  if (us.penalty == SF_PENALTY_NM_2_4 || us.penalty == SF_PENALTY_STRUCTURED_TOPN) {
-    if (us.penalty == SF_PENALTY_STRUCTURED_TOPN && (p->m_group != 4 || p->n_keep < 1 || p->n_keep > 3)) {
-      set_error("structured_topn penalty with N=%d M=%d: only M=4 is built on device", p->n_keep, p->m_group);
-      return SF_ERR_UNSUPPORTED;
-    }
-    SF_CHECK_ARG(us.penalty != SF_PENALTY_STRUCTURED_TOPN || p->cols % 4 == 0,
-                 "structured_topn penalty needs cols % M == 0 (the caller falls back to mid)");
-  }
-  us.pen_coef = p->penalty_coef;
-  us.binarize = p->binarize != 0.0f;
-  us.bin_lo = static_cast<float>(1.0 - static_cast<double>(p->binarize));
-  us.bin_hi = static_cast<float>(1.0 + static_cast<double>(p->binarize));
-  us.keep_a = static_cast<float>(1.0 - static_cast<double>(p->mask_lr));
-  // torch converts add_'s alpha to the op's dtype: bf16 when mask and G are both bf16
-  us.a = (mask_dtype == SF_DTYPE_BF16 && p->score_dtype == SF_DTYPE_BF16) ? round_bf16(p->mask_lr) : p->mask_lr;
-  us.apply_freeze = p->apply_freeze;
-  us.snap_high = p->snap_high;
-  us.freeze_low = p->freeze_low;
-  us.freeze_high = p->freeze_high;
-  us.hard_kind = p->hard_kind;
-  us.hard_n = p->hard_n;
-  if (p->hard_kind >= SF_HARD_NM_TAIL_KEEP && flips) {
-    if (p->hard_m != 4 || p->hard_n < 1 || p->hard_n > 3) {
-      set_error("flip count with N=%d M=%d: only M=4 is built on device", p->hard_n, p->hard_m);
-      return SF_ERR_UNSUPPORTED;
-    }
-    SF_CHECK_ARG(p->hard_kind != SF_HARD_NM_STRICT || p->cols % 4 == 0,
-                 "in_features (%lld) must be divisible by M (%d).", (long long)p->cols, p->hard_m);
-  }
+  if (int rc = make_update_spec(p, w_dtype, h_dtype, aux_dtype, mask_dtype, frozen_dtype, flips != nullptr, &us))
+    return rc;
   if (p->rows == 0 || p->cols == 0) return SF_OK;
   const int64_t gpr = ceil_div(p->cols, 4), groups = p->rows * gpr;
   const bool vec = vec_ok(p->cols, {{W, w_dtype}, {H, h_dtype}, {mask, mask_dtype},
@@ -997,6 +1084,82 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
     SF_LAUNCH_UPD(SF_DTYPE_BF16);
 #undef SF_LAUNCH_UPD
   return launch_status("sf_update_mask");
+}
+
+extern "C" int sf_joint_scores(const sf_mask_params* gate_p, const void* gate_W, const void* gate_H,
+                               const void* gate_aux, const sf_mask_params* up_p, const void* up_W, const void* up_H,
+                               const void* up_aux, int w_dtype, int h_dtype, int aux_dtype, void* S, int s_dtype,
+                               void* stream) {
+  if (int rc = check_common(gate_p)) return rc;
+  if (int rc = check_common(up_p)) return rc;
+  if (int rc = check_metric_operands(gate_p, gate_H, gate_aux)) return rc;
+  if (int rc = check_metric_operands(up_p, up_H, up_aux)) return rc;
+  SF_CHECK_ARG(gate_p->rows == up_p->rows && gate_p->cols == up_p->cols, "gate and up shapes differ");
+  SF_CHECK_ARG(dtype_ok(w_dtype) && dtype_ok(s_dtype), "bad dtype");
+  SF_CHECK_ARG((!gate_H && !up_H) || dtype_ok(h_dtype), "bad hessian dtype");
+  SF_CHECK_ARG((!gate_aux && !up_aux) || dtype_ok(aux_dtype), "bad aux dtype");
+  if (gate_p->rows == 0 || gate_p->cols == 0) return SF_OK;
+  SF_CHECK_ARG(gate_W && up_W && S, "null tensor");
+  if (!gate_H && !up_H) h_dtype = SF_DTYPE_F32;
+  const ScoreSpec sg = make_spec(gate_p, w_dtype, h_dtype, aux_dtype);
+  const ScoreSpec su = make_spec(up_p, w_dtype, h_dtype, aux_dtype);
+  const int64_t cols = gate_p->cols, gpr = ceil_div(cols, 4), groups = gate_p->rows * gpr;
+  const bool vec = vec_ok(cols, {{gate_W, w_dtype}, {up_W, w_dtype}, {gate_H, h_dtype}, {up_H, h_dtype},
+                                 {gate_aux, aux_dtype}, {up_aux, aux_dtype}, {S, s_dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  SF_DISPATCH_WH(w_dtype, h_dtype,
+                 joint_scores_kernel<WD_, HD_><<<grid, kBlock, 0, st>>>(sg, gate_W, gate_H, gate_aux, su, up_W, up_H,
+                                                                       up_aux, S, s_dtype, cols, groups, gpr, vec));
+  return launch_status("sf_joint_scores");
+}
+
+extern "C" int sf_glu_update_masks(const sf_mask_params* p, const void* S, int s_dtype, void* gate_mask,
+                                   void* up_mask, int mask_dtype, const void* gate_frozen, int frozen_dtype,
+                                   const float* stats, const float* tau, int up_hard_kind, int up_hard_n,
+                                   int64_t* gate_flips, int64_t* up_flips, void* stream) {
+  if (int rc = check_common(p)) return rc;
+  SF_CHECK_ARG(S && stats && gate_mask && up_mask, "null tensor");
+  SF_CHECK_ARG(dtype_ok(s_dtype) && dtype_ok(mask_dtype), "bad dtype");
+  SF_CHECK_ARG(p->score_dtype == mask_dtype, "the joint target lives in the mask dtype (score_dtype must equal it)");
+  SF_CHECK_ARG(p->gate != SF_GATE_UNSTRUCTURED || tau != nullptr, "unstructured gate needs tau");
+  SF_CHECK_ARG(!p->has_frozen || (gate_frozen && dtype_ok(frozen_dtype)), "has_frozen without frozen flags");
+  SF_CHECK_ARG(p->penalty >= SF_PENALTY_NONE && p->penalty <= SF_PENALTY_STRUCTURED_TOPN && p->penalty != SF_PENALTY_NM_2_4,
+               "the joint update pulls with the mid or structured_topn penalty only (got %d)", p->penalty);
+  SF_CHECK_ARG(p->hard_kind >= SF_HARD_NONE && p->hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", p->hard_kind);
+  SF_CHECK_ARG(up_hard_kind >= SF_HARD_NONE && up_hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", up_hard_kind);
+  if (up_hard_kind >= SF_HARD_NM_TAIL_KEEP && up_flips) {
+    if (up_hard_n < 1 || up_hard_n > 3) {
+      set_error("flip count with N=%d: only M=4, 1<=N<=3 is built on device", up_hard_n);
+      return SF_ERR_UNSUPPORTED;
+    }
+    SF_CHECK_ARG(up_hard_kind != SF_HARD_NM_STRICT || p->cols % 4 == 0, "in_features (%lld) must be divisible by M.",
+                 (long long)p->cols);
+  }
+  UpdateSpec us;
+  if (int rc = make_update_spec(p, s_dtype, s_dtype, SF_DTYPE_F32, mask_dtype, frozen_dtype, gate_flips != nullptr, &us))
+    return rc;
+  us.apply_freeze = 0;  // the joint update has no freeze step (:446-479)
+  if (p->rows == 0 || p->cols == 0) return SF_OK;
+  const int64_t gpr = ceil_div(p->cols, 4), groups = p->rows * gpr;
+  const bool vec = vec_ok(p->cols, {{S, s_dtype}, {gate_mask, mask_dtype}, {up_mask, mask_dtype},
+                                    {p->has_frozen ? gate_frozen : nullptr, frozen_dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+#define SF_LAUNCH_GLU(SDT, MDT)                                                                                  \
+  glu_update_kernel<SDT, MDT><<<grid, kBlock, 0, st>>>(us, S, gate_mask, up_mask, gate_frozen, stats, tau,       \
+                                                       up_hard_kind, up_hard_n, p->cols, groups, gpr, vec,       \
+                                                       gate_flips, up_flips)
+  if (s_dtype == SF_DTYPE_F32 && mask_dtype == SF_DTYPE_F32)
+    SF_LAUNCH_GLU(SF_DTYPE_F32, SF_DTYPE_F32);
+  else if (s_dtype == SF_DTYPE_F32)
+    SF_LAUNCH_GLU(SF_DTYPE_F32, SF_DTYPE_BF16);
+  else if (mask_dtype == SF_DTYPE_F32)
+    SF_LAUNCH_GLU(SF_DTYPE_BF16, SF_DTYPE_F32);
+  else
+    SF_LAUNCH_GLU(SF_DTYPE_BF16, SF_DTYPE_BF16);
+#undef SF_LAUNCH_GLU
+  return launch_status("sf_glu_update_masks");
 }
 
 // ---------------------------------------------------------------------------

@@ -166,3 +166,51 @@ def update_mask(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: to
                                    L.ptr(tau), L.ptr(flips), L.stream(dev)),
             "sf_update_mask",
         )
+
+
+# ---------------------------------------------------------------------------
+# GLU gate/up joint update (legacy/utils.py:363-643)
+# ---------------------------------------------------------------------------
+def joint_scores(pg: L.MaskParams, gate: MaskOperands, pu: L.MaskParams, up: MaskOperands,
+                 s_dtype: torch.dtype) -> torch.Tensor:
+    """S = score(gate) + score(up), rounded in s_dtype."""
+    dev = L.require_device(gate.weight, up.weight)
+    gate.device()
+    up.device()
+    if gate.weight.shape != up.weight.shape:
+        raise ValueError(f"gate {tuple(gate.weight.shape)} and up {tuple(up.weight.shape)} shapes differ")
+    for a, b, what in ((gate.weight, up.weight, "weight"), (gate.hessian, up.hessian, "hessian_diag"),
+                       (gate.aux, up.aux, "aux")):
+        if a is not None and b is not None and a.dtype != b.dtype:
+            raise NotImplementedError(f"joint scores with gate/up {what} dtypes {a.dtype} / {b.dtype}")
+    hd = gate.hessian if gate.hessian is not None else up.hessian
+    ad = gate.aux if gate.aux is not None else up.aux
+    S = torch.empty_like(gate.weight, dtype=s_dtype)
+    with _prof.region("sf_joint_scores", gate.score_bytes() + up.score_bytes() + S.numel() * S.element_size(), "B",
+                      dev):
+        L.check(L.lib().sf_joint_scores(ctypes.byref(pg), L.ptr(gate.weight), L.ptr(gate.hessian), L.ptr(gate.aux),
+                                        ctypes.byref(pu), L.ptr(up.weight), L.ptr(up.hessian), L.ptr(up.aux),
+                                        L.dtype_code(gate.weight), gate.dt(hd), gate.dt(ad), L.ptr(S),
+                                        L.dtype_code(S), L.stream(dev)),
+                "sf_joint_scores")
+    return S
+
+
+def glu_update_masks(p: L.MaskParams, S: torch.Tensor, gate_mask: torch.Tensor, up_mask: torch.Tensor,
+                     gate_frozen: torch.Tensor | None, stats: torch.Tensor, tau: torch.Tensor | None,
+                     up_hard_kind: int, up_hard_n: int, gate_flips: torch.Tensor | None,
+                     up_flips: torch.Tensor | None) -> None:
+    dev = L.require_device(S, gate_mask, up_mask, gate_frozen, stats, tau, gate_flips, up_flips)
+    for name, t in (("up mask", up_mask), ("gate mask", gate_mask), ("frozen_mask_flags", gate_frozen)):
+        if t is not None and t.shape != S.shape:
+            raise ValueError(f"{name} shape {tuple(t.shape)} != score shape {tuple(S.shape)}")
+    if gate_mask.dtype != up_mask.dtype:
+        raise NotImplementedError(f"joint update with gate/up mask dtypes {gate_mask.dtype} / {up_mask.dtype}")
+    nbytes = S.numel() * (S.element_size() + 4 * gate_mask.element_size())
+    with _prof.region("sf_glu_update_masks", nbytes, "B", dev):
+        L.check(L.lib().sf_glu_update_masks(ctypes.byref(p), L.ptr(S), L.dtype_code(S), L.ptr(gate_mask),
+                                            L.ptr(up_mask), L.dtype_code(gate_mask), L.ptr(gate_frozen),
+                                            L.dtype_code(gate_frozen) if gate_frozen is not None else L.DT_F32,
+                                            L.ptr(stats), L.ptr(tau), up_hard_kind, up_hard_n, L.ptr(gate_flips),
+                                            L.ptr(up_flips), L.stream(dev)),
+                "sf_glu_update_masks")

@@ -147,3 +147,34 @@ def test_update_mask_matches_reference_golden(case):
         assert flips == int(r[f"flips{j}"])
         assert hx == float(r[f"hx{j}"])
         mask = r[f"mask{j}"].copy()  # continue from the reference state
+
+
+def test_glu_joint_matches_reference_golden():
+    """_update_glu_joint_mask (legacy/utils.py:363-479) on a gate/up pair, three consecutive steps."""
+    r = load_golden("glu_joint_f32")
+    c = om.full_config(**ast.literal_eval(str(r["cfg"])))
+    Mg, Mu = r["init_Mg"], r["init_Mu"]
+    for j, step in enumerate((1, 2, 3)):
+        out = om.glu_joint_update(c, step, r["Wg"], r["Hg"], Mg, r["Wu"], r["Hu"], Mu, None, r[f"idx{j}"], 0.05)
+        ng, nu, fg, fu, hx = out
+        np.testing.assert_allclose(ng, r[f"Mg{j}"], rtol=0, atol=1e-6)
+        np.testing.assert_allclose(nu, r[f"Mu{j}"], rtol=0, atol=1e-6)
+        assert (fg, fu) == (int(r[f"flips_g{j}"]), int(r[f"flips_u{j}"]))
+        assert hx == float(r[f"hx{j}"])
+        Mg, Mu = r[f"Mg{j}"], r[f"Mu{j}"]
+
+
+def test_glu_joint_same_target_for_both_masks():
+    """Both masks move toward one G: with equal starting masks they stay equal, and the update of
+    either mask equals a single-layer EMA toward that G."""
+    rng = np.random.default_rng(4)
+    W1, W2 = rng.standard_normal((8, 16), dtype=np.float32), rng.standard_normal((8, 16), dtype=np.float32)
+    H1, H2 = rng.random((8, 16), dtype=np.float32), rng.random((8, 16), dtype=np.float32)
+    M = rng.random((8, 16), dtype=np.float32)
+    c = om.full_config(mask_type="structured", mask_metric="hessian_obd", sparsity_warmup_steps=0,
+                       mask_update_period=1, mask_lr=0.2)
+    ng, nu, _, _, _ = om.glu_joint_update(c, 5, W1, H1, M, W2, H2, M.copy(), None, None, 0.0)
+    assert np.array_equal(ng, nu)
+    G = (ng - np.float32(0.8) * M) / np.float32(0.2)  # EMA inverted: G is a structured sigmoid target
+    gg = G.reshape(8, 4, 4)
+    assert (np.abs(np.sort(gg, axis=-1)[..., 2] - 0.5) < 1e-5).all()  # the 2nd largest of each group sits at 0.5
