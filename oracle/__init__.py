@@ -25,6 +25,10 @@ sign or index, or a transposed operand):
                 first outputs for seed 1234567.
   linear.py     masked linear fwd/bwd against torch.matmul closed forms and
                 torch.autograd on the dense equivalent.
-  bsr.py        CSR build against a brute-force dense scan; BSR matmul
-                against the dense masked product.
+  bsr.py        CSR build against the reference's own output
+                (tests/golden/ref_bsr_basic_f32.npz) and a brute-force dense
+                scan; BSR products against the dense masked product.
+  masks.glu_joint_update  against the reference's own output for three
+                consecutive steps (tests/golden/ref_glu_joint_f32.npz) and
+                the shared-target invariants.
 """
