@@ -31,6 +31,8 @@
 // 8 M-tiles, which keeps the A and B k-slices of the concurrently resident
 // tiles of one XCD in that XCD's L2.
 
+#include <type_traits>
+
 #include "sf_common.hpp"
 
 namespace sf {
@@ -351,7 +353,33 @@ struct Loader {
       }
     }
   }
+  // Vector i of load(st, k0) alone (the same stage's vectors may be issued apart).
+  template <int MK>
+  __device__ __forceinline__ void load_one(Stage<T, MK>& st, int64_t k0, int i) {
+    if constexpr (L == 0) {
+      const bool k_ok = k0 + kchunk < k_end;
+      const uint32_t kb = (uint32_t)(k0 * (int64_t)sizeof(T));
+      const uint32_t o = k_ok ? off[i] : kOob;
+      st.v[i] = bload(rs, o, kb);
+      if constexpr (MK != kMaskNone) load_mask<MK>(st.e[i], o, kb);
+    } else {
+      st.v[i] = bload(rs, off[i], 0);
+      if constexpr (MK != kMaskNone) load_mask<MK>(st.e[i], off[i], 0);
+      off[i] = off[i] >= kOob ? kOob : off[i] + k_step;
+    }
+  }
 };
+
+// Vector i of store_kc (K-contiguous register path into a padded tile).
+template <typename T, int MK>
+__device__ __forceinline__ void store_kc_one(const Stage<T, MK>& st, T* lds, int i, bool has_scale, float s) {
+  constexpr int VEC = Tr<T>::VEC, BK = Tr<T>::BK, CPR = BK / VEC, P = Tr<T>::PITCH;
+  const int v = threadIdx.x + kThreads * i;
+  V4 x = st.v[i];
+  if constexpr (MK != kMaskNone) x = apply_mask<T, MK>(x, st.e[i], has_scale, s);
+  T* dst = lds + (v / CPR) * P + (v % CPR) * VEC;
+  *reinterpret_cast<uint4*>(dst) = make_uint4(x.w[0], x.w[1], x.w[2], x.w[3]);
+}
 
 template <typename T, int MK>
 __device__ __forceinline__ void store_kc(const Stage<T, MK>& st, T* lds, bool has_scale, float s) {
@@ -405,6 +433,23 @@ __device__ __forceinline__ void store_rc(const Stage<T, MK>& st, T* lds, bool ha
       }
     }
   }
+}
+
+// Output vector m of transpose_block<uint16_t> alone (k-values of column m
+// of the thread's 8 x 8 block), so the transpose can be spread over MFMAs.
+__device__ __forceinline__ V4 transpose_one(const V4 (&v)[8], int m) {
+  V4 o;
+  const uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o.w[j] = __builtin_amdgcn_perm(v[2 * j + 1].w[m >> 1], v[2 * j].w[m >> 1], sel);
+  return o;
+}
+// LDS write of transposed vector m of the thread's block (the store_rc layout).
+__device__ __forceinline__ void write_rc_one(const V4& x, uint16_t* lds, int m) {
+  constexpr int VEC = 8, KB = 64 / VEC, P = Tr<uint16_t>::PITCH;
+  const int b = threadIdx.x, kb = b % KB, rb = b / KB;
+  uint16_t* dst = lds + (rb * VEC + m) * P + kb * VEC;
+  *reinterpret_cast<uint4*>(dst) = make_uint4(x.w[0], x.w[1], x.w[2], x.w[3]);
 }
 
 // B operand gathered from a block-sparse-16 weight W: 16 x 16 blocks stored
@@ -516,6 +561,128 @@ __device__ __forceinline__ void tile_coords(int64_t pid, int64_t tiles_m, int64_
 }
 
 __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) { return load_as_f32(p, i, dtype); }
+
+// Epilogue shared by the GEMM kernels: the 4 x 4 accumulator blocks of each
+// wave (its 128 x 128 share of the 256 x 256 tile) go to C, a split-K partial
+// buffer or the kept blocks of a block-sparse C.
+template <typename T>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16_t (&acc)[kFragM * kFragN],
+                                              unsigned char* smem, int64_t m0, int64_t n0, int64_t kz) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  // Epilogue.  32x32 accumulator layout: lane holds column (lane % 32) and
+  // rows (e / 4) * 8 + (lane / 32) * 4 + e % 4, e = 0..15.  The accumulators
+  // go through LDS in two halves of 64 rows per wave (the operand buffers are
+  // free now); each lane then owns 8 consecutive columns of a row, so C is
+  // read and written with 16-byte accesses and the optional epilogue operands
+  // (bias, mask product, decay term, accumulation) are read coalesced.
+  float* ep = reinterpret_cast<float*>(smem) + wave * (64 * kEpiPitch);
+  const int64_t wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
+  const bool cbf = g.c_dtype == SF_DTYPE_BF16;
+  const bool plain = !g.emask && !g.accumulate;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = ii * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          ep[r * kEpiPitch + j * 32 + (lane & 31)] = acc[(2 * h + ii) * kFragN + j][e];
+        }
+    __syncthreads();
+    for (int it = 0; it < 16; ++it) {
+      const int flat = it * 64 + lane;
+      const int r = flat >> 4, c = (flat & 15) * 8;
+      const int64_t row = wrow0 + h * 64 + r, col = wcol0 + c;
+      if (row >= g.M || col >= g.N) continue;
+      float v[8];
+      const float4 p0 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c);
+      const float4 p1 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c + 4);
+      v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+      v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+      if (g.c_blocks) {
+        // block-sparse C (the SDDMM weight gradient): only kept 16 x 16 blocks are written,
+        // row (row % 16) of block c_map[row / 16][col / 16], 8 columns at a time
+        const int64_t bi = (row / 16 < g.c_map_rows && col / 16 < g.c_map_cols)
+                               ? g.c_map[(row / 16) * g.c_map_cols + col / 16] : -1;
+        if (bi >= 0) {
+          const int64_t o = bi * 256 + (row % 16) * 16 + (col % 16);
+          if (g.c_dtype == SF_DTYPE_BF16) {
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c_blocks) + o) =
+                make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+          } else {
+            float* cp = static_cast<float*>(g.c_blocks) + o;
+            *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4*>(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+          }
+        }
+        continue;
+      }
+      if (g.splits > 1) {
+        // split-K: raw f32 partial sums; sf_gemm's reduce kernel applies the epilogue
+        float* pp = g.partial + (kz * g.M + row) * g.N + col;
+        if (col + 8 <= g.N && (g.N & 3) == 0) {
+          *reinterpret_cast<float4*>(pp) = make_float4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<float4*>(pp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        } else {
+          for (int q = 0; q < 8 && col + q < g.N; ++q) pp[q] = v[q];
+        }
+        continue;
+      }
+      const int64_t off = row * g.ldc + col;
+      const bool vec = g.c_aligned && col + 8 <= g.N && (off & 7) == 0;
+      if (plain && vec) {
+        // result of the matmul in the output dtype, then + bias (rounded again)
+        if (g.bias) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float b = load_elem(g.bias, col + q, g.bias_dtype);
+            v[q] = cbf ? hround(v[q]) + b : v[q] + b;
+          }
+        }
+        if (cbf) {
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.C) + off) =
+              make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+        } else {
+          float* cp = static_cast<float*>(g.C) + off;
+          *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<float4*>(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        continue;
+      }
+      const int edt = Tr<T>::DT;
+      for (int q = 0; q < 8; ++q) {
+        if (col + q >= g.N) break;
+        const int64_t o = off + q;
+        float x = cbf ? hround(v[q]) : v[q];
+        if (g.bias) {
+          const float b = load_elem(g.bias, col + q, g.bias_dtype);
+          x = cbf ? hround(x + b) : x + b;
+        }
+        if (g.emask) {
+          const float em = load_elem(g.emask, o, edt);
+          if (g.dw) {
+            if (em < 0.5f) {
+              float d = g.decay * load_elem(g.dw, o, edt);
+              if (cbf) d = hround(d);
+              x = cbf ? hround(x + d) : x + d;
+            }
+          } else {
+            x = cbf ? hround(x * em) : x * em;
+          }
+        }
+        if (g.accumulate) x = load_elem(g.C, o, g.c_dtype) + x;
+        if (cbf)
+          static_cast<uint16_t*>(g.C)[o] = hbits(x);
+        else
+          static_cast<float*>(g.C)[o] = x;
+      }
+    }
+  }
+}
 
 template <typename T, int AL, int BL, int MASK>
 __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
@@ -671,10 +838,14 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
     const bool do_store = s + 1 < nk1, do_load = s + 2 < nk1;
     const int64_t k_next = kbase + (s + 2) * BK;
     mfma_stage(buf, [&](int q) {
-      if (q == 0 && do_store) store_a(sa, buf ^ 1);
-      if (q == 1 && do_store) store_b(buf ^ 1);
-      if (q == 2 && do_load) la.load(sa, k_next);
-      if (q == 3 && do_load) load_b(k_next);
+      if (q == 0 && do_store) {
+        store_a(sa, buf ^ 1);
+        if (do_load) la.load(sa, k_next);
+      }
+      if (q == 1 && do_store) {
+        store_b(buf ^ 1);
+        if (do_load) load_b(k_next);
+      }
     });
     __syncthreads();
   }
@@ -701,118 +872,401 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
     }
   }
 
-  // Epilogue.  32x32 accumulator layout: lane holds column (lane % 32) and
-  // rows (e / 4) * 8 + (lane / 32) * 4 + e % 4, e = 0..15.  The accumulators
-  // go through LDS in two halves of 64 rows per wave (the operand buffers are
-  // free now); each lane then owns 8 consecutive columns of a row, so C is
-  // read and written with 16-byte accesses and the optional epilogue operands
-  // (bias, mask product, decay term, accumulation) are read coalesced.
-  float* ep = reinterpret_cast<float*>(smem) + wave * (64 * kEpiPitch);
-  const int64_t wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
-  const bool cbf = g.c_dtype == SF_DTYPE_BF16;
-  const bool plain = !g.emask && !g.accumulate;
+  gemm_epilogue<T>(g, acc, smem, m0, n0, kz);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 kernel with direct-to-LDS staging (gfx950 `buffer_load_dwordx4 ... lds`).
+//
+// K-contiguous operands that reach LDS unchanged (A of the forward and
+// input-gradient products, B of an unmasked forward, both SLoRB operands of
+// the forward) are copied global -> LDS by the buffer unit without passing
+// through registers: one wave instruction moves 8 rows x 128 B (a 16-byte
+// chunk per lane) into 1 KiB of LDS.  Rows are unpadded and their chunks
+// XOR-swizzled, slot s of row r holding chunk s ^ f(r), f(r) = (r ^ r >> 3) & 7,
+// so the 16-byte fragment reads of 8 (and of 16) consecutive rows fall in
+// distinct banks.  A masked or M/N-contiguous operand keeps the register path
+// (mask product, 8 x 8 transpose) into the padded 144-byte-pitch layout.
+//
+// Stage s (LDS buffer b = s & 1 holds it):
+//   k-steps 0..2: MFMAs of k-step kk, fragment reads of k-step kk + 1
+//   wait for this wave's copies into b ^ 1 and its fragment reads, barrier:
+//     b ^ 1 (stage s + 1) is complete; b is no longer read by anyone
+//   copies of stage s + 2 into b (register stores, register loads of
+//     stage s + 3, DMA issue)
+//   k-step 3: MFMAs, fragment reads of k-step 0 of stage s + 1 from b ^ 1
+// LDS latency is covered by a k-step of MFMAs everywhere, and each copy has
+// a whole stage to land.
+// ---------------------------------------------------------------------------
+constexpr int kRowSw = 128;  // bytes per row of a swizzled (DMA) tile: 64 bf16
+constexpr int kWaitLgkmOnly = 0xC07F;  // s_waitcnt lgkmcnt(0) with vmcnt / expcnt left alone (gfx9 encoding)
+constexpr int kRowPad = 144; // bytes per row of a padded (register-path) tile
+
+__device__ __forceinline__ void dma16(Rsrc r, unsigned char* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// Direct copy of a K-contiguous bf16 operand tile (256 rows x 64 k) into a
+// swizzled LDS tile.  Wave w copies rows [64 w, 64 w + 64) with 8 instructions;
+// in instruction i lane l covers row 64 w + 8 i + l / 8, slot l % 8, i.e.
+// chunk c = (l % 8) ^ f(row) = (l % 8) ^ (l / 8) ^ i.
+struct DmaLoader {
+  Rsrc rs;
+  uint32_t off[8];  // lane byte offset (row, chunk) of instruction i; kOob for rows past the operand
+  int64_t k_end;
+
+  __device__ __forceinline__ void init(const void* base, int64_t ld, int64_t row0, int64_t rows_total,
+                                       int64_t kend) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    rs = make_rsrc(base, rows_total * ld * 2);
+    k_end = kend;
+    const int c0 = (lane & 7) ^ (lane >> 3);
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    __syncthreads();
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-      for (int j = 0; j < kFragN; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int r = ii * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-          ep[r * kEpiPitch + j * 32 + (lane & 31)] = acc[(2 * h + ii) * kFragN + j][e];
-        }
-    __syncthreads();
-    for (int it = 0; it < 16; ++it) {
-      const int flat = it * 64 + lane;
-      const int r = flat >> 4, c = (flat & 15) * 8;
-      const int64_t row = wrow0 + h * 64 + r, col = wcol0 + c;
-      if (row >= g.M || col >= g.N) continue;
-      float v[8];
-      const float4 p0 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c);
-      const float4 p1 = *reinterpret_cast<const float4*>(ep + r * kEpiPitch + c + 4);
-      v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
-      v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
-      if (g.c_blocks) {
-        // block-sparse C (the SDDMM weight gradient): only kept 16 x 16 blocks are written,
-        // row (row % 16) of block c_map[row / 16][col / 16], 8 columns at a time
-        const int64_t bi = (row / 16 < g.c_map_rows && col / 16 < g.c_map_cols)
-                               ? g.c_map[(row / 16) * g.c_map_cols + col / 16] : -1;
-        if (bi >= 0) {
-          const int64_t o = bi * 256 + (row % 16) * 16 + (col % 16);
-          if (g.c_dtype == SF_DTYPE_BF16) {
-            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.c_blocks) + o) =
-                make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
-          } else {
-            float* cp = static_cast<float*>(g.c_blocks) + o;
-            *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
-            *reinterpret_cast<float4*>(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
-          }
-        }
-        continue;
-      }
-      if (g.splits > 1) {
-        // split-K: raw f32 partial sums; sf_gemm's reduce kernel applies the epilogue
-        float* pp = g.partial + (kz * g.M + row) * g.N + col;
-        if (col + 8 <= g.N && (g.N & 3) == 0) {
-          *reinterpret_cast<float4*>(pp) = make_float4(v[0], v[1], v[2], v[3]);
-          *reinterpret_cast<float4*>(pp + 4) = make_float4(v[4], v[5], v[6], v[7]);
-        } else {
-          for (int q = 0; q < 8 && col + q < g.N; ++q) pp[q] = v[q];
-        }
-        continue;
-      }
-      const int64_t off = row * g.ldc + col;
-      const bool vec = g.c_aligned && col + 8 <= g.N && (off & 7) == 0;
-      if (plain && vec) {
-        // result of the matmul in the output dtype, then + bias (rounded again)
-        if (g.bias) {
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const float b = load_elem(g.bias, col + q, g.bias_dtype);
-            v[q] = cbf ? hround(v[q]) + b : v[q] + b;
-          }
-        }
-        if (cbf) {
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.C) + off) =
-              make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
-        } else {
-          float* cp = static_cast<float*>(g.C) + off;
-          *reinterpret_cast<float4*>(cp) = make_float4(v[0], v[1], v[2], v[3]);
-          *reinterpret_cast<float4*>(cp + 4) = make_float4(v[4], v[5], v[6], v[7]);
-        }
-        continue;
-      }
-      const int edt = Tr<T>::DT;
-      for (int q = 0; q < 8; ++q) {
-        if (col + q >= g.N) break;
-        const int64_t o = off + q;
-        float x = cbf ? hround(v[q]) : v[q];
-        if (g.bias) {
-          const float b = load_elem(g.bias, col + q, g.bias_dtype);
-          x = cbf ? hround(x + b) : x + b;
-        }
-        if (g.emask) {
-          const float em = load_elem(g.emask, o, edt);
-          if (g.dw) {
-            if (em < 0.5f) {
-              float d = g.decay * load_elem(g.dw, o, edt);
-              if (cbf) d = hround(d);
-              x = cbf ? hround(x + d) : x + d;
-            }
-          } else {
-            x = cbf ? hround(x * em) : x * em;
-          }
-        }
-        if (g.accumulate) x = load_elem(g.C, o, g.c_dtype) + x;
-        if (cbf)
-          static_cast<uint16_t*>(g.C)[o] = hbits(x);
-        else
-          static_cast<float*>(g.C)[o] = x;
-      }
+    for (int i = 0; i < 8; ++i) {
+      const int64_t row = row0 + w * 64 + i * 8 + (lane >> 3);
+      off[i] = row < rows_total ? (uint32_t)((row * ld + (c0 ^ i) * 8) * 2) : kOob;
     }
   }
+  // Instruction i of issue<false> alone.
+  __device__ __forceinline__ void issue_one(unsigned char* tile, int64_t k0, int i) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    dma16(rs, tile + w * 64 * kRowSw + i * 8 * kRowSw, off[i], (uint32_t)(k0 * 2));
+  }
+  // Issue the copy of the stage at k0 into `tile` (256 rows x 128 B).  TAIL:
+  // the stage may end past K (its chunks at or past K read zeros).
+  template <bool TAIL>
+  __device__ __forceinline__ void issue(unsigned char* tile, int64_t k0) const {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    unsigned char* dst = tile + w * 64 * kRowSw;
+    const uint32_t soff = (uint32_t)(k0 * 2);
+    if constexpr (!TAIL) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dma16(rs, dst + i * 8 * kRowSw, off[i], soff);
+    } else {
+      const int64_t kv = k_end - k0;  // valid k of this stage
+      const int c0 = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dma16(rs, dst + i * 8 * kRowSw, ((c0 ^ i) * 8 < kv) ? off[i] : kOob, soff);
+    }
+  }
+};
+
+// Byte offset, within its tile, of the lane's fragment row `r` at k-step 0;
+// k-step kk is at `base ^ (kk << 5)` (swizzled) or `base + kk * 32` (padded).
+template <bool SW>
+__device__ __forceinline__ uint32_t frag_base(int r) {
+  const int h = (threadIdx.x & 63) >> 5;  // second 8-element half of the 16-k step
+  if constexpr (SW) {
+    const int g = ((r ^ (r >> 3)) & 7) ^ h;
+    return (uint32_t)(r * kRowSw + (g << 4));
+  } else {
+    return (uint32_t)(r * kRowPad + h * 16);
+  }
+}
+template <bool SW>
+__device__ __forceinline__ uint32_t frag_at(uint32_t base, int kk) {
+  if constexpr (SW)
+    return base ^ (uint32_t)(kk << 5);
+  else
+    return base + (uint32_t)(kk * 32);
+}
+
+template <int AL, int BL, int MASK>
+__global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
+  using T = uint16_t;
+  constexpr int BK = 64;
+  constexpr bool DA = AL == 0;                       // A copied global -> LDS directly
+  constexpr bool DB = BL == 0 && MASK == kMaskNone;  // B likewise
+  constexpr uint32_t ABUF = 256u * (DA ? kRowSw : kRowPad), BBUF = 256u * (DB ? kRowSw : kRowPad);
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* const As = smem;
+  unsigned char* const Bs = smem + 2 * ABUF;
+
+  const int64_t tiles = g.tiles_m * g.tiles_n;
+  const int64_t kz = blockIdx.x / tiles;
+  int64_t tm, tn;
+  tile_coords(blockIdx.x - kz * tiles, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = tm * kTileM, n0 = tn * kTileN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int64_t nk1_all = ceil_div(g.K1, BK);
+  const int64_t s_begin = kz * g.split_stages;
+  const int64_t s_end = (s_begin + g.split_stages < nk1_all) ? s_begin + g.split_stages : nk1_all;
+  const int64_t nk = s_end > s_begin ? s_end - s_begin : 0;
+  const int64_t nk2 = (g.A2 && kz == g.splits - 1) ? ceil_div(g.K2, BK) : 0;
+  const int64_t kbase = s_begin * BK;
+  const bool has_scale = g.has_scale != 0;
+  const float bscale = g.bscale;
+
+  f32x16_t acc[kFragM * kFragN];
+#pragma unroll
+  for (int i = 0; i < kFragM * kFragN; ++i) acc[i] = f32x16_t{};
+
+  uint32_t aoff[4][kFragM], boff[4][kFragN];  // [k-step][fragment] byte offsets within a buffer
+#pragma unroll
+  for (int i = 0; i < kFragM; ++i) {
+    const uint32_t base = frag_base<DA>(wm * kWaveM + i * 32 + (lane & 31));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) aoff[kk][i] = frag_at<DA>(base, kk);
+  }
+#pragma unroll
+  for (int j = 0; j < kFragN; ++j) {
+    const uint32_t base = frag_base<DB>(wn * kWaveN + j * 32 + (lane & 31));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) boff[kk][j] = frag_at<DB>(base, kk);
+  }
+
+  bf16x8_t fa[2][kFragM], fb[2][kFragN];
+  auto read_frags = [&](int slot, int buf, int kk) {
+    const unsigned char* a = As + buf * ABUF;
+    const unsigned char* b = Bs + buf * BBUF;
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8_t*>(a + aoff[kk][i]);
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j) fb[slot][j] = *reinterpret_cast<const bf16x8_t*>(b + boff[kk][j]);
+  };
+  auto mfmas = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+      for (int i = 0; i < kFragM; ++i)
+        acc[i * kFragN + j] =
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], 0, 0, 0);
+  };
+
+  // Segment 1 copy machinery: DMA for direct operands, registers otherwise.
+  DmaLoader da, db;
+  Loader<T, AL> la;
+  Loader<T, BL> lb;
+  Stage<T, kMaskNone> sa;
+  Stage<T, MASK> sb;
+  if constexpr (DA)
+    da.init(g.A1, g.lda1, m0, g.M, g.K1);
+  else
+    la.init(g.A1, nullptr, g.lda1, m0, g.M, g.K1, false, kbase);
+  if constexpr (DB)
+    db.init(g.B1, g.ldb1, n0, g.N, g.K1);
+  else
+    lb.init(g.B1, MASK != kMaskNone ? g.bmask : nullptr, g.ldb1, n0, g.N, g.K1, MASK == kMaskByte, kbase);
+
+  auto reg_load = [&](int64_t k0) {  // register-path loads of the stage at k0
+    if constexpr (!DA) la.load(sa, k0);
+    if constexpr (!DB) lb.load(sb, k0);
+  };
+  auto reg_store = [&](int buf) {  // register-path stores into buffer `buf`
+    if constexpr (!DA) {
+      if (AL == 0)
+        store_kc<T, kMaskNone>(sa, reinterpret_cast<T*>(As + buf * ABUF), false, 1.0f);
+      else
+        store_rc<T, kMaskNone>(sa, reinterpret_cast<T*>(As + buf * ABUF), false, 1.0f);
+    }
+    if constexpr (!DB) {
+      if (BL == 0)
+        store_kc<T, MASK>(sb, reinterpret_cast<T*>(Bs + buf * BBUF), has_scale, bscale);
+      else
+        store_rc<T, MASK>(sb, reinterpret_cast<T*>(Bs + buf * BBUF), has_scale, bscale);
+    }
+  };
+  auto dma_issue = [&](auto tail, int buf, int64_t k0) {
+    constexpr bool TL = decltype(tail)::value;
+    if constexpr (DA) da.template issue<TL>(As + buf * ABUF, k0);
+    if constexpr (DB) db.template issue<TL>(Bs + buf * BBUF, k0);
+  };
+  using Tail = std::integral_constant<bool, true>;
+
+  // Prologue: stages 0 and 1 into buffers 0 and 1, registers hold stage 2.
+  if (nk > 0) {
+    reg_load(kbase);
+    dma_issue(Tail{}, 0, kbase);
+    reg_store(0);
+  }
+  if (nk > 1) {
+    reg_load(kbase + BK);
+    dma_issue(Tail{}, 1, kbase + BK);
+    reg_store(1);
+  }
+  if (nk > 2) reg_load(kbase + 2 * BK);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (nk > 0) read_frags(0, 0, 0);
+
+  // Steady state: stages s (buffer 0) and s + 1 (buffer 1), each copying a
+  // full stage s + 2 and loading s + 3, with compile-time LDS offsets and the
+  // instruction order fixed (a scheduling barrier after every MFMA):
+  //   k-steps 0..2: the 8 fragment reads of the next k-step after its first 4 MFMAs
+  //   k-step 3: the next stage's first fragment reads after MFMAs 0..3, then
+  //   one eighth of the stage's copies after each of MFMAs 4..11.
+  auto mfma1 = [&](int slot, int i, int j) {
+    acc[i * kFragN + j] =
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], 0, 0, 0);
+  };
+  auto read1 = [&](int slot, int buf, int kk, int f) {  // fragment f: A 0..3, B 4..7
+    if (f < kFragM)
+      fa[slot][f] = *reinterpret_cast<const bf16x8_t*>(As + buf * ABUF + aoff[kk][f]);
+    else
+      fb[slot][f - kFragM] = *reinterpret_cast<const bf16x8_t*>(Bs + buf * BBUF + boff[kk][f - kFragM]);
+  };
+  auto kstep = [&](int slot, auto&& after) {
+#pragma unroll
+    for (int idx = 0; idx < 16; ++idx) {
+      mfma1(slot, idx & 3, idx >> 2);
+      after(idx);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  V4 mb[8];  // masked B vectors of an N-contiguous masked B (before their transpose)
+  constexpr bool kRegPath = !DA || !DB;
+  auto steady = [&](auto bc, int64_t s) {
+    constexpr int B = decltype(bc)::value;
+    kstep(0, [&](int idx) {
+      if (idx < 4) {
+        read1(1, B, 1, 2 * idx);
+        read1(1, B, 1, 2 * idx + 1);
+      }
+    });
+    kstep(1, [&](int idx) {
+      if (idx < 4) {
+        read1(0, B, 2, 2 * idx);
+        read1(0, B, 2, 2 * idx + 1);
+      }
+    });
+    kstep(0, [&](int idx) {
+      if (idx < 4) {
+        read1(1, B, 3, 2 * idx);
+        read1(1, B, 3, 2 * idx + 1);
+      }
+    });
+    // this wave's copies into B ^ 1 landed and its k-step 3 fragments are in
+    // registers; without DMA the register loads of stage s + 3 stay in flight
+    if constexpr (DA || DB)
+      __builtin_amdgcn_s_waitcnt(0);
+    else
+      __builtin_amdgcn_s_waitcnt(kWaitLgkmOnly);
+    __syncthreads();
+    const int64_t k2 = kbase + (s + 2) * BK, k3 = kbase + (s + 3) * BK;
+    kstep(1, [&](int idx) {
+      if (idx < 4) {  // the next stage's first fragments (buffer B ^ 1)
+        read1(0, B ^ 1, 0, 2 * idx);
+        read1(0, B ^ 1, 0, 2 * idx + 1);
+      }
+      if constexpr (kRegPath) {
+        // register path: mask products of the staged B vectors (2 per MFMA
+        // over MFMAs 0..3), one transposed or masked vector per operand
+        // written to LDS after MFMAs 4..11, then the loads of stage s + 3 and
+        // the DMA copies after MFMAs 12..15 (after every LDS write: a DS
+        // write issued behind an LDS DMA would wait for it)
+        if constexpr (!DB && BL == 1 && MASK != kMaskNone) {
+          if (idx < 4) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              mb[2 * idx + h] = apply_mask<T, MASK>(sb.v[2 * idx + h], sb.e[2 * idx + h], has_scale, bscale);
+          }
+        }
+        if (idx >= 4 && idx < 12) {
+          const int p = idx - 4;
+          if constexpr (!DA) write_rc_one(transpose_one(sa.v, p), reinterpret_cast<T*>(As + B * ABUF), p);
+          if constexpr (!DB) {
+            if constexpr (BL == 0)
+              store_kc_one<T, MASK>(sb, reinterpret_cast<T*>(Bs + B * BBUF), p, has_scale, bscale);
+            else if constexpr (MASK != kMaskNone)
+              write_rc_one(transpose_one(mb, p), reinterpret_cast<T*>(Bs + B * BBUF), p);
+            else
+              write_rc_one(transpose_one(sb.v, p), reinterpret_cast<T*>(Bs + B * BBUF), p);
+          }
+        } else if (idx >= 12) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int p = 2 * (idx - 12) + h;
+            if constexpr (DA)
+              da.issue_one(As + B * ABUF, k2, p);
+            else
+              la.load_one(sa, k3, p);
+            if constexpr (DB)
+              db.issue_one(Bs + B * BBUF, k2, p);
+            else
+              lb.load_one(sb, k3, p);
+          }
+        }
+      } else if (idx >= 4 && idx < 12) {  // DMA only: one instruction per operand per MFMA
+        da.issue_one(As + B * ABUF, k2, idx - 4);
+        db.issue_one(Bs + B * BBUF, k2, idx - 4);
+      }
+    });
+  };
+  int64_t s = 0;
+  for (; s + 5 <= nk; s += 2) {
+    steady(std::integral_constant<int, 0>{}, s);
+    steady(std::integral_constant<int, 1>{}, s + 1);
+  }
+  // The last (up to four) stages, with run-time buffer offsets.
+  for (; s < nk; ++s) {
+    const int b = static_cast<int>(s & 1);
+    read_frags(1, b, 1);
+    mfmas(0);
+    read_frags(0, b, 2);
+    mfmas(1);
+    read_frags(1, b, 3);
+    mfmas(0);
+    if (s + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (s + 2 < nk) {
+        reg_store(b);
+        if (s + 3 < nk) reg_load(kbase + (s + 3) * BK);
+        dma_issue(std::integral_constant<bool, true>{}, b, kbase + (s + 2) * BK);
+      }
+      read_frags(0, b ^ 1, 0);
+    }
+    mfmas(1);
+  }
+
+  // Segment 2 (the SLoRB term A2 . B2^T, a few stages, never masked) through buffer 0.
+  if (nk2 > 0) {
+    DmaLoader da2, db2;
+    Loader<T, AL> la2;
+    Loader<T, BL> lb2;
+    if constexpr (DA)
+      da2.init(g.A2, g.lda2, m0, g.M, g.K2);
+    else
+      la2.init(g.A2, nullptr, g.lda2, m0, g.M, g.K2);
+    if constexpr (DB)
+      db2.init(g.B2, g.ldb2, n0, g.N, g.K2);
+    else
+      lb2.init(g.B2, nullptr, g.ldb2, n0, g.N, g.K2);
+    for (int64_t s2 = 0; s2 < nk2; ++s2) {
+      __syncthreads();  // every wave is done with buffer 0
+      if constexpr (DA) {
+        da2.issue<true>(As, s2 * BK);
+      } else {
+        Stage<T, kMaskNone> ta;
+        la2.load(ta, s2 * BK);
+        store_rc<T, kMaskNone>(ta, reinterpret_cast<T*>(As), false, 1.0f);
+      }
+      if constexpr (DB) {
+        db2.issue<true>(Bs, s2 * BK);
+      } else {
+        Stage<T, kMaskNone> tb;
+        lb2.load(tb, s2 * BK);
+        if constexpr (BL == 0)
+          store_kc<T, kMaskNone>(tb, reinterpret_cast<T*>(Bs), false, 1.0f);
+        else
+          store_rc<T, kMaskNone>(tb, reinterpret_cast<T*>(Bs), false, 1.0f);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      read_frags(0, 0, 0);
+      read_frags(1, 0, 1);
+      mfmas(0);
+      read_frags(0, 0, 2);
+      mfmas(1);
+      read_frags(1, 0, 3);
+      mfmas(0);
+      mfmas(1);
+    }
+  }
+
+  gemm_epilogue<T>(g, acc, smem, m0, n0, kz);
 }
 
 // Split-K reduction: C = epilogue(sum over splits of the f32 partials), the
@@ -858,11 +1312,25 @@ constexpr size_t smem_bytes() {
   return sizeof(T) * 2ull * (kTileM + kTileN) * Tr<T>::PITCH + 2 * 16 * (Tr<T>::BK / 16);
 }
 
+// bf16 dense B: the direct-to-LDS kernel; its LDS also hosts the epilogue staging.
+template <int AL, int BL, int MASK>
+constexpr size_t smem_bytes_bf16() {
+  constexpr size_t ops = 2ull * 256 * (AL == 0 ? kRowSw : kRowPad) + 2ull * 256 * (BL == 0 && MASK == kMaskNone ? kRowSw : kRowPad);
+  constexpr size_t epi = 4ull * 64 * kEpiPitch * sizeof(float);
+  return ops > epi ? ops : epi;
+}
+
 template <typename T, int AL, int BL, int MASK>
 int launch_gemm(const GemmArgs& g, hipStream_t st) {
   static bool attr_set = false;  // per instantiation; host code runs the attribute call once
-  auto kern = gemm_kernel<T, AL, BL, MASK>;
-  const size_t smem = smem_bytes<T>();
+  constexpr bool kDirect = sizeof(T) == 2 && BL < 2;
+  auto kern = [] {
+    if constexpr (kDirect)
+      return gemm_bf16_kernel<AL, (BL < 2 ? BL : 0), MASK>;
+    else
+      return gemm_kernel<T, AL, BL, MASK>;
+  }();
+  const size_t smem = kDirect ? smem_bytes_bf16<AL, (BL < 2 ? BL : 0), MASK>() : smem_bytes<T>();
   if (!attr_set) {
     SF_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(smem)));
