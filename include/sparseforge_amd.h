@@ -196,6 +196,15 @@ int sf_glu_update_masks(const sf_mask_params* p, const void* S, int s_dtype, voi
                         const float* stats, const float* tau, int up_hard_kind, int up_hard_n,
                         int64_t* gate_flips, int64_t* up_flips, void* stream);
 
+/*
+ * dst[c][r] = src[r][c] for a byte mask (src [rows, cols], dst [cols, rows]):
+ * the K-major form of the effective byte mask that the input-gradient GEMM
+ * reads beside the transposed weight tile (sf_gemm_desc.bmask_kmajor).  No
+ * counterpart of its own in the reference; part of the mask application of
+ * FusedMaskedLinearSTE.backward (legacy/sparse_modeling.py:113-115).
+ */
+int sf_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst, void* stream);
+
 /* ---- effective mask for the masked GEMMs (SparseLinear.forward, :759-771) */
 #define SF_EFF_SOFT 0 /* E = mask.to(weight dtype)                                  */
 #define SF_EFF_MIX 1  /* E = (hx * mask + (1 - hx) * hard(mask)).to(weight dtype)     */
@@ -256,6 +265,11 @@ typedef struct sf_gemm_desc {
                              c_blocks [nnz][16][16] (the SDDMM weight gradient)        */
   const int32_t* c_map;   /* [M/16][N/16] block indices of C, -1 = not stored            */
   int64_t c_map_rows, c_map_cols;
+  int bmask_kmajor;       /* with b_layout SF_LAYOUT_MN and a byte bmask: 1 = bmask is given
+                             K-major, [N][K1] with leading dimension ldbm (the transpose
+                             of B1's layout), so the input-gradient GEMM reads it beside
+                             the transposed weight tile; 0 = bmask has B1's layout      */
+  int64_t ldbm;
 } sf_gemm_desc;
 
 #define SF_BFMT_DENSE 0

@@ -132,6 +132,8 @@ class GemmDesc(ctypes.Structure):
         ("c_map", ctypes.c_void_p),
         ("c_map_rows", ctypes.c_int64),
         ("c_map_cols", ctypes.c_int64),
+        ("bmask_kmajor", ctypes.c_int),
+        ("ldbm", ctypes.c_int64),
     ]
 
 
@@ -176,6 +178,7 @@ SIGNATURES = {
     "sf_joint_scores": (_I, [_MP, _P, _P, _P, _MP, _P, _P, _P, _I, _I, _I, _P, _I, _P]),
     "sf_glu_update_masks": (_I, [_MP, _P, _I, _P, _P, _I, _P, _I, _P, _P, _I, _I, _P, _P, _P]),
     "sf_effective_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _F, _I, _I, _I, _P]),
+    "sf_transpose_u8": (_I, [_P, _I64, _I64, _P, _P]),
     "sf_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
     "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "sf_column_sum": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),

@@ -87,6 +87,9 @@ struct GemmArgs {
   void* c_blocks;
   const int32_t* c_map;
   int64_t c_map_rows, c_map_cols;
+  int64_t ldbm;      // leading dimension of a K-major byte mask ([N][K1])
+  int bmask_kmajor;  // bmask is K-major (input gradient: B = W^T, mask given transposed)
+  int dma_mask_ok;   // the byte mask can be copied 16 bytes at a time (bf16 direct kernel)
 };
 
 // Element traits.  bf16 uses v_mfma_f32_32x32x16_bf16 (8 k-values per lane),
@@ -902,8 +905,18 @@ constexpr int kRowSw = 128;  // bytes per row of a swizzled (DMA) tile: 64 bf16
 constexpr int kWaitLgkmOnly = 0xC07F;  // s_waitcnt lgkmcnt(0) with vmcnt / expcnt left alone (gfx9 encoding)
 constexpr int kRowPad = 144; // bytes per row of a padded (register-path) tile
 
-__device__ __forceinline__ void dma16(Rsrc r, unsigned char* lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+// One 16-byte-per-lane copy global -> LDS: lane l's 16 bytes land at lds + 16 l.
+// Issued as inline assembly so the compiler does not track it: it would
+// otherwise make every later LDS access that it cannot prove disjoint wait for
+// all copies in flight.  The kernels wait for their copies themselves
+// (s_waitcnt vmcnt(0) before the barrier that publishes a buffer).
+__device__ __forceinline__ void dma16(Rsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+// LDS byte address of a pointer into the kernel's dynamic LDS (`base` its start).
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* base) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char*)base;
 }
 
 // Direct copy of a K-contiguous bf16 operand tile (256 rows x 64 k) into a
@@ -928,16 +941,16 @@ struct DmaLoader {
     }
   }
   // Instruction i of issue<false> alone.
-  __device__ __forceinline__ void issue_one(unsigned char* tile, int64_t k0, int i) const {
+  __device__ __forceinline__ void issue_one(uint32_t tile, int64_t k0, int i) const {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     dma16(rs, tile + w * 64 * kRowSw + i * 8 * kRowSw, off[i], (uint32_t)(k0 * 2));
   }
   // Issue the copy of the stage at k0 into `tile` (256 rows x 128 B).  TAIL:
   // the stage may end past K (its chunks at or past K read zeros).
   template <bool TAIL>
-  __device__ __forceinline__ void issue(unsigned char* tile, int64_t k0) const {
+  __device__ __forceinline__ void issue(uint32_t tile, int64_t k0) const {
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    unsigned char* dst = tile + w * 64 * kRowSw;
+    const uint32_t dst = tile + w * 64 * kRowSw;
     const uint32_t soff = (uint32_t)(k0 * 2);
     if constexpr (!TAIL) {
 #pragma unroll
@@ -950,6 +963,108 @@ struct DmaLoader {
     }
   }
 };
+
+// Direct copy of a byte and-mask tile (256 rows x 64 k, one byte per element)
+// into LDS rows of 64 B.  Wave w copies rows [64 w, 64 w + 64) with 4
+// instructions; in instruction i lane l covers row 64 w + 16 i + l / 4, slot
+// l % 4, which holds 16-byte chunk (l % 4) ^ g(row), g(row) = (row >> 2) & 3
+// = (l >> 4) & 3.
+struct DmaMaskLoader {
+  Rsrc rs;
+  uint32_t off[4];
+  int64_t k_end;
+
+  __device__ __forceinline__ void init(const void* base, int64_t ld, int64_t row0, int64_t rows_total,
+                                       int64_t kend) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    rs = make_rsrc(base, rows_total * ld);
+    k_end = kend;
+    const int c = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t row = row0 + w * 64 + i * 16 + (lane >> 2);
+      off[i] = row < rows_total ? (uint32_t)(row * ld + c * 16) : kOob;
+    }
+  }
+  template <bool TAIL>
+  __device__ __forceinline__ void issue(uint32_t tile, int64_t k0) const {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t dst = tile + w * 64 * 64;
+    const int64_t kv = k_end - k0;
+    const int c = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(rs, dst + i * 16 * 64, (!TAIL || c * 16 < kv) ? off[i] : kOob, (uint32_t)k0);
+  }
+  __device__ __forceinline__ void issue_one(uint32_t tile, int64_t k0, int i) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    dma16(rs, tile + w * 64 * 64 + i * 16 * 64, off[i], (uint32_t)k0);
+  }
+};
+
+// A bf16 fragment with its 8 mask bytes (0x00 / 0xFF) applied.
+__device__ __forceinline__ bf16x8_t and_bytes(bf16x8_t x, uint2 m) {
+  uint4 w = __builtin_bit_cast(uint4, x);
+  w.x &= __builtin_amdgcn_perm(m.x, m.x, 0x01010000u);
+  w.y &= __builtin_amdgcn_perm(m.x, m.x, 0x03030202u);
+  w.z &= __builtin_amdgcn_perm(m.y, m.y, 0x01010000u);
+  w.w &= __builtin_amdgcn_perm(m.y, m.y, 0x03030202u);
+  return __builtin_bit_cast(bf16x8_t, w);
+}
+
+// Direct copy of an M/N-contiguous bf16 operand tile (64 k rows x 256 columns
+// of a row-major [K, cols] matrix) into LDS rows of 512 B.  Wave w copies rows
+// [16 w, 16 w + 16) with 8 instructions of 2 rows each; in instruction i lane l
+// covers row 16 w + 2 i + l / 32, slot l % 32, which holds 16-byte column chunk
+// (l % 32) ^ fmn(row), fmn(row) = 4 (row & 3).  Rows past K lie past the
+// resource extent and read zeros; the offsets advance by a stage per copy.
+struct DmaLoaderMN {
+  Rsrc rs;
+  uint32_t off[8];
+  uint32_t k_step;
+
+  __device__ __forceinline__ void init(const void* base, int64_t ld, int64_t col0, int64_t cols_total, int64_t kend,
+                                       int64_t kstart) {
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    rs = make_rsrc(base, kend * ld * 2);
+    k_step = (uint32_t)(64 * ld * 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 16 * w + 2 * i + (lane >> 5);
+      const int64_t col = col0 + 8 * ((lane & 31) ^ (4 * (row & 3)));
+      off[i] = col < cols_total ? (uint32_t)(((kstart + row) * ld + col) * 2) : kOob;
+    }
+  }
+  __device__ __forceinline__ void issue_one(uint32_t tile, int i) {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    dma16(rs, tile + w * 16 * 512 + i * 1024, off[i], 0);
+    off[i] = off[i] >= kOob ? kOob : off[i] + k_step;
+  }
+  __device__ __forceinline__ void issue(uint32_t tile) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) issue_one(tile, i);
+  }
+};
+
+// Lane byte offset in an M/N-contiguous tile of the transposed reads of MFMA
+// fragment rows [r0, r0 + 32) at k-step 0 (k-step kk adds kk * 8192, the
+// second 4 k-values 2048).  ds_read_b64_tr_b16 hands lane 4q + c of each
+// 16-lane group the c-th 16-bit value of the rows addressed by lanes
+// q, q + 4, q + 8, q + 12; lane L therefore addresses row k = L / 4 (+ 8 for
+// the second half-wave) at the 4 columns 4 (L % 4) of the group's 16.
+__device__ __forceinline__ uint32_t mn_frag_base(int r0) {
+  const int lane = threadIdx.x & 63, grp = lane >> 4, L = lane & 15, q = L >> 2;
+  const int k = 8 * (grp >> 1) + q;
+  const int col = r0 + 16 * (grp & 1) + 4 * (L & 3);
+  return (uint32_t)(k * 512 + (((col >> 3) ^ (4 * q)) << 4) + (col & 7) * 2);
+}
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8_t tr_frag(const unsigned char* p) {
+  typedef __attribute__((address_space(3))) v4i16_t lds_v4;
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(p));
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(p + 2048));
+  return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
 
 // Byte offset, within its tile, of the lane's fragment row `r` at k-step 0;
 // k-step kk is at `base ^ (kk << 5)` (swizzled) or `base + kk * 32` (padded).
@@ -975,12 +1090,14 @@ template <int AL, int BL, int MASK>
 __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
   using T = uint16_t;
   constexpr int BK = 64;
-  constexpr bool DA = AL == 0;                       // A copied global -> LDS directly
-  constexpr bool DB = BL == 0 && MASK == kMaskNone;  // B likewise
-  constexpr uint32_t ABUF = 256u * (DA ? kRowSw : kRowPad), BBUF = 256u * (DB ? kRowSw : kRowPad);
+  constexpr bool DM = MASK == kMaskByte;  // byte mask: K-major tile in LDS, applied to the B fragments
+  constexpr bool DB = MASK != kMaskMul;   // B copied by DMA (a multiplicative mask keeps the register path)
+  constexpr uint32_t ABUF = 32768u, BBUF = DB ? 32768u : 256u * kRowPad, MBUF = 256u * 64;
   extern __shared__ __align__(16) unsigned char smem[];
-  unsigned char* const As = smem;
-  unsigned char* const Bs = smem + 2 * ABUF;
+  unsigned char* const As = smem;           // [2] A tiles (256 rows x 128 B swizzled, or 64 k x 512 B)
+  unsigned char* const Bs = smem + 2 * ABUF;  // [2] B tiles (likewise, or padded for the register path)
+  unsigned char* const Ms = Bs + 2 * BBUF;    // [2][256 rows][64 B] byte masks (DM)
+  const uint32_t As_l = lds_addr(As), Bs_l = lds_addr(Bs), Ms_l = lds_addr(Ms);
 
   const int64_t tiles = g.tiles_m * g.tiles_n;
   const int64_t kz = blockIdx.x / tiles;
@@ -1003,75 +1120,138 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < kFragM * kFragN; ++i) acc[i] = f32x16_t{};
 
-  uint32_t aoff[4][kFragM], boff[4][kFragN];  // [k-step][fragment] byte offsets within a buffer
+  // Fragment offsets: K-contiguous tiles per (k-step, fragment); M/N-contiguous
+  // tiles per fragment (k-steps are immediate offsets).
+  uint32_t aoff[4][kFragM], boff[4][kFragN], moff[4][kFragN];
 #pragma unroll
   for (int i = 0; i < kFragM; ++i) {
-    const uint32_t base = frag_base<DA>(wm * kWaveM + i * 32 + (lane & 31));
+    const uint32_t base = AL == 0 ? frag_base<true>(wm * kWaveM + i * 32 + (lane & 31))
+                                  : mn_frag_base(wm * kWaveM + i * 32);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) aoff[kk][i] = frag_at<DA>(base, kk);
+    for (int kk = 0; kk < 4; ++kk) aoff[kk][i] = AL == 0 ? frag_at<true>(base, kk) : base + kk * 8192;
   }
 #pragma unroll
   for (int j = 0; j < kFragN; ++j) {
-    const uint32_t base = frag_base<DB>(wn * kWaveN + j * 32 + (lane & 31));
+    const int r = wn * kWaveN + j * 32 + (lane & 31);
+    uint32_t base;
+    if constexpr (!DB)
+      base = frag_base<false>(r);
+    else if constexpr (BL == 0)
+      base = frag_base<true>(r);
+    else
+      base = mn_frag_base(wn * kWaveN + j * 32);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) boff[kk][j] = frag_at<DB>(base, kk);
+    for (int kk = 0; kk < 4; ++kk) {
+      if constexpr (!DB)
+        boff[kk][j] = frag_at<false>(base, kk);
+      else if constexpr (BL == 0)
+        boff[kk][j] = frag_at<true>(base, kk);
+      else
+        boff[kk][j] = base + kk * 8192;
+      moff[kk][j] = (uint32_t)(r * 64 + ((kk ^ ((r >> 2) & 3)) << 4) + (lane >> 5) * 8);
+    }
   }
 
   bf16x8_t fa[2][kFragM], fb[2][kFragN];
-  auto read_frags = [&](int slot, int buf, int kk) {
-    const unsigned char* a = As + buf * ABUF;
-    const unsigned char* b = Bs + buf * BBUF;
+  uint2 mk[2][kFragN];
+  auto read_a = [&](int slot, int buf, int kk, int i) {
+    const unsigned char* p = As + buf * ABUF + aoff[kk][i];
+    if constexpr (AL == 0)
+      fa[slot][i] = *reinterpret_cast<const bf16x8_t*>(p);
+    else
+      fa[slot][i] = tr_frag(p);
+  };
+  // MK: the B fragment's mask bytes too (segment 1 of a DM kernel; segment 2 is never masked)
+  auto read_b = [&](auto mkc, int slot, int buf, int kk, int j) {
+    const unsigned char* p = Bs + buf * BBUF + boff[kk][j];
+    if constexpr (DB && BL == 1)
+      fb[slot][j] = tr_frag(p);
+    else
+      fb[slot][j] = *reinterpret_cast<const bf16x8_t*>(p);
+    if constexpr (decltype(mkc)::value) mk[slot][j] = *reinterpret_cast<const uint2*>(Ms + buf * MBUF + moff[kk][j]);
+  };
+  auto read_frags = [&](auto mkc, int slot, int buf, int kk) {
 #pragma unroll
-    for (int i = 0; i < kFragM; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8_t*>(a + aoff[kk][i]);
+    for (int i = 0; i < kFragM; ++i) read_a(slot, buf, kk, i);
 #pragma unroll
-    for (int j = 0; j < kFragN; ++j) fb[slot][j] = *reinterpret_cast<const bf16x8_t*>(b + boff[kk][j]);
+    for (int j = 0; j < kFragN; ++j) read_b(mkc, slot, buf, kk, j);
+  };
+  auto mfma1 = [&](int slot, int i, int j) {
+    acc[i * kFragN + j] =
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], 0, 0, 0);
+  };
+  auto apply_masks = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j) fb[slot][j] = and_bytes(fb[slot][j], mk[slot][j]);
   };
   auto mfmas = [&](int slot) {
 #pragma unroll
     for (int j = 0; j < kFragN; ++j)
 #pragma unroll
-      for (int i = 0; i < kFragM; ++i)
-        acc[i * kFragN + j] =
-            __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], 0, 0, 0);
+      for (int i = 0; i < kFragM; ++i) mfma1(slot, i, j);
   };
+  using Masked = std::integral_constant<bool, DM>;
+  using Plain = std::integral_constant<bool, false>;
 
-  // Segment 1 copy machinery: DMA for direct operands, registers otherwise.
-  DmaLoader da, db;
-  Loader<T, AL> la;
+  // Copy machinery of segment 1.
+  DmaLoader dak, dbk;
+  DmaLoaderMN dam, dbm;
+  DmaMaskLoader dm;
   Loader<T, BL> lb;
-  Stage<T, kMaskNone> sa;
   Stage<T, MASK> sb;
-  if constexpr (DA)
-    da.init(g.A1, g.lda1, m0, g.M, g.K1);
+  if constexpr (AL == 0)
+    dak.init(g.A1, g.lda1, m0, g.M, g.K1);
   else
-    la.init(g.A1, nullptr, g.lda1, m0, g.M, g.K1, false, kbase);
-  if constexpr (DB)
-    db.init(g.B1, g.ldb1, n0, g.N, g.K1);
+    dam.init(g.A1, g.lda1, m0, g.M, g.K1, kbase);
+  if constexpr (!DB)
+    lb.init(g.B1, g.bmask, g.ldb1, n0, g.N, g.K1, false, kbase);
+  else if constexpr (BL == 0)
+    dbk.init(g.B1, g.ldb1, n0, g.N, g.K1);
   else
-    lb.init(g.B1, MASK != kMaskNone ? g.bmask : nullptr, g.ldb1, n0, g.N, g.K1, MASK == kMaskByte, kbase);
+    dbm.init(g.B1, g.ldb1, n0, g.N, g.K1, kbase);
+  if constexpr (DM) dm.init(g.bmask, g.ldbm, n0, g.N, g.K1);
 
-  auto reg_load = [&](int64_t k0) {  // register-path loads of the stage at k0
-    if constexpr (!DA) la.load(sa, k0);
-    if constexpr (!DB) lb.load(sb, k0);
-  };
-  auto reg_store = [&](int buf) {  // register-path stores into buffer `buf`
-    if constexpr (!DA) {
-      if (AL == 0)
-        store_kc<T, kMaskNone>(sa, reinterpret_cast<T*>(As + buf * ABUF), false, 1.0f);
+  // piece p (0..7) of the DMA copy of the stage at k0 into buffer buf
+  auto dma_piece = [&](int buf, int64_t k0, int p) {
+    if constexpr (AL == 0)
+      dak.issue_one(As_l + buf * ABUF, k0, p);
+    else
+      dam.issue_one(As_l + buf * ABUF, p);
+    if constexpr (DB) {
+      if constexpr (BL == 0)
+        dbk.issue_one(Bs_l + buf * BBUF, k0, p);
       else
-        store_rc<T, kMaskNone>(sa, reinterpret_cast<T*>(As + buf * ABUF), false, 1.0f);
+        dbm.issue_one(Bs_l + buf * BBUF, p);
     }
+    if constexpr (DM) {
+      if (p < 4) dm.issue_one(Ms_l + buf * MBUF, k0, p);
+    }
+  };
+  // the whole copy; TAIL: the stage may end past K (K-contiguous chunks past K read zeros)
+  auto dma_issue = [&](auto tail, int buf, int64_t k0) {
+    constexpr bool TL = decltype(tail)::value;
+    if constexpr (AL == 0)
+      dak.template issue<TL>(As_l + buf * ABUF, k0);
+    else
+      dam.issue(As_l + buf * ABUF);
+    if constexpr (DB) {
+      if constexpr (BL == 0)
+        dbk.template issue<TL>(Bs_l + buf * BBUF, k0);
+      else
+        dbm.issue(Bs_l + buf * BBUF);
+    }
+    if constexpr (DM) dm.template issue<TL>(Ms_l + buf * MBUF, k0);
+  };
+  auto reg_store = [&](int buf) {  // register path (multiplicative mask) into buffer `buf`
     if constexpr (!DB) {
-      if (BL == 0)
+      if constexpr (BL == 0)
         store_kc<T, MASK>(sb, reinterpret_cast<T*>(Bs + buf * BBUF), has_scale, bscale);
       else
         store_rc<T, MASK>(sb, reinterpret_cast<T*>(Bs + buf * BBUF), has_scale, bscale);
     }
   };
-  auto dma_issue = [&](auto tail, int buf, int64_t k0) {
-    constexpr bool TL = decltype(tail)::value;
-    if constexpr (DA) da.template issue<TL>(As + buf * ABUF, k0);
-    if constexpr (DB) db.template issue<TL>(Bs + buf * BBUF, k0);
+  auto reg_load = [&](int64_t k0) {
+    if constexpr (!DB) lb.load(sb, k0);
   };
   using Tail = std::integral_constant<bool, true>;
 
@@ -1089,110 +1269,73 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
   if (nk > 2) reg_load(kbase + 2 * BK);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (nk > 0) read_frags(0, 0, 0);
+  if (nk > 0) {
+    read_frags(Masked{}, 0, 0, 0);
+    if constexpr (DM) apply_masks(0);
+  }
 
   // Steady state: stages s (buffer 0) and s + 1 (buffer 1), each copying a
-  // full stage s + 2 and loading s + 3, with compile-time LDS offsets and the
-  // instruction order fixed (a scheduling barrier after every MFMA):
-  //   k-steps 0..2: the 8 fragment reads of the next k-step after its first 4 MFMAs
+  // full stage s + 2 (and, on the register path, loading s + 3), with
+  // compile-time LDS offsets and the instruction order fixed (a scheduling
+  // barrier after every MFMA):
+  //   k-steps 0..2: the next k-step's fragment reads after MFMAs 0..3
   //   k-step 3: the next stage's first fragment reads after MFMAs 0..3, then
-  //   one eighth of the stage's copies after each of MFMAs 4..11.
-  auto mfma1 = [&](int slot, int i, int j) {
-    acc[i * kFragN + j] =
-        __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], 0, 0, 0);
-  };
-  auto read1 = [&](int slot, int buf, int kk, int f) {  // fragment f: A 0..3, B 4..7
-    if (f < kFragM)
-      fa[slot][f] = *reinterpret_cast<const bf16x8_t*>(As + buf * ABUF + aoff[kk][f]);
-    else
-      fb[slot][f - kFragM] = *reinterpret_cast<const bf16x8_t*>(Bs + buf * BBUF + boff[kk][f - kFragM]);
-  };
+  //   one eighth of the stage's copies after each of MFMAs 4..11
+  //   (DM) after MFMAs 12..15 of every k-step the mask of the other slot's B
+  //   fragments (read at its start), one fragment per MFMA.
   auto kstep = [&](int slot, auto&& after) {
 #pragma unroll
     for (int idx = 0; idx < 16; ++idx) {
       mfma1(slot, idx & 3, idx >> 2);
       after(idx);
+      if constexpr (DM) {
+        if (idx >= 12) fb[slot ^ 1][idx - 12] = and_bytes(fb[slot ^ 1][idx - 12], mk[slot ^ 1][idx - 12]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  V4 mb[8];  // masked B vectors of an N-contiguous masked B (before their transpose)
-  constexpr bool kRegPath = !DA || !DB;
+  auto read_pair = [&](int slot, int buf, int kk, int idx) {  // fragments 2 idx, 2 idx + 1 (A 0..3, B 4..7)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int f = 2 * idx + h;
+      if (f < kFragM)
+        read_a(slot, buf, kk, f);
+      else
+        read_b(Masked{}, slot, buf, kk, f - kFragM);
+    }
+  };
   auto steady = [&](auto bc, int64_t s) {
     constexpr int B = decltype(bc)::value;
     kstep(0, [&](int idx) {
-      if (idx < 4) {
-        read1(1, B, 1, 2 * idx);
-        read1(1, B, 1, 2 * idx + 1);
-      }
+      if (idx < 4) read_pair(1, B, 1, idx);
     });
     kstep(1, [&](int idx) {
-      if (idx < 4) {
-        read1(0, B, 2, 2 * idx);
-        read1(0, B, 2, 2 * idx + 1);
-      }
+      if (idx < 4) read_pair(0, B, 2, idx);
     });
     kstep(0, [&](int idx) {
-      if (idx < 4) {
-        read1(1, B, 3, 2 * idx);
-        read1(1, B, 3, 2 * idx + 1);
-      }
+      if (idx < 4) read_pair(1, B, 3, idx);
     });
-    // this wave's copies into B ^ 1 landed and its k-step 3 fragments are in
-    // registers; without DMA the register loads of stage s + 3 stay in flight
-    if constexpr (DA || DB)
-      __builtin_amdgcn_s_waitcnt(0);
-    else
-      __builtin_amdgcn_s_waitcnt(kWaitLgkmOnly);
+    // this wave's copies into B ^ 1 landed and its k-step 3 fragments are in registers
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const int64_t k2 = kbase + (s + 2) * BK, k3 = kbase + (s + 3) * BK;
     kstep(1, [&](int idx) {
-      if (idx < 4) {  // the next stage's first fragments (buffer B ^ 1)
-        read1(0, B ^ 1, 0, 2 * idx);
-        read1(0, B ^ 1, 0, 2 * idx + 1);
-      }
-      if constexpr (kRegPath) {
-        // register path: mask products of the staged B vectors (2 per MFMA
-        // over MFMAs 0..3), one transposed or masked vector per operand
-        // written to LDS after MFMAs 4..11, then the loads of stage s + 3 and
-        // the DMA copies after MFMAs 12..15 (after every LDS write: a DS
-        // write issued behind an LDS DMA would wait for it)
-        if constexpr (!DB && BL == 1 && MASK != kMaskNone) {
-          if (idx < 4) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-              mb[2 * idx + h] = apply_mask<T, MASK>(sb.v[2 * idx + h], sb.e[2 * idx + h], has_scale, bscale);
+      if (idx < 4) read_pair(0, B ^ 1, 0, idx);  // the next stage's first fragments
+      if (idx >= 4 && idx < 12) {
+        const int p = idx - 4;
+        if constexpr (!DB) {  // register path: one vector written, then its register reloaded
+          if constexpr (BL == 0) {
+            store_kc_one<T, MASK>(sb, reinterpret_cast<T*>(Bs + B * BBUF), p, has_scale, bscale);
+            lb.load_one(sb, k3, p);
           }
         }
-        if (idx >= 4 && idx < 12) {
-          const int p = idx - 4;
-          if constexpr (!DA) write_rc_one(transpose_one(sa.v, p), reinterpret_cast<T*>(As + B * ABUF), p);
-          if constexpr (!DB) {
-            if constexpr (BL == 0)
-              store_kc_one<T, MASK>(sb, reinterpret_cast<T*>(Bs + B * BBUF), p, has_scale, bscale);
-            else if constexpr (MASK != kMaskNone)
-              write_rc_one(transpose_one(mb, p), reinterpret_cast<T*>(Bs + B * BBUF), p);
-            else
-              write_rc_one(transpose_one(sb.v, p), reinterpret_cast<T*>(Bs + B * BBUF), p);
-          }
-        } else if (idx >= 12) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int p = 2 * (idx - 12) + h;
-            if constexpr (DA)
-              da.issue_one(As + B * ABUF, k2, p);
-            else
-              la.load_one(sa, k3, p);
-            if constexpr (DB)
-              db.issue_one(Bs + B * BBUF, k2, p);
-            else
-              lb.load_one(sb, k3, p);
-          }
-        }
-      } else if (idx >= 4 && idx < 12) {  // DMA only: one instruction per operand per MFMA
-        da.issue_one(As + B * ABUF, k2, idx - 4);
-        db.issue_one(Bs + B * BBUF, k2, idx - 4);
+        dma_piece(B, k2, p);
       }
     });
+    if constexpr (!DB && BL == 1) {  // N-contiguous multiplicative mask: block transpose, then reload
+      store_rc<T, MASK>(sb, reinterpret_cast<T*>(Bs + B * BBUF), has_scale, bscale);
+      lb.load(sb, k3);
+    }
   };
   int64_t s = 0;
   for (; s + 5 <= nk; s += 2) {
@@ -1202,65 +1345,70 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
   // The last (up to four) stages, with run-time buffer offsets.
   for (; s < nk; ++s) {
     const int b = static_cast<int>(s & 1);
-    read_frags(1, b, 1);
+    read_frags(Masked{}, 1, b, 1);
     mfmas(0);
-    read_frags(0, b, 2);
+    if constexpr (DM) apply_masks(1);
+    read_frags(Masked{}, 0, b, 2);
     mfmas(1);
-    read_frags(1, b, 3);
+    if constexpr (DM) apply_masks(0);
+    read_frags(Masked{}, 1, b, 3);
     mfmas(0);
+    if constexpr (DM) apply_masks(1);
     if (s + 1 < nk) {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       if (s + 2 < nk) {
         reg_store(b);
         if (s + 3 < nk) reg_load(kbase + (s + 3) * BK);
-        dma_issue(std::integral_constant<bool, true>{}, b, kbase + (s + 2) * BK);
+        dma_issue(Tail{}, b, kbase + (s + 2) * BK);
       }
-      read_frags(0, b ^ 1, 0);
+      read_frags(Masked{}, 0, b ^ 1, 0);
     }
     mfmas(1);
+    if constexpr (DM) apply_masks(0);
   }
 
   // Segment 2 (the SLoRB term A2 . B2^T, a few stages, never masked) through buffer 0.
   if (nk2 > 0) {
-    DmaLoader da2, db2;
-    Loader<T, AL> la2;
+    DmaLoader da2k, db2k;
+    DmaLoaderMN da2m, db2m;
     Loader<T, BL> lb2;
-    if constexpr (DA)
-      da2.init(g.A2, g.lda2, m0, g.M, g.K2);
+    if constexpr (AL == 0)
+      da2k.init(g.A2, g.lda2, m0, g.M, g.K2);
     else
-      la2.init(g.A2, nullptr, g.lda2, m0, g.M, g.K2);
-    if constexpr (DB)
-      db2.init(g.B2, g.ldb2, n0, g.N, g.K2);
-    else
+      da2m.init(g.A2, g.lda2, m0, g.M, g.K2, 0);
+    if constexpr (!DB)
       lb2.init(g.B2, nullptr, g.ldb2, n0, g.N, g.K2);
+    else if constexpr (BL == 0)
+      db2k.init(g.B2, g.ldb2, n0, g.N, g.K2);
+    else
+      db2m.init(g.B2, g.ldb2, n0, g.N, g.K2, 0);
     for (int64_t s2 = 0; s2 < nk2; ++s2) {
       __syncthreads();  // every wave is done with buffer 0
-      if constexpr (DA) {
-        da2.issue<true>(As, s2 * BK);
-      } else {
-        Stage<T, kMaskNone> ta;
-        la2.load(ta, s2 * BK);
-        store_rc<T, kMaskNone>(ta, reinterpret_cast<T*>(As), false, 1.0f);
-      }
-      if constexpr (DB) {
-        db2.issue<true>(Bs, s2 * BK);
-      } else {
+      if constexpr (AL == 0)
+        da2k.issue<true>(As_l, s2 * BK);
+      else
+        da2m.issue(As_l);
+      if constexpr (!DB) {
         Stage<T, kMaskNone> tb;
         lb2.load(tb, s2 * BK);
         if constexpr (BL == 0)
           store_kc<T, kMaskNone>(tb, reinterpret_cast<T*>(Bs), false, 1.0f);
         else
           store_rc<T, kMaskNone>(tb, reinterpret_cast<T*>(Bs), false, 1.0f);
+      } else if constexpr (BL == 0) {
+        db2k.issue<true>(Bs_l, s2 * BK);
+      } else {
+        db2m.issue(Bs_l);
       }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      read_frags(0, 0, 0);
-      read_frags(1, 0, 1);
+      read_frags(Plain{}, 0, 0, 0);
+      read_frags(Plain{}, 1, 0, 1);
       mfmas(0);
-      read_frags(0, 0, 2);
+      read_frags(Plain{}, 0, 0, 2);
       mfmas(1);
-      read_frags(1, 0, 3);
+      read_frags(Plain{}, 1, 0, 3);
       mfmas(0);
       mfmas(1);
     }
@@ -1315,26 +1463,41 @@ constexpr size_t smem_bytes() {
 // bf16 dense B: the direct-to-LDS kernel; its LDS also hosts the epilogue staging.
 template <int AL, int BL, int MASK>
 constexpr size_t smem_bytes_bf16() {
-  constexpr size_t ops = 2ull * 256 * (AL == 0 ? kRowSw : kRowPad) + 2ull * 256 * (BL == 0 && MASK == kMaskNone ? kRowSw : kRowPad);
+  constexpr size_t ops = 2ull * 32768 + 2ull * (MASK != kMaskMul ? 32768 : 256 * kRowPad) +
+                         (MASK == kMaskByte ? 2ull * 256 * 64 : 0);
   constexpr size_t epi = 4ull * 64 * kEpiPitch * sizeof(float);
   return ops > epi ? ops : epi;
 }
 
-template <typename T, int AL, int BL, int MASK>
-int launch_gemm(const GemmArgs& g, hipStream_t st) {
-  static bool attr_set = false;  // per instantiation; host code runs the attribute call once
-  constexpr bool kDirect = sizeof(T) == 2 && BL < 2;
-  auto kern = [] {
-    if constexpr (kDirect)
-      return gemm_bf16_kernel<AL, (BL < 2 ? BL : 0), MASK>;
-    else
-      return gemm_kernel<T, AL, BL, MASK>;
-  }();
-  const size_t smem = kDirect ? smem_bytes_bf16<AL, (BL < 2 ? BL : 0), MASK>() : smem_bytes<T>();
-  if (!attr_set) {
+template <typename K>
+int set_smem(K kern, size_t smem, bool& done) {
+  if (!done) {
     SF_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      static_cast<int>(smem)));
-    attr_set = true;
+    done = true;
+  }
+  return SF_OK;
+}
+
+template <typename T, int AL, int BL, int MASK>
+int launch_gemm(const GemmArgs& g, hipStream_t st) {
+  // bf16 dense B runs the direct-to-LDS kernel unless its byte mask cannot be copied as K-major rows
+  constexpr bool kDirectT = sizeof(T) == 2 && BL < 2;
+  const bool direct = kDirectT && (MASK != kMaskByte || g.dma_mask_ok);
+  static bool attr_direct = false, attr_reg = false;  // per instantiation; host code sets the attribute once
+  void (*kern)(GemmArgs);
+  size_t smem;
+  if constexpr (kDirectT) {
+    if (direct) {
+      kern = gemm_bf16_kernel<AL, (BL < 2 ? BL : 0), MASK>;
+      smem = smem_bytes_bf16<AL, (BL < 2 ? BL : 0), MASK>();
+      if (int rc = set_smem(kern, smem, attr_direct)) return rc;
+    }
+  }
+  if (!direct) {
+    kern = gemm_kernel<T, AL, BL, MASK>;
+    smem = smem_bytes<T>();
+    if (int rc = set_smem(kern, smem, attr_reg)) return rc;
   }
   const int64_t tiles = g.tiles_m * g.tiles_n;
   if (tiles == 0) return SF_OK;
@@ -1419,6 +1582,13 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     SF_CHECK_ARG(d->K1 % 16 == 0, "block-sparse B: K (%lld) must be a multiple of 16", (long long)d->K1);
     SF_CHECK_ARG(d->K1 == 0 || (d->B1 && al16(d->B1)), "block-sparse B: blocks must be 16-byte aligned");
   }
+  if (d->bmask_kmajor) {
+    SF_CHECK_ARG(d->bmask && d->bmask_bytes && d->b_layout == SF_LAYOUT_MN && d->dtype == SF_DTYPE_BF16,
+                 "a K-major mask is a bf16 byte mask of an N-contiguous B");
+    SF_CHECK_ARG(d->ldbm >= d->K1, "ldbm (%lld) < K1 (%lld)", (long long)d->ldbm, (long long)d->K1);
+    SF_CHECK_ARG(al16(d->bmask) && d->ldbm % 16 == 0, "a K-major mask needs 16-byte aligned rows (ldbm %% 16 == 0)");
+    SF_CHECK_ARG((int64_t)d->N * d->ldbm < (int64_t(1) << 31), "K-major mask of 2 GiB or more");
+  }
   if (d->c_blocks) {
     SF_CHECK_ARG(d->c_map && d->M % 16 == 0 && d->N % 16 == 0 && al16(d->c_blocks),
                  "block-sparse C needs its block map, M and N multiples of 16 and 16-byte aligned blocks");
@@ -1482,6 +1652,11 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   g.c_map = d->c_map;
   g.c_map_rows = d->c_map_rows;
   g.c_map_cols = d->c_map_cols;
+  g.bmask_kmajor = d->bmask_kmajor != 0;
+  g.ldbm = d->b_layout == SF_LAYOUT_K ? d->ldb1 : (d->bmask_kmajor ? d->ldbm : d->ldb1);
+  // the direct bf16 kernel copies a byte mask 16 bytes per lane from K-major rows
+  g.dma_mask_ok = d->bmask && d->bmask_bytes && al16(d->bmask) && g.ldbm % 16 == 0 &&
+                  (d->b_layout == SF_LAYOUT_K || g.bmask_kmajor);
   g.tiles_m = ceil_div(d->M, kTileM);
   g.tiles_n = ceil_div(d->N, kTileN);
   g.splits = 1;

@@ -1271,3 +1271,61 @@ extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, in
 #undef SF_LAUNCH_EFF
   return launch_status("sf_effective_mask");
 }
+
+// ---------------------------------------------------------------------------
+// Transpose of a byte mask ([rows, cols] -> [cols, rows]): the K-major byte
+// mask of the input-gradient GEMM (dx = dy (W.E), whose B operand is W read
+// along its columns).  64 x 64 byte tiles through LDS, 4-byte words in and out.
+// ---------------------------------------------------------------------------
+namespace sf {
+namespace {
+__global__ void __launch_bounds__(256) transpose_u8_kernel(const uint8_t* __restrict__ src, int64_t rows, int64_t cols,
+                                                           uint8_t* __restrict__ dst, bool vec) {
+  __shared__ uint32_t tile[64][17];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = t / 16 + 16 * j, w = t % 16;
+    const int64_t gr = r0 + r, gc = c0 + 4 * w;
+    uint32_t v = 0;
+    if (gr < rows) {
+      if (vec && gc + 4 <= cols) {
+        v = *reinterpret_cast<const uint32_t*>(src + gr * cols + gc);
+      } else {
+        for (int b = 0; b < 4; ++b)
+          if (gc + b < cols) v |= static_cast<uint32_t>(src[gr * cols + gc + b]) << (8 * b);
+      }
+    }
+    tile[r][w] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = t / 16 + 16 * j, w = t % 16;  // output row c0 + c, output bytes of input rows 4w .. 4w + 3
+    const int64_t orow = c0 + c, ocol = r0 + 4 * w;
+    if (orow >= cols) continue;
+    uint32_t v = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) v |= ((tile[4 * w + b][c >> 2] >> (8 * (c & 3))) & 0xffu) << (8 * b);
+    if (vec && ocol + 4 <= rows) {
+      *reinterpret_cast<uint32_t*>(dst + orow * rows + ocol) = v;
+    } else {
+      for (int b = 0; b < 4; ++b)
+        if (ocol + b < rows) dst[orow * rows + ocol + b] = static_cast<uint8_t>(v >> (8 * b));
+    }
+  }
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" int sf_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst, void* stream) {
+  SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  if (rows == 0 || cols == 0) return SF_OK;
+  SF_CHECK_ARG(src && dst, "null tensor");
+  SF_CHECK_ARG(ceil_div(cols, 64) < (1ll << 31) && ceil_div(rows, 64) < 65536, "transpose grid too large");
+  const bool vec = rows % 4 == 0 && cols % 4 == 0 && aligned(src, 4) && aligned(dst, 4);
+  dim3 grid(static_cast<unsigned>(ceil_div(cols, 64)), static_cast<unsigned>(ceil_div(rows, 64)));
+  transpose_u8_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(src, rows, cols, dst, vec);
+  return launch_status("sf_transpose_u8");
+}

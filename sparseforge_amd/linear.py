@@ -33,15 +33,18 @@ def _vec(dtype: torch.dtype) -> int:
 
 
 def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=None, bscale=1.0, bias=None,
-         emask=None, dw=None, decay=0.0, out=None, out_dtype=None, accumulate=False) -> torch.Tensor:
+         emask=None, dw=None, decay=0.0, out=None, out_dtype=None, accumulate=False, bmask_t=None) -> torch.Tensor:
     """C[M, N] = A1 . B1'^T (+ A2 . B2^T) on the device.
 
     a_layout: L.LAYOUT_K (A1 is [M, K]) or L.LAYOUT_MN (A1 is [K, M]);
     b_layout: L.LAYOUT_K (B1 is [N, K]) or L.LAYOUT_MN (B1 is [K, N]).
     bmask: effective mask of B1 in B1's dtype (multiplied in), or a uint8
     and-mask (0x00 / 0xFF per element) for a 0/1 mask.
+    bmask_t: optional K-major copy [N, K] of a uint8 bmask of an N-contiguous
+    B1 (transpose_u8(bmask)); the bf16 kernel then copies the mask with the
+    weight tile instead of staging both through registers.
     """
-    dev = L.require_device(A1, B1, A2, B2, bmask, bias, emask, dw, out)
+    dev = L.require_device(A1, B1, A2, B2, bmask, bias, emask, dw, out, bmask_t)
     dt = A1.dtype
 
     def _shape(t, want, name):
@@ -83,6 +86,12 @@ def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=
         d.lda2, d.ldb2 = A2.shape[1], B2.shape[1]
     d.bmask = L.ptr(bmask)
     d.bmask_bytes = int(bmask_bytes)
+    if (bmask_t is not None and bmask_bytes and b_layout == L.LAYOUT_MN and dt == torch.bfloat16
+            and K1 % 16 == 0 and bmask_t.data_ptr() % 16 == 0):
+        _shape(bmask_t, (N, K1), "bmask_t")
+        if bmask_t.dtype != torch.uint8:
+            raise TypeError("gemm: bmask_t must be a uint8 and-mask")
+        d.bmask, d.bmask_kmajor, d.ldbm = L.ptr(bmask_t), 1, K1
     d.bscale = float(bscale)
     d.C, d.ldc, d.c_dtype = L.ptr(out), out.shape[1], L.dtype_code(out)
     if bias is not None:
@@ -141,6 +150,18 @@ def effective_mask(mask: torch.Tensor, dtype: torch.dtype, mode: str, hx: float,
     return eff
 
 
+def transpose_u8(E: torch.Tensor) -> torch.Tensor:
+    """[rows, cols] uint8 -> its transpose [cols, rows] (sf_transpose_u8)."""
+    dev = L.require_device(E)
+    if E.dtype != torch.uint8 or E.dim() != 2:
+        raise TypeError("transpose_u8 expects a 2-D uint8 tensor")
+    out = torch.empty(E.shape[1], E.shape[0], dtype=torch.uint8, device=dev)
+    with _prof.region("sf_transpose_u8", 2 * E.numel(), "B", dev):
+        L.check(L.lib().sf_transpose_u8(L.ptr(E), E.shape[0], E.shape[1], L.ptr(out), L.stream(dev)),
+                "sf_transpose_u8")
+    return out
+
+
 def _as_values(E: torch.Tensor | None, dt: torch.dtype) -> torch.Tensor | None:
     """A byte and-mask as 0/1 values of dtype dt (for epilogue products); other masks unchanged."""
     if E is not None and E.dtype == torch.uint8:
@@ -179,10 +200,13 @@ class _MaskedLinearBackward(torch.autograd.Function):
         # written out explicitly in backward(), so the cached copy is detached.
         z = (z_fwd if z_fwd is not None else mm_nt(x, P)) if has_slorb else None
         dz = mm_nn(gy, S) if has_slorb else None
+        # a byte mask is read K-major beside the transposed weight tile of dx = gy (W.E)
+        E_t = transpose_u8(E) if E is not None and E.dtype == torch.uint8 and W.dtype == torch.bfloat16 else None
         if has_slorb:
-            dx = mm_nn(gy, W, bmask=E, A2=dz, B2=P, K2=P.shape[0])
+            dx = mm_nn(gy, W, bmask=E, bmask_t=E_t, A2=dz, B2=P, K2=P.shape[0])
         else:
-            dx = mm_nn(gy, W, bmask=E)
+            dx = mm_nn(gy, W, bmask=E, bmask_t=E_t)
+        del E_t
         if decay != 0.0:
             dW = mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay)
         else:

@@ -89,6 +89,35 @@ def test_gemm_byte_and_mask(cuda_device, dtype, tol, shape):
     got2 = lin.mm_nn(d(G), d(B), bmask=d(E8))
     ref2 = G.double() @ (B.double() * keep.double())
     assert rel_err(got2, ref2) < tol
+    # the same with the mask also given K-major ([K, N] here: B's columns are the GEMM's n)
+    got3 = lin.mm_nn(d(G), d(B), bmask=d(E8), bmask_t=lin.transpose_u8(d(E8)))
+    assert rel_err(got3, ref2) < tol
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (3, 5), (130, 67), (4096, 11008), (11008, 4096), (1, 1000)])
+def test_transpose_u8_exact(cuda_device, shape):
+    L, lin = _lin()
+    g = torch.Generator().manual_seed(shape[0] * 7 + shape[1])
+    E = torch.randint(0, 256, shape, generator=g, dtype=torch.int32).to(torch.uint8)
+    got = lin.transpose_u8(E.to(cuda_device)).cpu()
+    assert torch.equal(got, E.t().contiguous())
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 768, 1024), (300, 272, 208), (1024, 4096, 11008)])
+def test_gemm_input_grad_kmajor_mask(cuda_device, M, N, K):
+    """dx = G (W.E) with the byte mask copied K-major (bf16 direct kernel, transposed weight reads)."""
+    L, lin = _lin()
+    g = torch.Generator().manual_seed(M + N + K)
+    G = torch.randn(M, K, generator=g).bfloat16()
+    W = torch.randn(K, N, generator=g).bfloat16()   # [out = K, in = N]
+    keep = torch.rand(K, N, generator=g) < 0.5
+    E8 = keep.to(torch.uint8) * 255
+    d = lambda t: t.to(cuda_device)
+    got = lin.mm_nn(d(G), d(W), bmask=d(E8), bmask_t=lin.transpose_u8(d(E8)))
+    ref = G.double() @ (W.double() * keep.double())
+    assert rel_err(got, ref) < 2e-2
+    plain = lin.mm_nn(d(G), d(W))
+    assert rel_err(plain, G.double() @ W.double()) < 2e-2
 
 
 @pytest.mark.parametrize("mdt", [torch.float32, torch.bfloat16])
