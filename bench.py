@@ -151,15 +151,24 @@ def mask_params(L, rows, cols, temperature):
     return p
 
 
-def mask_step(torch, L, K, arena, step: int, flips, sample_idx):
+def mask_step(torch, L, K, arena, step: int, flips, sample_idx, overlap: bool = True):
+    """One mask update of every linear of the arena.  overlap: the layers' chains run on side
+    streams (the LayerPipeline that calculate_model_mask uses); otherwise one after another on the
+    current stream (used to time each kernel alone)."""
+    import contextlib
+
     temperature = 1.0 * (0.01 ** (min(step, 9) / 9.0))
+    pipe = K.LayerPipeline(arena[0][0].device) if overlap else None
     for W, H, M in arena:
         rows, cols = W.shape
         p = mask_params(L, rows, cols, temperature)
         ops = K.MaskOperands(weight=W, mask=M, hessian=H)
-        stats = K.score_stats(p, ops)
-        tau = K.tau_quantile(p, ops, stats, 0.5, sample_idx[(rows, cols)])
-        K.update_mask(p, ops, stats, tau, flips)
+        with pipe.next() if pipe else contextlib.nullcontext():
+            stats = K.score_stats(p, ops)
+            tau = K.tau_quantile(p, ops, stats, 0.5, sample_idx[(rows, cols)])
+            K.update_mask(p, ops, stats, tau, flips)
+    if pipe:
+        pipe.join()
 
 
 # ---------------------------------------------------------------------------
@@ -389,13 +398,16 @@ def main(argv=None) -> int:
     mask_step(torch, L, K, arena, 0, flips, sample_idx)  # warmup
     torch.cuda.synchronize()
     log(f"mask arena: {n_params / 1e9:.3f} G params; timing {a.mask_steps} updates")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(a.mask_steps):
+        mask_step(torch, L, K, arena, s, flips, sample_idx)
+    torch.cuda.synchronize()
+    mel = time.perf_counter() - t0
+    # per-kernel launch times from one more update with the layers one after another: overlapping
+    # kernels share the GPU and their individual durations would not describe either kernel
     with prof.kernel_timer() as mt:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for s in range(a.mask_steps):
-            mask_step(torch, L, K, arena, s, flips, sample_idx)
-        torch.cuda.synchronize()
-        mel = time.perf_counter() - t0
+        mask_step(torch, L, K, arena, a.mask_steps, flips, sample_idx, overlap=False)
     ms_ = mt.summary()
     mask_gbs = MASK_BYTES_PER_PARAM * n_params * a.mask_steps / mel / 1e9
     up = ms_["sf_update_mask"]

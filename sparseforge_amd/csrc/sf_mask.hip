@@ -98,17 +98,50 @@ struct Group {
   bool full;               // n == 4 (a complete N:M group)
 };
 
-__device__ __forceinline__ Group group_at(int64_t g, int64_t cols, int64_t gpr) {
-  Group G;
-  G.row = g / gpr;
-  int64_t gc = g - G.row * gpr;
-  G.col = gc * 4;
-  G.elem = G.row * cols + G.col;
-  int64_t rem = cols - G.col;
-  G.n = rem >= 4 ? 4 : static_cast<int>(rem);
-  G.full = G.n == 4;
-  return G;
-}
+// Grid-stride walk over the groups of a [rows, cols] matrix (gpr groups per
+// row).  The row / group-column / element of the current group are advanced
+// incrementally, so the loop does no 64-bit division (two per thread, once).
+struct GroupWalk {
+  int64_t gi, groups, stride;
+  int64_t row, gc, elem;   // current group
+  int64_t gpr, cols;
+  int64_t sdiv, smod;      // stride = sdiv * gpr + smod
+  int64_t estep, ewrap;    // element step per stride, correction when gc wraps
+  __device__ __forceinline__ GroupWalk(int64_t groups_, int64_t cols_, int64_t gpr_)
+      : groups(groups_), gpr(gpr_), cols(cols_) {
+    gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    stride = (int64_t)gridDim.x * blockDim.x;
+    row = gi / gpr;
+    gc = gi - row * gpr;
+    elem = row * cols + gc * 4;
+    sdiv = stride / gpr;
+    smod = stride - sdiv * gpr;
+    estep = sdiv * cols + smod * 4;
+    ewrap = cols - gpr * 4;
+  }
+  __device__ __forceinline__ bool live() const { return gi < groups; }
+  __device__ __forceinline__ void next() {
+    gi += stride;
+    row += sdiv;
+    gc += smod;
+    elem += estep;
+    if (gc >= gpr) {
+      gc -= gpr;
+      ++row;
+      elem += ewrap;
+    }
+  }
+  __device__ __forceinline__ Group group() const {
+    Group G;
+    G.row = row;
+    G.col = gc * 4;
+    G.elem = elem;
+    const int64_t rem = cols - G.col;
+    G.n = rem >= 4 ? 4 : static_cast<int>(rem);
+    G.full = G.n == 4;
+    return G;
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Score of one element (legacy/sparse_modeling.py:1041-1079).  w, h, a are the
@@ -120,33 +153,53 @@ struct ScoreSpec {
   float eps, movement_temp;
 };
 
+// Rounding to a compile-time dtype (the dtypes of W, H and the scores are
+// template parameters of the hot kernels, so the f32 cases cost nothing).
+template <int DT>
+__device__ __forceinline__ float rndc(float x) {
+  if constexpr (DT == SF_DTYPE_BF16)
+    return round_bf16(x);
+  else
+    return x;
+}
+
+template <int WD, int HD>
 __device__ __forceinline__ float score_of(const ScoreSpec& s, float w, float h, float a) {
+  constexpr int PWH = (WD == SF_DTYPE_F32 || HD == SF_DTYPE_F32) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
   switch (s.metric) {
     case SF_METRIC_HESSIAN_OBD: {  // (H + eps) * (W * W)
-      float hp = rnd(h + s.eps, s.h_dtype);
-      float ww = rnd(w * w, s.w_dtype);
-      return rnd(hp * ww, promote(s.h_dtype, s.w_dtype));
+      float hp = rndc<HD>(h + s.eps);
+      float ww = rndc<WD>(w * w);
+      return rndc<PWH>(hp * ww);
     }
     case SF_METRIC_HESSIAN_RATIO: {  // |W| / sqrt(H + eps)
-      float hp = rnd(h + s.eps, s.h_dtype);
-      float sq = rnd(sqrtf(hp), s.h_dtype);
-      return rnd(fabsf(w) / sq, promote(s.h_dtype, s.w_dtype));
+      float hp = rndc<HD>(h + s.eps);
+      float sq = rndc<HD>(sqrtf(hp));
+      return rndc<PWH>(fabsf(w) / sq);
     }
     case SF_METRIC_HESSIAN:
       return h;
     case SF_METRIC_WANDA: {  // |W| * sqrt(scaler + eps)
       float sp = rnd(a + s.eps, s.aux_dtype);
       float sq = rnd(sqrtf(sp), s.aux_dtype);
-      return rnd(fabsf(w) * sq, promote(s.aux_dtype, s.w_dtype));
+      return rnd(fabsf(w) * sq, promote(s.aux_dtype, WD));
     }
     case SF_METRIC_MOVEMENT: {  // |W * g| / max(temperature, eps)
-      int pd = promote(s.w_dtype, s.aux_dtype);
+      int pd = promote(WD, s.aux_dtype);
       float t = fabsf(rnd(w * a, pd));
       return rnd(t / s.movement_temp, pd);
     }
     default:  // magnitude
       return fabsf(w);
   }
+}
+// Run-time dtype variant (the sampled gather of the tau selection).
+__device__ __forceinline__ float score_of_rt(const ScoreSpec& s, float w, float h, float a) {
+  if (s.w_dtype == SF_DTYPE_F32)
+    return s.h_dtype == SF_DTYPE_F32 ? score_of<SF_DTYPE_F32, SF_DTYPE_F32>(s, w, h, a)
+                                     : score_of<SF_DTYPE_F32, SF_DTYPE_BF16>(s, w, h, a);
+  return s.h_dtype == SF_DTYPE_F32 ? score_of<SF_DTYPE_BF16, SF_DTYPE_F32>(s, w, h, a)
+                                   : score_of<SF_DTYPE_BF16, SF_DTYPE_BF16>(s, w, h, a);
 }
 
 // Gather the operands of a group and compute the 4 scores.
@@ -163,7 +216,7 @@ __device__ __forceinline__ void group_scores(const ScoreSpec& s, const void* W, 
       load4_any(aux, s.aux_dtype, g.elem, g.n, vec, a);  // grad_ema [rows, cols]
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sc[j] = j < g.n ? score_of(s, w[j], h[j], a[j]) : 0.0f;
+  for (int j = 0; j < 4; ++j) sc[j] = j < g.n ? score_of<WD, HD>(s, w[j], h[j], a[j]) : 0.0f;
 }
 
 __device__ __forceinline__ float score_at(const ScoreSpec& s, const void* W, const void* H, const void* aux,
@@ -172,7 +225,7 @@ __device__ __forceinline__ float score_at(const ScoreSpec& s, const void* W, con
   float h = H ? load_as_f32(H, e, s.h_dtype) : 0.0f;
   float a = 0.0f;
   if (aux) a = load_as_f32(aux, s.metric == SF_METRIC_WANDA ? e % cols : e, s.aux_dtype);
-  return score_of(s, w, h, a);
+  return score_of_rt(s, w, h, a);
 }
 
 ScoreSpec make_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_dtype) {
@@ -190,6 +243,23 @@ ScoreSpec make_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_d
 // z-normalised score in the score dtype: ((s - mu) / sigma).to(score dtype)  (:1085-1088)
 __device__ __forceinline__ float znorm(float s, float mu, float sigma, int score_dtype) {
   return rnd((s - mu) / sigma, score_dtype);
+}
+// a / b correctly rounded, given y = RN(1 / b): q = RN(a y), r = a - b q (exact
+// with an FMA), RN(q + r y) is RN(a / b) when nothing under- or overflows
+// (P. Markstein, IA-64 and Elementary Functions, 2000, thm. 8.10).  The rare
+// operands where that can fail take the IEEE division instead.
+__device__ __forceinline__ float div_by(float a, float b, float y) {
+  const float q = a * y;
+  const float r = fmaf(-b, q, a);
+  float d = fmaf(r, y, q);
+  // outside these ranges r = a - b q may be inexact (subnormal) or q may overflow;
+  // zeros also go here so that the sign of a zero quotient is IEEE's
+  if (!(fabsf(a) > 0x1p-75f && fabsf(q) < 0x1p+100f && fabsf(y) > 0x1p-100f)) d = a / b;
+  return d;
+}
+template <int SD>
+__device__ __forceinline__ float znorm_t(float s, float mu, float sigma, float rsigma) {
+  return rndc<SD>(div_by(s - mu, sigma, rsigma));
 }
 
 // ---------------------------------------------------------------------------
@@ -213,9 +283,8 @@ template <int SD, int OD>
 __global__ void __launch_bounds__(kBlock) hard_mask_kernel(const void* __restrict__ soft, void* __restrict__ hard,
                                                            int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                            int kind, int n_keep) {
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     float v[4], o[4];
     load4<SD>(soft, g.elem, g.n, vec && g.full, v);
     hard_of_group(v, g, kind, n_keep, o);
@@ -242,9 +311,8 @@ __global__ void __launch_bounds__(kBlock) flip_count_kernel(const void* __restri
                                                             int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                             int kind, int n_keep, int64_t* flips) {
   int64_t cnt = 0;
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     float a[4], b[4], ha[4], hb[4];
     load4<DT>(prev, g.elem, g.n, vec && g.full, a);
     load4<DT>(now, g.elem, g.n, vec && g.full, b);
@@ -260,7 +328,7 @@ __global__ void __launch_bounds__(kBlock) flip_count_kernel(const void* __restri
 // Score statistics: per-workgroup f64 partial sums, then one workgroup folds
 // them in a fixed order (deterministic for a fixed grid).
 // ---------------------------------------------------------------------------
-constexpr int kStatsGrid = 1024;
+constexpr int kStatsGrid = 4096;
 
 __device__ __forceinline__ void block_sum2_f64(double a, double b, double* out_a, double* out_b) {
   __shared__ double ra[kBlock / 64], rb[kBlock / 64];
@@ -291,9 +359,8 @@ __global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, cons
                                                                int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                                double* partial) {
   double sum = 0.0, sq = 0.0;
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     float sc[4];
     group_scores<WD, HD>(s, W, H, aux, g, vec && g.full, cols, sc);
 #pragma unroll
@@ -516,26 +583,28 @@ struct GateSpec {
   int has_frozen;
   int mask_dtype, frozen_dtype;
   float denom;        // T + 1e-8 in f32
+  float rdenom;       // RN(1 / denom)
   float beta_struct;  // 0 disables the mix
   float one_minus_beta;
 };
 
 // G of one group (compute_gate_target, :1083-1229).  mprev / frz: current mask
 // and frozen flags of the group (frz only read when has_frozen).
+// rsigma = RN(1 / sigma) (computed once per thread); gs.rdenom = RN(1 / denom).
+template <int SD>
 __device__ __forceinline__ void gate_of_group(const GateSpec& gs, const float sc[4], const Group& g, float mu,
-                                              float sigma, float tau, const float mprev[4], const float frz[4],
-                                              float G[4]) {
-  const int sd = gs.s.score_dtype;
+                                              float sigma, float rsigma, float tau, const float mprev[4],
+                                              const float frz[4], float G[4]) {
   float z[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) z[j] = znorm(sc[j], mu, sigma, sd);
+  for (int j = 0; j < 4; ++j) z[j] = znorm_t<SD>(sc[j], mu, sigma, rsigma);
   if (gs.gate == SF_GATE_UNSTRUCTURED) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) G[j] = rnd(sigmoidf_((z[j] - tau) / gs.denom), sd);
+    for (int j = 0; j < 4; ++j) G[j] = rndc<SD>(sigmoidf_(div_by(z[j] - tau, gs.denom, gs.rdenom)));
   } else if (gs.gate == SF_GATE_STRUCTURED) {
     float tg = kth_largest4(z, gs.n_keep);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) G[j] = rnd(sigmoidf_((z[j] - tg) / gs.denom), sd);
+    for (int j = 0; j < 4; ++j) G[j] = rndc<SD>(sigmoidf_(div_by(z[j] - tg, gs.denom, gs.rdenom)));
   } else {  // structured exact
     uint32_t keep = topk4_keep(z, gs.n_keep);
 #pragma unroll
@@ -546,17 +615,17 @@ __device__ __forceinline__ void gate_of_group(const GateSpec& gs, const float sc
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float t = g.full ? (((keep >> j) & 1u) ? 1.0f : 0.0f) : G[j];
-      G[j] = rnd(gs.one_minus_beta * G[j] + gs.beta_struct * t, sd);
+      G[j] = rndc<SD>(gs.one_minus_beta * G[j] + gs.beta_struct * t);
     }
   }
   if (gs.has_frozen) {  // G[frozen] = mask[frozen]  (:1227-1229)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (frz[j] != 0.0f) G[j] = rnd(mprev[j], sd);
+      if (frz[j] != 0.0f) G[j] = rndc<SD>(mprev[j]);
   }
 }
 
-template <int WD, int HD>
+template <int WD, int HD, int SD>
 __global__ void __launch_bounds__(kBlock) gate_target_kernel(GateSpec gs, const void* __restrict__ W,
                                                              const void* __restrict__ H, const void* __restrict__ aux,
                                                              const void* __restrict__ mask,
@@ -565,11 +634,10 @@ __global__ void __launch_bounds__(kBlock) gate_target_kernel(GateSpec gs, const 
                                                              const float* __restrict__ tau_p, void* __restrict__ Gout,
                                                              int g_dtype, int64_t cols, int64_t groups, int64_t gpr,
                                                              bool vec) {
-  const float mu = stats[0], sigma = stats[1];
+  const float mu = stats[0], sigma = stats[1], rsigma = 1.0f / sigma;
   const float tau = tau_p ? *tau_p : 0.0f;
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     const bool v = vec && g.full;
     float sc[4], mp[4] = {0, 0, 0, 0}, fz[4] = {0, 0, 0, 0}, G[4];
     group_scores<WD, HD>(gs.s, W, H, aux, g, v, cols, sc);
@@ -577,7 +645,7 @@ __global__ void __launch_bounds__(kBlock) gate_target_kernel(GateSpec gs, const 
       load4_any(frozen, gs.frozen_dtype, g.elem, g.n, v, fz);
       load4_any(mask, gs.mask_dtype, g.elem, g.n, v, mp);
     }
-    gate_of_group(gs, sc, g, mu, sigma, tau, mp, fz, G);
+    gate_of_group<SD>(gs, sc, g, mu, sigma, rsigma, tau, mp, fz, G);
     if (g_dtype == SF_DTYPE_F32)
       store4<SF_DTYPE_F32>(Gout, g.elem, g.n, v, G);
     else
@@ -600,23 +668,22 @@ struct UpdateSpec {
 // Penalty pull toward a target, then clamp (:1291-1573), and the
 // multiplicative binarisation push (:1576-1590).  mp: the mask the penalty
 // compares against; sd: dtype of G.
-template <int MD>
-__device__ __forceinline__ void pull_and_push(const UpdateSpec& us, int sd, const Group& g, const float mp[4],
-                                              float G[4]) {
+template <int MD, int SD>
+__device__ __forceinline__ void pull_and_push(const UpdateSpec& us, const Group& g, const float mp[4], float G[4]) {
   if (us.penalty != SF_PENALTY_NONE) {
     if (us.penalty == SF_PENALTY_MID) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float pg = rnd(rnd(1.0f - 2.0f * mp[j], MD), sd);
-        G[j] = rnd(G[j] - rnd(us.pen_coef * pg, sd), sd);
+        float pg = rndc<SD>(rndc<MD>(1.0f - 2.0f * mp[j]));
+        G[j] = rndc<SD>(G[j] - rndc<SD>(us.pen_coef * pg));
       }
     } else {  // nm_2_4 / structured_topn: target = topN(G) on full groups, 1 on the tail
       uint32_t keep = g.full ? topk4_keep(G, us.pen_n) : 0xfu;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float t = ((keep >> j) & 1u) ? 1.0f : 0.0f;
-        float delta = rnd(rnd(mp[j], sd) - t, sd);
-        G[j] = rnd(G[j] - rnd(us.pen_coef * delta, sd), sd);
+        float delta = rndc<SD>(rndc<SD>(mp[j]) - t);
+        G[j] = rndc<SD>(G[j] - rndc<SD>(us.pen_coef * delta));
       }
     }
 #pragma unroll
@@ -626,9 +693,9 @@ __device__ __forceinline__ void pull_and_push(const UpdateSpec& us, int sd, cons
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (G[j] < 0.5f)
-        G[j] = rnd(G[j] * us.bin_lo, sd);
+        G[j] = rndc<SD>(G[j] * us.bin_lo);
       else if (G[j] > 0.5f)
-        G[j] = rnd(G[j] * us.bin_hi, sd);
+        G[j] = rndc<SD>(G[j] * us.bin_hi);
     }
   }
 }
@@ -655,7 +722,7 @@ __device__ __forceinline__ int flips_of(const float a[4], const float b[4], cons
   return c;
 }
 
-template <int WD, int HD, int MD>
+template <int WD, int HD, int MD, int SD>
 __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, const void* __restrict__ W,
                                                              const void* __restrict__ H, const void* __restrict__ aux,
                                                              void* __restrict__ mask, void* __restrict__ frozen,
@@ -663,20 +730,18 @@ __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, cons
                                                              const float* __restrict__ tau_p, int64_t cols,
                                                              int64_t groups, int64_t gpr, bool vec, int64_t* flips) {
   const GateSpec& gs = us.gs;
-  const int sd = gs.s.score_dtype;
-  const float mu = stats[0], sigma = stats[1];
+  const float mu = stats[0], sigma = stats[1], rsigma = 1.0f / sigma;
   const float tau = tau_p ? *tau_p : 0.0f;
   int64_t cnt = 0;
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     const bool v = vec && g.full;
     float sc[4], mp[4], fz[4] = {0, 0, 0, 0}, G[4];
     group_scores<WD, HD>(gs.s, W, H, aux, g, v, cols, sc);
     load4<MD>(mask, g.elem, g.n, v, mp);
     if (gs.has_frozen) load4_any(frozen, gs.frozen_dtype, g.elem, g.n, v, fz);
-    gate_of_group(gs, sc, g, mu, sigma, tau, mp, fz, G);
-    pull_and_push<MD>(us, sd, g, mp, G);
+    gate_of_group<SD>(gs, sc, g, mu, sigma, rsigma, tau, mp, fz, G);
+    pull_and_push<MD, SD>(us, g, mp, G);
     float mn[4];
     ema_of<MD>(us, mp, G, mn);
     // freeze snaps and flags (:1621-1642)
@@ -720,9 +785,8 @@ __global__ void __launch_bounds__(kBlock) joint_scores_kernel(ScoreSpec sg, cons
                                                               const void* __restrict__ Hu, const void* __restrict__ au,
                                                               void* __restrict__ S, int s_dtype, int64_t cols,
                                                               int64_t groups, int64_t gpr, bool vec) {
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     const bool v = vec && g.full;
     float a[4], b[4], o[4];
     group_scores<WD, HD>(sg, Wg, Hg, ag, g, v, cols, a);
@@ -744,22 +808,20 @@ __global__ void __launch_bounds__(kBlock) glu_update_kernel(UpdateSpec us, const
                                                             const float* __restrict__ tau_p, int up_kind, int up_n,
                                                             int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                             int64_t* flips_g, int64_t* flips_u) {
-  const GateSpec& gs = us.gs;
-  const int sd = gs.s.score_dtype;  // the mask dtype: z and G live in it (:541-545)
-  const float mu = stats[0], sigma = stats[1];
+  const GateSpec& gs = us.gs;  // z and G live in the mask dtype (:541-545)
+  const float mu = stats[0], sigma = stats[1], rsigma = 1.0f / sigma;
   const float tau = tau_p ? *tau_p : 0.0f;
   int64_t cg = 0, cu = 0;
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     const bool v = vec && g.full;
     float sc[4], pg[4], pu[4], fz[4] = {0, 0, 0, 0}, G[4], ng[4], nu[4];
     load4<SD>(S, g.elem, g.n, v, sc);
     load4<MD>(mask_g, g.elem, g.n, v, pg);
     load4<MD>(mask_u, g.elem, g.n, v, pu);
     if (gs.has_frozen) load4_any(frozen_g, gs.frozen_dtype, g.elem, g.n, v, fz);
-    gate_of_group(gs, sc, g, mu, sigma, tau, pg, fz, G);
-    pull_and_push<MD>(us, sd, g, pg, G);  // the penalty compares against the gate mask (:615-641)
+    gate_of_group<MD>(gs, sc, g, mu, sigma, rsigma, tau, pg, fz, G);
+    pull_and_push<MD, MD>(us, g, pg, G);  // the penalty compares against the gate mask (:615-641)
     ema_of<MD>(us, pg, G, ng);
     ema_of<MD>(us, pu, G, nu);
     store4<MD>(mask_g, g.elem, g.n, v, ng);
@@ -981,6 +1043,7 @@ int make_gate_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_dt
   gs->mask_dtype = mask_dtype;
   gs->frozen_dtype = frozen_dtype;
   gs->denom = p->temperature + 1e-8f;
+  gs->rdenom = 1.0f / gs->denom;  // IEEE f32 division on the host: correctly rounded
   gs->beta_struct = p->beta_struct;
   gs->one_minus_beta = static_cast<float>(1.0 - static_cast<double>(p->beta_struct));
   return SF_OK;
@@ -1046,9 +1109,14 @@ extern "C" int sf_gate_target(const sf_mask_params* p, const void* W, int w_dtyp
                    (!aux || aligned(aux, 4 * esize(aux_dtype)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int grid = elementwise_grid(groups, kBlock);
-  SF_DISPATCH_WH(w_dtype, h_dtype,
-                 gate_target_kernel<WD_, HD_><<<grid, kBlock, 0, st>>>(gs, W, H, aux, mask, frozen, stats, tau, G,
-                                                                      g_dtype, p->cols, groups, gpr, vec));
+  if (p->score_dtype == SF_DTYPE_F32)
+    SF_DISPATCH_WH(w_dtype, h_dtype,
+                   gate_target_kernel<WD_, HD_, SF_DTYPE_F32><<<grid, kBlock, 0, st>>>(
+                       gs, W, H, aux, mask, frozen, stats, tau, G, g_dtype, p->cols, groups, gpr, vec));
+  else
+    SF_DISPATCH_WH(w_dtype, h_dtype,
+                   gate_target_kernel<WD_, HD_, SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(
+                       gs, W, H, aux, mask, frozen, stats, tau, G, g_dtype, p->cols, groups, gpr, vec));
   return launch_status("sf_gate_target");
 }
 
@@ -1074,14 +1142,22 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
                    (!aux || aligned(aux, 4 * esize(aux_dtype)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int grid = elementwise_grid(groups, kBlock);
-#define SF_LAUNCH_UPD(MDT)                                                                                   \
-  SF_DISPATCH_WH(w_dtype, h_dtype,                                                                           \
-                 update_mask_kernel<WD_, HD_, MDT><<<grid, kBlock, 0, st>>>(us, W, H, aux, mask, frozen, stats, \
-                                                                            tau, p->cols, groups, gpr, vec, flips))
-  if (mask_dtype == SF_DTYPE_F32)
-    SF_LAUNCH_UPD(SF_DTYPE_F32);
-  else
-    SF_LAUNCH_UPD(SF_DTYPE_BF16);
+#define SF_LAUNCH_UPD(MDT, SDT)                                                                             \
+  SF_DISPATCH_WH(w_dtype, h_dtype,                                                                          \
+                 update_mask_kernel<WD_, HD_, MDT, SDT><<<grid, kBlock, 0, st>>>(                           \
+                     us, W, H, aux, mask, frozen, stats, tau, p->cols, groups, gpr, vec, flips))
+  const bool sf32 = p->score_dtype == SF_DTYPE_F32;
+  if (mask_dtype == SF_DTYPE_F32) {
+    if (sf32)
+      SF_LAUNCH_UPD(SF_DTYPE_F32, SF_DTYPE_F32);
+    else
+      SF_LAUNCH_UPD(SF_DTYPE_F32, SF_DTYPE_BF16);
+  } else {
+    if (sf32)
+      SF_LAUNCH_UPD(SF_DTYPE_BF16, SF_DTYPE_F32);
+    else
+      SF_LAUNCH_UPD(SF_DTYPE_BF16, SF_DTYPE_BF16);
+  }
 #undef SF_LAUNCH_UPD
   return launch_status("sf_update_mask");
 }
@@ -1175,9 +1251,8 @@ __global__ void __launch_bounds__(kBlock) effective_mask_kernel(const void* __re
                                                                 int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                                 int mix, float hx, float one_minus_hx, int kind,
                                                                 int n_keep) {
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     const bool v = vec && g.full;
     float m[4], e[4];
     load4<MD>(mask, g.elem, g.n, v, m);
@@ -1198,9 +1273,8 @@ template <int MD>
 __global__ void __launch_bounds__(kBlock) hard_bytes_kernel(const void* __restrict__ mask, uint8_t* __restrict__ out,
                                                             int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                             int kind, int n_keep) {
-  for (int64_t gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; gi < groups;
-       gi += (int64_t)gridDim.x * blockDim.x) {
-    Group g = group_at(gi, cols, gpr);
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
     const bool v = vec && g.full;
     float m[4], h[4];
     load4<MD>(mask, g.elem, g.n, v, m);

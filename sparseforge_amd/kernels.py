@@ -214,3 +214,45 @@ def glu_update_masks(p: L.MaskParams, S: torch.Tensor, gate_mask: torch.Tensor, 
                                             L.ptr(stats), L.ptr(tau), up_hard_kind, up_hard_n, L.ptr(gate_flips),
                                             L.ptr(up_flips), L.stream(dev)),
                 "sf_glu_update_masks")
+
+
+# ---------------------------------------------------------------------------
+# Cross-layer overlap of the mask updates
+# ---------------------------------------------------------------------------
+_SIDE_STREAMS: dict = {}
+
+
+class LayerPipeline:
+    """Spread independent per-layer mask updates over a few side streams.
+
+    A layer's update is a chain of kernels (score statistics, the tau
+    selection passes, the fused update) whose middle part is latency-bound;
+    on separate streams the chains of different layers overlap, so those
+    kernels hide behind the memory-bound ones of other layers.  The side
+    streams first wait for the current stream's work, and join() makes the
+    current stream wait for them.  Streams keep the default priority.
+    """
+
+    def __init__(self, device: torch.device, n: int = 4):
+        key = (device.index, n)
+        if key not in _SIDE_STREAMS:
+            _SIDE_STREAMS[key] = [torch.cuda.Stream(device=device) for _ in range(n)]
+        self.main = torch.cuda.current_stream(device)
+        self.streams = _SIDE_STREAMS[key]
+        start = torch.cuda.Event()
+        start.record(self.main)
+        for st in self.streams:
+            st.wait_event(start)
+        self.i = 0
+
+    def next(self):
+        """Context manager: run the next layer's update on the next side stream."""
+        st = self.streams[self.i % len(self.streams)]
+        self.i += 1
+        return torch.cuda.stream(st)
+
+    def join(self) -> None:
+        for st in self.streams:
+            ev = torch.cuda.Event()
+            ev.record(st)
+            self.main.wait_event(ev)

@@ -50,6 +50,18 @@ def test_nm24_hard_mask_bit_exact(cuda_device, dtype, cols):
     assert np.array_equal(got.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("rows, cols", [(4500, 1023), (1100, 4094)])
+def test_nm24_hard_mask_multi_stride(cuda_device, rows, cols):
+    """More groups than the grid has threads (> 4096 x 256), ragged rows: each thread walks several strides."""
+    L, K = _K()
+    rng = np.random.default_rng(rows)
+    soft = rng.random((rows, cols), dtype=np.float32)
+    soft[rng.random((rows, cols)) < 0.3] = 0.5  # ties
+    ref = om.hard_mask_from_soft(soft, "nm_2_4")
+    got = K.hard_mask(torch.from_numpy(soft).to(cuda_device), L.HARD_NM_TAIL_KEEP, 2, 4)
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("n_keep", [1, 2, 3])
 def test_structured_hard_mask_bit_exact(cuda_device, n_keep):
     L, K = _K()
@@ -183,6 +195,32 @@ def test_update_mask_cfg1_shape_matches_oracle(cuda_device, wdt):
         assert abs(int(layer.weight.flipped_mask) - flips) <= max(2, flips // 10000)
     hard_gpu = layer._hard_mask_from_soft(layer.mask).float().cpu().numpy()
     assert np.array_equal(hard_gpu, om.hard_mask_from_soft(got, "nm_2_4"))
+
+
+def test_update_mask_multi_stride_ragged(cuda_device):
+    """[4500, 1023]: 1.15 M groups of 4 with a 3-wide tail per row, more than one grid stride per thread."""
+    sm = _sm()
+    kw = dict(mask_type="unstructured", hard_mask_type="nm_2_4", mask_metric="hessian_ratio", sparsity_warmup_steps=0,
+              mask_update_period=1, mask_penalty_mode="nm_2_4", mask_penalty_lr=0.1, mask_lr=0.1, temp_init=0.5)
+    cfg = sm.SparseLinearConfig(**kw)
+    cfg.enable_hutchinson = True
+    rows, cols = 4500, 1023
+    g = torch.Generator().manual_seed(5)
+    W = torch.randn(rows, cols, generator=g) * 0.02
+    H = torch.rand(rows, cols, generator=g) * 1e-3
+    M0 = torch.rand(rows, cols, generator=g)
+    layer = sm.SparseLinear(cols, rows, sparselinear_config=cfg, bias=False).to(cuda_device)
+    with torch.no_grad():
+        layer.weight.copy_(W)
+        layer.hessian_diag.copy_(H)
+        layer.mask.copy_(M0)
+    idx = torch.randint(0, W.numel(), (262144,), generator=g)
+    layer.update_mask(3, lambda_mid=0.05, sample_idx=idx.to(cuda_device))
+    new, _, flips, _ = om.layer_update_mask(om.full_config(**kw), 3, W.numpy(), H.numpy(), M0.numpy(), None,
+                                            idx.numpy(), 0.05)
+    np.testing.assert_allclose(layer.mask.cpu().numpy(), new, rtol=0, atol=1e-6)
+    # near-ties within the tolerance may flip a hard decision
+    assert abs(int(layer.weight.flipped_mask) - flips) <= max(2, flips // 10000)
 
 
 def test_tau_quantile_matches_torch(cuda_device):
