@@ -56,9 +56,105 @@ def kth_largest(groups: np.ndarray, k: int) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# bs x bs blocks of the fully covered core [:rows // bs * bs, :cols // bs * bs]
+# ---------------------------------------------------------------------------
+BLOCK_SPARSE = ("block_sparse16", "block_sparse32")
+BLOCK_SIZE = {"block16": 16, "block_sparse16": 16, "block_sparse32": 32}
+
+
+def block_core(shape, bs: int):
+    rows, cols = shape
+    return (rows // bs) * bs, (cols // bs) * bs
+
+
+def block_tiles(x: np.ndarray, bs: int) -> np.ndarray:
+    """[ob, ib, bs*bs]: each tile's elements in row-major order (the reference's permute(0, 2, 1, 3))."""
+    of, inf = block_core(x.shape, bs)
+    ob, ib = of // bs, inf // bs
+    return np.asarray(x, dtype=np.float32)[:of, :inf].reshape(ob, bs, ib, bs).transpose(0, 2, 1, 3).reshape(
+        ob, ib, bs * bs)
+
+
+def block_expand(b: np.ndarray, bs: int) -> np.ndarray:
+    """[ob, ib] -> [ob*bs, ib*bs], every element of a block set to the block's value."""
+    return np.repeat(np.repeat(np.asarray(b, dtype=np.float32), bs, axis=0), bs, axis=1)
+
+
+def block_mean(x: np.ndarray, bs: int) -> np.ndarray:
+    """tiles.mean() in float32 per block ([ob, ib]).  The mean is taken in float64 and rounded
+    once; torch accumulates in float32, so the two may differ in the last bits (both are exact
+    for blocks whose elements are all equal)."""
+    return block_tiles(x, bs).astype(np.float64).mean(-1).astype(np.float32)
+
+
+def block_rms(x: np.ndarray, bs: int) -> np.ndarray:
+    """(tiles ** 2).mean().sqrt() per block: square in f32, mean as in block_mean, sqrt in f32."""
+    t = block_tiles(x, bs)
+    sq = (t * t).astype(np.float32)
+    return np.sqrt(sq.astype(np.float64).mean(-1).astype(np.float32)).astype(np.float32)
+
+
+def topk_keep_desc(v: np.ndarray, k: int) -> np.ndarray:
+    """Boolean mask of the k largest entries of the last axis (torch.topk, NaN largest).
+
+    torch.topk leaves the order of equal values unspecified; here the higher index wins,
+    which is what torch's CPU kernel does when all values are equal (the all-ones initial
+    mask).  Other tie patterns are not pinned to torch."""
+    v = np.asarray(v, dtype=np.float32)
+    n = v.shape[-1]
+    keys = ordered_keys(v).astype(np.int64)
+    idx = np.broadcast_to(np.arange(n, dtype=np.int64), v.shape)
+    comp = keys * (n + 1) + idx  # key first, then the higher index
+    order = np.argsort(-comp, axis=-1, kind="stable")
+    keep = np.zeros(v.shape, dtype=bool)
+    np.put_along_axis(keep, order[..., :k], True, axis=-1)
+    return keep
+
+
+def keep_count(frac_kept: float, total: int) -> int:
+    """int(round((1 - sr) * total)) clipped to [0, total] (Python round: half to even)."""
+    return max(0, min(total, int(round(frac_kept * total))))
+
+
+def block_hard(soft: np.ndarray, hard_type: str, sparsity_ratio: float) -> np.ndarray:
+    """block16 (:537-575): top-k elements inside each 16x16 tile, k = round((1 - sr) 256);
+    block_sparse16 / 32 (:607-718): the round((1 - sr) nblocks) blocks of largest RMS kept whole.
+    Elements outside the fully covered core stay 1."""
+    bs = BLOCK_SIZE[hard_type]
+    hard = np.ones_like(soft, dtype=np.float32)
+    of, inf = block_core(soft.shape, bs)
+    if of == 0 or inf == 0:
+        return hard
+    ob, ib = of // bs, inf // bs
+    if hard_type == "block16":
+        k = keep_count(1.0 - sparsity_ratio, bs * bs)
+        keep = topk_keep_desc(block_tiles(soft, bs), k).astype(np.float32)
+        hard[:of, :inf] = keep.reshape(ob, ib, bs, bs).transpose(0, 2, 1, 3).reshape(of, inf)
+    else:
+        k = keep_count(1.0 - sparsity_ratio, ob * ib)
+        keep = topk_keep_desc(block_rms(soft, bs).ravel(), k).reshape(ob, ib)
+        hard[:of, :inf] = block_expand(keep, bs)
+    return hard
+
+
+def blockify(t: np.ndarray, hard_type: str, dt: str) -> np.ndarray:
+    """_blockify_tensor (:460-507): block mean over the core for block_sparse16/32, cast to dt."""
+    if hard_type not in BLOCK_SPARSE or np.asarray(t).ndim != 2:
+        return t
+    bs = BLOCK_SIZE[hard_type]
+    of, inf = block_core(t.shape, bs)
+    if of == 0 or inf == 0:
+        return t
+    out = np.asarray(t, dtype=np.float32).copy()
+    out[:of, :inf] = rnd(block_expand(block_mean(t, bs), bs), dt)
+    return out
+
+
+# ---------------------------------------------------------------------------
 # _hard_mask_from_soft (sparse_modeling.py:510-735)
 # ---------------------------------------------------------------------------
-def hard_mask_from_soft(soft: np.ndarray, hard_type: str, N: int = 2, M: int = 4) -> np.ndarray:
+def hard_mask_from_soft(soft: np.ndarray, hard_type: str, N: int = 2, M: int = 4,
+                        sparsity_ratio: float = 0.5) -> np.ndarray:
     soft = np.asarray(soft, dtype=np.float32)
     if hard_type == "none":  # :523-524
         return np.ones_like(soft)
@@ -79,8 +175,8 @@ def hard_mask_from_soft(soft: np.ndarray, hard_type: str, N: int = 2, M: int = 4
         assert M == 4
         g = soft.reshape(rows, cols // M, M)
         return topk_keep(g, N).reshape(rows, cols).astype(np.float32)
-    if hard_type in ("block16", "block_sparse16", "block_sparse32"):
-        raise NotImplementedError(hard_type)
+    if hard_type in BLOCK_SIZE:
+        return block_hard(soft, hard_type, sparsity_ratio)
     raise ValueError(f"Invalid hard mask_type: {hard_type}")
 
 
@@ -203,11 +299,21 @@ def quantile_linear(sample, q: float) -> np.float32:
 # unstructured / structured without block_sparse hard types
 # ---------------------------------------------------------------------------
 def gate_target(z: np.ndarray, sdt: str, mask_type: str, T: float, tau=None, N: int = 2, M: int = 4,
-                structured_exact: bool = False, beta_s: float = 0.0, mask=None, frozen=None) -> np.ndarray:
+                structured_exact: bool = False, beta_s: float = 0.0, mask=None, frozen=None,
+                hard_type: str = "match", sparsity: float = 0.0) -> np.ndarray:
     """G from the z-normalised scores z (already in the score dtype)."""
     denom = np.float32(np.float32(T) + np.float32(1e-8))
     rows, cols = z.shape
-    if mask_type == "unstructured":  # :1162
+    block_core_ok = hard_type in BLOCK_SPARSE and all(block_core(z.shape, BLOCK_SIZE[hard_type]))
+    if mask_type == "unstructured" and block_core_ok:  # :1122-1158: G per block from the blocks' RMS
+        bs = BLOCK_SIZE[hard_type]
+        of, inf = block_core(z.shape, bs)
+        rms = block_rms(z, bs)
+        tau_b = quantile_linear(rms.ravel(), sparsity)
+        Gb = sigmoid_f32((rms - tau_b) / denom)
+        G = np.ones_like(z, dtype=np.float32)
+        G[:of, :inf] = rnd(block_expand(Gb, bs), sdt)
+    elif mask_type == "unstructured":  # :1162
         G = rnd(sigmoid_f32((z - np.float32(tau)) / denom), sdt)
     elif mask_type == "structured":  # :1164-1185
         if cols % M != 0:
@@ -220,7 +326,7 @@ def gate_target(z: np.ndarray, sdt: str, mask_type: str, T: float, tau=None, N: 
             G = rnd(sigmoid_f32((g - tg) / denom), sdt).reshape(rows, cols)
     else:
         raise ValueError(f"Invalid mask_type: {mask_type}")
-    if beta_s > 0.0:  # :1199-1225
+    if beta_s > 0.0 and hard_type not in BLOCK_SPARSE:  # :1199-1225
         full = (cols // M) * M
         if full > 0:
             target = G.copy()
@@ -232,7 +338,7 @@ def gate_target(z: np.ndarray, sdt: str, mask_type: str, T: float, tau=None, N: 
         if fz.any():
             G = G.copy()
             G[fz] = rnd(np.asarray(mask, dtype=np.float32), sdt)[fz]
-    return G.astype(np.float32)
+    return blockify(G, hard_type, sdt).astype(np.float32)  # :1237
 
 
 # ---------------------------------------------------------------------------
@@ -261,9 +367,32 @@ def ema(prev: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: float) -> 
     return np.clip(m2, 0.0, 1.0).astype(np.float32)
 
 
+def block_penalty_target(mode: str, G: np.ndarray, prev: np.ndarray, sparsity_ratio: float) -> np.ndarray:
+    """Hard target of the block penalty modes, or None when the core is empty (-> 'mid').
+
+    block16 (:1298-1347): top-k of G inside each 16x16 tile, k = round((1 - sr) 256).
+    block_sparse16 / 32 (:1395-1529): the round((1 - sr) nblocks) blocks of largest mask mean."""
+    bs = BLOCK_SIZE[mode]
+    of, inf = block_core(G.shape, bs)
+    if of == 0 or inf == 0:
+        return None
+    ob, ib = of // bs, inf // bs
+    target = np.ones_like(G, dtype=np.float32)
+    if mode == "block16":
+        k = keep_count(1.0 - sparsity_ratio, bs * bs)
+        keep = topk_keep_desc(block_tiles(G, bs), k).astype(np.float32)
+        target[:of, :inf] = keep.reshape(ob, ib, bs, bs).transpose(0, 2, 1, 3).reshape(of, inf)
+    else:
+        k = keep_count(1.0 - sparsity_ratio, ob * ib)
+        keep = topk_keep_desc(block_mean(prev, bs).ravel(), k).reshape(ob, ib)
+        target[:of, :inf] = block_expand(keep, bs)
+    return target
+
+
 def update_mask(mask: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: float, penalty_mode: str = "none",
                 penalty_coef: float = 0.0, N: int = 2, M: int = 4, binarize: float = 0.0, freeze_low: float = 0.0,
-                freeze_high: float = 1.0, step: int = 0, frozen=None, hard_type: str = "nm_2_4"):
+                freeze_high: float = 1.0, step: int = 0, frozen=None, hard_type: str = "nm_2_4",
+                sparsity_ratio: float = 0.5):
     """Returns (new_mask, new_frozen_flags_or_None, flips).  G from gate_target."""
     prev = np.asarray(mask, dtype=np.float32).copy()
     G = np.asarray(G, dtype=np.float32).copy()
@@ -271,6 +400,13 @@ def update_mask(mask: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: fl
     c = np.float32(penalty_coef)
     if penalty_coef != 0.0:
         mode = penalty_mode
+        if mode in BLOCK_SIZE:
+            target = block_penalty_target(mode, G, prev, sparsity_ratio)
+            if target is None:
+                mode = "mid"
+            else:
+                delta = rnd(rnd(prev, sdt) - target, sdt)
+                G = rnd(G - rnd(c * delta, sdt), sdt)
         if mode == "nm_2_4" and (cols // 4) * 4 == 0:
             mode = "mid"
         if mode == "structured_topn" and cols % M != 0:
@@ -289,6 +425,7 @@ def update_mask(mask: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: fl
         G = np.clip(G, 0.0, 1.0).astype(np.float32)
     G = binarize_push(G, binarize, sdt)
     new = ema(prev, G, sdt, mdt, mask_lr)
+    new = blockify(new, hard_type, mdt)  # :1598-1601
     new_frozen = None
     if freeze_low > 0.0 or freeze_high < 1.0:  # :1621-1642
         f0 = new <= np.float32(freeze_low)
@@ -300,8 +437,8 @@ def update_mask(mask: np.ndarray, G: np.ndarray, sdt: str, mdt: str, mask_lr: fl
             applied |= f1
         if frozen is not None:
             new_frozen = np.maximum(np.asarray(frozen, dtype=np.float32), applied.astype(np.float32))
-    hp = hard_mask_from_soft(prev, hard_type, N, M) > 0.5
-    hn = hard_mask_from_soft(new, hard_type, N, M) > 0.5
+    hp = hard_mask_from_soft(prev, hard_type, N, M, sparsity_ratio) > 0.5
+    hn = hard_mask_from_soft(new, hard_type, N, M, sparsity_ratio) > 0.5
     return new, new_frozen, int((hp ^ hn).sum())
 
 
@@ -370,11 +507,8 @@ def layer_gate_target(c: dict, step: int, W, H, mask, frozen, sample_idx, w_dt=F
         flat = z.ravel()
         sample = flat[np.asarray(sample_idx)] if sample_idx is not None else flat
         tau = quantile_linear(sample, sch["sparsity"])
-    beta_s = sch["beta_s"]
-    if effective_hard_type(c) in ("block_sparse16", "block_sparse32"):
-        raise NotImplementedError("block_sparse gate targets")
     return gate_target(z, sdt, c["mask_type"], sch["T"], tau, int(c["N"]), int(c["M"]), bool(c["structured_exact"]),
-                       beta_s, mask, frozen)
+                       sch["beta_s"], mask, frozen, c["hard_mask_type"] or "match", sch["sparsity"])
 
 
 def layer_update_mask(c: dict, step: int, W, H, mask, frozen, sample_idx, lambda_mid: float, w_dt=F32, h_dt=F32,
@@ -392,12 +526,10 @@ def layer_update_mask(c: dict, step: int, W, H, mask, frozen, sample_idx, lambda
     pen_lr = float(c["mask_penalty_lr"]) if c["mask_penalty_lr"] is not None else float(c["mask_lr"])
     lam = float(lambda_mid or 0.0)
     mode = c["mask_penalty_mode"] or "mid"
-    if mode in ("block16", "block_sparse16", "block_sparse32"):
-        raise NotImplementedError(mode)
     new, new_frozen, flips = update_mask(
         mask, G, sdt, m_dt, float(c["mask_lr"]), mode if lam != 0.0 else "none", pen_lr * lam, int(c["N"]),
         int(c["M"]), float(c["mask_binarize_decay"] or 0.0), float(c["freeze_low"]), float(c["freeze_high"]), step,
-        frozen, effective_hard_type(c))
+        frozen, effective_hard_type(c), float(c["sparsity_ratio"]))
     hx = layer_schedule(c, step)["hx"]
     return new, new_frozen, flips, hx
 

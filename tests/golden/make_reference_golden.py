@@ -13,6 +13,9 @@ never travels with them.  Functions covered (reference file:line):
   linear_*    FusedMaskedLinearSTE + SLoRB fwd/bwd legacy/sparse_modeling.py:56-132, :737-796
   kl_*        Distill_Model.kl_loss                legacy/sparse_modeling.py:1749-1828
   bsr_*       convert_to_block_sparse              legacy/triton_block_sparse.py:46-103
+  hardblk_*   _hard_mask_from_soft, block types    legacy/sparse_modeling.py:537-718
+  gateblk_*   compute_gate_target, block_sparse    legacy/sparse_modeling.py:1100-1158, :1237
+  updblk_*    update_mask, block penalties/blockify legacy/sparse_modeling.py:1298-1529, :1598-1601
 
 The reference module imports wandb at top level without using it
 (legacy/sparse_modeling.py:20); an empty module object is registered under
@@ -299,6 +302,95 @@ def bsr_case(out):
                                 col_idx=col_idx.numpy())
 
 
+def block_cases(ref_sm, out):
+    """Block hard types, the block_sparse gate and the block penalty modes on ragged shapes
+    (edges outside the fully covered core) with distinct random values, plus all-equal inputs
+    (the tie case whose torch.topk order is fixed: the higher index wins)."""
+    hard = {
+        "hardblk_block16_f32": ("block16", (40, 56), 0.5, "rand"),
+        "hardblk_block16_sr03_f32": ("block16", (40, 56), 0.3, "rand"),
+        "hardblk_block16_ones_f32": ("block16", (16, 32), 0.5, "ones"),
+        "hardblk_bs16_f32": ("block_sparse16", (72, 100), 0.5, "rand"),
+        "hardblk_bs16_sr03_f32": ("block_sparse16", (72, 100), 0.3, "rand"),
+        "hardblk_bs16_ones_f32": ("block_sparse16", (64, 64), 0.5, "ones"),
+        "hardblk_bs32_f32": ("block_sparse32", (100, 70), 0.5, "rand"),
+    }
+    for i, (name, (ht, shape, sr, kind)) in enumerate(hard.items()):
+        layer, _ = make_layer(ref_sm, shape[0], shape[1], torch.float32, 900 + i, mask_type="unstructured",
+                              hard_mask_type=ht, sparsity_ratio=sr)
+        g = torch.Generator().manual_seed(950 + i)
+        soft = torch.rand(shape, generator=g) if kind == "rand" else torch.ones(shape)
+        hard_ = layer._hard_mask_from_soft(soft)
+        out[name] = dict(soft=np32(soft), hard=np32(hard_), hard_type=np.array(ht), sr=np.float64(sr))
+
+    gates = {
+        "gateblk_bs16_f32": dict(shape=(40, 72), mask_type="unstructured", hard_mask_type="block_sparse16",
+                                 mask_metric="hessian_ratio", tau_sample_size=512, sparsity_warmup_steps=100,
+                                 step=60, freeze_low=0.05),
+        "gateblk_bs32_struct_f32": dict(shape=(64, 96), mask_type="structured", hard_mask_type="block_sparse32",
+                                        mask_metric="magnitude", step=9, beta_structural_start=0,
+                                        beta_structural_end=20),
+        "gateblk_bs16_small_f32": dict(shape=(12, 40), mask_type="unstructured", hard_mask_type="block_sparse16",
+                                       mask_metric="magnitude", tau_sample_size=100, step=5),
+    }
+    for i, (name, kw) in enumerate(gates.items()):
+        kw = dict(kw)
+        shape, step = kw.pop("shape"), kw.pop("step")
+        layer, cfg = make_layer(ref_sm, shape[0], shape[1], torch.float32, 920 + i, **kw)
+        seed = 9200 + i
+        torch.manual_seed(seed)
+        G = layer.compute_gate_target(step)
+        n = layer.weight.numel()
+        m = int(cfg.tau_sample_size)
+        torch.manual_seed(seed)
+        idx = torch.randint(0, n, (m,)) if (m > 0 and n > m) else torch.arange(n)
+        out[name] = dict(W=np32(layer.weight), H=np32(layer.hessian_diag), mask=np32(layer.mask),
+                         frozen=np32(layer.frozen_mask_flags), idx=idx.numpy().astype(np.int64), G=np32(G),
+                         step=np.int64(step), T=np.float64(layer._temperature(step)),
+                         sparsity=np.float64(layer._effective_sparsity(step)), dtype=np.array(str(torch.float32)),
+                         cfg=np.array(repr(kw)))
+
+    updates = {
+        "updblk_bs16_f32": dict(shape=(50, 84), mask_type="unstructured", hard_mask_type="block_sparse16",
+                                mask_metric="hessian_ratio", tau_sample_size=512, sparsity_warmup_steps=0,
+                                mask_update_period=1, mask_penalty_mode="block_sparse16", mask_penalty_lr=0.1,
+                                mask_binarize_decay=0.05, mask_lr=0.2, lam=0.2),
+        "updblk_block16_pen_f32": dict(shape=(36, 50), mask_type="unstructured", hard_mask_type="nm_2_4",
+                                       mask_metric="magnitude", tau_sample_size=512, sparsity_warmup_steps=0,
+                                       mask_update_period=1, mask_penalty_mode="block16", mask_penalty_lr=0.2,
+                                       mask_lr=0.15, lam=0.3),
+        "updblk_bs32_freeze_f32": dict(shape=(64, 70), mask_type="unstructured", hard_mask_type="block_sparse32",
+                                       mask_metric="magnitude", tau_sample_size=100000, sparsity_warmup_steps=0,
+                                       mask_update_period=1, mask_penalty_mode="mid", freeze_low=0.3,
+                                       freeze_high=0.7, mask_lr=0.4, lam=0.1, steps=(1999, 2000, 2001)),
+        "updblk_block16_hard_f32": dict(shape=(32, 48), mask_type="structured", hard_mask_type="block16",
+                                        mask_metric="hessian_obd", sparsity_warmup_steps=0, mask_update_period=1,
+                                        mask_penalty_mode="block_sparse32", mask_lr=0.2, lam=0.2),
+    }
+    for i, (name, kw) in enumerate(updates.items()):
+        kw = dict(kw)
+        shape, lam = kw.pop("shape"), kw.pop("lam")
+        steps = kw.pop("steps", (1, 2, 3, 4))
+        layer, cfg = make_layer(ref_sm, shape[0], shape[1], torch.float32, 940 + i, **kw)
+        rec = dict(W=np32(layer.weight), H=np32(layer.hessian_diag), init_mask=np32(layer.mask),
+                   init_frozen=np32(layer.frozen_mask_flags), dtype=np.array(str(torch.float32)),
+                   cfg=np.array(repr(kw)), lam=np.float64(lam), steps=np.array(steps, dtype=np.int64))
+        n = layer.weight.numel()
+        m = int(cfg.tau_sample_size)
+        for j, step in enumerate(steps):
+            seed = 9400 + 10 * i + j
+            torch.manual_seed(seed)
+            idx = torch.randint(0, n, (m,)) if (m > 0 and n > m) else torch.arange(n)
+            torch.manual_seed(seed)
+            layer.update_mask(step, lambda_mid=lam)
+            rec[f"idx{j}"] = idx.numpy().astype(np.int64)
+            rec[f"mask{j}"] = np32(layer.mask)
+            rec[f"frozen{j}"] = np32(layer.frozen_mask_flags)
+            rec[f"flips{j}"] = np.int64(layer.weight.flipped_mask)
+            rec[f"hx{j}"] = np.float64(layer.hardening_x)
+        out[name] = rec
+
+
 def main():
     ref_sm, ref_utils, ref_adamw = _import_reference()
     torch.set_num_threads(1)
@@ -311,6 +403,7 @@ def main():
     linear_case(ref_sm, out)
     kl_case(ref_sm, out)
     bsr_case(out)
+    block_cases(ref_sm, out)
     for name, rec in out.items():
         path = os.path.join(OUT, f"ref_{name}.npz")
         np.savez_compressed(path, torch_version=np.array(torch.__version__), **rec)

@@ -178,3 +178,87 @@ def test_glu_joint_same_target_for_both_masks():
     G = (ng - np.float32(0.8) * M) / np.float32(0.2)  # EMA inverted: G is a structured sigmoid target
     gg = G.reshape(8, 4, 4)
     assert (np.abs(np.sort(gg, axis=-1)[..., 2] - 0.5) < 1e-5).all()  # the 2nd largest of each group sits at 0.5
+
+
+# ---------------------------------------------------------------------------
+# block hard types, block_sparse gate, block penalties (sparse_modeling.py:460-507, :537-718,
+# :1100-1158, :1237, :1298-1529, :1598-1601)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("case", ["hardblk_block16_f32", "hardblk_block16_sr03_f32", "hardblk_block16_ones_f32",
+                                  "hardblk_bs16_f32", "hardblk_bs16_sr03_f32", "hardblk_bs16_ones_f32",
+                                  "hardblk_bs32_f32"])
+def test_block_hard_masks_match_reference_golden(case):
+    r = load_golden(case)
+    got = om.hard_mask_from_soft(r["soft"], str(r["hard_type"]), sparsity_ratio=float(r["sr"]))
+    assert np.array_equal(got, r["hard"])
+
+
+def test_block_topk_matches_torch_on_distinct_values():
+    """Global / per-tile top-k against torch.topk + scatter where no two values are equal."""
+    rng = np.random.default_rng(11)
+    v = rng.permutation(5000).astype(np.float32).reshape(10, 500) / 7.0
+    for k in (0, 1, 17, 250, 499, 500):
+        assert np.array_equal(om.topk_keep_desc(v, k), torch_keep(v, k) if 0 < k else np.zeros_like(v, bool))
+
+
+def test_block_rms_and_mean_closed_forms():
+    """Constant blocks give exactly their value (mean) and |value| (RMS); a block of +-a gives a."""
+    x = np.zeros((32, 48), np.float32)
+    x[:16, :16] = 0.3
+    x[16:, 16:32] = -0.7
+    x[:16, 32:] = np.where((np.indices((16, 16)).sum(0) % 2) == 0, 0.25, -0.25)
+    m = om.block_mean(x, 16)
+    r = om.block_rms(x, 16)
+    assert m[0, 0] == np.float32(0.3) and m[1, 1] == np.float32(-0.7) and m[0, 2] == 0.0
+    assert r[0, 0] == np.sqrt(np.float32(0.3) * np.float32(0.3)) and r[1, 1] == np.float32(0.7)
+    assert r[0, 2] == np.float32(0.25) and r[1, 0] == 0.0
+    b = om.blockify(x, "block_sparse16", F32)
+    assert (b[:16, :16] == np.float32(0.3)).all() and (b[:16, 32:] == 0.0).all()
+
+
+def test_block16_keeps_exact_count_per_tile():
+    rng = np.random.default_rng(3)
+    soft = rng.random((48, 40)).astype(np.float32)
+    for sr, k in ((0.5, 128), (0.25, 192), (0.3, 179), (1.0, 0)):
+        h = om.hard_mask_from_soft(soft, "block16", sparsity_ratio=sr)
+        tiles = om.block_tiles(h, 16)
+        assert (tiles.sum(-1) == k).all()
+        assert (h[:, 32:] == 1).all() and (h[48:] == 1).all()
+        # each kept element is >= every dropped element of its tile
+        s = om.block_tiles(soft, 16)
+        kept = np.where(tiles > 0, s, np.inf).min(-1)
+        dropped = np.where(tiles > 0, -np.inf, s).max(-1)
+        assert (kept >= dropped).all()
+
+
+@pytest.mark.parametrize("case", ["gateblk_bs16_f32", "gateblk_bs32_struct_f32", "gateblk_bs16_small_f32"])
+def test_block_gate_matches_reference_golden(case):
+    r = load_golden(case)
+    c = _cfg(r)
+    step = int(r["step"])
+    sch = om.layer_schedule(c, step)
+    assert sch["T"] == float(r["T"]) and sch["sparsity"] == float(r["sparsity"])
+    frozen = r["frozen"] if r["frozen"].shape == r["W"].shape else None
+    G = om.layer_gate_target(c, step, r["W"], r["H"], r["mask"], frozen, r["idx"])
+    np.testing.assert_allclose(G, r["G"], rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("case", ["updblk_bs16_f32", "updblk_block16_pen_f32", "updblk_bs32_freeze_f32",
+                                  "updblk_block16_hard_f32"])
+def test_block_update_matches_reference_golden(case):
+    r = load_golden(case)
+    c = _cfg(r)
+    mask = r["init_mask"].copy()
+    frozen = r["init_frozen"].copy() if r["init_frozen"].shape == r["W"].shape else None
+    for j, step in enumerate(r["steps"]):
+        out = om.layer_update_mask(c, int(step), r["W"], r["H"], mask, frozen, r[f"idx{j}"], float(r["lam"]))
+        assert out is not None
+        mask, nf, flips, hx = out
+        if nf is not None:
+            frozen = nf
+        np.testing.assert_allclose(mask, r[f"mask{j}"], rtol=0, atol=1e-6)
+        if frozen is not None:
+            assert (frozen == r[f"frozen{j}"]).all()
+        assert flips == int(r[f"flips{j}"])
+        assert hx == float(r[f"hx{j}"])
+        mask = r[f"mask{j}"].copy()
