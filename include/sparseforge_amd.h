@@ -56,12 +56,20 @@ extern "C" {
 #define SF_GATE_UNSTRUCTURED 0 /* sigmoid((z - tau) / (T + 1e-8)), global tau  (:1097-1162) */
 #define SF_GATE_STRUCTURED 1   /* sigmoid((z - tau_g) / (T + 1e-8)), tau_g = N-th largest of group (:1164-1185) */
 #define SF_GATE_STRUCTURED_EXACT 2 /* top-N scatter of ones (:1176-1182) */
+#define SF_GATE_ZSCORE 3 /* z = ((s - mu) / sigma) in the score dtype: the input the block_sparse gate
+                            pools per block (:1083-1088, :1122-1131); sf_gate_target only */
 
 /* ---- penalty pull applied to G inside update_mask (:1291-1573) ---------- */
 #define SF_PENALTY_NONE 0
 #define SF_PENALTY_MID 1            /* G -= c * (1 - 2 m)                 (:1567-1570) */
 #define SF_PENALTY_NM_2_4 2         /* G -= c * (m - top2(G)), tail target 1 (:1350-1393) */
 #define SF_PENALTY_STRUCTURED_TOPN 3 /* G -= c * (m - topN(G)), cols % M == 0 (:1531-1565) */
+#define SF_PENALTY_TARGET 4 /* G -= c * (m - target), target given: the block16 / block_sparse16 /
+                               block_sparse32 modes (:1298-1347, :1395-1529); sf_apply_gate only */
+
+/* ---- per-block statistics (bs x bs tiles of the fully covered core) ---- */
+#define SF_BLOCK_MEAN 0 /* mean(x)            (_blockify_tensor :495-497; block penalty :1436-1438) */
+#define SF_BLOCK_RMS 1  /* sqrt(mean(x * x))  (block_sparse hard mask :632-633; block gate :1131)   */
 
 const char* sf_last_error(void);
 int sf_version(void);
@@ -205,6 +213,74 @@ int sf_glu_update_masks(const sf_mask_params* p, const void* S, int s_dtype, voi
  */
 int sf_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst, void* stream);
 
+/*
+ * Block statistic of each bs x bs block (bs = 16 or 32) of the fully covered
+ * core [:rows/bs*bs, :cols/bs*bs] of x [rows, cols]: out[br * (cols/bs) + bc]
+ * (device float[(rows/bs) * (cols/bs)]), SF_BLOCK_MEAN or SF_BLOCK_RMS.  The
+ * sum runs in f64 and is rounded to f32 once (torch sums in f32, so results
+ * agree to a few ulp and exactly for blocks of equal elements).  Replaces the
+ * tile means of _blockify_tensor (legacy/sparse_modeling.py:488-497), of the
+ * block_sparse penalty (:1431-1438) and the block RMS of the block_sparse hard
+ * mask (:624-633) and gate (:1126-1131).
+ */
+int sf_block_stat(const void* x, int x_dtype, int64_t rows, int64_t cols, int bs, int stat, float* out,
+                  void* stream);
+
+/*
+ * keep[i] = 1.0f for the k largest entries of v[n] (device floats), else 0.0f:
+ * the torch.topk(flat, k) + scatter of the block_sparse hard mask
+ * (legacy/sparse_modeling.py:641-655, :699-713) and penalty target
+ * (:1441-1451).  NaN ranks largest; among equal values the higher index is
+ * kept first (torch's CPU order for all-equal input, e.g. the initial all-ones
+ * mask; torch leaves other tie orders unspecified).  k <= 0: all 0; k >= n: all 1.
+ */
+int sf_topk_keep(const float* v, int64_t n, int64_t k, float* keep, void* stream);
+
+/*
+ * block16 projection: in each 16 x 16 tile of the core of x [rows, cols] the k
+ * largest elements become 1 and the rest 0; elements outside the core become
+ * 1 (legacy/sparse_modeling.py:537-575 for the hard mask, :1318-1341 for the
+ * block16 penalty target).  Ties as sf_topk_keep, by position inside the tile
+ * (row-major).  bs must be 16.  out: [rows, cols] in out_dtype.
+ */
+int sf_tile_topk(const void* x, int x_dtype, int64_t rows, int64_t cols, int bs, int64_t k, void* out,
+                 int out_dtype, void* stream);
+
+/*
+ * Expand per-block values over the core of out [rows, cols]:
+ *   out = (bvals[block]).to(out dtype), or with tau (device float[1])
+ *   out = sigmoid((bvals[block] - *tau) / (temperature + 1e-8)) in f32, then cast
+ *   (the block_sparse gate, legacy/sparse_modeling.py:1144-1154).
+ * Outside the core: unchanged (edge_write = 0, as _blockify_tensor :505-507)
+ * or edge_val (hard masks, targets and G keep 1 there).  Where ov_flags != 0
+ * the element takes ov_src instead, cast to the out dtype (the frozen override
+ * G[frozen] = mask[frozen], :1227-1229).  Used for blockify (bvals = block
+ * means, edge_write 0), block hard masks / targets (bvals = sf_topk_keep
+ * flags, edge_val 1) and the block gate.
+ */
+int sf_block_fill(const float* bvals, int64_t rows, int64_t cols, int bs, const float* tau, float temperature,
+                  void* out, int out_dtype, int edge_write, float edge_val, const void* ov_src, int ov_src_dtype,
+                  const void* ov_flags, int ov_flags_dtype, void* stream);
+
+/*
+ * The update half of update_mask for a gate target G already in memory
+ * (p->score_dtype): penalty pull (p->penalty, with SF_PENALTY_TARGET reading
+ * `target`), clamp, binarisation push, EMA of `mask` and, with do_freeze, the
+ * freeze snaps and flags (legacy/sparse_modeling.py:1291-1642 without the
+ * flip count).  The staged path of the block hard types and block penalty
+ * modes uses it; blockify and sf_freeze_mask follow when the hard type is
+ * block_sparse16/32.
+ */
+int sf_apply_gate(const sf_mask_params* p, const void* G, const void* target, int target_dtype, void* mask,
+                  int mask_dtype, void* frozen, int frozen_dtype, int do_freeze, void* stream);
+
+/*
+ * Freeze snaps and flags of update_mask (legacy/sparse_modeling.py:1621-1642)
+ * as a pass of its own: after the mask blockify of the block_sparse types.
+ */
+int sf_freeze_mask(const sf_mask_params* p, void* mask, int mask_dtype, void* frozen, int frozen_dtype,
+                   void* stream);
+
 /* ---- effective mask for the masked GEMMs (SparseLinear.forward, :759-771) */
 #define SF_EFF_SOFT 0 /* E = mask.to(weight dtype)                                  */
 #define SF_EFF_MIX 1  /* E = (hx * mask + (1 - hx) * hard(mask)).to(weight dtype)     */
@@ -219,6 +295,14 @@ int sf_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, uint8_t* dst
  */
 int sf_effective_mask(const void* mask, int mask_dtype, void* eff, int eff_dtype, int64_t rows, int64_t cols,
                       int mode, float hx, int hard_kind, int hard_n, int hard_m, void* stream);
+
+/*
+ * sf_effective_mask with the hard projection given as a tensor (`hard`,
+ * [rows, cols], values {0, 1}) instead of computed per group: the block hard
+ * types, whose projection is not group-local (legacy/sparse_modeling.py:770).
+ */
+int sf_effective_mask_given(const void* mask, int mask_dtype, const void* hard, int hard_dtype, void* eff,
+                            int eff_dtype, int64_t rows, int64_t cols, int mode, float hx, void* stream);
 
 /* ---- GEMM engine (FusedMaskedLinearSTE, :56-132, and the SLoRB F.linear pair, :790-794) */
 #define SF_LAYOUT_K 0  /* operand stored K-contiguous: X[row * ld + k]                        */

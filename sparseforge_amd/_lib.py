@@ -44,11 +44,16 @@ METRIC = {
 GATE_UNSTRUCTURED = 0
 GATE_STRUCTURED = 1
 GATE_STRUCTURED_EXACT = 2
+GATE_ZSCORE = 3
 
 PENALTY_NONE = 0
 PENALTY_MID = 1
 PENALTY_NM_2_4 = 2
 PENALTY_STRUCTURED_TOPN = 3
+PENALTY_TARGET = 4
+
+BLOCK_MEAN = 0
+BLOCK_RMS = 1
 
 EFF_SOFT = 0
 EFF_MIX = 1
@@ -178,6 +183,13 @@ SIGNATURES = {
     "sf_joint_scores": (_I, [_MP, _P, _P, _P, _MP, _P, _P, _P, _I, _I, _I, _P, _I, _P]),
     "sf_glu_update_masks": (_I, [_MP, _P, _I, _P, _P, _I, _P, _I, _P, _P, _I, _I, _P, _P, _P]),
     "sf_effective_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _F, _I, _I, _I, _P]),
+    "sf_effective_mask_given": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I64, _I, _F, _P]),
+    "sf_block_stat": (_I, [_P, _I, _I64, _I64, _I, _I, _P, _P]),
+    "sf_topk_keep": (_I, [_P, _I64, _I64, _P, _P]),
+    "sf_tile_topk": (_I, [_P, _I, _I64, _I64, _I, _I64, _P, _I, _P]),
+    "sf_block_fill": (_I, [_P, _I64, _I64, _I, _P, _F, _P, _I, _I, _F, _P, _I, _P, _I, _P]),
+    "sf_apply_gate": (_I, [_MP, _P, _P, _I, _P, _I, _P, _I, _I, _P]),
+    "sf_freeze_mask": (_I, [_MP, _P, _I, _P, _I, _P]),
     "sf_transpose_u8": (_I, [_P, _I64, _I64, _P, _P]),
     "sf_gemm": (_I, [ctypes.POINTER(GemmDesc), _P]),
     "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),

@@ -605,10 +605,13 @@ __device__ __forceinline__ void gate_of_group(const GateSpec& gs, const float sc
     float tg = kth_largest4(z, gs.n_keep);
 #pragma unroll
     for (int j = 0; j < 4; ++j) G[j] = rndc<SD>(sigmoidf_(div_by(z[j] - tg, gs.denom, gs.rdenom)));
-  } else {  // structured exact
+  } else if (gs.gate == SF_GATE_STRUCTURED_EXACT) {
     uint32_t keep = topk4_keep(z, gs.n_keep);
 #pragma unroll
     for (int j = 0; j < 4; ++j) G[j] = ((keep >> j) & 1u) ? 1.0f : 0.0f;
+  } else {  // SF_GATE_ZSCORE: z itself, pooled per block by the block_sparse gate
+#pragma unroll
+    for (int j = 0; j < 4; ++j) G[j] = z[j];
   }
   if (gs.beta_struct > 0.0f) {  // (:1199-1225): target = topN(z) on full groups, G itself on the tail
     uint32_t keep = g.full ? topk4_keep(z, gs.n_keep) : 0u;
@@ -668,10 +671,18 @@ struct UpdateSpec {
 // Penalty pull toward a target, then clamp (:1291-1573), and the
 // multiplicative binarisation push (:1576-1590).  mp: the mask the penalty
 // compares against; sd: dtype of G.
+// tg: the explicit target of SF_PENALTY_TARGET (block16 / block_sparse modes).
 template <int MD, int SD>
-__device__ __forceinline__ void pull_and_push(const UpdateSpec& us, const Group& g, const float mp[4], float G[4]) {
+__device__ __forceinline__ void pull_and_push(const UpdateSpec& us, const Group& g, const float mp[4], float G[4],
+                                              const float* tg = nullptr) {
   if (us.penalty != SF_PENALTY_NONE) {
-    if (us.penalty == SF_PENALTY_MID) {
+    if (us.penalty == SF_PENALTY_TARGET) {  // G -= c * (mask.to(G.dtype) - target)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float delta = rndc<SD>(rndc<SD>(mp[j]) - tg[j]);
+        G[j] = rndc<SD>(G[j] - rndc<SD>(us.pen_coef * delta));
+      }
+    } else if (us.penalty == SF_PENALTY_MID) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float pg = rndc<SD>(rndc<MD>(1.0f - 2.0f * mp[j]));
@@ -711,6 +722,30 @@ __device__ __forceinline__ void ema_of(const UpdateSpec& us, const float mp[4], 
   }
 }
 
+// Freeze snaps of the new mask and the frozen flags (:1621-1642).  fz: current flags.
+__device__ __forceinline__ void freeze_group(const UpdateSpec& us, const Group& g, bool v, float mn[4],
+                                             const float fz[4], void* frozen) {
+  float fl[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bool f0 = mn[j] <= us.freeze_low;
+    bool f1 = mn[j] >= us.freeze_high;
+    bool applied = f0;
+    if (f0) mn[j] = 0.0f;
+    if (us.snap_high) {
+      if (f1) mn[j] = 1.0f;
+      applied = applied || f1;
+    }
+    fl[j] = fmaxf(fz[j], applied ? 1.0f : 0.0f);
+  }
+  if (us.gs.has_frozen) {
+    if (us.gs.frozen_dtype == SF_DTYPE_F32)
+      store4<SF_DTYPE_F32>(frozen, g.elem, g.n, v, fl);
+    else
+      store4<SF_DTYPE_BF16>(frozen, g.elem, g.n, v, fl);
+  }
+}
+
 // Positions of a group where the hard views of a and b differ (:1659-1661).
 __device__ __forceinline__ int flips_of(const float a[4], const float b[4], const Group& g, int kind, int n) {
   float ha[4], hb[4];
@@ -744,28 +779,7 @@ __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, cons
     pull_and_push<MD, SD>(us, g, mp, G);
     float mn[4];
     ema_of<MD>(us, mp, G, mn);
-    // freeze snaps and flags (:1621-1642)
-    if (us.apply_freeze) {
-      float fl[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bool f0 = mn[j] <= us.freeze_low;
-        bool f1 = mn[j] >= us.freeze_high;
-        bool applied = f0;
-        if (f0) mn[j] = 0.0f;
-        if (us.snap_high) {
-          if (f1) mn[j] = 1.0f;
-          applied = applied || f1;
-        }
-        fl[j] = fmaxf(fz[j], applied ? 1.0f : 0.0f);
-      }
-      if (gs.has_frozen) {
-        if (gs.frozen_dtype == SF_DTYPE_F32)
-          store4<SF_DTYPE_F32>(frozen, g.elem, g.n, v, fl);
-        else
-          store4<SF_DTYPE_BF16>(frozen, g.elem, g.n, v, fl);
-      }
-    }
+    if (us.apply_freeze) freeze_group(us, g, v, mn, fz, frozen);
     store4<MD>(mask, g.elem, g.n, v, mn);
     if (flips) cnt += flips_of(mp, mn, g, us.hard_kind, us.hard_n);
   }
@@ -1026,14 +1040,16 @@ namespace sf {
 namespace {
 int make_gate_spec(const sf_mask_params* p, int w_dtype, int h_dtype, int aux_dtype, int mask_dtype, int frozen_dtype,
                    GateSpec* gs) {
-  SF_CHECK_ARG(p->gate >= SF_GATE_UNSTRUCTURED && p->gate <= SF_GATE_STRUCTURED_EXACT, "bad gate %d", p->gate);
-  if (p->gate != SF_GATE_UNSTRUCTURED || p->beta_struct > 0.0f) {
+  SF_CHECK_ARG(p->gate >= SF_GATE_UNSTRUCTURED && p->gate <= SF_GATE_ZSCORE, "bad gate %d", p->gate);
+  SF_CHECK_ARG(p->gate != SF_GATE_ZSCORE || (p->beta_struct == 0.0f && !p->has_frozen),
+               "the z-score output takes no beta mix and no frozen override");
+  if ((p->gate != SF_GATE_UNSTRUCTURED && p->gate != SF_GATE_ZSCORE) || p->beta_struct > 0.0f) {
     if (p->m_group != 4 || p->n_keep < 1 || p->n_keep > 3) {
       set_error("structured gate with N=%d M=%d: only M=4 is built on device", p->n_keep, p->m_group);
       return SF_ERR_UNSUPPORTED;
     }
   }
-  if (p->gate != SF_GATE_UNSTRUCTURED)
+  if (p->gate == SF_GATE_STRUCTURED || p->gate == SF_GATE_STRUCTURED_EXACT)
     SF_CHECK_ARG(p->cols % p->m_group == 0, "in_features (%lld) must be divisible by M (%d).", (long long)p->cols,
                  p->m_group);
   gs->s = make_spec(p, w_dtype, h_dtype, aux_dtype);
@@ -1131,6 +1147,7 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
   SF_CHECK_ARG(!p->has_frozen || frozen, "has_frozen without frozen flags");
   SF_CHECK_ARG(p->penalty >= SF_PENALTY_NONE && p->penalty <= SF_PENALTY_STRUCTURED_TOPN, "bad penalty %d", p->penalty);
   SF_CHECK_ARG(p->hard_kind >= SF_HARD_NONE && p->hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", p->hard_kind);
+  SF_CHECK_ARG(p->gate != SF_GATE_ZSCORE, "the z-score gate form is an output of sf_gate_target only");
   if (!H) h_dtype = SF_DTYPE_F32;
   UpdateSpec us;
   if (int rc = make_update_spec(p, w_dtype, h_dtype, aux_dtype, mask_dtype, frozen_dtype, flips != nullptr, &us))
@@ -1203,6 +1220,7 @@ extern "C" int sf_glu_update_masks(const sf_mask_params* p, const void* S, int s
   SF_CHECK_ARG(p->penalty >= SF_PENALTY_NONE && p->penalty <= SF_PENALTY_STRUCTURED_TOPN && p->penalty != SF_PENALTY_NM_2_4,
                "the joint update pulls with the mid or structured_topn penalty only (got %d)", p->penalty);
   SF_CHECK_ARG(p->hard_kind >= SF_HARD_NONE && p->hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", p->hard_kind);
+  SF_CHECK_ARG(p->gate != SF_GATE_ZSCORE, "the z-score gate form is an output of sf_gate_target only");
   SF_CHECK_ARG(up_hard_kind >= SF_HARD_NONE && up_hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", up_hard_kind);
   if (up_hard_kind >= SF_HARD_NM_TAIL_KEEP && up_flips) {
     if (up_hard_n < 1 || up_hard_n > 3) {
@@ -1246,11 +1264,12 @@ extern "C" int sf_glu_update_masks(const sf_mask_params* p, const void* S, int s
 // ---------------------------------------------------------------------------
 namespace sf {
 namespace {
+// hsrc: a precomputed hard mask (hdt) used in place of the group projection (the block types).
 template <int MD, int ED>
 __global__ void __launch_bounds__(kBlock) effective_mask_kernel(const void* __restrict__ mask, void* __restrict__ eff,
                                                                 int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                                 int mix, float hx, float one_minus_hx, int kind,
-                                                                int n_keep) {
+                                                                int n_keep, const void* __restrict__ hsrc, int hdt) {
   for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
     Group g = w.group();
     const bool v = vec && g.full;
@@ -1258,7 +1277,10 @@ __global__ void __launch_bounds__(kBlock) effective_mask_kernel(const void* __re
     load4<MD>(mask, g.elem, g.n, v, m);
     if (mix) {
       float h[4];
-      hard_of_group(m, g, kind, n_keep, h);
+      if (hsrc)
+        load4_any(hsrc, hdt, g.elem, g.n, v, h);
+      else
+        hard_of_group(m, g, kind, n_keep, h);
 #pragma unroll
       for (int j = 0; j < 4; ++j) e[j] = rnd(rnd(hx * m[j], MD) + rnd(one_minus_hx * h[j], MD), MD);
     } else {
@@ -1272,13 +1294,18 @@ __global__ void __launch_bounds__(kBlock) effective_mask_kernel(const void* __re
 template <int MD>
 __global__ void __launch_bounds__(kBlock) hard_bytes_kernel(const void* __restrict__ mask, uint8_t* __restrict__ out,
                                                             int64_t cols, int64_t groups, int64_t gpr, bool vec,
-                                                            int kind, int n_keep) {
+                                                            int kind, int n_keep, const void* __restrict__ hsrc,
+                                                            int hdt) {
   for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
     Group g = w.group();
     const bool v = vec && g.full;
     float m[4], h[4];
-    load4<MD>(mask, g.elem, g.n, v, m);
-    hard_of_group(m, g, kind, n_keep, h);
+    if (hsrc) {
+      load4_any(hsrc, hdt, g.elem, g.n, v, h);
+    } else {
+      load4<MD>(mask, g.elem, g.n, v, m);
+      hard_of_group(m, g, kind, n_keep, h);
+    }
     if (v) {
       uint32_t w = 0;
 #pragma unroll
@@ -1294,9 +1321,34 @@ __global__ void __launch_bounds__(kBlock) hard_bytes_kernel(const void* __restri
 }  // namespace
 }  // namespace sf
 
+namespace sf {
+namespace {
+int effective_mask_impl(const void* mask, int mask_dtype, const void* hsrc, int hdt, void* eff, int eff_dtype,
+                        int64_t rows, int64_t cols, int mode, float hx, int hard_kind, int hard_n, int hard_m,
+                        void* stream);
+}  // namespace
+}  // namespace sf
+
 extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, int eff_dtype, int64_t rows,
                                  int64_t cols, int mode, float hx, int hard_kind, int hard_n, int hard_m,
                                  void* stream) {
+  return effective_mask_impl(mask, mask_dtype, nullptr, SF_DTYPE_F32, eff, eff_dtype, rows, cols, mode, hx, hard_kind,
+                             hard_n, hard_m, stream);
+}
+
+extern "C" int sf_effective_mask_given(const void* mask, int mask_dtype, const void* hard, int hard_dtype, void* eff,
+                                       int eff_dtype, int64_t rows, int64_t cols, int mode, float hx, void* stream) {
+  SF_CHECK_ARG(dtype_ok(hard_dtype), "bad hard-mask dtype");
+  SF_CHECK_ARG(rows == 0 || cols == 0 || hard != nullptr, "null hard mask");
+  return effective_mask_impl(mask, mask_dtype, hard, hard_dtype, eff, eff_dtype, rows, cols, mode, hx,
+                             SF_HARD_THRESHOLD, 2, 4, stream);
+}
+
+namespace sf {
+namespace {
+int effective_mask_impl(const void* mask, int mask_dtype, const void* hsrc, int hdt, void* eff, int eff_dtype,
+                        int64_t rows, int64_t cols, int mode, float hx, int hard_kind, int hard_n, int hard_m,
+                        void* stream) {
   SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
   SF_CHECK_ARG(mode == SF_EFF_SOFT || mode == SF_EFF_MIX || mode == SF_EFF_HARD, "bad effective-mask mode %d", mode);
   SF_CHECK_ARG(dtype_ok(mask_dtype) && (dtype_ok(eff_dtype) || (mode == SF_EFF_HARD && eff_dtype == SF_DTYPE_U8)),
@@ -1318,18 +1370,18 @@ extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, in
   }
   const int64_t gpr = ceil_div(cols, 4), groups = rows * gpr;
   if (eff_dtype == SF_DTYPE_U8) {
-    const bool vb = vec_ok(cols, {{mask, mask_dtype}}) && aligned(eff, 4);
+    const bool vb = vec_ok(cols, {{mask, mask_dtype}, {hsrc, hdt}}) && aligned(eff, 4);
     hipStream_t sb = static_cast<hipStream_t>(stream);
     const int gb = elementwise_grid(groups, kBlock);
     if (mask_dtype == SF_DTYPE_F32)
       hard_bytes_kernel<SF_DTYPE_F32><<<gb, kBlock, 0, sb>>>(mask, static_cast<uint8_t*>(eff), cols, groups, gpr, vb,
-                                                             hard_kind, hard_n);
+                                                             hard_kind, hard_n, hsrc, hdt);
     else
       hard_bytes_kernel<SF_DTYPE_BF16><<<gb, kBlock, 0, sb>>>(mask, static_cast<uint8_t*>(eff), cols, groups, gpr, vb,
-                                                              hard_kind, hard_n);
+                                                              hard_kind, hard_n, hsrc, hdt);
     return launch_status("sf_effective_mask");
   }
-  const bool vec = vec_ok(cols, {{mask, mask_dtype}, {eff, eff_dtype}});
+  const bool vec = vec_ok(cols, {{mask, mask_dtype}, {eff, eff_dtype}, {hsrc, hdt}});
   // (1 - hx) computed in double as in Python, then the f32 scalar of the op
   const float omh = static_cast<float>(1.0 - static_cast<double>(hx));
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1337,7 +1389,7 @@ extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, in
   const int mix = mode == SF_EFF_MIX;
 #define SF_LAUNCH_EFF(MDT, EDT)                                                                              \
   effective_mask_kernel<MDT, EDT><<<grid, kBlock, 0, st>>>(mask, eff, cols, groups, gpr, vec, mix, hx, omh, \
-                                                           hard_kind, hard_n)
+                                                           hard_kind, hard_n, hsrc, hdt)
   if (mask_dtype == SF_DTYPE_F32 && eff_dtype == SF_DTYPE_F32) SF_LAUNCH_EFF(SF_DTYPE_F32, SF_DTYPE_F32);
   else if (mask_dtype == SF_DTYPE_F32) SF_LAUNCH_EFF(SF_DTYPE_F32, SF_DTYPE_BF16);
   else if (eff_dtype == SF_DTYPE_F32) SF_LAUNCH_EFF(SF_DTYPE_BF16, SF_DTYPE_F32);
@@ -1345,6 +1397,8 @@ extern "C" int sf_effective_mask(const void* mask, int mask_dtype, void* eff, in
 #undef SF_LAUNCH_EFF
   return launch_status("sf_effective_mask");
 }
+}  // namespace
+}  // namespace sf
 
 // ---------------------------------------------------------------------------
 // Transpose of a byte mask ([rows, cols] -> [cols, rows]): the K-major byte
@@ -1402,4 +1456,443 @@ extern "C" int sf_transpose_u8(const uint8_t* src, int64_t rows, int64_t cols, u
   dim3 grid(static_cast<unsigned>(ceil_div(cols, 64)), static_cast<unsigned>(ceil_div(rows, 64)));
   transpose_u8_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(src, rows, cols, dst, vec);
   return launch_status("sf_transpose_u8");
+}
+
+// ---------------------------------------------------------------------------
+// Block hard types and block_sparse soft masks (legacy/sparse_modeling.py:
+// _blockify_tensor :460-507, block16 / block_sparse16 / block_sparse32 hard
+// projections :537-718, block-level gate :1100-1158, G blockify :1237, block
+// penalties :1298-1529, mask blockify :1598-1601).  Blocks are the bs x bs
+// tiles of the fully covered core [:rows/bs*bs, :cols/bs*bs]; block (br, bc)
+// is entry br * ib + bc of a block vector.  Elements outside the core keep
+// their value (blockify) or take a fixed one (hard masks, targets, G).
+// ---------------------------------------------------------------------------
+namespace sf {
+namespace {
+
+__device__ __forceinline__ float load1_any(const void* base, int dtype, int64_t i) {
+  return dtype == SF_DTYPE_F32 ? static_cast<const float*>(base)[i]
+                               : bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+}
+
+// One wave per block: mean of x (stat 0) or sqrt(mean(x * x)) (stat 1, the square in f32).
+// The sum runs in f64 in a fixed tree order and is rounded to f32 once.
+__global__ void __launch_bounds__(kBlock) block_stat_kernel(const void* __restrict__ x, int x_dtype, int64_t cols,
+                                                            int bs, int64_t ib, int64_t nb, int rms,
+                                                            float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int lg = bs == 16 ? 4 : 5;
+  for (int64_t b = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; b < nb; b += waves) {
+    const int64_t br = b / ib, bc = b - br * ib;
+    const int64_t base = br * bs * cols + bc * bs;
+    double acc = 0.0;
+    for (int e = lane; e < bs * bs; e += 64) {
+      float v = load1_any(x, x_dtype, base + (int64_t)(e >> lg) * cols + (e & (bs - 1)));
+      if (rms) v = v * v;
+      acc += static_cast<double>(v);
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) {
+      const float m = static_cast<float>(acc / static_cast<double>(bs * bs));
+      out[b] = rms ? sqrtf(m) : m;
+    }
+  }
+}
+
+// keep[i] = 1 for the k largest v (ordered keys: NaN largest, -0 == +0); among
+// equal values the higher index is kept first.  One workgroup: an MSB-first
+// radix select of the k-th largest key (4 passes of 8 bits over an LDS
+// histogram), then one pass in descending index order that keeps the keys
+// above it and the first `want` keys equal to it.
+constexpr int kTopkBlock = 1024;
+__global__ void __launch_bounds__(kTopkBlock) topk_keep_kernel(const float* __restrict__ v, int64_t n, int64_t k,
+                                                               float* __restrict__ keep) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t s_prefix, s_want;
+  __shared__ uint32_t wave_cnt[kTopkBlock / 64];
+  __shared__ uint32_t s_run;
+  const int tid = threadIdx.x;
+  if (k <= 0 || k >= n) {
+    for (int64_t i = tid; i < n; i += blockDim.x) keep[i] = k > 0 ? 1.0f : 0.0f;
+    return;
+  }
+  if (tid == 0) {
+    s_prefix = 0u;
+    s_want = static_cast<uint32_t>(k);
+    s_run = 0u;
+  }
+  uint32_t mask_hi = 0u;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = tid; i < 256; i += blockDim.x) hist[i] = 0u;
+    __syncthreads();
+    const uint32_t prefix = s_prefix;
+    for (int64_t i = tid; i < n; i += blockDim.x) {
+      const uint32_t key = ordered_key(v[i]);
+      if ((key & mask_hi) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t want = s_want, cum = 0u;
+      int bin = 255;
+      for (; bin > 0; --bin) {
+        if (cum + hist[bin] >= want) break;
+        cum += hist[bin];
+      }
+      s_want = want - cum;
+      s_prefix = prefix | (static_cast<uint32_t>(bin) << shift);
+    }
+    mask_hi |= 255u << shift;
+    __syncthreads();
+  }
+  const uint32_t kth = s_prefix, want = s_want;  // keep keys > kth, and `want` keys == kth
+  const int lane = tid & 63, wv = tid >> 6;
+  for (int64_t c0 = 0; c0 < n; c0 += blockDim.x) {
+    const int64_t i = n - 1 - (c0 + tid);
+    uint32_t key = 0u;
+    bool eq = false;
+    if (i >= 0) {
+      key = ordered_key(v[i]);
+      eq = key == kth;
+    }
+    const uint64_t bal = __ballot(eq);
+    const uint32_t below = static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)));
+    if (lane == 0) wave_cnt[wv] = static_cast<uint32_t>(__popcll(bal));
+    __syncthreads();
+    uint32_t before = s_run;
+    for (int w = 0; w < wv; ++w) before += wave_cnt[w];
+    if (i >= 0) keep[i] = (key > kth || (eq && before + below < want)) ? 1.0f : 0.0f;
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t t = 0u;
+      for (int w = 0; w < (int)(blockDim.x / 64); ++w) t += wave_cnt[w];
+      s_run += t;
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ int wave_sum_i(int x) {
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// block16: top-k of each 16 x 16 tile, one wave per tile, 4 consecutive
+// elements of a tile row per lane (lane L holds tile positions 4L .. 4L + 3).
+// The k-th largest key comes from a bitwise search over the 32 key bits;
+// equal keys are kept from the highest tile position down.
+template <int XD, int OD>
+__global__ void __launch_bounds__(kBlock) tile_topk_kernel(const void* __restrict__ x, int64_t cols, int64_t ib,
+                                                           int64_t nb, int k, bool vec, void* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t b = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; b < nb; b += waves) {
+    const int64_t br = b / ib, bc = b - br * ib;
+    const int64_t e0 = (br * 16 + (lane >> 2)) * cols + bc * 16 + 4 * (lane & 3);
+    float xv[4], o[4];
+    load4<XD>(x, e0, 4, vec, xv);
+    uint32_t key[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) key[j] = ordered_key(xv[j]);
+    uint32_t kth = 0u;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = kth | (1u << bit);
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c += key[j] >= cand ? 1 : 0;
+      if (wave_sum_i(c) >= k) kth = cand;
+    }
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      gt += key[j] > kth ? 1 : 0;
+      eq += key[j] == kth ? 1 : 0;
+    }
+    const int want = k - wave_sum_i(gt);
+    // equal keys at higher tile positions: lanes above this one, then j' > j inside it
+    int incl = eq;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    const int total = __shfl(incl, 63, 64);
+    int above = total - incl;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      const bool e = key[j] == kth;
+      o[j] = (key[j] > kth || (e && above < want)) ? 1.0f : 0.0f;
+      above += e ? 1 : 0;
+    }
+    store4<OD>(out, e0, 4, vec, o);
+  }
+}
+
+// out = val on the elements outside the core (rows >= of, or cols >= inf).
+template <int OD>
+__global__ void __launch_bounds__(kBlock) edge_fill_kernel(void* __restrict__ out, int64_t rows, int64_t cols,
+                                                           int64_t of, int64_t inf, float val) {
+  const int64_t n1 = (rows - of) * cols, w2 = cols - inf, n = n1 + of * w2;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int64_t e;
+    if (i < n1) {
+      e = of * cols + i;
+    } else {
+      const int64_t j = i - n1, r = j / w2;
+      e = r * cols + inf + (j - r * w2);
+    }
+    if (OD == SF_DTYPE_F32)
+      static_cast<float*>(out)[e] = val;
+    else
+      static_cast<uint16_t*>(out)[e] = f32_to_bf16(val);
+  }
+}
+
+// Expand per-block values over the core: out = rnd(f(bvals[block])), f the
+// identity or, with tau, sigmoid((b - tau) / denom) in f32.  Outside the core
+// the element keeps its value (edge_write 0) or becomes edge_val.  Where
+// ov_flags != 0 the element takes rnd(ov_src) instead (frozen override).
+struct FillSpec {
+  int64_t of, inf, ib;
+  int lg;  // log2(bs)
+  int edge_write;
+  float edge_val;
+  float denom, rdenom;
+  int ov_src_dt, ov_flags_dt;
+};
+
+template <int OD>
+__global__ void __launch_bounds__(kBlock) block_fill_kernel(FillSpec f, const float* __restrict__ bvals,
+                                                            const float* __restrict__ tau_p, void* __restrict__ out,
+                                                            const void* __restrict__ ov_src,
+                                                            const void* __restrict__ ov_flags, int64_t cols,
+                                                            int64_t groups, int64_t gpr, bool vec) {
+  const float tau = tau_p ? *tau_p : 0.0f;
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
+    const bool v = vec && g.full;
+    float o[4], fz[4] = {0, 0, 0, 0}, src[4];
+    const bool row_in = g.row < f.of;
+    if (!f.edge_write) load4<OD>(out, g.elem, g.n, v, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t c = g.col + j;
+      if (row_in && c < f.inf) {
+        float b = bvals[(g.row >> f.lg) * f.ib + (c >> f.lg)];
+        if (tau_p) b = sigmoidf_(div_by(b - tau, f.denom, f.rdenom));
+        o[j] = rndc<OD>(b);
+      } else if (f.edge_write) {
+        o[j] = rndc<OD>(f.edge_val);
+      }
+    }
+    if (ov_flags) {
+      load4_any(ov_flags, f.ov_flags_dt, g.elem, g.n, v, fz);
+      load4_any(ov_src, f.ov_src_dt, g.elem, g.n, v, src);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (fz[j] != 0.0f) o[j] = rndc<OD>(src[j]);
+    }
+    store4<OD>(out, g.elem, g.n, v, o);
+  }
+}
+
+// A gate target G already in memory (the staged block path): penalty pull
+// (explicit target or the in-group modes), clamp, binarisation push, EMA and,
+// with do_freeze, the freeze snaps and flags.
+template <int MD, int SD>
+__global__ void __launch_bounds__(kBlock) apply_gate_kernel(UpdateSpec us, const void* __restrict__ G,
+                                                            const void* __restrict__ target, int target_dt,
+                                                            void* __restrict__ mask, void* __restrict__ frozen,
+                                                            int do_freeze, int64_t cols, int64_t groups, int64_t gpr,
+                                                            bool vec) {
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
+    const bool v = vec && g.full;
+    float gv[4], mp[4], tg[4] = {0, 0, 0, 0}, mn[4], fz[4] = {0, 0, 0, 0};
+    load4<SD>(G, g.elem, g.n, v, gv);
+    load4<MD>(mask, g.elem, g.n, v, mp);
+    if (target) load4_any(target, target_dt, g.elem, g.n, v, tg);
+    pull_and_push<MD, SD>(us, g, mp, gv, tg);
+    ema_of<MD>(us, mp, gv, mn);
+    if (do_freeze) {
+      if (us.gs.has_frozen) load4_any(frozen, us.gs.frozen_dtype, g.elem, g.n, v, fz);
+      freeze_group(us, g, v, mn, fz, frozen);
+    }
+    store4<MD>(mask, g.elem, g.n, v, mn);
+  }
+}
+
+template <int MD>
+__global__ void __launch_bounds__(kBlock) freeze_kernel(UpdateSpec us, void* __restrict__ mask,
+                                                        void* __restrict__ frozen, int64_t cols, int64_t groups,
+                                                        int64_t gpr, bool vec) {
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
+    const bool v = vec && g.full;
+    float mn[4], fz[4] = {0, 0, 0, 0};
+    load4<MD>(mask, g.elem, g.n, v, mn);
+    if (us.gs.has_frozen) load4_any(frozen, us.gs.frozen_dtype, g.elem, g.n, v, fz);
+    freeze_group(us, g, v, mn, fz, frozen);
+    store4<MD>(mask, g.elem, g.n, v, mn);
+  }
+}
+
+int check_block(int64_t rows, int64_t cols, int bs) {
+  SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  SF_CHECK_ARG(bs == 16 || bs == 32, "block size %d: only 16 and 32 exist", bs);
+  return SF_OK;
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" int sf_block_stat(const void* x, int x_dtype, int64_t rows, int64_t cols, int bs, int stat, float* out,
+                             void* stream) {
+  if (int rc = check_block(rows, cols, bs)) return rc;
+  SF_CHECK_ARG(dtype_ok(x_dtype), "bad dtype");
+  SF_CHECK_ARG(stat == SF_BLOCK_MEAN || stat == SF_BLOCK_RMS, "bad block statistic %d", stat);
+  const int64_t ob = rows / bs, ib = cols / bs, nb = ob * ib;
+  if (nb == 0) return SF_OK;
+  SF_CHECK_ARG(x && out, "null tensor");
+  block_stat_kernel<<<elementwise_grid(nb * 64, kBlock), kBlock, 0, static_cast<hipStream_t>(stream)>>>(
+      x, x_dtype, cols, bs, ib, nb, stat == SF_BLOCK_RMS, out);
+  return launch_status("sf_block_stat");
+}
+
+extern "C" int sf_topk_keep(const float* v, int64_t n, int64_t k, float* keep, void* stream) {
+  SF_CHECK_ARG(n >= 0, "negative length");
+  if (n == 0) return SF_OK;
+  SF_CHECK_ARG(v && keep, "null tensor");
+  SF_CHECK_ARG(n < (1ll << 31), "top-k over more than 2^31 entries");
+  topk_keep_kernel<<<1, kTopkBlock, 0, static_cast<hipStream_t>(stream)>>>(v, n, k, keep);
+  return launch_status("sf_topk_keep");
+}
+
+extern "C" int sf_tile_topk(const void* x, int x_dtype, int64_t rows, int64_t cols, int bs, int64_t k, void* out,
+                            int out_dtype, void* stream) {
+  if (int rc = check_block(rows, cols, bs)) return rc;
+  SF_CHECK_ARG(dtype_ok(x_dtype) && dtype_ok(out_dtype), "bad dtype");
+  if (bs != 16) {
+    set_error("per-tile top-k is built for 16 x 16 tiles (block16) only");
+    return SF_ERR_UNSUPPORTED;
+  }
+  if (rows == 0 || cols == 0) return SF_OK;
+  SF_CHECK_ARG(x && out, "null tensor");
+  const int64_t of = rows / 16 * 16, inf = cols / 16 * 16, ib = inf / 16, nb = (of / 16) * ib;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = vec_ok(cols, {{x, x_dtype}, {out, out_dtype}});
+  if (nb > 0) {
+    // k = 0 / 256 need no special case: the search then yields all zeros / all ones
+    const int kk = static_cast<int>(k <= 0 ? 0 : (k >= 256 ? 256 : k));
+#define SF_LAUNCH_TILE(XD, OD) \
+  tile_topk_kernel<XD, OD><<<elementwise_grid(nb * 64, kBlock), kBlock, 0, st>>>(x, cols, ib, nb, kk, vec, out)
+    if (x_dtype == SF_DTYPE_F32 && out_dtype == SF_DTYPE_F32) SF_LAUNCH_TILE(SF_DTYPE_F32, SF_DTYPE_F32);
+    else if (x_dtype == SF_DTYPE_F32) SF_LAUNCH_TILE(SF_DTYPE_F32, SF_DTYPE_BF16);
+    else if (out_dtype == SF_DTYPE_F32) SF_LAUNCH_TILE(SF_DTYPE_BF16, SF_DTYPE_F32);
+    else SF_LAUNCH_TILE(SF_DTYPE_BF16, SF_DTYPE_BF16);
+#undef SF_LAUNCH_TILE
+  }
+  if (of < rows || inf < cols) {
+    const int64_t ne = (rows - of) * cols + of * (cols - inf);
+    if (out_dtype == SF_DTYPE_F32)
+      edge_fill_kernel<SF_DTYPE_F32><<<elementwise_grid(ne, kBlock), kBlock, 0, st>>>(out, rows, cols, of, inf, 1.0f);
+    else
+      edge_fill_kernel<SF_DTYPE_BF16><<<elementwise_grid(ne, kBlock), kBlock, 0, st>>>(out, rows, cols, of, inf, 1.0f);
+  }
+  return launch_status("sf_tile_topk");
+}
+
+extern "C" int sf_block_fill(const float* bvals, int64_t rows, int64_t cols, int bs, const float* tau, float temperature,
+                             void* out, int out_dtype, int edge_write, float edge_val, const void* ov_src,
+                             int ov_src_dtype, const void* ov_flags, int ov_flags_dtype, void* stream) {
+  if (int rc = check_block(rows, cols, bs)) return rc;
+  SF_CHECK_ARG(dtype_ok(out_dtype), "bad dtype");
+  SF_CHECK_ARG(!ov_flags || (ov_src && dtype_ok(ov_src_dtype) && dtype_ok(ov_flags_dtype)), "bad override operands");
+  if (rows == 0 || cols == 0) return SF_OK;
+  SF_CHECK_ARG(out, "null tensor");
+  FillSpec f;
+  f.of = rows / bs * bs;
+  f.inf = cols / bs * bs;
+  f.ib = f.inf / bs;
+  SF_CHECK_ARG(bvals || f.of == 0 || f.inf == 0, "null block values");
+  f.lg = bs == 16 ? 4 : 5;
+  f.edge_write = edge_write;
+  f.edge_val = edge_val;
+  f.denom = temperature + 1e-8f;
+  f.rdenom = 1.0f / f.denom;
+  f.ov_src_dt = ov_src_dtype;
+  f.ov_flags_dt = ov_flags_dtype;
+  const int64_t gpr = ceil_div(cols, 4), groups = rows * gpr;
+  const bool vec = vec_ok(cols, {{out, out_dtype}, {ov_flags ? ov_src : nullptr, ov_src_dtype},
+                                 {ov_flags, ov_flags_dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  if (out_dtype == SF_DTYPE_F32)
+    block_fill_kernel<SF_DTYPE_F32><<<grid, kBlock, 0, st>>>(f, bvals, tau, out, ov_src, ov_flags, cols, groups, gpr,
+                                                             vec);
+  else
+    block_fill_kernel<SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(f, bvals, tau, out, ov_src, ov_flags, cols, groups, gpr,
+                                                              vec);
+  return launch_status("sf_block_fill");
+}
+
+extern "C" int sf_apply_gate(const sf_mask_params* p, const void* G, const void* target, int target_dtype, void* mask,
+                             int mask_dtype, void* frozen, int frozen_dtype, int do_freeze, void* stream) {
+  if (int rc = check_common(p)) return rc;
+  SF_CHECK_ARG(dtype_ok(mask_dtype) && (!target || dtype_ok(target_dtype)), "bad dtype");
+  SF_CHECK_ARG(p->penalty >= SF_PENALTY_NONE && p->penalty <= SF_PENALTY_TARGET, "bad penalty %d", p->penalty);
+  SF_CHECK_ARG(p->penalty != SF_PENALTY_TARGET || p->penalty_coef == 0.0f || target, "target penalty needs a target");
+  SF_CHECK_ARG(!do_freeze || !p->has_frozen || frozen, "has_frozen without frozen flags");
+  UpdateSpec us;
+  sf_mask_params q = *p;
+  q.gate = SF_GATE_UNSTRUCTURED;  // the gate form is not used here
+  q.beta_struct = 0.0f;
+  if (int rc = make_update_spec(&q, SF_DTYPE_F32, SF_DTYPE_F32, SF_DTYPE_F32, mask_dtype, frozen_dtype, false, &us))
+    return rc;
+  us.apply_freeze = do_freeze && p->apply_freeze;
+  if (p->rows == 0 || p->cols == 0) return SF_OK;
+  SF_CHECK_ARG(G && mask, "null tensor");
+  const int64_t gpr = ceil_div(p->cols, 4), groups = p->rows * gpr;
+  const bool vec = vec_ok(p->cols, {{G, p->score_dtype}, {mask, mask_dtype}, {target, target_dtype},
+                                    {us.apply_freeze && p->has_frozen ? frozen : nullptr, frozen_dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  const int fr = us.apply_freeze;
+#define SF_LAUNCH_APPLY(MDT, SDT)                                                                             \
+  apply_gate_kernel<MDT, SDT><<<grid, kBlock, 0, st>>>(us, G, target, target_dtype, mask, frozen, fr, p->cols, \
+                                                       groups, gpr, vec)
+  const bool sf32 = p->score_dtype == SF_DTYPE_F32;
+  if (mask_dtype == SF_DTYPE_F32) {
+    if (sf32) SF_LAUNCH_APPLY(SF_DTYPE_F32, SF_DTYPE_F32);
+    else SF_LAUNCH_APPLY(SF_DTYPE_F32, SF_DTYPE_BF16);
+  } else {
+    if (sf32) SF_LAUNCH_APPLY(SF_DTYPE_BF16, SF_DTYPE_F32);
+    else SF_LAUNCH_APPLY(SF_DTYPE_BF16, SF_DTYPE_BF16);
+  }
+#undef SF_LAUNCH_APPLY
+  return launch_status("sf_apply_gate");
+}
+
+extern "C" int sf_freeze_mask(const sf_mask_params* p, void* mask, int mask_dtype, void* frozen, int frozen_dtype,
+                              void* stream) {
+  if (int rc = check_common(p)) return rc;
+  SF_CHECK_ARG(dtype_ok(mask_dtype), "bad dtype");
+  SF_CHECK_ARG(!p->has_frozen || frozen, "has_frozen without frozen flags");
+  UpdateSpec us;
+  sf_mask_params q = *p;
+  q.gate = SF_GATE_UNSTRUCTURED;
+  q.beta_struct = 0.0f;
+  q.penalty = SF_PENALTY_NONE;
+  if (int rc = make_update_spec(&q, SF_DTYPE_F32, SF_DTYPE_F32, SF_DTYPE_F32, mask_dtype, frozen_dtype, false, &us))
+    return rc;
+  if (p->rows == 0 || p->cols == 0 || !p->apply_freeze) return SF_OK;
+  SF_CHECK_ARG(mask, "null tensor");
+  const int64_t gpr = ceil_div(p->cols, 4), groups = p->rows * gpr;
+  const bool vec = vec_ok(p->cols, {{mask, mask_dtype}, {p->has_frozen ? frozen : nullptr, frozen_dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  if (mask_dtype == SF_DTYPE_F32)
+    freeze_kernel<SF_DTYPE_F32><<<grid, kBlock, 0, st>>>(us, mask, frozen, p->cols, groups, gpr, vec);
+  else
+    freeze_kernel<SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(us, mask, frozen, p->cols, groups, gpr, vec);
+  return launch_status("sf_freeze_mask");
 }

@@ -45,7 +45,8 @@ def _joint_params(gate, step: int, rows: int, cols: int, mask_dtype: torch.dtype
     p.movement_temp = 1.0
     p.beta_struct = gate._beta_structural(step) if cols >= M else 0.0
     p.has_frozen = int(has_frozen)
-    kind, hn, hm = gate._hard_kind()
+    # block hard types count flips from whole-tensor projections after the pass
+    kind, hn, hm = (L.HARD_THRESHOLD, 2, 4) if gate._is_block_hard() else gate._hard_kind()
     p.hard_kind, p.hard_n, p.hard_m = kind, hn, hm
     p.penalty, p.penalty_coef = L.PENALTY_NONE, 0.0
     lam = float(lambda_mid) if lambda_mid is not None else 0.0
@@ -129,9 +130,14 @@ def glu_joint_update(gate_module, up_module, step, lambda_mid, sample_idx=None):
         tau = K.tau_quantile(p, ops_s, stats, gate_module._effective_sparsity(step), sample_idx)
         if not getattr(gate_module, "_in_summon_context", False):
             tau = _all_reduce_mean(tau)
-    up_kind, up_n, _ = up_module._hard_kind()
+    up_kind, up_n, _ = (L.HARD_THRESHOLD, 2, 4) if up_module._is_block_hard() else up_module._hard_kind()
     flips = torch.zeros(2, dtype=torch.int64, device=S.device)
-    K.glu_update_masks(p, S, mask_g, mask_u, frozen, stats, tau, up_kind, up_n, flips[0:1], flips[1:2])
+    prev = [m.clone() if mod._is_block_hard() else None for m, mod in ((mask_g, gate_module), (mask_u, up_module))]
+    K.glu_update_masks(p, S, mask_g, mask_u, frozen, stats, tau, up_kind, up_n,
+                       None if prev[0] is not None else flips[0:1], None if prev[1] is not None else flips[1:2])
+    for i, (m, mod) in enumerate(((mask_g, gate_module), (mask_u, up_module))):
+        if prev[i] is not None:
+            mod._flip_count(prev[i], m, flips[i:i + 1])
 
     hx = gate_module._hardening_schedule(step)
     gate_module.hardening_x = hx

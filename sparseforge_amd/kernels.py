@@ -169,6 +169,89 @@ def update_mask(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: to
 
 
 # ---------------------------------------------------------------------------
+# block hard types and block_sparse masks (sparse_modeling.py:460-507, :537-718,
+# :1100-1158, :1237, :1298-1529, :1598-1601)
+# ---------------------------------------------------------------------------
+def block_stat(x: torch.Tensor, bs: int, stat: int) -> torch.Tensor:
+    """Per-block mean (L.BLOCK_MEAN) or RMS (L.BLOCK_RMS) of the core of x: f32 [(rows//bs) * (cols//bs)]."""
+    dev = L.require_device(x)
+    if x.dim() != 2:
+        raise ValueError("block_stat expects a 2-D tensor")
+    x = x.contiguous()
+    rows, cols = x.shape
+    out = torch.empty((rows // bs) * (cols // bs), dtype=torch.float32, device=dev)
+    with _prof.region("sf_block_stat", x.numel() * x.element_size(), "B", dev):
+        L.check(L.lib().sf_block_stat(L.ptr(x), L.dtype_code(x), rows, cols, bs, stat, L.ptr(out), L.stream(dev)),
+                "sf_block_stat")
+    return out
+
+
+def topk_keep(v: torch.Tensor, k: int) -> torch.Tensor:
+    """f32 flags of the k largest entries of a 1-D f32 tensor (ties: higher index first)."""
+    dev = L.require_device(v)
+    if v.dim() != 1 or v.dtype != torch.float32:
+        raise ValueError("topk_keep expects a 1-D float32 tensor")
+    keep = torch.empty_like(v)
+    L.check(L.lib().sf_topk_keep(L.ptr(v), v.numel(), int(k), L.ptr(keep), L.stream(dev)), "sf_topk_keep")
+    return keep
+
+
+def tile_topk(x: torch.Tensor, k: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """block16 projection: top-k of each 16 x 16 tile of the core -> 1, rest 0, outside the core 1."""
+    dev = L.require_device(x)
+    x = x.contiguous()
+    rows, cols = x.shape
+    out = torch.empty(rows, cols, dtype=out_dtype, device=dev)
+    with _prof.region("sf_tile_topk", x.numel() * (x.element_size() + out.element_size()), "B", dev):
+        L.check(L.lib().sf_tile_topk(L.ptr(x), L.dtype_code(x), rows, cols, 16, int(k), L.ptr(out),
+                                     L.dtype_code(out), L.stream(dev)), "sf_tile_topk")
+    return out
+
+
+def block_fill(bvals: torch.Tensor | None, out: torch.Tensor, bs: int, tau: torch.Tensor | None = None,
+               temperature: float = 0.0, edge_val: float | None = None, ov_src: torch.Tensor | None = None,
+               ov_flags: torch.Tensor | None = None) -> torch.Tensor:
+    """out[core] = bvals[block] (or sigmoid((b - tau) / (T + 1e-8)) with tau), cast to out's dtype, in place.
+
+    edge_val None leaves the elements outside the core unchanged; ov_flags != 0 selects ov_src instead."""
+    dev = L.require_device(out, bvals, tau, ov_src, ov_flags)
+    if not out.is_contiguous() or out.dim() != 2:
+        raise ValueError("block_fill writes a contiguous 2-D tensor")
+    rows, cols = out.shape
+    for t in (ov_src, ov_flags):
+        if t is not None and (tuple(t.shape) != (rows, cols) or not t.is_contiguous()):
+            raise ValueError("override operands must be contiguous and shaped like out")
+    L.check(L.lib().sf_block_fill(L.ptr(bvals), rows, cols, bs, L.ptr(tau), float(temperature), L.ptr(out),
+                                  L.dtype_code(out), int(edge_val is not None),
+                                  float(edge_val if edge_val is not None else 0.0), L.ptr(ov_src),
+                                  L.dtype_code(ov_src) if ov_src is not None else L.DT_F32, L.ptr(ov_flags),
+                                  L.dtype_code(ov_flags) if ov_flags is not None else L.DT_F32, L.stream(dev)),
+            "sf_block_fill")
+    return out
+
+
+def apply_gate(p: L.MaskParams, G: torch.Tensor, target: torch.Tensor | None, mask: torch.Tensor,
+               frozen: torch.Tensor | None, do_freeze: bool) -> None:
+    dev = L.require_device(G, target, mask, frozen)
+    nbytes = G.numel() * G.element_size() + 2 * mask.numel() * mask.element_size()
+    if target is not None:
+        nbytes += target.numel() * target.element_size()
+    with _prof.region("sf_apply_gate", nbytes, "B", dev):
+        L.check(L.lib().sf_apply_gate(ctypes.byref(p), L.ptr(G), L.ptr(target),
+                                      L.dtype_code(target) if target is not None else L.DT_F32, L.ptr(mask),
+                                      L.dtype_code(mask), L.ptr(frozen),
+                                      L.dtype_code(frozen) if frozen is not None else L.DT_F32, int(do_freeze),
+                                      L.stream(dev)), "sf_apply_gate")
+
+
+def freeze_mask(p: L.MaskParams, mask: torch.Tensor, frozen: torch.Tensor | None) -> None:
+    dev = L.require_device(mask, frozen)
+    L.check(L.lib().sf_freeze_mask(ctypes.byref(p), L.ptr(mask), L.dtype_code(mask), L.ptr(frozen),
+                                   L.dtype_code(frozen) if frozen is not None else L.DT_F32, L.stream(dev)),
+            "sf_freeze_mask")
+
+
+# ---------------------------------------------------------------------------
 # GLU gate/up joint update (legacy/utils.py:363-643)
 # ---------------------------------------------------------------------------
 def joint_scores(pg: L.MaskParams, gate: MaskOperands, pu: L.MaskParams, up: MaskOperands,

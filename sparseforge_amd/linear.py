@@ -150,6 +150,23 @@ def effective_mask(mask: torch.Tensor, dtype: torch.dtype, mode: str, hx: float,
     return eff
 
 
+def effective_mask_given(mask: torch.Tensor, hard: torch.Tensor, dtype: torch.dtype, mode: str,
+                         hx: float) -> torch.Tensor:
+    """effective_mask with the hard projection passed in (the block hard types)."""
+    dev = L.require_device(mask, hard)
+    if hard.shape != mask.shape:
+        raise ValueError("hard mask shape differs from the soft mask")
+    eff = torch.empty(mask.shape, dtype=dtype, device=dev)
+    m = {"mix": L.EFF_MIX, "hard": L.EFF_HARD}.get(mode, L.EFF_SOFT)
+    code = L.DT_U8 if dtype == torch.uint8 else L.dtype_code(eff)
+    nbytes = mask.numel() * (mask.element_size() + hard.element_size() + eff.element_size())
+    with _prof.region("sf_effective_mask", nbytes, "B", dev):
+        L.check(L.lib().sf_effective_mask_given(L.ptr(mask), L.dtype_code(mask), L.ptr(hard), L.dtype_code(hard),
+                                                L.ptr(eff), code, mask.shape[0], mask.shape[1], m, float(hx),
+                                                L.stream(dev)), "sf_effective_mask_given")
+    return eff
+
+
 def transpose_u8(E: torch.Tensor) -> torch.Tensor:
     """[rows, cols] uint8 -> its transpose [cols, rows] (sf_transpose_u8)."""
     dev = L.require_device(E)
@@ -319,11 +336,12 @@ def _compute_dtype(x: torch.Tensor, W: torch.Tensor) -> torch.dtype:
 
 
 def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale, P=None, S=None, decay=0.0,
-                  eff=None):
+                  eff=None, hard=None):
     """y = x (W.E.s)^T + (x P^T) S^T + b with STE gradients.
 
     mask_mode: 'none' (E = 1), 'soft' (E = mask) or 'mix' (E = hx*mask + (1-hx)*hard(mask)).
     eff: a precomputed E in the compute dtype (skips the mask pass).
+    hard: a precomputed hard(mask) (block hard types); else hard_kind / hard_n project per group.
     """
     L.require_device(x, weight, bias, mask, P, S)
     dt = _compute_dtype(x, weight)
@@ -339,7 +357,10 @@ def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale
     if eff is None and mask_mode != "none":
         if mask_mode == "mix" and hx <= 0.0 and scale == 1.0:
             # E = hard(mask) exactly: staged as a byte and-mask (W * 1 = W, W * 0 = 0)
-            eff = effective_mask(mask, torch.uint8, "hard", 0.0, hard_kind, hard_n)
+            eff = (effective_mask_given(mask, hard, torch.uint8, "hard", 0.0) if hard is not None
+                   else effective_mask(mask, torch.uint8, "hard", 0.0, hard_kind, hard_n))
+        elif hard is not None and mask_mode == "mix":
+            eff = effective_mask_given(mask, hard, dt, mask_mode, hx)
         else:
             eff = effective_mask(mask, dt, mask_mode, hx, hard_kind, hard_n)
     if mask_mode == "none":
