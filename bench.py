@@ -20,6 +20,11 @@ Metric (BASELINE.json): SparseLinear fwd+bwd TFLOP/s at LLaMA-2-7B shapes;
 * ``adamw`` -- one step = the fused mask-aware AdamW update of every masked
   linear of the 7B model (f32 master weight, bf16 gradient, f32 moments and
   soft mask, bf16 working copy written back): 32 B per parameter.
+* ``block_sparse`` -- fwd + dx + SDDMM dW of a block-sparse-16 linear at the
+  gate/up shape, block densities 0.5 and 0.25, kept-block FLOPs.
+* ``distill_kl`` -- the fused distillation KL of Distill_Model: forward and
+  student gradient over bf16 logits [16384, 32000]; GB/s counts 10 B per
+  logit (forward reads s, t; backward reads s, t and writes ds).
 * ``roofline`` -- the dominant kernel (the sf_gemm MFMA GEMM): algorithmic
   FLOPs of the step over the summed device time of its sf_gemm launches,
   timed with HIP events on the launch stream inside the timed region.
@@ -230,6 +235,47 @@ def bsr_leg(torch, dev, tokens: int, density: float, steps: int, warmup: int) ->
     return res
 
 
+KL_SHAPE = (8 * 2048, 32000)  # student / teacher logits of the distillation config (batch 8 x seq 2048, vocab 32000)
+
+
+def kl_leg(torch, dev, steps: int, warmup: int = 2) -> dict:
+    """Distillation KL forward + student gradient over bf16 logits [16384, 32000]."""
+    from sparseforge_amd import profiling as prof
+    from sparseforge_amd.distill import chunked_kl_loss
+
+    gen = torch.Generator(device=dev).manual_seed(5)
+    s = (torch.randn(KL_SHAPE, generator=gen, device=dev) * 4).to(torch.bfloat16).requires_grad_(True)
+    t = (torch.randn(KL_SHAPE, generator=gen, device=dev) * 4).to(torch.bfloat16)
+
+    def step():
+        s.grad = None
+        chunked_kl_loss(s, t, 2).backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with prof.kernel_timer() as kt:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+    n = s.numel()
+    nbytes = n * 2 * (2 + 3)  # forward reads s, t; backward reads s, t and writes ds (bf16)
+    ks = kt.summary()
+    f, b = ks["sf_kl_forward"], ks["sf_kl_backward"]
+    res = {"value": round(nbytes * steps / el / 1e9, 2), "unit": "GB/s", "shape": list(KL_SHAPE), "dtype": "bf16",
+           "ms_per_step": round(el * 1e3 / steps, 4), "bytes_per_element": 10,
+           "roofline": {"bound": "hbm", "kernel": "sf_kl_forward", "achieved": round(f.rate / 1e9, 2),
+                        "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(f.rate / 1e9 / PEAK_HBM_GBS, 4),
+                        "avg_launch_ms": round(f.avg_ms, 4)},
+           "backward": {"kernel": "sf_kl_backward", "achieved": round(b.rate / 1e9, 2), "unit": "GB/s",
+                        "avg_launch_ms": round(b.avg_ms, 4)}}
+    log(f"kl: {res['ms_per_step']:.3f} ms/step (fwd + grad), {res['value']:.0f} GB/s; sf_kl_forward "
+        f"{f.rate / 1e9:.0f} GB/s, sf_kl_backward {b.rate / 1e9:.0f} GB/s")
+    return res
+
+
 def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
     import numpy as np
 
@@ -328,6 +374,7 @@ def main(argv=None) -> int:
     ap.add_argument("--mask-steps", type=int, default=10)
     ap.add_argument("--adamw-steps", type=int, default=5)
     ap.add_argument("--bsr-steps", type=int, default=5, help="steps of the block-sparse leg (0 skips it)")
+    ap.add_argument("--kl-steps", type=int, default=10, help="steps of the distillation-KL leg (0 skips it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--calib", action="store_true",
                     help="first run one plain 256 MiB device copy (a known-size reference for HBM byte counters)")
@@ -452,6 +499,9 @@ def main(argv=None) -> int:
     bsr = [bsr_leg(torch, dev, a.tokens, d, a.bsr_steps, 2) for d in (0.5, 0.25)] if a.bsr_steps > 0 else []
     torch.cuda.empty_cache()
 
+    kl = kl_leg(torch, dev, a.kl_steps) if a.kl_steps > 0 else None
+    torch.cuda.empty_cache()
+
     traffic = profiled_traffic()
     out = {
         "metric": "SparseLinear fwd+bwd TFLOP/s @7B shapes; 2:4 mask-update HBM GB/s",
@@ -498,6 +548,8 @@ def main(argv=None) -> int:
     }
     if bsr:
         out["block_sparse"] = bsr
+    if kl:
+        out["distill_kl"] = kl
     if not a.no_cpu:
         log("timing CPU baseline (numpy oracle)")
         out["cpu_baseline"] = cpu_baseline()

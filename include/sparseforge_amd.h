@@ -304,6 +304,40 @@ int sf_effective_mask(const void* mask, int mask_dtype, void* eff, int eff_dtype
 int sf_effective_mask_given(const void* mask, int mask_dtype, const void* hard, int hard_dtype, void* eff,
                             int eff_dtype, int64_t rows, int64_t cols, int mode, float hx, void* stream);
 
+/* ---- distillation KL (Distill_Model.kl_loss, legacy/sparse_modeling.py:1749-1828) ---- */
+
+/* Token rows per chunk of the reference's loop for a vocabulary size: 128 above
+ * 100000, 512 above 50000, else 2048 (:1772-1777). */
+int64_t sf_kl_chunk_rows(int64_t vocab);
+
+/* Workspace bytes of sf_kl_forward for `rows` token rows. */
+size_t sf_kl_workspace_size(int64_t rows);
+
+/*
+ * KL(P_teacher || Q_student) of Distill_Model.kl_loss: logits [rows, vocab]
+ * (dtype), clamped to +-100 and divided by `temperature`, log-softmax per row;
+ * per chunk of `chunk_rows` rows the sum of p (log p - log q) is added unless a
+ * log-probability of the chunk is NaN or the sum is not finite; the loss
+ * (total * T^2 / rows in f32) is written to out[0] in out_dtype, or 0 if not
+ * finite.  row_lse: device double[rows][2] = log-sum-exp of student and teacher
+ * rows; row_scale: device float[rows] = T / rows for rows of kept chunks, else
+ * 0; both are inputs of sf_kl_backward.  Sums run in f64; the reference sums
+ * in f32, so losses agree to about 1e-6 relative.
+ */
+int sf_kl_forward(const void* student, const void* teacher, int dtype, int64_t rows, int64_t vocab,
+                  float temperature, int64_t chunk_rows, void* out, int out_dtype, double* row_lse,
+                  float* row_scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Gradient of that loss with respect to the student logits (the autograd of
+ * the reference's chunk loop): grad_student = g * row_scale[r] * (q - p) where
+ * -100 <= s <= 100, else 0 (clamp's gradient), in the logits dtype.
+ * grad_out: the loss gradient g (device scalar, grad_out_dtype).
+ */
+int sf_kl_backward(const void* student, const void* teacher, int dtype, int64_t rows, int64_t vocab,
+                   float temperature, const double* row_lse, const float* row_scale, const void* grad_out,
+                   int grad_out_dtype, void* grad_student, void* stream);
+
 /* ---- GEMM engine (FusedMaskedLinearSTE, :56-132, and the SLoRB F.linear pair, :790-794) */
 #define SF_LAYOUT_K 0  /* operand stored K-contiguous: X[row * ld + k]                        */
 #define SF_LAYOUT_MN 1 /* operand stored M/N-contiguous: X[k * ld + row] (a transposed view)  */

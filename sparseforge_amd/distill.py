@@ -1,36 +1,68 @@
-"""Distillation KL of Distill_Model (legacy/sparse_modeling.py:1749-1828).
+"""Distillation KL of Distill_Model (legacy/sparse_modeling.py:1749-1828) on the HIP kernels.
 
 KL(P_teacher || Q_student) at temperature T over the vocabulary, logits
-clamped to +-100, computed in float32 chunks of tokens; a chunk whose
-log-probabilities contain NaN is skipped, a non-finite chunk sum is dropped,
-and the total is scaled by T^2 / num_tokens.  This wrapper sits at the edge
-of the hot path (after the student forward) and uses torch's device ops.
+clamped to +-100; per chunk of token rows (sf_kl_chunk_rows: 2048, 512 or 128
+by vocabulary size) a chunk with a NaN log-probability is skipped and a
+non-finite chunk sum dropped; the total is scaled by T^2 / tokens and cast to
+the student dtype (0 if not finite).  One fused pass reads both logit rows
+(sf_kl_forward); the backward re-reads them (sf_kl_backward) and gives the
+student gradient g (T / tokens) (q - p) inside the clamp range.  The teacher
+takes no gradient (the reference computes it under no_grad).
+
+Difference from the reference: for float32 logits the reference's
+`.float().clamp_().mul_()` rewrites the caller's tensors in place; here the
+inputs are left unchanged (the loss is the same).
 """
 from __future__ import annotations
 
 import torch
-from torch.nn import functional as F
+
+from . import _lib as L
+from . import profiling as _prof
+
+
+class _KL(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, s2: torch.Tensor, t2: torch.Tensor, temperature: float, out_dtype: torch.dtype):
+        dev = L.require_device(s2, t2)
+        rows, vocab = s2.shape
+        out = torch.empty((), dtype=out_dtype, device=dev)
+        lse = torch.empty(rows, 2, dtype=torch.float64, device=dev)
+        scale = torch.empty(rows, dtype=torch.float32, device=dev)
+        lib = L.lib()
+        ws = torch.empty(max(int(lib.sf_kl_workspace_size(rows)), 1), dtype=torch.uint8, device=dev)
+        with _prof.region("sf_kl_forward", 2 * s2.numel() * s2.element_size(), "B", dev):
+            L.check(lib.sf_kl_forward(L.ptr(s2), L.ptr(t2), L.dtype_code(s2), rows, vocab, float(temperature),
+                                      int(lib.sf_kl_chunk_rows(vocab)), L.ptr(out), L.dtype_code(out), L.ptr(lse),
+                                      L.ptr(scale), L.ptr(ws), ws.numel(), L.stream(dev)), "sf_kl_forward")
+        ctx.save_for_backward(s2, t2, lse, scale)
+        ctx.temperature = float(temperature)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        s2, t2, lse, scale = ctx.saved_tensors
+        dev = s2.device
+        g = g.contiguous()
+        if g.dtype not in (torch.float32, torch.bfloat16):
+            g = g.float()
+        gs = torch.empty_like(s2)
+        rows, vocab = s2.shape
+        with _prof.region("sf_kl_backward", 3 * s2.numel() * s2.element_size(), "B", dev):
+            L.check(L.lib().sf_kl_backward(L.ptr(s2), L.ptr(t2), L.dtype_code(s2), rows, vocab, ctx.temperature,
+                                           L.ptr(lse), L.ptr(scale), L.ptr(g), L.dtype_code(g), L.ptr(gs),
+                                           L.stream(dev)), "sf_kl_backward")
+        return gs, None, None, None
 
 
 def chunked_kl_loss(student_logits: torch.Tensor, teacher_logits: torch.Tensor, temperature=2) -> torch.Tensor:
+    """Distill_Model.kl_loss(student_logits, teacher_logits, temperature) (:1749-1828)."""
     shape = student_logits.shape
-    device, dtype = student_logits.device, student_logits.dtype
-    s_flat = student_logits.reshape(-1, shape[-1])
-    t_flat = teacher_logits.reshape(-1, shape[-1])
-    n_tok, vocab = s_flat.shape
-    chunk = 128 if vocab > 100000 else (512 if vocab > 50000 else 2048)
-    inv_t = 1.0 / temperature
-    total = torch.tensor(0.0, device=device, dtype=torch.float32)
-    for i in range(0, n_tok, chunk):
-        j = min(i + chunk, n_tok)
-        s_lp = F.log_softmax(s_flat[i:j].float().clamp(-100.0, 100.0) * inv_t, dim=-1)
-        t_lp = F.log_softmax(t_flat[i:j].float().clamp(-100.0, 100.0) * inv_t, dim=-1)
-        if torch.isnan(s_lp).any() or torch.isnan(t_lp).any():
-            continue
-        c = ((t_lp - s_lp) * t_lp.exp()).sum()
-        if torch.isfinite(c):
-            total = total + c
-    kl = (total * (temperature ** 2) / n_tok).to(dtype)
-    if not torch.isfinite(kl):
-        return torch.tensor(0.0, device=device, dtype=dtype)
-    return kl
+    dtype = student_logits.dtype
+    s2 = student_logits.reshape(-1, shape[-1])
+    t2 = teacher_logits.reshape(-1, shape[-1]).detach()
+    if t2.dtype != s2.dtype:
+        t2 = t2.to(s2.dtype)
+    if s2.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"kl_loss: logits dtype {s2.dtype} (float32 / bfloat16 only)")
+    return _KL.apply(s2.contiguous(), t2.contiguous(), float(temperature), dtype)

@@ -282,8 +282,12 @@ def kl_case(ref_sm, out):
     s[0, 3, 7] = 250.0  # exercises the +-100 clamp
     t[1, 5, 9] = -400.0
     d = ref_sm.Distill_Model.__new__(ref_sm.Distill_Model)
-    kl = ref_sm.Distill_Model.kl_loss(d, s, t)
-    out["kl_basic_f32"] = dict(s=np32(s), t=np32(t), kl=np.float64(kl.item()))
+    # kl_loss clamps and scales float32 logits in place (.float() aliases them, :1788-1796):
+    # it gets copies, and the copies are recorded after the call as s_after / t_after
+    s_in, t_in = s.clone(), t.clone()
+    kl = ref_sm.Distill_Model.kl_loss(d, s_in, t_in)
+    out["kl_basic_f32"] = dict(s=np32(s), t=np32(t), kl=np.float64(kl.item()), s_after=np32(s_in),
+                               t_after=np32(t_in))
 
 
 def bsr_case(out):

@@ -1,0 +1,114 @@
+"""GPU parity of the fused distillation KL (sf_kl_forward / sf_kl_backward) through Distill_Model.kl_loss.
+
+Bar: f32 loss within 2e-6 relative of the oracle (oracle/distill.py, pinned to the reference's
+own output) and of the reference fixture; f32 student gradient within 1e-5 of max |grad|; bf16
+logits against the oracle on the same bf16 values: the bf16 loss within one bf16 ulp, the bf16
+gradient within 2^-7 relative plus 1e-3 of max |grad|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from oracle import distill as od
+
+pytestmark = pytest.mark.gpu
+
+
+def _kl():
+    from sparseforge_amd.distill import chunked_kl_loss
+
+    return chunked_kl_loss
+
+
+def test_kl_matches_reference_golden(cuda_device):
+    r = load_golden("kl_basic_f32")
+    s = torch.from_numpy(r["s"]).to(cuda_device)
+    t = torch.from_numpy(r["t"]).to(cuda_device)
+    kl = _kl()(s, t, 2)
+    np.testing.assert_allclose(kl.item(), float(r["kl"]), rtol=2e-6)
+    assert torch.equal(s.cpu(), torch.from_numpy(r["s"]))  # inputs untouched
+
+
+@pytest.mark.parametrize("rows, vocab, T", [(300, 32000, 2.0), (4100, 64, 2.0), (64, 50257, 1.0), (33, 100003, 3.0),
+                                           (5, 7, 2.0)])
+def test_kl_fwd_bwd_f32_matches_oracle(cuda_device, rows, vocab, T):
+    g = torch.Generator().manual_seed(rows + vocab)
+    s = torch.randn(rows, vocab, generator=g) * 8
+    t = torch.randn(rows, vocab, generator=g) * 8
+    s[0, 0], t[-1, -1] = 300.0, -250.0
+    sd = s.to(cuda_device).requires_grad_(True)
+    kl = _kl()(sd, t.to(cuda_device), T)
+    np.testing.assert_allclose(kl.item(), od.kl_loss(s.numpy(), t.numpy(), T), rtol=2e-6)
+    (kl * 3.0).backward()
+    ref = od.kl_grad(s.numpy(), t.numpy(), T, g=3.0)
+    got = sd.grad.cpu().numpy()
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5 * np.abs(ref).max())
+    assert got[0, 0] == 0.0  # beyond the clamp
+
+
+def test_kl_nan_chunk_skipped(cuda_device):
+    g = torch.Generator().manual_seed(5)
+    s = torch.randn(5000, 64, generator=g)
+    t = torch.randn(5000, 64, generator=g)
+    s[3000, 5] = float("nan")
+    sd = s.to(cuda_device).requires_grad_(True)
+    kl = _kl()(sd, t.to(cuda_device), 2)
+    np.testing.assert_allclose(kl.item(), od.kl_loss(s.numpy(), t.numpy(), 2.0), rtol=2e-6)
+    kl.backward()
+    gr = sd.grad.cpu().numpy()
+    assert (gr[2048:4096] == 0).all() and np.isfinite(gr).all()
+    ref = od.kl_grad(s.numpy(), t.numpy(), 2.0)
+    np.testing.assert_allclose(gr, ref, rtol=0, atol=1e-5 * np.abs(ref).max())
+
+
+def test_kl_all_nan_gives_zero(cuda_device):
+    s = torch.full((10, 16), float("nan"), device=cuda_device, requires_grad=True)
+    t = torch.zeros(10, 16, device=cuda_device)
+    kl = _kl()(s, t, 2)
+    assert kl.item() == 0.0
+    kl.backward()
+    assert (s.grad == 0).all()
+
+
+def test_kl_bf16_matches_oracle(cuda_device):
+    g = torch.Generator().manual_seed(11)
+    s = (torch.randn(2, 256, 32000, generator=g) * 6).to(torch.bfloat16)
+    t = (torch.randn(2, 256, 32000, generator=g) * 6).to(torch.bfloat16)
+    sd = s.to(cuda_device).requires_grad_(True)
+    kl = _kl()(sd, t.to(cuda_device), 2)
+    assert kl.dtype == torch.bfloat16
+    ref = od.kl_loss(s.float().numpy(), t.float().numpy(), 2.0)
+    np.testing.assert_allclose(kl.float().item(), float(torch.tensor(ref).to(torch.bfloat16)), rtol=2 ** -8)
+    kl.backward()
+    gref = od.kl_grad(s.float().numpy(), t.float().numpy(), 2.0)
+    got = sd.grad.float().cpu().numpy()
+    np.testing.assert_allclose(got, gref, rtol=2 ** -7, atol=1e-3 * np.abs(gref).max())
+
+
+def test_distill_model_returns_kl(cuda_device):
+    from sparseforge_amd.sparse_modeling import Distill_Model
+
+    class Tiny(torch.nn.Module):
+        def __init__(self, seed):
+            super().__init__()
+            torch.manual_seed(seed)
+            self.emb = torch.nn.Embedding(50, 16)
+            self.head = torch.nn.Linear(16, 50)
+            self.config = type("C", (), {})()
+
+        def forward(self, idx, targets=None):
+            logits = self.head(self.emb(idx))
+            loss = None if targets is None else torch.nn.functional.cross_entropy(logits.view(-1, 50), targets.view(-1))
+            return logits, loss, None
+
+    student, teacher = Tiny(0).to(cuda_device), Tiny(1).to(cuda_device)
+    dm = Distill_Model(student, teacher)
+    idx = torch.randint(0, 50, (3, 9), device=cuda_device)
+    logits, task, lw, kl = dm(idx, idx)
+    with torch.no_grad():
+        tl, _, _ = teacher(idx)
+    np.testing.assert_allclose(kl.item(), od.kl_loss(logits.detach().cpu().numpy(), tl.cpu().numpy(), 2.0),
+                               rtol=2e-6)
+    (task + kl).backward()
+    assert student.head.weight.grad is not None and teacher.head.weight.grad is None
