@@ -14,17 +14,19 @@
 //
 // Tiling: 256 threads = 4 waves in a 2 x 2 grid; a workgroup owns a 256 x 256
 // tile of C, each wave 128 x 128 as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16
-// (256 fp32 accumulators per lane, held in AGPRs).  One k-stage (64 bf16) of
-// the A and B tiles is staged through double-buffered LDS with k contiguous
-// per row and a 144-byte row pitch, so a fragment is one conflict-free 16-byte
-// LDS read per lane.
+// (256 fp32 accumulators per lane, held in AGPRs).  One k-stage (64 k) of the
+// A and B tiles is staged through double-buffered LDS laid out so that each
+// MFMA fragment is one conflict-free 16-byte LDS read per lane.
 //
-// Pipeline: the global loads of stage s+2 are issued right after stage s+1 is
-// written to LDS, so a whole stage of MFMAs covers their latency; the raw
-// words sit in registers until the LDS write, where the mask multiply (B only)
-// and, for M/N-contiguous operands, an 8 x 8 register transpose happen.  No
-// masked copy of W is ever written to memory.  Inside a stage the LDS reads of
-// k-step kk+1 are issued before the MFMAs of kk.
+// Two kernels share this tiling.  gemm_bf16_kernel (bf16 operands, the
+// SparseLinear products) copies tiles global -> LDS with the buffer unit's
+// direct-to-LDS loads (see its section below).  gemm_kernel (f32 operands, the
+// block-sparse modes, masks whose rows are not 16-byte aligned) stages through
+// registers: the global loads of stage s+2 are issued right after stage s+1 is
+// written to LDS, and the mask multiply (B only) and, for M/N-contiguous
+// operands, an 8 x 8 register transpose happen at the LDS write.  Neither
+// writes a masked copy of W to memory.  Inside a stage the LDS reads of k-step
+// kk+1 are issued before the MFMAs of kk.
 //
 // Tile order: dispatch ids are spread round-robin over the 8 XCDs; they are
 // remapped so each XCD walks a contiguous range of tiles, ordered in bands of
@@ -881,28 +883,33 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_kernel(GemmArgs g) {
 // ---------------------------------------------------------------------------
 // bf16 kernel with direct-to-LDS staging (gfx950 `buffer_load_dwordx4 ... lds`).
 //
-// K-contiguous operands that reach LDS unchanged (A of the forward and
-// input-gradient products, B of an unmasked forward, both SLoRB operands of
-// the forward) are copied global -> LDS by the buffer unit without passing
-// through registers: one wave instruction moves 8 rows x 128 B (a 16-byte
-// chunk per lane) into 1 KiB of LDS.  Rows are unpadded and their chunks
-// XOR-swizzled, slot s of row r holding chunk s ^ f(r), f(r) = (r ^ r >> 3) & 7,
-// so the 16-byte fragment reads of 8 (and of 16) consecutive rows fall in
-// distinct banks.  A masked or M/N-contiguous operand keeps the register path
-// (mask product, 8 x 8 transpose) into the padded 144-byte-pitch layout.
+// Operands are copied global -> LDS by the buffer unit without passing through
+// registers; one wave instruction moves 64 x 16 B into 1 KiB of LDS.
+//  * K-contiguous tiles (x, dy, W of the forward, the SLoRB operands): 256 rows
+//    x 128 B, unpadded, chunks XOR-swizzled (slot s of row r holds chunk
+//    s ^ f(r), f(r) = (r ^ r >> 3) & 7) so that the 16-byte fragment reads of 8
+//    and of 16 consecutive rows fall in distinct banks.
+//  * M/N-contiguous tiles (W of the input gradient, dy and x of the weight
+//    gradient): 64 k-rows x 512 B with chunk c of row k at c ^ 4 (k & 3); the
+//    MFMA fragments are read transposed with ds_read_b64_tr_b16.
+//  * The hard 2:4 byte and-mask: K-major 256 rows x 64 B (the input-gradient
+//    product reads its transposed copy, sf_transpose_u8), applied to the B
+//    fragments with a byte permute + AND after they are read.
+// Only a multiplicative (soft / mixed) mask keeps the register path for B:
+// load, multiply, store into the padded 144-byte-pitch layout.
 //
 // Stage s (LDS buffer b = s & 1 holds it):
 //   k-steps 0..2: MFMAs of k-step kk, fragment reads of k-step kk + 1
 //   wait for this wave's copies into b ^ 1 and its fragment reads, barrier:
 //     b ^ 1 (stage s + 1) is complete; b is no longer read by anyone
-//   copies of stage s + 2 into b (register stores, register loads of
-//     stage s + 3, DMA issue)
-//   k-step 3: MFMAs, fragment reads of k-step 0 of stage s + 1 from b ^ 1
-// LDS latency is covered by a k-step of MFMAs everywhere, and each copy has
-// a whole stage to land.
+//   k-step 3: MFMAs interleaved with the fragment reads of k-step 0 of stage
+//     s + 1 (from b ^ 1) and the copies of stage s + 2 into b
+// LDS latency is covered by a k-step of MFMAs everywhere, and each copy has a
+// whole stage to land.  A scheduling barrier after every MFMA keeps this
+// interleave; the steady-state loop is unrolled twice so buffer offsets are
+// immediates.
 // ---------------------------------------------------------------------------
 constexpr int kRowSw = 128;  // bytes per row of a swizzled (DMA) tile: 64 bf16
-constexpr int kWaitLgkmOnly = 0xC07F;  // s_waitcnt lgkmcnt(0) with vmcnt / expcnt left alone (gfx9 encoding)
 constexpr int kRowPad = 144; // bytes per row of a padded (register-path) tile
 
 // One 16-byte-per-lane copy global -> LDS: lane l's 16 bytes land at lds + 16 l.
