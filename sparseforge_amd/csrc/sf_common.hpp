@@ -112,11 +112,50 @@ __constant__ static const uint8_t kTopkTies4[3][256] = {
      0,0,13,13,0,0,11,11,14,11,0,0,14,11,0,0,0,0,13,13,0,0,0,0,14,0,0,0,14,0,0,0,13,13,0,0,14,0,0,0,0,0,0,0,0,0,0,0,14,13,0,0,14,0,0,0,0,0,0,0,0,0,0,0,
      13,0,13,0,0,11,11,0,14,11,0,0,0,0,0,0,0,13,13,0,14,0,0,0,14,0,0,0,0,0,0,0,13,13,0,0,14,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0,0}};
 
+// torch.topk(2) of a group of 4 in closed form, equal to the k = 2 table on all
+// 75 weak orderings.  bij: member j ranks at or above member i (j > i, so j
+// wins a tie), eij: members i and j are equal.  A member is kept unless two
+// others outrank it, except when member 0 is the unique maximum: then the
+// second kept member is the lowest index among the tied maxima of members
+// 1..3, or member 2 when all three tie.  Pure boolean logic on comparison
+// results (lane masks), no table gather.
+__host__ __device__ __forceinline__ uint32_t topk2_keep_rel(bool b01, bool b02, bool b03, bool b12, bool b13,
+                                                            bool b23, bool e12, bool e13, bool e23) {
+  auto maj = [](bool x, bool y, bool z) { return (x && y) || (x && z) || (y && z); };
+  bool k0 = !maj(b01, b02, b03), k1 = !maj(!b01, b12, b13), k2 = !maj(!b02, !b12, b23), k3 = !maj(!b03, !b13, !b23);
+  const bool top0 = !b01 && !b02 && !b03;
+  const bool ge1 = (!b12 || e12) && (!b13 || e13), ge2 = b12 && (!b23 || e23), ge3 = b13 && b23;
+  const bool all3 = ge1 && ge2 && ge3;
+  if (top0) {
+    k1 = !all3 && ge1;
+    k2 = all3 || (!ge1 && ge2);
+    k3 = !all3 && !ge1 && !ge2;
+  }
+  return (k0 ? 1u : 0u) | (k1 ? 2u : 0u) | (k2 ? 4u : 0u) | (k3 ? 8u : 0u);
+}
+
+__host__ __device__ __forceinline__ uint32_t topk2_keep_keys(const uint32_t k[4]) {
+  return topk2_keep_rel(k[1] >= k[0], k[2] >= k[0], k[3] >= k[0], k[2] >= k[1], k[3] >= k[1], k[3] >= k[2],
+                        k[1] == k[2], k[1] == k[3], k[2] == k[3]);
+}
+
+// Without NaN the float comparisons give torch's order directly (-0 == +0).
+__device__ __forceinline__ uint32_t topk2_keep_f(const float v[4]) {
+  return topk2_keep_rel(v[1] >= v[0], v[2] >= v[0], v[3] >= v[0], v[2] >= v[1], v[3] >= v[1], v[3] >= v[2],
+                        v[1] == v[2], v[1] == v[3], v[2] == v[3]);
+}
+
+__device__ __forceinline__ bool any_nan4(const float v[4]) {
+  return __builtin_isunordered(v[0], v[1]) || __builtin_isunordered(v[2], v[3]);
+}
+
 // Kept members (bitmask over 4) of torch.topk(k) on the group v[0..3].
 __device__ __forceinline__ uint32_t topk4_keep(const float v[4], int k) {
+  if (k == 2 && !any_nan4(v)) return topk2_keep_f(v);
   uint32_t key[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) key[i] = ordered_key(v[i]);
+  if (k == 2) return topk2_keep_keys(key);
   uint32_t idx = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

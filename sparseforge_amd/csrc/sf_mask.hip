@@ -29,7 +29,13 @@ __host__ __device__ __forceinline__ int promote(int a, int b) {
   return (a == SF_DTYPE_F32 || b == SF_DTYPE_F32) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// sigmoid(x) = 1 / (1 + exp(-x)) from the hardware base-2 exponential and
+// reciprocal (v_exp_f32, v_rcp_f32, each within 1 ulp): within a few ulp of the
+// f32 formula the reference evaluates (its own exp is not correctly rounded
+// either); exactly 0.5 at x = 0, exactly 1 once exp(-x) < 2^-24, 0 at -inf.
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
 
 // Load up to 4 consecutive elements [i, i + n) as f32; vector path when the
 // group is full and aligned.
@@ -215,8 +221,25 @@ __device__ __forceinline__ void group_scores(const ScoreSpec& s, const void* W, 
     else
       load4_any(aux, s.aux_dtype, g.elem, g.n, vec, a);  // grad_ema [rows, cols]
   }
+  // one switch per group, the element loop inside each case
+  switch (s.metric) {
+#define SF_SCORES_CASE(M)                                                                            \
+  case M: {                                                                                          \
+    ScoreSpec sm = s;                                                                                \
+    sm.metric = M;                                                                                   \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) sc[j] = j < g.n ? score_of<WD, HD>(sm, w[j], h[j], a[j]) : 0.0f; \
+    break;                                                                                           \
+  }
+    SF_SCORES_CASE(SF_METRIC_HESSIAN_RATIO)
+    SF_SCORES_CASE(SF_METRIC_HESSIAN_OBD)
+    SF_SCORES_CASE(SF_METRIC_HESSIAN)
+    SF_SCORES_CASE(SF_METRIC_WANDA)
+    SF_SCORES_CASE(SF_METRIC_MOVEMENT)
+#undef SF_SCORES_CASE
+    default:
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sc[j] = j < g.n ? score_of<WD, HD>(s, w[j], h[j], a[j]) : 0.0f;
+      for (int j = 0; j < 4; ++j) sc[j] = j < g.n ? fabsf(w[j]) : 0.0f;
+  }
 }
 
 __device__ __forceinline__ float score_at(const ScoreSpec& s, const void* W, const void* H, const void* aux,
@@ -253,13 +276,31 @@ __device__ __forceinline__ float div_by(float a, float b, float y) {
   const float r = fmaf(-b, q, a);
   float d = fmaf(r, y, q);
   // outside these ranges r = a - b q may be inexact (subnormal) or q may overflow;
-  // zeros also go here so that the sign of a zero quotient is IEEE's
-  if (!(fabsf(a) > 0x1p-75f && fabsf(q) < 0x1p+100f && fabsf(y) > 0x1p-100f)) d = a / b;
-  return d;
+  // zeros also go here so that the sign of a zero quotient is IEEE's.
+  const bool slow = !(fabsf(a) > 0x1p-75f && fabsf(q) < 0x1p+100f && fabsf(y) > 0x1p-100f);
+  float alt = 0.0f;
+  if (__builtin_expect(slow, 0)) alt = a / b;
+  return slow ? alt : d;
 }
-template <int SD>
-__device__ __forceinline__ float znorm_t(float s, float mu, float sigma, float rsigma) {
-  return rndc<SD>(div_by(s - mu, sigma, rsigma));
+// d[j] = a[j] / b for a group (d must not alias a), with one fallback branch for the four quotients.
+__device__ __forceinline__ void div4_by(const float a[4], float b, float y, float d[4]) {
+  bool slow = !(fabsf(y) > 0x1p-100f);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float q = a[j] * y;
+    const float r = fmaf(-b, q, a[j]);
+    d[j] = fmaf(r, y, q);
+    slow = slow || !(fabsf(a[j]) > 0x1p-75f && fabsf(q) < 0x1p+100f);
+  }
+  // The fallback goes to its own array and is selected afterwards: overwriting d[]
+  // inside the branch was compiled into wrong results for some callers here.
+  float alt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (__builtin_expect(slow, 0)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) alt[j] = a[j] / b;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) d[j] = slow ? alt[j] : d[j];
 }
 
 // ---------------------------------------------------------------------------
@@ -595,16 +636,20 @@ template <int SD>
 __device__ __forceinline__ void gate_of_group(const GateSpec& gs, const float sc[4], const Group& g, float mu,
                                               float sigma, float rsigma, float tau, const float mprev[4],
                                               const float frz[4], float G[4]) {
-  float z[4];
+  float z[4], t[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) z[j] = znorm_t<SD>(sc[j], mu, sigma, rsigma);
-  if (gs.gate == SF_GATE_UNSTRUCTURED) {
+  for (int j = 0; j < 4; ++j) t[j] = sc[j] - mu;
+  div4_by(t, sigma, rsigma, z);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) G[j] = rndc<SD>(sigmoidf_(div_by(z[j] - tau, gs.denom, gs.rdenom)));
-  } else if (gs.gate == SF_GATE_STRUCTURED) {
-    float tg = kth_largest4(z, gs.n_keep);
+  for (int j = 0; j < 4; ++j) z[j] = rndc<SD>(z[j]);
+  if (gs.gate == SF_GATE_UNSTRUCTURED || gs.gate == SF_GATE_STRUCTURED) {
+    const float th = gs.gate == SF_GATE_UNSTRUCTURED ? tau : kth_largest4(z, gs.n_keep);
+    float x[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) G[j] = rndc<SD>(sigmoidf_(div_by(z[j] - tg, gs.denom, gs.rdenom)));
+    for (int j = 0; j < 4; ++j) t[j] = z[j] - th;
+    div4_by(t, gs.denom, gs.rdenom, x);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) G[j] = rndc<SD>(sigmoidf_(x[j]));
   } else if (gs.gate == SF_GATE_STRUCTURED_EXACT) {
     uint32_t keep = topk4_keep(z, gs.n_keep);
 #pragma unroll
@@ -698,7 +743,7 @@ __device__ __forceinline__ void pull_and_push(const UpdateSpec& us, const Group&
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) G[j] = fminf(fmaxf(G[j], 0.0f), 1.0f);
+    for (int j = 0; j < 4; ++j) G[j] = G[j] != G[j] ? G[j] : fminf(fmaxf(G[j], 0.0f), 1.0f);  // clamp keeps NaN
   }
   if (us.binarize) {
 #pragma unroll
@@ -718,7 +763,7 @@ __device__ __forceinline__ void ema_of(const UpdateSpec& us, const float mp[4], 
   for (int j = 0; j < 4; ++j) {
     float m1 = rnd(mp[j] * us.keep_a, MD);
     float m2 = rnd(fmaf(G[j], us.a, m1), MD);
-    mn[j] = fminf(fmaxf(m2, 0.0f), 1.0f);
+    mn[j] = m2 != m2 ? m2 : fminf(fmaxf(m2, 0.0f), 1.0f);  // clamp_ keeps NaN
   }
 }
 
@@ -746,18 +791,26 @@ __device__ __forceinline__ void freeze_group(const UpdateSpec& us, const Group& 
   }
 }
 
-// Positions of a group where the hard views of a and b differ (:1659-1661).
-__device__ __forceinline__ int flips_of(const float a[4], const float b[4], const Group& g, int kind, int n) {
-  float ha[4], hb[4];
-  hard_of_group(a, g, kind, n, ha);
-  hard_of_group(b, g, kind, n, hb);
-  int c = 0;
+// Kept members (bit j = member j) of the hard projection of one group.
+__device__ __forceinline__ uint32_t hard_bits(const float v[4], const Group& g, int kind, int n_keep) {
+  if (kind == SF_HARD_NONE) return 0xfu;
+  if (kind == SF_HARD_THRESHOLD) {
+    uint32_t b = 0u;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) c += (j < g.n && ((ha[j] > 0.5f) != (hb[j] > 0.5f))) ? 1 : 0;
-  return c;
+    for (int j = 0; j < 4; ++j) b |= (v[j] > 0.5f ? 1u : 0u) << j;
+    return b;
+  }
+  return g.full ? topk4_keep(v, n_keep) : 0xfu;  // a tail group keeps every column
 }
 
-template <int WD, int HD, int MD, int SD>
+// Positions of a group where the hard views of a and b differ (:1659-1661).
+__device__ __forceinline__ int flips_of(const float a[4], const float b[4], const Group& g, int kind, int n) {
+  return __popc((hard_bits(a, g, kind, n) ^ hard_bits(b, g, kind, n)) & ((1u << g.n) - 1u));
+}
+
+// VEC: cols % 4 == 0 and every operand 16-byte aligned, so every group is a
+// full, vector-loadable group of 4 (known at compile time: no tail branches).
+template <int WD, int HD, int MD, int SD, bool VEC>
 __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, const void* __restrict__ W,
                                                              const void* __restrict__ H, const void* __restrict__ aux,
                                                              void* __restrict__ mask, void* __restrict__ frozen,
@@ -770,7 +823,11 @@ __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, cons
   int64_t cnt = 0;
   for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
     Group g = w.group();
-    const bool v = vec && g.full;
+    if constexpr (VEC) {
+      g.n = 4;
+      g.full = true;
+    }
+    const bool v = VEC || (vec && g.full);
     float sc[4], mp[4], fz[4] = {0, 0, 0, 0}, G[4];
     group_scores<WD, HD>(gs.s, W, H, aux, g, v, cols, sc);
     load4<MD>(mask, g.elem, g.n, v, mp);
@@ -1160,9 +1217,16 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int grid = elementwise_grid(groups, kBlock);
 #define SF_LAUNCH_UPD(MDT, SDT)                                                                             \
-  SF_DISPATCH_WH(w_dtype, h_dtype,                                                                          \
-                 update_mask_kernel<WD_, HD_, MDT, SDT><<<grid, kBlock, 0, st>>>(                           \
-                     us, W, H, aux, mask, frozen, stats, tau, p->cols, groups, gpr, vec, flips))
+  do {                                                                                                      \
+    if (vec)                                                                                                \
+      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                      \
+                     update_mask_kernel<WD_, HD_, MDT, SDT, true><<<grid, kBlock, 0, st>>>(                 \
+                         us, W, H, aux, mask, frozen, stats, tau, p->cols, groups, gpr, vec, flips));       \
+    else                                                                                                    \
+      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                      \
+                     update_mask_kernel<WD_, HD_, MDT, SDT, false><<<grid, kBlock, 0, st>>>(                \
+                         us, W, H, aux, mask, frozen, stats, tau, p->cols, groups, gpr, vec, flips));       \
+  } while (0)
   const bool sf32 = p->score_dtype == SF_DTYPE_F32;
   if (mask_dtype == SF_DTYPE_F32) {
     if (sf32)
