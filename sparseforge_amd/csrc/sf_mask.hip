@@ -394,7 +394,8 @@ __device__ __forceinline__ void block_sum2_f64(double a, double b, double* out_a
   }
 }
 
-template <int WD, int HD>
+// VEC: every group full and vector-loadable (as in update_mask_kernel).
+template <int WD, int HD, bool VEC>
 __global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, const void* __restrict__ W,
                                                                const void* __restrict__ H, const void* __restrict__ aux,
                                                                int64_t cols, int64_t groups, int64_t gpr, bool vec,
@@ -402,8 +403,12 @@ __global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, cons
   double sum = 0.0, sq = 0.0;
   for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
     Group g = w.group();
+    if constexpr (VEC) {
+      g.n = 4;
+      g.full = true;
+    }
     float sc[4];
-    group_scores<WD, HD>(s, W, H, aux, g, vec && g.full, cols, sc);
+    group_scores<WD, HD>(s, W, H, aux, g, VEC || (vec && g.full), cols, sc);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (j < g.n) {
@@ -1046,9 +1051,14 @@ extern "C" int sf_score_stats(const sf_mask_params* p, const void* W, int w_dtyp
                    (!aux || p->metric != SF_METRIC_WANDA || aligned(aux, 4 * esize(aux_dtype)));
   double* partial = static_cast<double*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  SF_DISPATCH_WH(w_dtype, h_dtype,
-                 stats_partial_kernel<WD_, HD_><<<kStatsGrid, kBlock, 0, st>>>(s, W, H, aux, p->cols, groups, gpr, vec,
-                                                                              partial));
+  if (vec)
+    SF_DISPATCH_WH(w_dtype, h_dtype,
+                   stats_partial_kernel<WD_, HD_, true><<<kStatsGrid, kBlock, 0, st>>>(s, W, H, aux, p->cols, groups,
+                                                                                      gpr, vec, partial));
+  else
+    SF_DISPATCH_WH(w_dtype, h_dtype,
+                   stats_partial_kernel<WD_, HD_, false><<<kStatsGrid, kBlock, 0, st>>>(s, W, H, aux, p->cols, groups,
+                                                                                       gpr, vec, partial));
   stats_final_kernel<<<1, kBlock, 0, st>>>(partial, kStatsGrid, n, stats_out);
   return launch_status("sf_score_stats");
 }
