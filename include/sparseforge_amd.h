@@ -338,6 +338,17 @@ int sf_kl_backward(const void* student, const void* teacher, int dtype, int64_t 
                    float temperature, const double* row_lse, const float* row_scale, const void* grad_out,
                    int grad_out_dtype, void* grad_student, void* stream);
 
+/*
+ * Masked weight W_eff = (W * E).to(W dtype), then (W_eff * scale).to(W dtype)
+ * when scale != 1: the `w = weight * mask_cast` (and `* scale_factor`) of
+ * FusedMaskedLinearSTE.forward (legacy/sparse_modeling.py:72-81); with scale 1
+ * the `weight * mask_cast` of its backward (:113-115).  E: an SF_DTYPE_U8 byte
+ * and-mask (0x00 / 0xFF, from sf_effective_mask) or an effective mask in the
+ * weight dtype.  W, E, out: [rows, cols].  The GEMMs then run unmasked.
+ */
+int sf_apply_mask(const void* W, int w_dtype, const void* E, int e_dtype, float scale, void* out, int64_t rows,
+                  int64_t cols, void* stream);
+
 /* ---- GEMM engine (FusedMaskedLinearSTE, :56-132, and the SLoRB F.linear pair, :790-794) */
 #define SF_LAYOUT_K 0  /* operand stored K-contiguous: X[row * ld + k]                        */
 #define SF_LAYOUT_MN 1 /* operand stored M/N-contiguous: X[k * ld + row] (a transposed view)  */

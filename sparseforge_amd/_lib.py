@@ -190,6 +190,7 @@ SIGNATURES = {
     "sf_block_fill": (_I, [_P, _I64, _I64, _I, _P, _F, _P, _I, _I, _F, _P, _I, _P, _I, _P]),
     "sf_apply_gate": (_I, [_MP, _P, _P, _I, _P, _I, _P, _I, _I, _P]),
     "sf_freeze_mask": (_I, [_MP, _P, _I, _P, _I, _P]),
+    "sf_apply_mask": (_I, [_P, _I, _P, _I, _F, _P, _I64, _I64, _P]),
     "sf_kl_chunk_rows": (_I64, [_I64]),
     "sf_kl_workspace_size": (ctypes.c_size_t, [_I64]),
     "sf_kl_forward": (_I, [_P, _P, _I, _I64, _I64, _F, _I64, _P, _I, _P, _P, _P, ctypes.c_size_t, _P]),

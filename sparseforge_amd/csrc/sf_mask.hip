@@ -1970,3 +1970,78 @@ extern "C" int sf_freeze_mask(const sf_mask_params* p, void* mask, int mask_dtyp
     freeze_kernel<SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(us, mask, frozen, p->cols, groups, gpr, vec);
   return launch_status("sf_freeze_mask");
 }
+
+// ---------------------------------------------------------------------------
+// Masked weight of FusedMaskedLinearSTE: out = round(W * E), then round(out * s)
+// when s != 1 (legacy/sparse_modeling.py:72-81; the backward's W . E at :113-115
+// is the s = 1 case).  E is a byte and-mask or values in W's dtype.  8
+// consecutive elements per thread per step (16-byte loads for bf16 W).
+// ---------------------------------------------------------------------------
+namespace sf {
+namespace {
+template <int WD, int ED>
+__global__ void __launch_bounds__(kBlock) apply_mask_kernel(const void* __restrict__ W, const void* __restrict__ E,
+                                                            float scale, int has_scale, void* __restrict__ out,
+                                                            int64_t n, bool vec) {
+  const int64_t n8 = (n + 7) / 8;
+  for (int64_t i8 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i8 < n8; i8 += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e0 = i8 * 8;
+    const int m = n - e0 >= 8 ? 8 : static_cast<int>(n - e0);
+    const bool v = vec && m == 8;
+    float w[8], e[8], o[8];
+    load4<WD>(W, e0, m, v, w);
+    load4<WD>(W, e0 + 4, m - 4, v, w + 4);
+    if (ED == SF_DTYPE_U8) {
+      const uint8_t* eb = static_cast<const uint8_t*>(E) + e0;
+      uint32_t lo = 0, hi = 0;
+      if (v) {
+        const uint2 q = *reinterpret_cast<const uint2*>(eb);
+        lo = q.x;
+        hi = q.y;
+      } else {
+        for (int j = 0; j < m; ++j) (j < 4 ? lo : hi) |= static_cast<uint32_t>(eb[j]) << (8 * (j & 3));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[j] = (((j < 4 ? lo : hi) >> (8 * (j & 3))) & 0xffu) ? 1.0f : 0.0f;
+    } else {
+      load4<ED>(E, e0, m, v, e);
+      load4<ED>(E, e0 + 4, m - 4, v, e + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float x = rndc<WD>(w[j] * e[j]);
+      if (has_scale) x = rndc<WD>(x * scale);
+      o[j] = x;
+    }
+    store4<WD>(out, e0, m, v, o);
+    store4<WD>(out, e0 + 4, m - 4, v, o + 4);
+  }
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" int sf_apply_mask(const void* W, int w_dtype, const void* E, int e_dtype, float scale, void* out,
+                             int64_t rows, int64_t cols, void* stream) {
+  SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  SF_CHECK_ARG(dtype_ok(w_dtype), "bad weight dtype");
+  SF_CHECK_ARG(e_dtype == SF_DTYPE_U8 || e_dtype == w_dtype, "the mask must be a byte mask or in the weight dtype");
+  const int64_t n = rows * cols;
+  if (n == 0) return SF_OK;
+  SF_CHECK_ARG(W && E && out, "null tensor");
+  const bool vec = aligned(W, 16) && aligned(out, 16) &&
+                   (e_dtype == SF_DTYPE_U8 ? aligned(E, 8) : aligned(E, 16));
+  const int has_scale = scale != 1.0f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid((n + 7) / 8, kBlock);
+#define SF_LAUNCH_APPLY_MASK(WDT, EDT) \
+  apply_mask_kernel<WDT, EDT><<<grid, kBlock, 0, st>>>(W, E, scale, has_scale, out, n, vec)
+  if (w_dtype == SF_DTYPE_BF16) {
+    if (e_dtype == SF_DTYPE_U8) SF_LAUNCH_APPLY_MASK(SF_DTYPE_BF16, SF_DTYPE_U8);
+    else SF_LAUNCH_APPLY_MASK(SF_DTYPE_BF16, SF_DTYPE_BF16);
+  } else {
+    if (e_dtype == SF_DTYPE_U8) SF_LAUNCH_APPLY_MASK(SF_DTYPE_F32, SF_DTYPE_U8);
+    else SF_LAUNCH_APPLY_MASK(SF_DTYPE_F32, SF_DTYPE_F32);
+  }
+#undef SF_LAUNCH_APPLY_MASK
+  return launch_status("sf_apply_mask");
+}

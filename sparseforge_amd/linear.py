@@ -167,6 +167,19 @@ def effective_mask_given(mask: torch.Tensor, hard: torch.Tensor, dtype: torch.dt
     return eff
 
 
+def apply_mask(W: torch.Tensor, E: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """(W * E).to(W dtype) [* scale, rounded again]: the masked weight the unmasked GEMMs read."""
+    dev = L.require_device(W, E)
+    if E.shape != W.shape:
+        raise ValueError(f"mask shape {tuple(E.shape)} != weight shape {tuple(W.shape)}")
+    out = torch.empty_like(W)
+    code = L.DT_U8 if E.dtype == torch.uint8 else L.dtype_code(E)
+    with _prof.region("sf_apply_mask", W.numel() * (2 * W.element_size() + E.element_size()), "B", dev):
+        L.check(L.lib().sf_apply_mask(L.ptr(W), L.dtype_code(W), L.ptr(E), code, float(scale), L.ptr(out),
+                                      W.shape[0], W.shape[1], L.stream(dev)), "sf_apply_mask")
+    return out
+
+
 def transpose_u8(E: torch.Tensor) -> torch.Tensor:
     """[rows, cols] uint8 -> its transpose [cols, rows] (sf_transpose_u8)."""
     dev = L.require_device(E)
@@ -217,13 +230,14 @@ class _MaskedLinearBackward(torch.autograd.Function):
         # written out explicitly in backward(), so the cached copy is detached.
         z = (z_fwd if z_fwd is not None else mm_nt(x, P)) if has_slorb else None
         dz = mm_nn(gy, S) if has_slorb else None
-        # a byte mask is read K-major beside the transposed weight tile of dx = gy (W.E)
-        E_t = transpose_u8(E) if E is not None and E.dtype == torch.uint8 and W.dtype == torch.bfloat16 else None
+        # dx = gy (W.E): the masked weight is rebuilt (one elementwise pass) rather than kept from the
+        # forward, so the saved state is x, W and E as in the reference
+        Wm = apply_mask(W, E) if E is not None else W
         if has_slorb:
-            dx = mm_nn(gy, W, bmask=E, bmask_t=E_t, A2=dz, B2=P, K2=P.shape[0])
+            dx = mm_nn(gy, Wm, A2=dz, B2=P, K2=P.shape[0])
         else:
-            dx = mm_nn(gy, W, bmask=E, bmask_t=E_t)
-        del E_t
+            dx = mm_nn(gy, Wm)
+        del Wm
         if decay != 0.0:
             dW = mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay)
         else:
@@ -311,11 +325,14 @@ class _MaskedLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x2, W, bias, P, S, E, scale, decay):
         z = None
+        # y = x (W.E.s)^T: one elementwise pass writes the masked weight, the GEMM runs unmasked
+        Wm, s = (apply_mask(W, E, scale), 1.0) if E is not None else (W, scale)
         if P is not None:
             z = mm_nt(x2, P)
-            y = mm_nt(x2, W, bmask=E, bscale=scale, A2=z, B2=S, K2=P.shape[0], bias=bias)
+            y = mm_nt(x2, Wm, bscale=s, A2=z, B2=S, K2=P.shape[0], bias=bias)
         else:
-            y = mm_nt(x2, W, bmask=E, bscale=scale, bias=bias)
+            y = mm_nt(x2, Wm, bscale=s, bias=bias)
+        del Wm
         ctx.save_for_backward(x2, W, P, S, E, z)
         ctx.decay = decay
         ctx.has_bias = bias is not None
