@@ -523,7 +523,7 @@ def main(argv=None) -> int:
                      "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic.get("sf_gemm_bytes_per_launch"), "traffic_unit": "B/launch",
                      "traffic_source": TRAFFIC_SUMMARY,
-                     "kernel": "sf_gemm (gemm_kernel<bf16>)", "launches": g.launches,
+                     "kernel": "sf_gemm (gemm_bf16_kernel)", "launches": g.launches,
                      "avg_launch_ms": round(g.avg_ms, 4)},
         "kernels": other,
         "mask_update": {
