@@ -192,7 +192,10 @@ extern "C" int sf_adamw_step(void* param, int param_dtype, const void* grad, int
   a.neg_lr = static_cast<float>(-hp->lr);
   a.amsgrad = hp->amsgrad;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int grid = elementwise_grid((n + 3) / 4, kBlock);
+  // one 4-element vector per thread (no grid-stride reuse of a thread): measured faster than a
+  // capped grid for this 10-stream read / write mix
+  const int64_t blocks = ceil_div((n + 3) / 4, kBlock);
+  const int grid = static_cast<int>(blocks < (1ll << 30) ? blocks : (1ll << 30));
   auto al = [](const void* q, int dt) { return !q || (reinterpret_cast<uintptr_t>(q) % (dt == SF_DTYPE_F32 ? 16 : 8)) == 0; };
   const bool aligned = al(param, param_dtype) && al(grad, grad_dtype) && al(exp_avg, state_dtype) &&
                        al(exp_avg_sq, state_dtype) && al(a.vmax, state_dtype) && al(mask, a.m_dt) &&
