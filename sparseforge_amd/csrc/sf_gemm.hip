@@ -1218,6 +1218,21 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
     dbm.init(g.B1, g.ldb1, n0, g.N, g.K1, kbase);
   if constexpr (DM) dm.init(g.bmask, g.ldbm, n0, g.N, g.K1);
 
+  // A / B halves of copy piece p (the unmasked all-DMA case spreads them, below)
+  auto dma_piece_a = [&](int buf, int64_t k0, int p) {
+    if constexpr (AL == 0)
+      dak.issue_one(As_l + buf * ABUF, k0, p);
+    else
+      dam.issue_one(As_l + buf * ABUF, p);
+  };
+  auto dma_piece_b = [&](int buf, int64_t k0, int p) {
+    if constexpr (DB) {
+      if constexpr (BL == 0)
+        dbk.issue_one(Bs_l + buf * BBUF, k0, p);
+      else
+        dbm.issue_one(Bs_l + buf * BBUF, p);
+    }
+  };
   // piece p (0..7) of the DMA copy of the stage at k0 into buffer buf
   auto dma_piece = [&](int buf, int64_t k0, int p) {
     if constexpr (AL == 0)
@@ -1311,10 +1326,27 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
         read_b(Masked{}, slot, buf, kk, f - kFragM);
     }
   };
+  // SPREAD (A and B both copied by DMA, no byte mask): the 16 copy instructions of
+  // a stage go one per MFMA slot, half in k-step 3 of stage s (pieces 0..3 of
+  // stage s + 2) and half in k-step 0 of stage s + 1 (pieces 4..7), so the
+  // buffer unit is never handed a whole stage's copies in one k-step.  They still
+  // land before the barrier of stage s + 1 that publishes them.
+  constexpr bool SPREAD = DB && !DM;
+  auto spread_piece = [&](int buf, int64_t k0, int slot) {  // slot 0..7: A / B of pieces base + slot / 2
+    if (slot & 1)
+      dma_piece_b(buf, k0, slot >> 1);
+    else
+      dma_piece_a(buf, k0, slot >> 1);
+  };
   auto steady = [&](auto bc, int64_t s) {
     constexpr int B = decltype(bc)::value;
+    const bool pend = SPREAD && s > 0;  // pieces 4..7 of stage s + 1 (into B ^ 1) are still to be issued
+    const int64_t k1 = kbase + (s + 1) * BK;
     kstep(0, [&](int idx) {
       if (idx < 4) read_pair(1, B, 1, idx);
+      if constexpr (SPREAD) {
+        if (pend && idx >= 4 && idx < 12) spread_piece(B ^ 1, k1, 8 + (idx - 4));
+      }
     });
     kstep(1, [&](int idx) {
       if (idx < 4) read_pair(0, B, 2, idx);
@@ -1328,7 +1360,9 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
     const int64_t k2 = kbase + (s + 2) * BK, k3 = kbase + (s + 3) * BK;
     kstep(1, [&](int idx) {
       if (idx < 4) read_pair(0, B ^ 1, 0, idx);  // the next stage's first fragments
-      if (idx >= 4 && idx < 12) {
+      if constexpr (SPREAD) {
+        if (idx >= 4 && idx < 12) spread_piece(B, k2, idx - 4);
+      } else if (idx >= 4 && idx < 12) {
         const int p = idx - 4;
         if constexpr (!DB) {  // register path: one vector written, then its register reloaded
           if constexpr (BL == 0) {
@@ -1349,9 +1383,16 @@ __global__ void __launch_bounds__(kThreads, 1) gemm_bf16_kernel(GemmArgs g) {
     steady(std::integral_constant<int, 0>{}, s);
     steady(std::integral_constant<int, 1>{}, s + 1);
   }
+  bool pend = SPREAD && s > 0;  // the last steady stage left pieces 4..7 of stage s + 1
   // The last (up to four) stages, with run-time buffer offsets.
   for (; s < nk; ++s) {
     const int b = static_cast<int>(s & 1);
+    if constexpr (SPREAD) {
+      if (pend) {
+        for (int sl = 8; sl < 16; ++sl) spread_piece(b ^ 1, kbase + (s + 1) * BK, sl);
+        pend = false;
+      }
+    }
     read_frags(Masked{}, 1, b, 1);
     mfmas(0);
     if constexpr (DM) apply_masks(1);
