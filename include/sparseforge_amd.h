@@ -497,6 +497,65 @@ int sf_rademacher_dot(const void* g, int g_dtype, const void* v, int v_dtype, in
 int sf_hutchinson_update(void* H, int h_dtype, const void* hvp, int hvp_dtype, const void* v, int v_dtype, int64_t n,
                          uint64_t seed, double beta, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Mask statistics and penalties: one fused pass per mask tensor
+ * (legacy/utils.py mid_penalty :876-938, sparsity_penalty :942-1025,
+ * nm_2_4_tile_stats :1029-1234, mask_stats :2069-2280).  Each call writes the
+ * SF_MSTAT_COUNT sums of one tensor (device doubles, in a fixed order, so the
+ * result is deterministic); the host composes the reference's scalars from
+ * the rows of all layers after a single copy.
+ * ------------------------------------------------------------------------- */
+#define SF_MSTAT_SUM 0        /* sum m                                                        */
+#define SF_MSTAT_SUM2 1       /* sum m * m                                                    */
+#define SF_MSTAT_ENTROPY 2    /* sum -(c log c) - ((1 - c) log(1 - c)), c = clamp(m, eps, 1 - eps)
+                                 in the mask dtype, the logs in f64 (NaN once some c == 1)    */
+#define SF_MSTAT_LT05 3       /* count m < 0.5   (each threshold rounded to the mask dtype)   */
+#define SF_MSTAT_LT01 4       /* count m < 0.1                                                */
+#define SF_MSTAT_LT001 5      /* count m < 0.01                                               */
+#define SF_MSTAT_GT90 6       /* count m > 0.9                                                */
+#define SF_MSTAT_GT99 7       /* count m > 0.99                                               */
+#define SF_MSTAT_GT05 8       /* count m > 0.5                                                */
+#define SF_MSTAT_SUM_LT05 9   /* sum of m over m < 0.5                                        */
+#define SF_MSTAT_SUM_GT05 10  /* sum of m over m > 0.5                                        */
+#define SF_MSTAT_MID 11       /* sum m * (1 - m), 1 - m and the product rounded to the mask dtype */
+#define SF_MSTAT_NONFINITE 12 /* count of NaN and +-inf                                       */
+#define SF_MSTAT_TOP2 13      /* over every full group of 4 along a row: sum of its 2 largest
+                                 (descending sort order, NaN largest)                         */
+#define SF_MSTAT_BOT2 14      /* ... sum of its 2 smallest                                    */
+#define SF_MSTAT_TAIL_LT05 15 /* count m < 0.5 in columns >= tail_col                         */
+#define SF_MSTAT_COUNT 16
+
+/* Scratch bytes of sf_mask_stats (per-workgroup partial sums). */
+size_t sf_mask_stats_workspace_size(void);
+
+/*
+ * out[0..SF_MSTAT_COUNT) (device doubles) = the sums above over mask [rows, cols]
+ * (row-major, dtype SF_DTYPE_F32 or SF_DTYPE_BF16).  eps: the entropy clamp of
+ * mask_stats (:2131-2132).  tail_col: first column of the sparsity_penalty
+ * threshold tail, (cols / M) * M (:983-993).  Groups of 4 for TOP2 / BOT2 start
+ * at column 0 of every row; the partial last group of a row is left out, as
+ * nm_2_4_tile_stats does (:1099-1104).
+ */
+int sf_mask_stats(const void* mask, int dtype, int64_t rows, int64_t cols, int64_t tail_col, float eps, double* out,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * hist[b] += number of idx[i] (i < take) with lo <= x <= hi and
+ * b = (int)((x - lo) * bins / (hi - lo)) (clamped to bins - 1), x = mask[idx[i]]
+ * as f32: the torch.histc of the sampled mask values in mask_stats
+ * (:2147-2152) with its device binning formula; NaN and values outside
+ * [lo, hi] are not counted.  hist: device uint64[bins], accumulated.
+ */
+int sf_mask_hist(const void* mask, int dtype, int64_t n, const int64_t* idx, int64_t take, int bins, float lo,
+                 float hi, unsigned long long* hist, void* stream);
+
+/*
+ * out[0] = sum of v[i] with keep[i] != 0, out[1] = sum of the others (device
+ * doubles, fixed order): the upper- and lower-half sums of the sorted block
+ * means in mask_stats (:2158-2181), with keep = sf_topk_keep(v, n - n / 2).
+ */
+int sf_keep_split_sum(const float* v, const float* keep, int64_t n, double* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

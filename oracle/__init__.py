@@ -31,4 +31,10 @@ sign or index, or a transposed operand):
   masks.glu_joint_update  against the reference's own output for three
                 consecutive steps (tests/golden/ref_glu_joint_f32.npz) and
                 the shared-target invariants.
+  stats.py      mid_penalty / sparsity_penalty / nm_2_4_tile_stats /
+                mask_stats against the reference's own outputs on small models
+                (tests/golden/ref_stats_*.npz: f32 and bf16 masks, threshold
+                neighbours, ragged rows, NaN and exact-1 entries), the group
+                sort against sorted(), the histogram binning against
+                torch.histc, and constant-mask closed forms.
 """

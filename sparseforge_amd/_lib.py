@@ -55,6 +55,13 @@ PENALTY_TARGET = 4
 BLOCK_MEAN = 0
 BLOCK_RMS = 1
 
+# sums of sf_mask_stats (one row of MSTAT_COUNT doubles per mask)
+MSTAT_SUM, MSTAT_SUM2, MSTAT_ENTROPY = 0, 1, 2
+MSTAT_LT05, MSTAT_LT01, MSTAT_LT001, MSTAT_GT90, MSTAT_GT99, MSTAT_GT05 = 3, 4, 5, 6, 7, 8
+MSTAT_SUM_LT05, MSTAT_SUM_GT05, MSTAT_MID, MSTAT_NONFINITE = 9, 10, 11, 12
+MSTAT_TOP2, MSTAT_BOT2, MSTAT_TAIL_LT05 = 13, 14, 15
+MSTAT_COUNT = 16
+
 EFF_SOFT = 0
 EFF_MIX = 1
 EFF_HARD = 2
@@ -208,6 +215,10 @@ SIGNATURES = {
     "sf_rademacher_dot_workspace_size": (_SZ, []),
     "sf_rademacher_dot": (_I, [_P, _I, _P, _I, _I64, ctypes.c_uint64, _P, _P, _SZ, _P]),
     "sf_hutchinson_update": (_I, [_P, _I, _P, _I, _P, _I, _I64, ctypes.c_uint64, ctypes.c_double, _P]),
+    "sf_mask_stats_workspace_size": (_SZ, []),
+    "sf_mask_stats": (_I, [_P, _I, _I64, _I64, _I64, _F, _P, _P, _SZ, _P]),
+    "sf_mask_hist": (_I, [_P, _I, _I64, _P, _I64, _I, _F, _F, _P, _P]),
+    "sf_keep_split_sum": (_I, [_P, _P, _I64, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -97,58 +97,6 @@ __device__ __forceinline__ void load4_any(const void* base, int dtype, int64_t i
     load4<SF_DTYPE_BF16>(base, i, n, vec, out);
 }
 
-// Group geometry: group g of the flattened [rows, ceil(cols/4)] grid.
-struct Group {
-  int64_t row, col, elem;  // first column / flat element of the group
-  int n;                   // valid members (4, or the tail width)
-  bool full;               // n == 4 (a complete N:M group)
-};
-
-// Grid-stride walk over the groups of a [rows, cols] matrix (gpr groups per
-// row).  The row / group-column / element of the current group are advanced
-// incrementally, so the loop does no 64-bit division (two per thread, once).
-struct GroupWalk {
-  int64_t gi, groups, stride;
-  int64_t row, gc, elem;   // current group
-  int64_t gpr, cols;
-  int64_t sdiv, smod;      // stride = sdiv * gpr + smod
-  int64_t estep, ewrap;    // element step per stride, correction when gc wraps
-  __device__ __forceinline__ GroupWalk(int64_t groups_, int64_t cols_, int64_t gpr_)
-      : groups(groups_), gpr(gpr_), cols(cols_) {
-    gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    stride = (int64_t)gridDim.x * blockDim.x;
-    row = gi / gpr;
-    gc = gi - row * gpr;
-    elem = row * cols + gc * 4;
-    sdiv = stride / gpr;
-    smod = stride - sdiv * gpr;
-    estep = sdiv * cols + smod * 4;
-    ewrap = cols - gpr * 4;
-  }
-  __device__ __forceinline__ bool live() const { return gi < groups; }
-  __device__ __forceinline__ void next() {
-    gi += stride;
-    row += sdiv;
-    gc += smod;
-    elem += estep;
-    if (gc >= gpr) {
-      gc -= gpr;
-      ++row;
-      elem += ewrap;
-    }
-  }
-  __device__ __forceinline__ Group group() const {
-    Group G;
-    G.row = row;
-    G.col = gc * 4;
-    G.elem = elem;
-    const int64_t rem = cols - G.col;
-    G.n = rem >= 4 ? 4 : static_cast<int>(rem);
-    G.full = G.n == 4;
-    return G;
-  }
-};
-
 // ---------------------------------------------------------------------------
 // Score of one element (legacy/sparse_modeling.py:1041-1079).  w, h, a are the
 // stored values (already widened to f32); each reference op rounds to its

@@ -1,0 +1,275 @@
+// Mask statistics and penalties (legacy/utils.py mid_penalty :876-938,
+// sparsity_penalty :942-1025, nm_2_4_tile_stats :1029-1234, mask_stats
+// :2069-2280).
+//
+// The reference walks every SparseLinear with a dozen separate torch
+// reductions per layer (sum, sum of squares, entropy, six threshold counts, two
+// conditional sums, m * (1 - m), a NaN scan, a sort of every group of 4) and a
+// host sync per scalar.  Here one HBM pass per mask produces all of them:
+// each thread walks groups of 4 along a row (16-byte loads for f32, 8-byte for
+// bf16), keeps the 16 sums in f64 registers, the workgroup folds them, and a
+// one-workgroup pass adds the per-workgroup partials in index order.  The
+// number of workgroups depends only on the shape, so results are bitwise
+// reproducible.  The host composes mid_penalty / sparsity_penalty /
+// nm_2_4_tile_stats / mask_stats from the rows of all layers after one copy.
+#include "sf_common.hpp"
+
+namespace sf {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kParts = 1024;  // most workgroups of the partial pass
+constexpr int kSlots = SF_MSTAT_COUNT;
+
+struct StatSpec {
+  int64_t cols, groups, gpr, tail_col;
+  float lo, hi;                // entropy clamp bounds: f32 values of eps and 1 - eps
+  float t01, t001, t90, t99;   // 0.1, 0.01, 0.9, 0.99 as the mask dtype holds them
+  bool vec;                    // every group full and vector-aligned
+};
+
+template <int DT>
+__device__ __forceinline__ float rnd(float x) {
+  if constexpr (DT == SF_DTYPE_BF16)
+    return round_bf16(x);
+  else
+    return x;
+}
+
+template <int DT>
+__device__ __forceinline__ void load_group(const void* p, int64_t i, int n, bool vec, float v[4]) {
+  if (vec) {
+    if constexpr (DT == SF_DTYPE_F32) {
+      const float4 q = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+      v[0] = q.x;
+      v[1] = q.y;
+      v[2] = q.z;
+      v[3] = q.w;
+    } else {
+      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+      v[0] = bf16_to_f32(static_cast<uint16_t>(q.x & 0xffffu));
+      v[1] = bf16_to_f32(static_cast<uint16_t>(q.x >> 16));
+      v[2] = bf16_to_f32(static_cast<uint16_t>(q.y & 0xffffu));
+      v[3] = bf16_to_f32(static_cast<uint16_t>(q.y >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = j < n ? load_as_f32(p, i + j, DT) : 0.0f;
+  }
+}
+
+// The per-element terms of every slot but TOP2 / BOT2.
+template <int DT>
+__device__ __forceinline__ void add_element(const StatSpec& s, float x, bool tail, double (&a)[kSlots]) {
+  const double d = static_cast<double>(x);
+  a[SF_MSTAT_SUM] += d;
+  a[SF_MSTAT_SUM2] += d * d;
+  // m.clamp(eps, 1 - eps) in the mask dtype (NaN passes through), then f64
+  float c = x < s.lo ? s.lo : (x > s.hi ? s.hi : x);
+  c = rnd<DT>(c);
+  const double cd = static_cast<double>(c), cm = 1.0 - cd;
+  a[SF_MSTAT_ENTROPY] += -(cd * log(cd)) - (cm * log(cm));
+  const bool lt05 = x < 0.5f, gt05 = x > 0.5f;
+  a[SF_MSTAT_LT05] += lt05 ? 1.0 : 0.0;
+  a[SF_MSTAT_LT01] += x < s.t01 ? 1.0 : 0.0;
+  a[SF_MSTAT_LT001] += x < s.t001 ? 1.0 : 0.0;
+  a[SF_MSTAT_GT90] += x > s.t90 ? 1.0 : 0.0;
+  a[SF_MSTAT_GT99] += x > s.t99 ? 1.0 : 0.0;
+  a[SF_MSTAT_GT05] += gt05 ? 1.0 : 0.0;
+  a[SF_MSTAT_SUM_LT05] += lt05 ? d : 0.0;
+  a[SF_MSTAT_SUM_GT05] += gt05 ? d : 0.0;
+  // m * (1 - m): both operations rounded to the mask dtype, as torch evaluates them
+  const float om = rnd<DT>(1.0f - x);
+  a[SF_MSTAT_MID] += static_cast<double>(rnd<DT>(x * om));
+  a[SF_MSTAT_NONFINITE] += isfinite(x) ? 0.0 : 1.0;
+  a[SF_MSTAT_TAIL_LT05] += (tail && lt05) ? 1.0 : 0.0;
+}
+
+// TOP2 / BOT2 of a full group: members ranked by the descending sort order
+// (ordered keys: NaN largest, -0 == +0; equal keys by position).
+__device__ __forceinline__ void add_tile(const float v[4], double (&a)[kSlots]) {
+  uint32_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) key[i] = ordered_key(v[i]);
+  float top[2] = {0.0f, 0.0f}, bot[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int r = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r += (key[j] > key[i]) || (j < i && key[j] == key[i]);
+    if (r == 0) top[0] = v[i];
+    if (r == 1) top[1] = v[i];
+    if (r == 2) bot[0] = v[i];
+    if (r == 3) bot[1] = v[i];
+  }
+  a[SF_MSTAT_TOP2] += static_cast<double>(top[0]) + static_cast<double>(top[1]);
+  a[SF_MSTAT_BOT2] += static_cast<double>(bot[0]) + static_cast<double>(bot[1]);
+}
+
+// Sum of each slot over the workgroup in a fixed tree order; thread t < kSlots
+// of the workgroup gets slot t.
+__device__ __forceinline__ double block_fold(double (&a)[kSlots]) {
+  __shared__ double red[kBlock / 64][kSlots];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) {
+    double v = a[k];
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    a[k] = v;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) red[wv][k] = a[k];
+  }
+  __syncthreads();
+  double t = 0.0;
+  if (threadIdx.x < kSlots)
+    for (int w = 0; w < kBlock / 64; ++w) t += red[w][threadIdx.x];
+  return t;
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kBlock) mask_stats_partial_kernel(StatSpec s, const void* __restrict__ mask,
+                                                                    double* __restrict__ partial) {
+  double a[kSlots];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) a[k] = 0.0;
+  for (GroupWalk w(s.groups, s.cols, s.gpr); w.live(); w.next()) {
+    const Group g = w.group();
+    float v[4];
+    load_group<DT>(mask, g.elem, g.n, VEC || (s.vec && g.full), v);
+    const int n = VEC ? 4 : g.n;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (j < n) add_element<DT>(s, v[j], g.col + j >= s.tail_col, a);
+    if (VEC || n == 4) add_tile(v, a);
+  }
+  const double t = block_fold(a);
+  if (threadIdx.x < kSlots) partial[blockIdx.x * (int64_t)kSlots + threadIdx.x] = t;
+}
+
+// out[k] = sum over parts in index order (thread k of one workgroup).
+__global__ void __launch_bounds__(64) mask_stats_final_kernel(const double* __restrict__ partial, int nparts,
+                                                              double* __restrict__ out) {
+  const int k = threadIdx.x;
+  if (k >= kSlots) return;
+  double t = 0.0;
+  for (int p = 0; p < nparts; ++p) t += partial[p * (int64_t)kSlots + k];
+  out[k] = t;
+}
+
+__global__ void __launch_bounds__(kBlock) mask_hist_kernel(const void* __restrict__ mask, int dtype, int64_t n,
+                                                           const int64_t* __restrict__ idx, int64_t take, int bins,
+                                                           float lo, float hi, unsigned long long* __restrict__ hist) {
+  const float span = hi - lo, fb = static_cast<float>(bins);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < take; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t j = idx[i];
+    if (j < 0 || j >= n) continue;
+    const float x = load_as_f32(mask, j, dtype);
+    if (!(x >= lo && x <= hi)) continue;
+    int b = static_cast<int>((x - lo) * fb / span);
+    if (b >= bins) b = bins - 1;
+    atomicAdd(&hist[b], 1ull);
+  }
+}
+
+__global__ void __launch_bounds__(kBlock) keep_split_sum_kernel(const float* __restrict__ v,
+                                                                const float* __restrict__ keep, int64_t n,
+                                                                double* __restrict__ out) {
+  double up = 0.0, lo = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += kBlock) {
+    const double x = static_cast<double>(v[i]);
+    if (keep[i] != 0.0f)
+      up += x;
+    else
+      lo += x;
+  }
+  __shared__ double red[2][kBlock];
+  red[0][threadIdx.x] = up;
+  red[1][threadIdx.x] = lo;
+  __syncthreads();
+  for (int h = kBlock / 2; h > 0; h >>= 1) {
+    if (threadIdx.x < h) {
+      red[0][threadIdx.x] += red[0][threadIdx.x + h];
+      red[1][threadIdx.x] += red[1][threadIdx.x + h];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[0] = red[0][0];
+    out[1] = red[1][0];
+  }
+}
+
+}  // namespace
+}  // namespace sf
+
+using namespace sf;
+
+extern "C" size_t sf_mask_stats_workspace_size(void) { return sizeof(double) * kParts * kSlots; }
+
+extern "C" int sf_mask_stats(const void* mask, int dtype, int64_t rows, int64_t cols, int64_t tail_col, float eps,
+                             double* out, void* workspace, size_t workspace_bytes, void* stream) {
+  SF_CHECK_ARG(dtype == SF_DTYPE_F32 || dtype == SF_DTYPE_BF16, "bad mask dtype %d", dtype);
+  SF_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  SF_CHECK_ARG(out, "null output");
+  SF_CHECK_ARG(rows * cols == 0 || mask, "null mask");
+  SF_CHECK_ARG(workspace && workspace_bytes >= sf_mask_stats_workspace_size(), "workspace too small");
+  StatSpec s;
+  s.cols = cols;
+  s.gpr = ceil_div(cols, 4);
+  s.groups = rows * s.gpr;
+  s.tail_col = tail_col < 0 ? 0 : tail_col;
+  s.lo = eps;
+  s.hi = static_cast<float>(1.0 - static_cast<double>(eps));
+  auto in_dtype = [&](float t) { return dtype == SF_DTYPE_BF16 ? round_bf16(t) : t; };
+  s.t01 = in_dtype(0.1f);
+  s.t001 = in_dtype(0.01f);
+  s.t90 = in_dtype(0.9f);
+  s.t99 = in_dtype(0.99f);
+  const int64_t align = dtype == SF_DTYPE_F32 ? 16 : 8;
+  s.vec = cols % 4 == 0 && (reinterpret_cast<uintptr_t>(mask) % align) == 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  double* partial = static_cast<double*>(workspace);
+  int nparts = 0;
+  if (s.groups > 0) {
+    nparts = static_cast<int>(ceil_div(s.groups, kBlock) < kParts ? ceil_div(s.groups, kBlock) : kParts);
+    if (dtype == SF_DTYPE_F32) {
+      if (s.vec)
+        mask_stats_partial_kernel<SF_DTYPE_F32, true><<<nparts, kBlock, 0, st>>>(s, mask, partial);
+      else
+        mask_stats_partial_kernel<SF_DTYPE_F32, false><<<nparts, kBlock, 0, st>>>(s, mask, partial);
+    } else {
+      if (s.vec)
+        mask_stats_partial_kernel<SF_DTYPE_BF16, true><<<nparts, kBlock, 0, st>>>(s, mask, partial);
+      else
+        mask_stats_partial_kernel<SF_DTYPE_BF16, false><<<nparts, kBlock, 0, st>>>(s, mask, partial);
+    }
+    if (int rc = launch_status("sf_mask_stats")) return rc;
+  }
+  mask_stats_final_kernel<<<1, 64, 0, st>>>(partial, nparts, out);
+  return launch_status("sf_mask_stats (final)");
+}
+
+extern "C" int sf_mask_hist(const void* mask, int dtype, int64_t n, const int64_t* idx, int64_t take, int bins,
+                            float lo, float hi, unsigned long long* hist, void* stream) {
+  SF_CHECK_ARG(dtype == SF_DTYPE_F32 || dtype == SF_DTYPE_BF16, "bad mask dtype %d", dtype);
+  SF_CHECK_ARG(n >= 0 && take >= 0, "negative size");
+  SF_CHECK_ARG(bins > 0, "bins must be positive");
+  SF_CHECK_ARG(hi > lo, "histogram range: hi (%g) must exceed lo (%g)", (double)hi, (double)lo);
+  SF_CHECK_ARG(hist, "null histogram");
+  if (take == 0 || n == 0) return SF_OK;
+  SF_CHECK_ARG(mask && idx, "null tensor");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  mask_hist_kernel<<<elementwise_grid(take, kBlock), kBlock, 0, st>>>(mask, dtype, n, idx, take, bins, lo, hi, hist);
+  return launch_status("sf_mask_hist");
+}
+
+extern "C" int sf_keep_split_sum(const float* v, const float* keep, int64_t n, double* out, void* stream) {
+  SF_CHECK_ARG(n >= 0, "negative size");
+  SF_CHECK_ARG(out, "null output");
+  SF_CHECK_ARG(n == 0 || (v && keep), "null tensor");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  keep_split_sum_kernel<<<1, kBlock, 0, st>>>(v, keep, n, out);
+  return launch_status("sf_keep_split_sum");
+}

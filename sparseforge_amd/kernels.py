@@ -300,6 +300,51 @@ def glu_update_masks(p: L.MaskParams, S: torch.Tensor, gate_mask: torch.Tensor, 
 
 
 # ---------------------------------------------------------------------------
+# mask statistics and penalties (legacy/utils.py :876-1234, :2069-2280)
+# ---------------------------------------------------------------------------
+def mask_stats_workspace(device: torch.device) -> torch.Tensor:
+    return _ws(L.lib().sf_mask_stats_workspace_size(), device)
+
+
+def mask_stats(mask: torch.Tensor, out: torch.Tensor, tail_col: int = 0, eps: float = 1e-8,
+               workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """out (f64 [MSTAT_COUNT], device) = the fused sums of one mask (rows x cols; a 1-D mask is one row)."""
+    dev = L.require_device(mask, out)
+    if out.dtype != torch.float64 or out.numel() != L.MSTAT_COUNT:
+        raise ValueError("mask_stats: out must be a contiguous float64 tensor of MSTAT_COUNT elements")
+    if mask.dim() not in (1, 2):
+        raise ValueError("mask_stats expects a 1-D or 2-D mask")
+    rows, cols = (1, mask.numel()) if mask.dim() == 1 else mask.shape
+    ws = workspace if workspace is not None else mask_stats_workspace(dev)
+    with _prof.region("sf_mask_stats", mask.numel() * mask.element_size(), "B", dev):
+        L.check(L.lib().sf_mask_stats(L.ptr(mask), L.dtype_code(mask), rows, cols, int(tail_col), float(eps),
+                                      L.ptr(out), L.ptr(ws), ws.numel(), L.stream(dev)), "sf_mask_stats")
+    return out
+
+
+def mask_hist(mask: torch.Tensor, idx: torch.Tensor, bins: int, lo: float, hi: float,
+              hist: torch.Tensor) -> torch.Tensor:
+    """hist (int64 [bins], device) += torch.histc-style counts of mask.flatten()[idx] over [lo, hi]."""
+    dev = L.require_device(mask, idx, hist)
+    if idx.dtype != torch.int64 or hist.dtype != torch.int64 or hist.numel() != int(bins):
+        raise ValueError("mask_hist: idx and hist must be int64, hist of `bins` elements")
+    L.check(L.lib().sf_mask_hist(L.ptr(mask), L.dtype_code(mask), mask.numel(), L.ptr(idx), idx.numel(), int(bins),
+                                 float(lo), float(hi), L.ptr(hist), L.stream(dev)), "sf_mask_hist")
+    return hist
+
+
+def keep_split_sum(v: torch.Tensor, keep: torch.Tensor) -> torch.Tensor:
+    """f64 [2] (device): sum of v where keep != 0, sum of the rest."""
+    dev = L.require_device(v, keep)
+    if v.dtype != torch.float32 or keep.dtype != torch.float32 or v.shape != keep.shape or v.dim() != 1:
+        raise ValueError("keep_split_sum expects two 1-D float32 tensors of one shape")
+    out = torch.empty(2, dtype=torch.float64, device=dev)
+    L.check(L.lib().sf_keep_split_sum(L.ptr(v), L.ptr(keep), v.numel(), L.ptr(out), L.stream(dev)),
+            "sf_keep_split_sum")
+    return out
+
+
+# ---------------------------------------------------------------------------
 # Cross-layer overlap of the mask updates
 # ---------------------------------------------------------------------------
 _SIDE_STREAMS: dict = {}

@@ -16,6 +16,8 @@ never travels with them.  Functions covered (reference file:line):
   hardblk_*   _hard_mask_from_soft, block types    legacy/sparse_modeling.py:537-718
   gateblk_*   compute_gate_target, block_sparse    legacy/sparse_modeling.py:1100-1158, :1237
   updblk_*    update_mask, block penalties/blockify legacy/sparse_modeling.py:1298-1529, :1598-1601
+  stats_*     mid_penalty, sparsity_penalty,       legacy/utils.py:876-1234, :2069-2280
+              nm_2_4_tile_stats, mask_stats
 
 The reference module imports wandb at top level without using it
 (legacy/sparse_modeling.py:20); an empty module object is registered under
@@ -23,7 +25,11 @@ that name before the import.  The tau sample of _tau_unstructured draws
 torch.randint right after torch.manual_seed(seed) inside compute_gate_target,
 so the same indices are recorded by replaying that draw.
 
-Run:  python tests/golden/make_reference_golden.py   (needs /root/reference)
+mask_stats samples torch.randint indices per layer; the draws are replayed
+after the same torch.manual_seed and stored with the fixture.
+
+Run:  python tests/golden/make_reference_golden.py [group ...]   (needs /root/reference;
+      groups: gate update glu adamw hutch linear kl bsr block stats, default all)
 """
 from __future__ import annotations
 
@@ -395,19 +401,101 @@ def block_cases(ref_sm, out):
         out[name] = rec
 
 
+def _bf16_neighbours(vals):
+    """bf16 values at and one bf16 step either side of each value."""
+    b = torch.tensor(vals, dtype=torch.float32).bfloat16()
+    bits = b.view(torch.int16)
+    out = [b, (bits + 1).view(torch.bfloat16), (bits - 1).view(torch.bfloat16)]
+    return torch.cat(out).float()
+
+
+def stats_cases(ref_sm, ref_utils, out):
+    """Penalties and mask statistics over small models of several SparseLinear layers: f32 and
+    bf16 masks, a ragged tail (in % 4 != 0), structured / unstructured / block_sparse types,
+    values on and next to the thresholds, and a layer holding NaN and an exact 1."""
+    specials = [0.0, 1e-9, 0.01, 0.1, 0.5, 0.9, 0.99, 0.999999]
+    models = {
+        "stats_f32": (torch.float32, [((24, 36), "structured", "nm_2_4"), ((20, 30), "unstructured", "nm_2_4"),
+                                      ((32, 48), "unstructured", "block_sparse16"),
+                                      ((10, 30), "structured", "nm_2_4")], "specials"),
+        "stats_bf16": (torch.bfloat16, [((16, 40), "structured", "nm_2_4"),
+                                        ((64, 40), "unstructured", "block_sparse32"),
+                                        ((12, 22), "structured", "nm_2_4")], "bf16edges"),
+        "stats_nan_f32": (torch.float32, [((8, 16), "structured", "nm_2_4"), ((8, 12), "unstructured", "nm_2_4")],
+                          "nan"),
+    }
+    for mi, (name, (dtype, layers, kind)) in enumerate(models.items()):
+        model = torch.nn.Module()
+        g = torch.Generator().manual_seed(1200 + mi)
+        rec = {}
+        for li, ((o, i), mt, ht) in enumerate(layers):
+            layer, _ = make_layer(ref_sm, o, i, dtype, 1300 + 10 * mi + li, mask_type=mt, hard_mask_type=ht)
+            m = torch.rand(o, i, generator=g)
+            if li == 1 and kind == "specials":
+                m.view(-1)[: len(specials)] = torch.tensor(specials)
+            if li == 0 and kind == "bf16edges":
+                e = _bf16_neighbours([0.01, 0.1, 0.5, 0.9, 0.99])
+                m.view(-1)[: e.numel()] = e
+            if li == 0 and kind == "nan":
+                m[0, 1] = float("nan")
+                m[3, 2] = 1.0
+            with torch.no_grad():
+                layer.mask.copy_(m.to(dtype))
+            model.add_module(f"l{li}", layer)
+            rec[f"mask{li}"] = np32(layer.mask)
+            rec[f"mask_type{li}"] = np.array(mt)
+            rec[f"hard_type{li}"] = np.array(ht)
+        rec["dtype"] = np.array("bf16" if dtype == torch.bfloat16 else "f32")
+        rec["n_layers"] = np.int64(len(layers))
+        rec["mid"] = np.float64(ref_utils.mid_penalty(model, 0.7).item())
+        pen, cur = ref_utils.sparsity_penalty(model, 0.4, 2.0)
+        rec["sp_pen"], rec["sp_cur"] = np.float64(pen.item()), np.float64(cur)
+        ts = ref_utils.nm_2_4_tile_stats(model)
+        rec["tile_keys"] = np.array(sorted(ts))
+        rec["tile_vals"] = np.array([ts[k] for k in sorted(ts)], dtype=np.float64)
+        seed, sample = 1400 + mi, 300
+        torch.manual_seed(seed)
+        ms = ref_utils.mask_stats(model, bins=100, sample_per_layer=sample)
+        rec["ms_keys"] = np.array(sorted(ms))
+        rec["ms_vals"] = np.array([ms[k] for k in sorted(ms)], dtype=np.float64)
+        torch.manual_seed(seed)  # replay the per-layer sample draws of mask_stats (:2145-2148)
+        for li, ((o, i), _, _) in enumerate(layers):
+            rec[f"idx{li}"] = torch.randint(0, o * i, (min(o * i, sample),)).numpy()
+        rec["sample"] = np.int64(sample)
+        out[name] = rec
+
+
+GROUPS = ("gate", "update", "glu", "adamw", "hutch", "linear", "kl", "bsr", "block", "stats")
+
+
 def main():
     ref_sm, ref_utils, ref_adamw = _import_reference()
     torch.set_num_threads(1)
+    groups = set(sys.argv[1:]) or set(GROUPS)
+    unknown = groups - set(GROUPS)
+    if unknown:
+        raise SystemExit(f"unknown groups {sorted(unknown)}; known: {GROUPS}")
     out = {}
-    gate_cases(ref_sm, out)
-    update_cases(ref_sm, out)
-    glu_case(ref_sm, ref_utils, out)
-    adamw_cases(ref_adamw, out)
-    hutchinson_case(ref_sm, ref_utils, out)
-    linear_case(ref_sm, out)
-    kl_case(ref_sm, out)
-    bsr_case(out)
-    block_cases(ref_sm, out)
+    if "gate" in groups:
+        gate_cases(ref_sm, out)
+    if "update" in groups:
+        update_cases(ref_sm, out)
+    if "glu" in groups:
+        glu_case(ref_sm, ref_utils, out)
+    if "adamw" in groups:
+        adamw_cases(ref_adamw, out)
+    if "hutch" in groups:
+        hutchinson_case(ref_sm, ref_utils, out)
+    if "linear" in groups:
+        linear_case(ref_sm, out)
+    if "kl" in groups:
+        kl_case(ref_sm, out)
+    if "bsr" in groups:
+        bsr_case(out)
+    if "block" in groups:
+        block_cases(ref_sm, out)
+    if "stats" in groups:
+        stats_cases(ref_sm, ref_utils, out)
     for name, rec in out.items():
         path = os.path.join(OUT, f"ref_{name}.npz")
         np.savez_compressed(path, torch_version=np.array(torch.__version__), **rec)
