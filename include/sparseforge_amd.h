@@ -556,6 +556,51 @@ int sf_mask_hist(const void* mask, int dtype, int64_t n, const int64_t* idx, int
  */
 int sf_keep_split_sum(const float* v, const float* keep, int64_t n, double* out, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * 2:4 packed weights and the sparse-MFMA forward of finalized models.  The
+ * reference hardens every mask and multiplies it into its weight at the end
+ * of training (legacy/main_llama.py:2499-2568) and then runs the plain
+ * forward F.linear(x, W_hard) (legacy/eval_wiki_ppl.py:548-651); for a 2:4
+ * hard mask the build stores W_hard as
+ *   vals [out, in / 2] bf16: the two kept values of every group of 4, in
+ *        column order;
+ *   idx  u32 [out / 32][in / 64][2][32] (out * in / 8 bytes): for row block
+ *        rb, 64-column chunk q, half h, row rb * 32 + r: bits 2j + 1 : 2j give
+ *        the column inside its group of the j-th kept value (j = 0..7) of
+ *        columns [64 q + 16 h, +16) in the low 16 bits and of
+ *        [64 q + 32 + 16 h, +16) in the high 16 bits,
+ * the operand layout of gfx950's v_smfmac_f32_32x32x32_bf16.  Needs
+ * out % 32 == 0 and in % 64 == 0.
+ * ------------------------------------------------------------------------- */
+
+/* Bytes of vals (returned) and of idx (*idx_bytes) for an out x in weight. */
+size_t sf_pack_2to4_sizes(int64_t out_features, int64_t in_features, size_t* idx_bytes);
+
+/*
+ * Pack W * mask (columns with mask != 0 kept; W, mask [out, in], f32 or bf16)
+ * into vals / idx.  A group with fewer than two kept columns is padded with
+ * zeros; groups with more than two are added to *bad_groups (device uint64,
+ * accumulated): the caller rejects the packing when it is nonzero.
+ */
+int sf_pack_2to4(const void* W, int w_dtype, const void* mask, int mask_dtype, int64_t out_features,
+                 int64_t in_features, void* vals, void* idx, unsigned long long* bad_groups, void* stream);
+
+/* Dense W [out, in] (f32 or bf16) from vals / idx: the inverse of sf_pack_2to4. */
+int sf_unpack_2to4(const void* vals, const void* idx, int64_t out_features, int64_t in_features, void* W, int w_dtype,
+                   void* stream);
+
+/*
+ * y [tokens, out] (row pitch ldy, f32 or bf16) = x [tokens, in] (bf16, row
+ * pitch ldx) . W_hard^T (+ bias [out]) with W_hard given packed: the forward
+ * F.linear(x, W * M_hard, b) of a finalized SparseLinear
+ * (legacy/sparse_modeling.py:737-739 dense_forward after
+ * legacy/eval_wiki_ppl.py:548-651).  f32 accumulation; a bf16 y is the
+ * rounded product plus the bias, rounded again.
+ */
+int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const void* vals, const void* idx, int64_t out_features,
+                 int64_t in_features, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

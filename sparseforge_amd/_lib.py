@@ -219,6 +219,10 @@ SIGNATURES = {
     "sf_mask_stats": (_I, [_P, _I, _I64, _I64, _I64, _F, _P, _P, _SZ, _P]),
     "sf_mask_hist": (_I, [_P, _I, _I64, _P, _I64, _I, _F, _F, _P, _P]),
     "sf_keep_split_sum": (_I, [_P, _P, _I64, _P, _P]),
+    "sf_pack_2to4_sizes": (_SZ, [_I64, _I64, ctypes.POINTER(ctypes.c_size_t)]),
+    "sf_pack_2to4": (_I, [_P, _I, _P, _I, _I64, _I64, _P, _P, _P, _P]),
+    "sf_unpack_2to4": (_I, [_P, _P, _I64, _I64, _P, _I, _P]),
+    "sf_gemm_2to4": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I, _P, _I, _I64, _P]),
 }
 
 _lock = threading.Lock()

@@ -1765,3 +1765,387 @@ extern "C" int sf_column_sum(const void* A, int a_dtype, int64_t rows, int64_t c
                      rows, cols, out, out_dtype);
   return launch_status("sf_column_sum");
 }
+
+// ---------------------------------------------------------------------------
+// 2:4 packed weights and the sparse-MFMA forward (finalized / inference
+// models: legacy/main_llama.py:2499-2568 hardens the masks and multiplies
+// them into the weights; legacy/eval_wiki_ppl.py:548-651 then runs the plain
+// forward).  A hardened 2:4 weight W [M = out, K = in] keeps two of every four
+// consecutive k; it is stored as
+//   vals [M, K / 2] bf16: the kept values of each group in column order;
+//   idx  u32 [M / 32][K / 64][2][32]: for row block rb, 64-column chunk q, half
+//        h and row rb * 32 + r, word (bits 2j + 1 : 2j = column in its group
+//        of the j-th kept value, j = 0..7) for columns [q * 64 + 16 h, +16) in
+//        the low 16 bits and [q * 64 + 32 + 16 h, +16) in the high 16 bits.
+// That is the operand layout of v_smfmac_f32_32x32x32_bf16 (A sparse, lane l:
+// row l % 32, dense k [16 (l / 32), +16) as 8 values + 16 index bits, the
+// index register's half picked by abid = the k-step), so the kernel moves
+// vals and idx straight from HBM to LDS and into the instruction.  The MFMA
+// computes y^T tiles (out x tokens); the epilogue writes them transposed.
+// ---------------------------------------------------------------------------
+namespace sf {
+namespace {
+
+typedef __bf16 bf16x16_t __attribute__((ext_vector_type(16)));
+
+struct Gemm24Args {
+  const void* x;       // [N = tokens, K] bf16, row pitch ldx
+  int64_t ldx;
+  const void* vals;    // [M, K / 2] bf16
+  const void* idx;     // u32 [M / 32][K / 64][2][32]
+  int64_t M, N, K;
+  const void* bias;    // [M] or null
+  int bias_dtype;
+  void* y;             // [N, M], row pitch ldy
+  int y_dtype;
+  int64_t ldy;
+  int64_t tiles_m, tiles_n;
+  int y_aligned;
+};
+
+constexpr int kEpi24Pitch = 68;  // f32 pitch of the transposed staging: 128 token rows x 64 out columns per wave
+constexpr uint32_t k24ABuf = 256u * 64;   // compressed W: 256 rows x 64 B (32 kept values of a 64-k stage)
+constexpr uint32_t k24IBuf = 8u * 64 * 4; // indices: 8 row blocks x 2 halves x 32 rows x u32
+constexpr uint32_t k24BBuf = 256u * kRowSw;
+constexpr uint32_t k24Stage = k24ABuf + k24IBuf + k24BBuf;
+
+// One 4-byte-per-lane copy global -> LDS: lane l's word lands at lds + 4 l.
+__device__ __forceinline__ void dma4(Rsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
+__global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const uint32_t base_l = lds_addr(smem);
+  int64_t tm, tn;
+  tile_coords(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = tm * kTileM, n0 = tn * kTileN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t nk = g.K / 64;
+
+  f32x16_t acc[kFragM * kFragN];
+#pragma unroll
+  for (int i = 0; i < kFragM * kFragN; ++i) acc[i] = f32x16_t{};
+
+  // fragment offsets inside a stage buffer
+  uint32_t aoff[2][kFragM], ioff[kFragM], boff[4][kFragN];
+#pragma unroll
+  for (int i = 0; i < kFragM; ++i) {
+    const int r = wm * kWaveM + i * 32 + (lane & 31), h = lane >> 5;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) aoff[kk][i] = (uint32_t)(r * 64 + (((kk * 2 + h) ^ ((r >> 2) & 3)) << 4));
+    ioff[i] = k24ABuf + (uint32_t)((((wm * 4 + i) * 2 + h) * 32 + (lane & 31)) * 4);
+  }
+#pragma unroll
+  for (int j = 0; j < kFragN; ++j) {
+    const uint32_t b = frag_base<true>(wn * kWaveN + j * 32 + (lane & 31));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) boff[q][j] = k24ABuf + k24IBuf + frag_at<true>(b, q);
+  }
+
+  // copies: compressed W rows (64-byte rows), index words (row blocks of 256 B), x rows
+  DmaMaskLoader da;
+  da.init(g.vals, g.K, m0, g.M, g.K);  // K bytes per row: K / 2 bf16
+  DmaLoader db;
+  db.init(g.x, g.ldx, n0, g.N, g.K);
+  const Rsrc ri = make_rsrc(g.idx, (g.M / 32) * nk * 256);
+  // wave w copies row blocks 2 w, 2 w + 1 of the tile: 256 contiguous bytes each per stage
+  uint32_t ivo[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int64_t rb = m0 / 32 + wave * 2 + q;
+    ivo[q] = rb < g.M / 32 ? (uint32_t)((rb * nk * 64 + lane) * 4) : kOob;
+  }
+  auto issue = [&](int buf, int64_t s) {
+    const uint32_t st = base_l + (uint32_t)buf * k24Stage;
+    da.issue<false>(st, s * 64);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      dma4(ri, st + k24ABuf + (uint32_t)((wave * 2 + q) * 256), ivo[q] >= kOob ? kOob : ivo[q], (uint32_t)(s * 256));
+    db.issue<false>(st + k24ABuf + k24IBuf, s * 64);
+  };
+
+  bf16x8_t fa[2][kFragM];
+  bf16x16_t fb[2][kFragN];
+  uint32_t fi[kFragM];
+  auto read_frags = [&](int slot, int buf, int kk) {
+    const unsigned char* st = smem + buf * k24Stage;
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8_t*>(st + aoff[kk][i]);
+    if (kk == 0) {
+#pragma unroll
+      for (int i = 0; i < kFragM; ++i) fi[i] = *reinterpret_cast<const uint32_t*>(st + ioff[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j) {
+      const bf16x8_t lo = *reinterpret_cast<const bf16x8_t*>(st + boff[2 * kk][j]);
+      const bf16x8_t hi = *reinterpret_cast<const bf16x8_t*>(st + boff[2 * kk + 1][j]);
+      fb[slot][j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+    }
+  };
+  // k-step 0 takes the low index half (abid 0), k-step 1 the high half (abid 1)
+  auto mfmas0 = [&](int slot) {
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+      for (int i = 0; i < kFragM; ++i)
+        acc[i * kFragN + j] =
+            __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], (int)fi[i], 0, 0);
+  };
+  auto mfmas1 = [&](int slot, const uint32_t (&ix)[kFragM]) {
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+      for (int i = 0; i < kFragM; ++i)
+        acc[i * kFragN + j] =
+            __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], (int)ix[i], 0, 1);
+  };
+
+  // Stage s in buffer s & 1: k-step 1 fragments read during the k-step 0
+  // products; one barrier a stage publishes stage s + 1 and frees buffer
+  // s & 1 for the copy of stage s + 2.
+  if (nk > 0) issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (nk > 0) read_frags(0, 0, 0);
+  for (int64_t s = 0; s < nk; ++s) {
+    const int b = static_cast<int>(s & 1);
+    uint32_t ix[kFragM];
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i) ix[i] = fi[i];
+    read_frags(1, b, 1);
+    mfmas0(0);
+    if (s + 1 < nk) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (s + 2 < nk) issue(b, s + 2);
+      read_frags(0, b ^ 1, 0);
+    }
+    mfmas1(1, ix);
+  }
+
+  // Epilogue: acc block (i, j) holds y^T rows (out) m = i * 32 + (e / 4) * 8 +
+  // (lane / 32) * 4 + e % 4 and column (token) n = j * 32 + lane % 32.  Each
+  // wave stages 64 out columns x its 128 tokens transposed, then every lane
+  // writes 8 consecutive outputs of one token row.
+  float* ep = reinterpret_cast<float*>(smem) + wave * (128 * kEpi24Pitch);
+  const bool ybf = g.y_dtype == SF_DTYPE_BF16;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int o = ii * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          ep[(j * 32 + (lane & 31)) * kEpi24Pitch + o] = acc[(2 * h + ii) * kFragN + j][e];
+        }
+    __syncthreads();
+    for (int it = 0; it < 16; ++it) {
+      const int flat = it * 64 + lane;
+      const int t = flat >> 3, oc = (flat & 7) * 8;
+      const int64_t row = n0 + wn * kWaveN + t, col = m0 + wm * kWaveM + h * 64 + oc;
+      if (row >= g.N || col >= g.M) continue;
+      float v[8];
+      const float4 p0 = *reinterpret_cast<const float4*>(ep + t * kEpi24Pitch + oc);
+      const float4 p1 = *reinterpret_cast<const float4*>(ep + t * kEpi24Pitch + oc + 4);
+      v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+      v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+      const int64_t off = row * g.ldy + col;
+      const int nv = col + 8 <= g.M ? 8 : static_cast<int>(g.M - col);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (q < nv && g.bias) {
+          const float bq = load_elem(g.bias, col + q, g.bias_dtype);
+          v[q] = ybf ? hround(hround(v[q]) + bq) : v[q] + bq;
+        }
+      }
+      if (nv == 8 && g.y_aligned && (off & 7) == 0) {
+        if (ybf) {
+          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(g.y) + off) =
+              make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+        } else {
+          float* yp = static_cast<float*>(g.y) + off;
+          *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+          *reinterpret_cast<float4*>(yp + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+      } else {
+        for (int q = 0; q < nv; ++q) {
+          if (ybf)
+            static_cast<uint16_t*>(g.y)[off + q] = hbits(v[q]);
+          else
+            static_cast<float*>(g.y)[off + q] = v[q];
+        }
+      }
+    }
+  }
+}
+
+constexpr size_t smem24_bytes() {
+  constexpr size_t ops = 2ull * k24Stage, epi = 4ull * 128 * kEpi24Pitch * sizeof(float);
+  return ops > epi ? ops : epi;
+}
+
+// Pack: one thread per (row, 16 columns): 4 groups -> 8 kept values (16 bytes)
+// and a 16-bit index word.  A group keeping fewer than two columns is padded
+// with zero values at its lowest unused columns; more than two is counted in
+// `bad` (the caller treats a nonzero count as an error).
+__global__ void __launch_bounds__(256) pack24_kernel(const void* __restrict__ W, int w_dtype, const void* __restrict__ mask,
+                                                     int m_dtype, int64_t M, int64_t K, uint16_t* __restrict__ vals,
+                                                     uint16_t* __restrict__ idx, unsigned long long* __restrict__ bad) {
+  const int64_t per_row = K / 16, total = M * per_row, nk = K / 64;
+  unsigned long long nbad = 0;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = t / per_row, c16 = t - row * per_row;
+    const int64_t e0 = row * K + c16 * 16;
+    uint16_t out[8];
+    uint32_t bits = 0;
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      int pos[2] = {-1, -1}, n = 0;
+      float v[2] = {0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int64_t e = e0 + grp * 4 + c;
+        const float m = load_as_f32(mask, e, m_dtype);
+        if (m != 0.0f) {
+          if (n < 2) {
+            pos[n] = c;
+            v[n] = load_as_f32(W, e, w_dtype) * m;
+          }
+          ++n;
+        }
+      }
+      if (n > 2) ++nbad;
+      // pad to two distinct columns with zero values
+      for (int c = 0; c < 4 && (pos[0] < 0 || pos[1] < 0); ++c) {
+        if (c == pos[0] || c == pos[1]) continue;
+        if (pos[0] < 0) pos[0] = c;
+        else pos[1] = c;
+      }
+      if (pos[1] < pos[0]) {  // column order
+        const int tp = pos[0]; pos[0] = pos[1]; pos[1] = tp;
+        const float tv = v[0]; v[0] = v[1]; v[1] = tv;
+      }
+      out[2 * grp] = f32_to_bf16(v[0]);
+      out[2 * grp + 1] = f32_to_bf16(v[1]);
+      bits |= (uint32_t)pos[0] << (4 * grp);
+      bits |= (uint32_t)pos[1] << (4 * grp + 2);
+    }
+    uint16_t* vp = vals + row * (K / 2) + c16 * 8;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) vp[q] = out[q];
+    const int64_t q64 = c16 >> 2, sub = c16 & 3;  // 16-column block inside its 64-column chunk
+    const int64_t word = (((row >> 5) * nk + q64) * 2 + (sub & 1)) * 32 + (row & 31);
+    idx[word * 2 + (sub >> 1)] = static_cast<uint16_t>(bits);
+  }
+  if (nbad) atomicAdd(bad, nbad);
+}
+
+__global__ void __launch_bounds__(256) unpack24_kernel(const uint16_t* __restrict__ vals, const uint16_t* __restrict__ idx,
+                                                       int64_t M, int64_t K, void* __restrict__ W, int w_dtype) {
+  const int64_t per_row = K / 16, total = M * per_row, nk = K / 64;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = t / per_row, c16 = t - row * per_row;
+    const int64_t q64 = c16 >> 2, sub = c16 & 3;
+    const int64_t word = (((row >> 5) * nk + q64) * 2 + (sub & 1)) * 32 + (row & 31);
+    const uint32_t bits = idx[word * 2 + (sub >> 1)];
+    float d[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) d[q] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int p = (bits >> (2 * j)) & 3;
+      d[(j >> 1) * 4 + p] += bf16_to_f32(vals[row * (K / 2) + c16 * 8 + j]);
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) store_from_f32(W, row * K + c16 * 16 + q, w_dtype, d[q]);
+  }
+}
+
+}  // namespace
+}  // namespace sf
+
+extern "C" size_t sf_pack_2to4_sizes(int64_t out_features, int64_t in_features, size_t* idx_bytes) {
+  if (idx_bytes) *idx_bytes = out_features > 0 && in_features > 0 ? (size_t)(out_features * in_features / 8) : 0;
+  return out_features > 0 && in_features > 0 ? (size_t)(out_features * (in_features / 2) * 2) : 0;
+}
+
+extern "C" int sf_pack_2to4(const void* W, int w_dtype, const void* mask, int mask_dtype, int64_t out_features,
+                            int64_t in_features, void* vals, void* idx, unsigned long long* bad_groups,
+                            void* stream) {
+  SF_CHECK_ARG((w_dtype == SF_DTYPE_F32 || w_dtype == SF_DTYPE_BF16) &&
+                   (mask_dtype == SF_DTYPE_F32 || mask_dtype == SF_DTYPE_BF16),
+               "bad dtype");
+  SF_CHECK_ARG(out_features > 0 && in_features > 0, "empty weight");
+  SF_CHECK_ARG(out_features % 32 == 0 && in_features % 64 == 0,
+               "2:4 packing needs out %% 32 == 0 and in %% 64 == 0 (got %lld x %lld)", (long long)out_features,
+               (long long)in_features);
+  SF_CHECK_ARG(W && mask && vals && idx && bad_groups, "null tensor");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t work = out_features * (in_features / 16);
+  pack24_kernel<<<elementwise_grid(work, 256), 256, 0, st>>>(W, w_dtype, mask, mask_dtype, out_features, in_features,
+                                                            static_cast<uint16_t*>(vals), static_cast<uint16_t*>(idx),
+                                                            bad_groups);
+  return launch_status("sf_pack_2to4");
+}
+
+extern "C" int sf_unpack_2to4(const void* vals, const void* idx, int64_t out_features, int64_t in_features, void* W,
+                              int w_dtype, void* stream) {
+  SF_CHECK_ARG(w_dtype == SF_DTYPE_F32 || w_dtype == SF_DTYPE_BF16, "bad dtype");
+  SF_CHECK_ARG(out_features > 0 && in_features > 0 && out_features % 32 == 0 && in_features % 64 == 0,
+               "bad packed shape %lld x %lld", (long long)out_features, (long long)in_features);
+  SF_CHECK_ARG(W && vals && idx, "null tensor");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t work = out_features * (in_features / 16);
+  unpack24_kernel<<<elementwise_grid(work, 256), 256, 0, st>>>(static_cast<const uint16_t*>(vals),
+                                                              static_cast<const uint16_t*>(idx), out_features,
+                                                              in_features, W, w_dtype);
+  return launch_status("sf_unpack_2to4");
+}
+
+extern "C" int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const void* vals, const void* idx,
+                            int64_t out_features, int64_t in_features, const void* bias, int bias_dtype, void* y,
+                            int y_dtype, int64_t ldy, void* stream) {
+  SF_CHECK_ARG(y_dtype == SF_DTYPE_F32 || y_dtype == SF_DTYPE_BF16, "bad output dtype");
+  SF_CHECK_ARG(!bias || bias_dtype == SF_DTYPE_F32 || bias_dtype == SF_DTYPE_BF16, "bad bias dtype");
+  SF_CHECK_ARG(tokens >= 0 && out_features > 0 && in_features > 0, "bad shape");
+  SF_CHECK_ARG(out_features % 32 == 0 && in_features % 64 == 0,
+               "2:4 product needs out %% 32 == 0 and in %% 64 == 0 (got %lld x %lld)", (long long)out_features,
+               (long long)in_features);
+  if (tokens == 0) return SF_OK;
+  SF_CHECK_ARG(x && vals && idx && y, "null tensor");
+  SF_CHECK_ARG(ldx >= in_features && ldx % 8 == 0 && al16(x) && al16(vals) && al16(idx),
+               "x rows, vals and idx must be 16-byte aligned (ldx %% 8 == 0)");
+  SF_CHECK_ARG(ldy >= out_features, "ldy < out_features");
+  SF_CHECK_ARG(tokens * ldx * 2 < (int64_t(1) << 31) && out_features * in_features < (int64_t(1) << 31),
+               "2:4 product: operands of 2 GiB or more are not supported");
+  Gemm24Args g;
+  g.x = x;
+  g.ldx = ldx;
+  g.vals = vals;
+  g.idx = idx;
+  g.M = out_features;
+  g.N = tokens;
+  g.K = in_features;
+  g.bias = bias;
+  g.bias_dtype = bias_dtype;
+  g.y = y;
+  g.y_dtype = y_dtype;
+  g.ldy = ldy;
+  g.tiles_m = ceil_div(out_features, kTileM);
+  g.tiles_n = ceil_div(tokens, kTileN);
+  g.y_aligned = al16(y);
+  static bool attr = false;
+  if (int rc = set_smem(gemm24_kernel, smem24_bytes(), attr)) return rc;
+  const int64_t tiles = g.tiles_m * g.tiles_n;
+  SF_CHECK_ARG(tiles < (1ll << 31), "grid too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(gemm24_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), smem24_bytes(), st, g);
+  return launch_status("sf_gemm_2to4");
+}
