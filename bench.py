@@ -25,6 +25,10 @@ Metric (BASELINE.json): SparseLinear fwd+bwd TFLOP/s at LLaMA-2-7B shapes;
 * ``distill_kl`` -- the fused distillation KL of Distill_Model: forward and
   student gradient over bf16 logits [16384, 32000]; GB/s counts 10 B per
   logit (forward reads s, t; backward reads s, t and writes ds).
+* ``sparse24_forward`` -- inference forward of a finalized decoder layer: the
+  seven linears with hard 2:4 weights packed (kept values + 2-bit indices)
+  through gfx950's sparse MFMA, beside the dense forward of the same weights;
+  dense-equivalent 2 T in out FLOPs.
 * ``roofline`` -- the dominant kernel (the sf_gemm MFMA GEMM): algorithmic
   FLOPs of the step over the summed device time of its sf_gemm launches,
   timed with HIP events on the launch stream inside the timed region.
@@ -276,6 +280,58 @@ def kl_leg(torch, dev, steps: int, warmup: int = 2) -> dict:
     return res
 
 
+def sparse24_leg(torch, dev, tokens: int, steps: int, warmup: int = 2) -> dict:
+    """Inference forward of a finalized 7B decoder layer: the seven linears with hard 2:4 weights packed
+    (sf_pack_2to4) through the sparse-MFMA product, beside the dense forward of the same weights."""
+    from sparseforge_amd import _lib as L
+    from sparseforge_amd import finalize as F
+    from sparseforge_amd import kernels as K
+    from sparseforge_amd import linear as lin
+    from sparseforge_amd import profiling as prof
+
+    gen = torch.Generator(device=dev).manual_seed(11)
+    layers = []
+    for _name, fin, fout in LINEARS:
+        W = (torch.randn(fout, fin, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        M = K.hard_mask(torch.rand(fout, fin, generator=gen, device=dev), L.HARD_NM_TAIL_KEEP, 2, 4).to(torch.bfloat16)
+        Wm = lin.apply_mask(W, M)
+        layers.append((F.pack_2to4(W, M), Wm, torch.randn(tokens, fin, generator=gen, device=dev).to(torch.bfloat16)))
+    flops = sum(2.0 * tokens * fin * fout for _n, fin, fout in LINEARS)
+
+    def run(sparse: bool):
+        for p, Wm, x in layers:
+            F.gemm_2to4(x, p) if sparse else lin.mm_nt(x, Wm)
+
+    res = {}
+    for sparse in (True, False):
+        for _ in range(warmup):
+            run(sparse)
+        torch.cuda.synchronize()
+        with prof.kernel_timer() as kt:
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                run(sparse)
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t0
+        k = kt.summary()["sf_gemm_2to4" if sparse else "sf_gemm"]
+        res[sparse] = (el, flops * steps / (k.total_ms * 1e-3) / 1e12, k)
+    el, ktf, k = res[True]
+    del_, dtf, _ = res[False]
+    out = {"value": round(flops * steps / el / 1e12, 3),
+           "unit": "TFLOP/s (dense-equivalent 2 T in out of the seven forwards)",
+           "ms_per_step": round(el * 1e3 / steps, 4), "tokens": tokens,
+           "dense_forward": {"value": round(flops * steps / del_ / 1e12, 3), "kernel_tflops": round(dtf, 3),
+                             "ms_per_step": round(del_ * 1e3 / steps, 4)},
+           "speedup_vs_dense": round(del_ / el, 3),
+           "roofline": {"bound": "mfma", "kernel": "sf_gemm_2to4 (gemm24_kernel, v_smfmac_f32_32x32x32_bf16)",
+                        "achieved": round(ktf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s dense-equivalent",
+                        "frac": round(ktf / PEAK_BF16_TFLOPS, 4), "launches": k.launches,
+                        "avg_launch_ms": round(k.avg_ms, 4)}}
+    log(f"2:4 forward: {out['value']:.0f} TFLOP/s dense-equivalent ({out['ms_per_step']:.3f} ms), dense "
+        f"{out['dense_forward']['value']:.0f} TFLOP/s, x{out['speedup_vs_dense']:.2f}")
+    return out
+
+
 def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
     import numpy as np
 
@@ -375,6 +431,8 @@ def main(argv=None) -> int:
     ap.add_argument("--adamw-steps", type=int, default=5)
     ap.add_argument("--bsr-steps", type=int, default=5, help="steps of the block-sparse leg (0 skips it)")
     ap.add_argument("--kl-steps", type=int, default=10, help="steps of the distillation-KL leg (0 skips it)")
+    ap.add_argument("--s24-steps", type=int, default=10,
+                    help="steps of the 2:4 packed inference-forward leg (0 skips it)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--calib", action="store_true",
                     help="first run one plain 256 MiB device copy (a known-size reference for HBM byte counters)")
@@ -462,6 +520,19 @@ def main(argv=None) -> int:
     st_gbs = ms_["sf_score_stats"].rate / 1e9
     log(f"mask update: {mel * 1e3 / a.mask_steps:.2f} ms/update of the arena, {mask_gbs:.0f} GB/s; "
         f"sf_update_mask {up_gbs:.0f} GB/s, sf_score_stats {st_gbs:.0f} GB/s")
+    # mask statistics / penalties of the whole model: one fused sf_mask_stats pass per soft mask (4 B/param)
+    srows = torch.empty((len(arena), L.MSTAT_COUNT), dtype=torch.float64, device=dev)
+    sws = K.mask_stats_workspace(dev)
+    for i, (_W, _H, M) in enumerate(arena):
+        K.mask_stats(M, srows[i], 0, 1e-8, sws)
+    torch.cuda.synchronize()
+    with prof.kernel_timer() as mst:
+        for i, (_W, _H, M) in enumerate(arena):
+            K.mask_stats(M, srows[i], 0, 1e-8, sws)
+        torch.cuda.synchronize()
+    msk = mst.summary()["sf_mask_stats"]
+    mstats_gbs = msk.rate / 1e9
+    log(f"mask statistics: sf_mask_stats {mstats_gbs:.0f} GB/s over {len(arena)} masks")
     # ---- mask-aware AdamW leg (same arena: W is the bf16 copy, M the mask) ---
     from sparseforge_amd.adamw import adamw_step_
 
@@ -500,6 +571,7 @@ def main(argv=None) -> int:
     torch.cuda.empty_cache()
 
     kl = kl_leg(torch, dev, a.kl_steps) if a.kl_steps > 0 else None
+    s24 = sparse24_leg(torch, dev, a.tokens, a.s24_steps) if a.s24_steps > 0 else None
     torch.cuda.empty_cache()
 
     traffic = profiled_traffic()
@@ -534,6 +606,9 @@ def main(argv=None) -> int:
                          "traffic": traffic.get("sf_update_mask_bytes_per_launch"), "traffic_unit": "B/launch",
                          "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4)},
             "score_stats_gbs": round(st_gbs, 2),
+            "mask_stats": {"kernel": "sf_mask_stats", "GB/s": round(mstats_gbs, 2), "bytes_per_param": 4,
+                           "frac": round(mstats_gbs / PEAK_HBM_GBS, 4), "launches": msk.launches,
+                           "avg_launch_ms": round(msk.avg_ms, 4)},
             "kernels": {n: {"launches": s.launches, "avg_ms": round(s.avg_ms, 4), "total_ms": round(s.total_ms, 3)}
                         for n, s in ms_.items()},
         },
@@ -550,6 +625,8 @@ def main(argv=None) -> int:
         out["block_sparse"] = bsr
     if kl:
         out["distill_kl"] = kl
+    if s24:
+        out["sparse24_forward"] = s24
     if not a.no_cpu:
         log("timing CPU baseline (numpy oracle)")
         out["cpu_baseline"] = cpu_baseline()

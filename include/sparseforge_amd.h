@@ -508,7 +508,8 @@ int sf_hutchinson_update(void* H, int h_dtype, const void* hvp, int hvp_dtype, c
 #define SF_MSTAT_SUM 0        /* sum m                                                        */
 #define SF_MSTAT_SUM2 1       /* sum m * m                                                    */
 #define SF_MSTAT_ENTROPY 2    /* sum -(c log c) - ((1 - c) log(1 - c)), c = clamp(m, eps, 1 - eps)
-                                 in the mask dtype, the logs in f64 (NaN once some c == 1)    */
+                                 in the mask dtype; terms in f32, summed in f64 (the reference
+                                 takes f64 logs: a few f32 ulp per term); NaN once some c == 1 */
 #define SF_MSTAT_LT05 3       /* count m < 0.5   (each threshold rounded to the mask dtype)   */
 #define SF_MSTAT_LT01 4       /* count m < 0.1                                                */
 #define SF_MSTAT_LT001 5      /* count m < 0.01                                               */

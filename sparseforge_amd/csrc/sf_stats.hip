@@ -7,8 +7,9 @@
 // conditional sums, m * (1 - m), a NaN scan, a sort of every group of 4) and a
 // host sync per scalar.  Here one HBM pass per mask produces all of them:
 // each thread walks groups of 4 along a row (16-byte loads for f32, 8-byte for
-// bf16), keeps the 16 sums in f64 registers, the workgroup folds them, and a
-// one-workgroup pass adds the per-workgroup partials in index order.  The
+// bf16), keeps the sums in f64 and the counts in u32 registers (the entropy
+// terms in f32), the workgroup folds them, and a
+// one-workgroup pass adds the per-workgroup partials in a fixed order.  The
 // number of workgroups depends only on the shape, so results are bitwise
 // reproducible.  The host composes mid_penalty / sparsity_penalty /
 // nm_2_4_tile_stats / mask_stats from the rows of all layers after one copy.
@@ -58,36 +59,45 @@ __device__ __forceinline__ void load_group(const void* p, int64_t i, int n, bool
   }
 }
 
-// The per-element terms of every slot but TOP2 / BOT2.
+// Per-thread accumulators: f64 sums (f32 inputs add exactly), u32 counts.
+struct Acc {
+  double s[kSlots];
+  uint32_t n[kSlots];
+};
+
+// The per-element terms of every slot but TOP2 / BOT2.  The entropy term is
+// evaluated in f32 (logf, log1pf) and summed in f64: within a few f32 ulp of
+// the reference's f64 logs per element (the f64 logs would cost more than
+// the memory pass).
 template <int DT>
-__device__ __forceinline__ void add_element(const StatSpec& s, float x, bool tail, double (&a)[kSlots]) {
+__device__ __forceinline__ void add_element(const StatSpec& s, float x, bool tail, Acc& a) {
   const double d = static_cast<double>(x);
-  a[SF_MSTAT_SUM] += d;
-  a[SF_MSTAT_SUM2] += d * d;
-  // m.clamp(eps, 1 - eps) in the mask dtype (NaN passes through), then f64
+  a.s[SF_MSTAT_SUM] += d;
+  a.s[SF_MSTAT_SUM2] += d * d;
+  // m.clamp(eps, 1 - eps) in the mask dtype (NaN passes through)
   float c = x < s.lo ? s.lo : (x > s.hi ? s.hi : x);
   c = rnd<DT>(c);
-  const double cd = static_cast<double>(c), cm = 1.0 - cd;
-  a[SF_MSTAT_ENTROPY] += -(cd * log(cd)) - (cm * log(cm));
+  const float ent = -(c * logf(c)) - ((1.0f - c) * log1pf(-c));  // c == 1: 0 * -inf = NaN, as in f64
+  a.s[SF_MSTAT_ENTROPY] += static_cast<double>(ent);
   const bool lt05 = x < 0.5f, gt05 = x > 0.5f;
-  a[SF_MSTAT_LT05] += lt05 ? 1.0 : 0.0;
-  a[SF_MSTAT_LT01] += x < s.t01 ? 1.0 : 0.0;
-  a[SF_MSTAT_LT001] += x < s.t001 ? 1.0 : 0.0;
-  a[SF_MSTAT_GT90] += x > s.t90 ? 1.0 : 0.0;
-  a[SF_MSTAT_GT99] += x > s.t99 ? 1.0 : 0.0;
-  a[SF_MSTAT_GT05] += gt05 ? 1.0 : 0.0;
-  a[SF_MSTAT_SUM_LT05] += lt05 ? d : 0.0;
-  a[SF_MSTAT_SUM_GT05] += gt05 ? d : 0.0;
+  a.n[SF_MSTAT_LT05] += lt05;
+  a.n[SF_MSTAT_LT01] += x < s.t01;
+  a.n[SF_MSTAT_LT001] += x < s.t001;
+  a.n[SF_MSTAT_GT90] += x > s.t90;
+  a.n[SF_MSTAT_GT99] += x > s.t99;
+  a.n[SF_MSTAT_GT05] += gt05;
+  a.s[SF_MSTAT_SUM_LT05] += lt05 ? d : 0.0;
+  a.s[SF_MSTAT_SUM_GT05] += gt05 ? d : 0.0;
   // m * (1 - m): both operations rounded to the mask dtype, as torch evaluates them
   const float om = rnd<DT>(1.0f - x);
-  a[SF_MSTAT_MID] += static_cast<double>(rnd<DT>(x * om));
-  a[SF_MSTAT_NONFINITE] += isfinite(x) ? 0.0 : 1.0;
-  a[SF_MSTAT_TAIL_LT05] += (tail && lt05) ? 1.0 : 0.0;
+  a.s[SF_MSTAT_MID] += static_cast<double>(rnd<DT>(x * om));
+  a.n[SF_MSTAT_NONFINITE] += !isfinite(x);
+  a.n[SF_MSTAT_TAIL_LT05] += tail && lt05;
 }
 
 // TOP2 / BOT2 of a full group: members ranked by the descending sort order
 // (ordered keys: NaN largest, -0 == +0; equal keys by position).
-__device__ __forceinline__ void add_tile(const float v[4], double (&a)[kSlots]) {
+__device__ __forceinline__ void add_tile(const float v[4], Acc& a) {
   uint32_t key[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) key[i] = ordered_key(v[i]);
@@ -102,8 +112,8 @@ __device__ __forceinline__ void add_tile(const float v[4], double (&a)[kSlots]) 
     if (r == 2) bot[0] = v[i];
     if (r == 3) bot[1] = v[i];
   }
-  a[SF_MSTAT_TOP2] += static_cast<double>(top[0]) + static_cast<double>(top[1]);
-  a[SF_MSTAT_BOT2] += static_cast<double>(bot[0]) + static_cast<double>(bot[1]);
+  a.s[SF_MSTAT_TOP2] += static_cast<double>(top[0]) + static_cast<double>(top[1]);
+  a.s[SF_MSTAT_BOT2] += static_cast<double>(bot[0]) + static_cast<double>(bot[1]);
 }
 
 // Sum of each slot over the workgroup in a fixed tree order; thread t < kSlots
@@ -131,9 +141,12 @@ __device__ __forceinline__ double block_fold(double (&a)[kSlots]) {
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(kBlock) mask_stats_partial_kernel(StatSpec s, const void* __restrict__ mask,
                                                                     double* __restrict__ partial) {
-  double a[kSlots];
+  Acc a;
 #pragma unroll
-  for (int k = 0; k < kSlots; ++k) a[k] = 0.0;
+  for (int k = 0; k < kSlots; ++k) {
+    a.s[k] = 0.0;
+    a.n[k] = 0u;
+  }
   for (GroupWalk w(s.groups, s.cols, s.gpr); w.live(); w.next()) {
     const Group g = w.group();
     float v[4];
@@ -144,18 +157,34 @@ __global__ void __launch_bounds__(kBlock) mask_stats_partial_kernel(StatSpec s, 
       if (j < n) add_element<DT>(s, v[j], g.col + j >= s.tail_col, a);
     if (VEC || n == 4) add_tile(v, a);
   }
-  const double t = block_fold(a);
-  if (threadIdx.x < kSlots) partial[blockIdx.x * (int64_t)kSlots + threadIdx.x] = t;
+  double t[kSlots];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) t[k] = a.s[k] + static_cast<double>(a.n[k]);  // each slot is a sum or a count
+  const double tot = block_fold(t);
+  if (threadIdx.x < kSlots) partial[blockIdx.x * (int64_t)kSlots + threadIdx.x] = tot;
 }
 
-// out[k] = sum over parts in index order (thread k of one workgroup).
-__global__ void __launch_bounds__(64) mask_stats_final_kernel(const double* __restrict__ partial, int nparts,
-                                                              double* __restrict__ out) {
-  const int k = threadIdx.x;
-  if (k >= kSlots) return;
-  double t = 0.0;
-  for (int p = 0; p < nparts; ++p) t += partial[p * (int64_t)kSlots + k];
-  out[k] = t;
+// out[k] = sum over the parts: thread t adds parts t, t + 256, ..., then a
+// fixed tree over the threads (deterministic).
+__global__ void __launch_bounds__(kBlock) mask_stats_final_kernel(const double* __restrict__ partial, int nparts,
+                                                                  double* __restrict__ out) {
+  __shared__ double red[kSlots][kBlock];
+  double t[kSlots];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) t[k] = 0.0;
+  for (int p = threadIdx.x; p < nparts; p += kBlock)
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) t[k] += partial[p * (int64_t)kSlots + k];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) red[k][threadIdx.x] = t[k];
+  __syncthreads();
+  for (int h = kBlock / 2; h > 0; h >>= 1) {
+    if (threadIdx.x < h)
+#pragma unroll
+      for (int k = 0; k < kSlots; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x < kSlots) out[threadIdx.x] = red[threadIdx.x][0];
 }
 
 __global__ void __launch_bounds__(kBlock) mask_hist_kernel(const void* __restrict__ mask, int dtype, int64_t n,
@@ -247,7 +276,7 @@ extern "C" int sf_mask_stats(const void* mask, int dtype, int64_t rows, int64_t 
     }
     if (int rc = launch_status("sf_mask_stats")) return rc;
   }
-  mask_stats_final_kernel<<<1, 64, 0, st>>>(partial, nparts, out);
+  mask_stats_final_kernel<<<1, kBlock, 0, st>>>(partial, nparts, out);
   return launch_status("sf_mask_stats (final)");
 }
 

@@ -26,6 +26,7 @@ import torch
 
 from . import _lib as L
 from . import linear as LIN
+from . import profiling as _prof
 from .sparse_modeling import SparseLinear
 
 
@@ -79,9 +80,10 @@ def gemm_2to4(x: torch.Tensor, p: Packed2to4, bias: torch.Tensor | None = None,
     if bias is not None and bias.shape != (p.out_features,):
         raise ValueError("gemm_2to4: bias must be [out_features]")
     y = torch.empty(x.shape[0], p.out_features, dtype=out_dtype or x.dtype, device=dev)
-    L.check(L.lib().sf_gemm_2to4(L.ptr(x), x.shape[1], x.shape[0], L.ptr(p.vals), L.ptr(p.idx), p.out_features,
-                                 p.in_features, L.ptr(bias), L.dtype_code(bias) if bias is not None else L.DT_F32,
-                                 L.ptr(y), L.dtype_code(y), p.out_features, L.stream(dev)), "sf_gemm_2to4")
+    with _prof.region("sf_gemm_2to4", 2.0 * x.shape[0] * p.in_features * p.out_features, "FLOP", dev):
+        L.check(L.lib().sf_gemm_2to4(L.ptr(x), x.shape[1], x.shape[0], L.ptr(p.vals), L.ptr(p.idx), p.out_features,
+                                     p.in_features, L.ptr(bias), L.dtype_code(bias) if bias is not None else L.DT_F32,
+                                     L.ptr(y), L.dtype_code(y), p.out_features, L.stream(dev)), "sf_gemm_2to4")
     return y
 
 
