@@ -31,7 +31,10 @@ Metric (BASELINE.json): SparseLinear fwd+bwd TFLOP/s at LLaMA-2-7B shapes;
   dense-equivalent 2 T in out FLOPs.
 * ``roofline`` -- the dominant kernel (the sf_gemm MFMA GEMM): algorithmic
   FLOPs of the step over the summed device time of its sf_gemm launches,
-  timed with HIP events on the launch stream inside the timed region.
+  timed with HIP events on the launch stream inside the timed region.  ``peak`` is the published dense bf16 figure; ``mfma_sustained`` is what
+  an MFMA-only loop (sf_mfma_probe, operands distributed like the GEMM's, no
+  memory traffic)
+  sustains on the same GPU, the practical ceiling under that figure.
 * ``cpu_baseline`` -- the numpy oracle (oracle/linear.py, a CPU restatement of
   the reference's FusedMaskedLinearSTE + SLoRB path) on the host cores, on a
   bounded token sample of the same seven shapes (rank 0, N = 1 only).
@@ -332,6 +335,27 @@ def sparse24_leg(torch, dev, tokens: int, steps: int, warmup: int = 2) -> dict:
     return out
 
 
+def mfma_sustained(torch, dev, iters: int = 4000, blocks: int = 1024, reps: int = 6) -> float:
+    """TFLOP/s of sf_mfma_probe (MFMA-only loop, bf16 register operands distributed like the GEMM's):
+    the rate this GPU sustains on the bf16 MFMA pipe alone, best of `reps` after a clock ramp-up."""
+    from sparseforge_amd import _lib as L
+
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    flops = blocks * 4.0 * iters * 16 * 32768
+    best = 0.0
+    for r in range(reps + 3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        L.check(L.lib().sf_mfma_probe(iters, blocks, L.ptr(out), L.stream(dev)), "sf_mfma_probe")
+        e1.record(st)
+        e1.synchronize()
+        if r >= 3:
+            best = max(best, flops / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+    log(f"MFMA-only probe: {best:.0f} TFLOP/s sustained (bf16 32x32x16, normal-like operands)")
+    return best
+
+
 def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
     import numpy as np
 
@@ -572,6 +596,7 @@ def main(argv=None) -> int:
 
     kl = kl_leg(torch, dev, a.kl_steps) if a.kl_steps > 0 else None
     s24 = sparse24_leg(torch, dev, a.tokens, a.s24_steps) if a.s24_steps > 0 else None
+    sustained = mfma_sustained(torch, dev)
     torch.cuda.empty_cache()
 
     traffic = profiled_traffic()
@@ -596,6 +621,7 @@ def main(argv=None) -> int:
                      "traffic": traffic.get("sf_gemm_bytes_per_launch"), "traffic_unit": "B/launch",
                      "traffic_source": TRAFFIC_SUMMARY,
                      "kernel": "sf_gemm (gemm_bf16_kernel)", "launches": g.launches,
+                     "mfma_sustained": round(sustained, 1), "frac_of_sustained": round(gemm_tflops / sustained, 4),
                      "avg_launch_ms": round(g.avg_ms, 4)},
         "kernels": other,
         "mask_update": {

@@ -602,6 +602,16 @@ int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const void* vals, c
                  int64_t in_features, const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
                  void* stream);
 
+/*
+ * Sustained MFMA rate probe, a measurement aid with no counterpart in the
+ * reference (bench.py reports the rate beside the published dense peak):
+ * `blocks` workgroups of 4 waves, each wave iters x 16
+ * v_mfma_f32_32x32x16_bf16 on register operands distributed like a GEMM's
+ * (about N(0, 1) and N(0, 0.02)), no memory traffic in the loop; FLOPs = blocks * 4 * iters * 16 * 32768.  out: device
+ * float[blocks * 256] checksums.
+ */
+int sf_mfma_probe(int iters, int blocks, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

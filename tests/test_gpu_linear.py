@@ -310,3 +310,12 @@ def test_gemm_split_k_deterministic(cuda_device):
     r1 = lin.mm_tn(x, y)
     r2 = lin.mm_tn(x, y)
     assert torch.equal(r1, r2)
+
+
+def test_mfma_probe_runs(cuda_device):
+    """The sustained-rate probe bench.py reports beside the peak: runs and yields finite checksums."""
+    L, _ = _lin()
+    out = torch.empty(8 * 256, dtype=torch.float32, device=cuda_device)
+    L.check(L.lib().sf_mfma_probe(10, 8, L.ptr(out), L.stream(cuda_device)), "sf_mfma_probe")
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all() and (out != 0).any()
