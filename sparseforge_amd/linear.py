@@ -224,15 +224,15 @@ class _MaskedLinearBackward(torch.autograd.Function):
     """(gy, x, W, P, S, b?) -> (dx, dW, db, dP, dS); differentiable for the HVP."""
 
     @staticmethod
-    def forward(ctx, gy, x, W, P, S, E, decay, has_bias, z_fwd=None):
+    def forward(ctx, gy, x, W, P, S, E, decay, has_bias, z_fwd=None, wm_fwd=None):
         has_slorb = P is not None
         # z = x P^T is kept from the forward; its dependence on x and P is
         # written out explicitly in backward(), so the cached copy is detached.
         z = (z_fwd if z_fwd is not None else mm_nt(x, P)) if has_slorb else None
         dz = mm_nn(gy, S) if has_slorb else None
-        # dx = gy (W.E): the masked weight is rebuilt (one elementwise pass) rather than kept from the
-        # forward, so the saved state is x, W and E as in the reference
-        Wm = apply_mask(W, E) if E is not None else W
+        # dx = gy (W.E): the forward's masked weight when it kept one (no weight-scaling factor),
+        # else rebuilt with one elementwise pass
+        Wm = wm_fwd if wm_fwd is not None else (apply_mask(W, E) if E is not None else W)
         if has_slorb:
             dx = mm_nn(gy, Wm, A2=dz, B2=P, K2=P.shape[0])
         else:
@@ -318,7 +318,7 @@ class _MaskedLinearBackward(torch.autograd.Function):
                 gP = mm_tn(w, x)
             if u is not None:
                 gS = mm_tn(gy, u)
-        return ggy, gx, gW, gP, gS, None, None, None, None
+        return ggy, gx, gW, gP, gS, None, None, None, None, None
 
 
 class _MaskedLinear(torch.autograd.Function):
@@ -332,6 +332,9 @@ class _MaskedLinear(torch.autograd.Function):
             y = mm_nt(x2, Wm, bscale=s, A2=z, B2=S, K2=P.shape[0], bias=bias)
         else:
             y = mm_nt(x2, Wm, bscale=s, bias=bias)
+        # Without a weight-scaling factor the input gradient needs the same W.E: it stays in HBM until
+        # the backward (2 B/param of bf16 weight) instead of being rebuilt there by another pass.
+        ctx.wm = Wm if (E is not None and scale == 1.0) else None
         del Wm
         ctx.save_for_backward(x2, W, P, S, E, z)
         ctx.decay = decay
@@ -342,7 +345,8 @@ class _MaskedLinear(torch.autograd.Function):
     def backward(ctx, gy):
         x2, W, P, S, E, z = ctx.saved_tensors
         gy = gy.contiguous().to(W.dtype)
-        dx, dW, db, dP, dS = _MaskedLinearBackward.apply(gy, x2, W, P, S, E, ctx.decay, ctx.has_bias, z)
+        wm, ctx.wm = ctx.wm, None
+        dx, dW, db, dP, dS = _MaskedLinearBackward.apply(gy, x2, W, P, S, E, ctx.decay, ctx.has_bias, z, wm)
         return dx, dW, db, dP, dS, None, None, None
 
 
