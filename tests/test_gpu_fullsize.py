@@ -1,0 +1,91 @@
+"""GPU checks at the benchmark's full sizes, through size-independent properties and torch's
+own float32 GPU results (the float64 CPU oracle would take minutes at these sizes).
+
+* SparseLinear fwd / dX / dW at the gate / down shapes of a LLaMA-2-7B layer (T = 8192) with
+  the hard 2:4 mask: against torch float32 products of the same bf16 operands, rtol 2e-2
+  (bf16) relative to the output scale.
+* the fused mask update over a full [11008, 4096] layer: the new mask stays in [0, 1], its
+  hard 2:4 projection keeps exactly two of every four, and the flip count equals the number
+  of changed hard-mask entries counted independently.
+* the distillation KL over the full [16384, 32000] logits: against torch's float32
+  log-softmax KL rounded to the logits' dtype, within one bf16 ulp.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(got, ref):
+    got, ref = got.detach().float(), ref.detach().float()
+    return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("in_f,out_f", [(4096, 11008), (11008, 4096)])
+def test_sparse_linear_full_shape(cuda_device, in_f, out_f):
+    from sparseforge_amd import _lib as L
+    from sparseforge_amd import kernels as K
+    from sparseforge_amd.linear import masked_linear
+
+    print(f"[fullsize] linear {in_f}->{out_f}", flush=True)
+    T = 8192
+    g = torch.Generator(device=cuda_device).manual_seed(in_f + out_f)
+    x = torch.randn(T, in_f, generator=g, device=cuda_device).to(torch.bfloat16).requires_grad_(True)
+    W = (torch.randn(out_f, in_f, generator=g, device=cuda_device) * 0.02).to(torch.bfloat16).requires_grad_(True)
+    soft = torch.rand(out_f, in_f, generator=g, device=cuda_device)
+    y = masked_linear(x, W, None, soft, "mix", 0.0, L.HARD_NM_TAIL_KEEP, 2, 1.0)
+    gy = torch.randn(T, out_f, generator=g, device=cuda_device).to(torch.bfloat16)
+    y.backward(gy)
+    E = K.hard_mask(soft, L.HARD_NM_TAIL_KEEP, 2, 4).float()
+    Wm = W.detach().float() * E
+    xf, gyf = x.detach().float(), gy.float()
+    assert rel_err(y, xf @ Wm.t()) < 2e-2
+    assert rel_err(x.grad, gyf @ Wm) < 2e-2                  # dX = dY (W . M)
+    assert rel_err(W.grad, gyf.t() @ xf) < 2e-2              # dW = dY^T X (straight-through, unmasked)
+
+
+def test_update_mask_full_layer_properties(cuda_device):
+    from sparseforge_amd import _lib as L
+    from sparseforge_amd import kernels as K
+    from sparseforge_amd import sparse_modeling as sm
+
+    print("[fullsize] update_mask 11008x4096", flush=True)
+    out_f, in_f = 11008, 4096
+    cfg = sm.SparseLinearConfig(mask_type="unstructured", hard_mask_type="nm_2_4", mask_metric="hessian_ratio",
+                                sparsity_warmup_steps=0, mask_update_period=1, tau_sample_size=262144,
+                                temp_init=0.5)
+    cfg.enable_hutchinson = True
+    layer = sm.SparseLinear(in_f, out_f, sparselinear_config=cfg, bias=False).to(cuda_device)
+    g = torch.Generator(device=cuda_device).manual_seed(5)
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(out_f, in_f, generator=g, device=cuda_device) * 0.02)
+        layer.hessian_diag.copy_(torch.rand(out_f, in_f, generator=g, device=cuda_device) * 1e-3 + 1e-6)
+        layer.mask.copy_(torch.rand(out_f, in_f, generator=g, device=cuda_device))
+    before = K.hard_mask(layer.mask.detach().contiguous(), L.HARD_NM_TAIL_KEEP, 2, 4)
+    layer.update_mask(10)
+    m = layer.mask.detach()
+    assert bool(((m >= 0) & (m <= 1)).all())
+    after = K.hard_mask(m.contiguous(), L.HARD_NM_TAIL_KEEP, 2, 4)
+    kept = after.view(out_f, in_f // 4, 4).sum(-1)
+    assert bool((kept == 2).all())
+    changed = int((before != after).sum())
+    assert int(layer.weight.flipped_mask) == changed
+
+
+def test_distill_kl_full_logits(cuda_device):
+    from sparseforge_amd.distill import chunked_kl_loss
+
+    print("[fullsize] kl 16384x32000", flush=True)
+    g = torch.Generator(device=cuda_device).manual_seed(9)
+    s = (torch.randn(16384, 32000, generator=g, device=cuda_device) * 4).to(torch.bfloat16)
+    t = (torch.randn(16384, 32000, generator=g, device=cuda_device) * 4).to(torch.bfloat16)
+    loss = chunked_kl_loss(s, t, 2)
+    ref = 0.0
+    for i in range(0, 16384, 2048):  # torch float32 log-softmax KL per 2048-row chunk (the reference's chunking)
+        ls = torch.log_softmax(s[i:i + 2048].float() / 2, -1)
+        lt = torch.log_softmax(t[i:i + 2048].float() / 2, -1)
+        ref += float((lt.exp() * (lt - ls)).sum(dtype=torch.float64))
+    ref = ref * 4 / 16384
+    # the loss comes back in the logits' dtype (bf16 here), as the reference returns it
+    want = float(torch.tensor(ref, dtype=torch.float32).to(loss.dtype))
+    assert float(loss) == pytest.approx(want, rel=8e-3)  # within one bf16 ulp of the rounded float32 value
