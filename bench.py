@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the SparseForge sparse-training hot path on one MI355X.
 
-Metric: SparseLinear fwd+bwd TFLOP/s at LLaMA-2-7B shapes;
+Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLaMA-2-7B shapes;
 2:4 mask-update HBM GB/s.
 
 * ``value`` -- one step = forward + backward of the seven SparseLinear layers
