@@ -18,6 +18,7 @@ never travels with them.  Functions covered (reference file:line):
   updblk_*    update_mask, block penalties/blockify legacy/sparse_modeling.py:1298-1529, :1598-1601
   stats_*     mid_penalty, sparsity_penalty,       legacy/utils.py:876-1234, :2069-2280
               nm_2_4_tile_stats, mask_stats
+  harden_*    harden_fraction                      legacy/utils.py:1236-1276
 
 The reference module imports wandb at top level without using it
 (legacy/sparse_modeling.py:20); an empty module object is registered under
@@ -29,7 +30,7 @@ mask_stats samples torch.randint indices per layer; the draws are replayed
 after the same torch.manual_seed and stored with the fixture.
 
 Run:  python tests/golden/make_reference_golden.py [group ...]   (needs /root/reference;
-      groups: gate update glu adamw hutch linear kl bsr block stats, default all)
+      groups: gate update glu adamw hutch linear kl bsr block stats harden, default all)
 """
 from __future__ import annotations
 
@@ -465,7 +466,32 @@ def stats_cases(ref_sm, ref_utils, out):
         out[name] = rec
 
 
-GROUPS = ("gate", "update", "glu", "adamw", "hutch", "linear", "kl", "bsr", "block", "stats")
+def harden_case(ref_sm, ref_utils, out):
+    """harden_fraction over two layers with real frozen flags: masks spread around 0.5 (some on the
+    band edges, some already frozen, repeated values at the threshold)."""
+    model = torch.nn.Module()
+    g = torch.Generator().manual_seed(1500)
+    rec = {}
+    for li, (o, i) in enumerate([(16, 24), (8, 40)]):
+        layer, _ = make_layer(ref_sm, o, i, torch.float32, 1510 + li, mask_type="unstructured",
+                              hard_mask_type="nm_2_4", freeze_low=0.05, freeze_high=0.95)
+        m = 0.3 + 0.4 * torch.rand(o, i, generator=g)
+        m.view(-1)[:6] = torch.tensor([0.4, 0.6, 0.5, 0.5, 0.45, 0.55])
+        fz = (torch.rand(o, i, generator=g) < 0.1).float()
+        with torch.no_grad():
+            layer.mask.copy_(m)
+            layer.frozen_mask_flags.copy_(fz)
+        model.add_module(f"l{li}", layer)
+        rec[f"mask_in{li}"] = np32(layer.mask)
+        rec[f"frozen_in{li}"] = np32(layer.frozen_mask_flags)
+    rec["count"] = np.int64(ref_utils.harden_fraction(model, 0.2, 0.4, 0.6))
+    for li, layer in enumerate(model.children()):
+        rec[f"mask_out{li}"] = np32(layer.mask)
+        rec[f"frozen_out{li}"] = np32(layer.frozen_mask_flags)
+    out["harden_f32"] = rec
+
+
+GROUPS = ("gate", "update", "glu", "adamw", "hutch", "linear", "kl", "bsr", "block", "stats", "harden")
 
 
 def main():
@@ -496,6 +522,8 @@ def main():
         block_cases(ref_sm, out)
     if "stats" in groups:
         stats_cases(ref_sm, ref_utils, out)
+    if "harden" in groups:
+        harden_case(ref_sm, ref_utils, out)
     for name, rec in out.items():
         path = os.path.join(OUT, f"ref_{name}.npz")
         np.savez_compressed(path, torch_version=np.array(torch.__version__), **rec)

@@ -194,3 +194,22 @@ def test_mid_penalty_zero_lambda_and_empty(cuda_device):
     empty = torch.nn.Module()
     assert U.mask_stats(empty)["mask_mean"] == 1.0
     assert U.nm_2_4_tile_stats(empty)["top2_avg"] == 0.0
+
+
+def test_harden_fraction_matches_reference(cuda_device):
+    _, _, sm, U = _mods()
+    g = load_golden("harden_f32")
+    model = torch.nn.Module()
+    for li in range(2):
+        m = torch.from_numpy(g[f"mask_in{li}"])
+        cfg = sm.SparseLinearConfig(mask_type="unstructured", hard_mask_type="nm_2_4", freeze_low=0.05,
+                                    freeze_high=0.95)
+        layer = sm.SparseLinear(m.shape[1], m.shape[0], sparselinear_config=cfg, bias=False).to(cuda_device)
+        with torch.no_grad():
+            layer.mask.copy_(m)
+            layer.frozen_mask_flags.copy_(torch.from_numpy(g[f"frozen_in{li}"]))
+        model.add_module(f"l{li}", layer)
+    assert U.harden_fraction(model, 0.2, 0.4, 0.6) == int(g["count"])
+    for li, layer in enumerate(model.children()):
+        assert (layer.mask.detach().cpu().numpy() == g[f"mask_out{li}"]).all()
+        assert (layer.frozen_mask_flags.detach().float().cpu().numpy() == g[f"frozen_out{li}"]).all()
