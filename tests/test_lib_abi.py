@@ -60,3 +60,25 @@ def test_device_tie_table_matches_fixture():
         for key, row in fx[str(k)].items():
             expect[int(key)] = row["keep"]
         assert tables[k - 1] == expect, f"k={k}"
+
+
+def test_product_package_never_uses_the_oracle_or_scratch_files():
+    """The product path (sparseforge_amd/) imports nothing from oracle/ (test infrastructure) and
+    reads nothing under _work/ (the builder's scratch space)."""
+    import ast
+    import pathlib
+
+    pkg = pathlib.Path(__file__).resolve().parents[1] / "sparseforge_amd"
+    for path in pkg.rglob("*.py"):
+        tree = ast.parse(path.read_text())
+        for node in ast.walk(tree):
+            if isinstance(node, ast.Import):
+                names = [a.name for a in node.names]
+            elif isinstance(node, ast.ImportFrom):
+                names = [node.module or ""]
+            else:
+                continue
+            assert not any(n == "oracle" or n.startswith("oracle.") for n in names), f"{path} imports the oracle"
+        assert "_work" not in path.read_text(), f"{path} refers to _work"
+    for path in list(pkg.rglob("*.hip")) + list(pkg.rglob("*.hpp")):
+        assert "_work" not in path.read_text(), f"{path} refers to _work"
