@@ -79,6 +79,6 @@ def test_product_package_never_uses_the_oracle_or_scratch_files():
             else:
                 continue
             assert not any(n == "oracle" or n.startswith("oracle.") for n in names), f"{path} imports the oracle"
-        assert "_work" not in path.read_text(), f"{path} refers to _work"
+        assert "_work/" not in path.read_text(), f"{path} refers to _work/"
     for path in list(pkg.rglob("*.hip")) + list(pkg.rglob("*.hpp")):
-        assert "_work" not in path.read_text(), f"{path} refers to _work"
+        assert "_work/" not in path.read_text(), f"{path} refers to _work/"
