@@ -139,11 +139,36 @@ __host__ __device__ __forceinline__ uint32_t topk2_keep_keys(const uint32_t k[4]
                         k[1] == k[2], k[1] == k[3], k[2] == k[3]);
 }
 
-// Without NaN the float comparisons give torch's order directly (-0 == +0).
-__device__ __forceinline__ uint32_t topk2_keep_f(const float v[4]) {
-  return topk2_keep_rel(v[1] >= v[0], v[2] >= v[0], v[3] >= v[0], v[2] >= v[1], v[3] >= v[1], v[3] >= v[2],
-                        v[1] == v[2], v[1] == v[3], v[2] == v[3]);
+// The same keep set as topk2_keep_rel for NaN-free values (-0 == +0), computed
+// as integer arithmetic so that it runs as a few selects and adds per group
+// rather than as lane-mask logic.  Member j outranks member i (i < j) when
+// v_j >= v_i, otherwise i outranks j; each of the 6 pairs adds one to the
+// rank of the member it does not favour, rank_i held in bits [2i, 2i + 2)
+// (at most 3, so the fields never carry).  A member is kept when its rank is
+// below 2, i.e. bit 2i + 1 is clear.  When member 0 outranks all three others
+// the second kept member is the lowest index among the maxima of members
+// 1..3, or member 2 when all three are equal.  Result: bit 2i + 1 set when
+// member i is kept (the "spread" form, which flip counting uses directly).
+__host__ __device__ __forceinline__ uint32_t topk2_spread_f(const float v[4]) {
+  const bool c01 = v[1] >= v[0], c02 = v[2] >= v[0], c03 = v[3] >= v[0];
+  const bool c12 = v[2] >= v[1], c13 = v[3] >= v[1], c23 = v[3] >= v[2];
+  const uint32_t r = (c01 ? 1u : 4u) + (c02 ? 1u : 16u) + (c03 ? 1u : 64u) + (c12 ? 4u : 16u) +
+                     (c13 ? 4u : 64u) + (c23 ? 16u : 64u);
+  const uint32_t keep = ~r & 0xaau;
+  const bool top0 = !(c01 || c02 || c03);
+  const bool ge1 = v[1] >= v[2] && v[1] >= v[3], ge2 = c12 && v[2] >= v[3];
+  const bool all3 = v[1] == v[2] && v[2] == v[3];
+  const uint32_t second = all3 ? 0x20u : (ge1 ? 0x08u : (ge2 ? 0x20u : 0x80u));
+  return top0 ? (0x02u | second) : keep;
 }
+
+// Spread form (bit 2i + 1) -> plain form (bit i).
+__host__ __device__ __forceinline__ uint32_t unspread4(uint32_t s) {
+  return ((s >> 1) & 1u) | ((s >> 2) & 2u) | ((s >> 3) & 4u) | ((s >> 4) & 8u);
+}
+
+// Without NaN the float comparisons give torch's order directly (-0 == +0).
+__host__ __device__ __forceinline__ uint32_t topk2_keep_f(const float v[4]) { return unspread4(topk2_spread_f(v)); }
 
 __device__ __forceinline__ bool any_nan4(const float v[4]) {
   return __builtin_isunordered(v[0], v[1]) || __builtin_isunordered(v[2], v[3]);

@@ -758,6 +758,9 @@ __device__ __forceinline__ uint32_t hard_bits(const float v[4], const Group& g, 
 
 // Positions of a group where the hard views of a and b differ (:1659-1661).
 __device__ __forceinline__ int flips_of(const float a[4], const float b[4], const Group& g, int kind, int n) {
+  // 2:4 on a full NaN-free group (the common case): compare the spread keep sets directly
+  if (kind >= SF_HARD_NM_TAIL_KEEP && n == 2 && g.full && !any_nan4(a) && !any_nan4(b))
+    return __popc(topk2_spread_f(a) ^ topk2_spread_f(b));
   return __popc((hard_bits(a, g, kind, n) ^ hard_bits(b, g, kind, n)) & ((1u << g.n) - 1u));
 }
 
