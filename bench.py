@@ -34,7 +34,10 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
   timed with HIP events on the launch stream inside the timed region.  ``peak`` is the published dense bf16 figure; ``mfma_sustained`` is what
   an MFMA-only loop (sf_mfma_probe, operands distributed like the GEMM's, no
   memory traffic)
-  sustains on the same GPU, the practical ceiling under that figure.
+  sustains on the same GPU, the practical ceiling under that figure.  The
+  HBM legs' roofline objects carry ``copy_sustained``, the rate of a plain
+  1 GiB device-to-device copy on the same GPU (read + written bytes), and
+  their fraction of it.
 * ``cpu_baseline`` -- the numpy oracle (oracle/linear.py, a CPU restatement of
   the reference's FusedMaskedLinearSTE + SLoRB path) on the host cores, on a
   bounded token sample of the same seven shapes (rank 0, N = 1 only).
@@ -356,6 +359,26 @@ def mfma_sustained(torch, dev, iters: int = 4000, blocks: int = 1024, reps: int 
     return best
 
 
+def copy_sustained(torch, dev, mib: int = 1024, reps: int = 5) -> float:
+    """GB/s (read + written bytes) of a plain 1 GiB device-to-device copy (torch copy_, the runtime's copy
+    kernel): the streaming rate this GPU's HBM sustains in practice, best of `reps` after a warm-up."""
+    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    st = torch.cuda.current_stream(dev)
+    best = 0.0
+    for r in range(reps + 2):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        dst.copy_(src)
+        e1.record(st)
+        e1.synchronize()
+        if r >= 2:
+            best = max(best, 2.0 * src.numel() * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    del src, dst
+    log(f"device copy: {best:.0f} GB/s sustained (1 GiB f32, read + write)")
+    return best
+
+
 def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
     import numpy as np
 
@@ -597,6 +620,7 @@ def main(argv=None) -> int:
     kl = kl_leg(torch, dev, a.kl_steps) if a.kl_steps > 0 else None
     s24 = sparse24_leg(torch, dev, a.tokens, a.s24_steps) if a.s24_steps > 0 else None
     sustained = mfma_sustained(torch, dev)
+    copy_gbs = copy_sustained(torch, dev)
     torch.cuda.empty_cache()
 
     traffic = profiled_traffic()
@@ -630,7 +654,8 @@ def main(argv=None) -> int:
             "roofline": {"bound": "hbm", "kernel": "sf_update_mask", "achieved": round(up_gbs, 2),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(up_gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic.get("sf_update_mask_bytes_per_launch"), "traffic_unit": "B/launch",
-                         "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4)},
+                         "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4),
+                         "copy_sustained": round(copy_gbs, 1), "frac_of_copy": round(up_gbs / copy_gbs, 4)},
             "score_stats_gbs": round(st_gbs, 2),
             "mask_stats": {"kernel": "sf_mask_stats", "GB/s": round(mstats_gbs, 2), "bytes_per_param": 4,
                            "frac": round(mstats_gbs / PEAK_HBM_GBS, 4), "launches": msk.launches,
@@ -645,7 +670,8 @@ def main(argv=None) -> int:
         "roofline": {"bound": "hbm", "kernel": "sf_adamw_step", "achieved": round(as_.rate / 1e9, 2),
                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(as_.rate / 1e9 / PEAK_HBM_GBS, 4),
                      "traffic": traffic.get("sf_adamw_step_bytes_per_launch"), "traffic_unit": "B/launch",
-                     "avg_launch_ms": round(as_.avg_ms, 4)},
+                     "avg_launch_ms": round(as_.avg_ms, 4), "copy_sustained": round(copy_gbs, 1),
+                     "frac_of_copy": round(as_.rate / 1e9 / copy_gbs, 4)},
     }
     if bsr:
         out["block_sparse"] = bsr
