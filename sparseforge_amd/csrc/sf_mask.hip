@@ -370,10 +370,37 @@ __global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, cons
 
 __global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __restrict__ partial, int nparts,
                                                              int64_t n, float* stats) {
+  // 8 partials per thread and round, their loads issued together: the partials
+  // were just written by workgroups on every XCD, so each round costs a memory
+  // latency, and a one-at-a-time loop paid it 16 times
+  constexpr int kU = 8;
+  double s8[kU], q8[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) s8[u] = q8[u] = 0.0;
+  const int stride = blockDim.x;
+  int i = threadIdx.x;
+  for (; i + (kU - 1) * stride < nparts; i += kU * stride) {
+    double a[kU], b[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      a[u] = partial[2 * (i + u * stride)];
+      b[u] = partial[2 * (i + u * stride) + 1];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      s8[u] += a[u];
+      q8[u] += b[u];
+    }
+  }
+  for (; i < nparts; i += stride) {
+    s8[0] += partial[2 * i];
+    q8[0] += partial[2 * i + 1];
+  }
   double sum = 0.0, sq = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
-    sum += partial[2 * i];
-    sq += partial[2 * i + 1];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    sum += s8[u];
+    sq += q8[u];
   }
   __shared__ double tot[2];
   block_sum2_f64(sum, sq, &tot[0], &tot[1]);
@@ -526,13 +553,25 @@ __global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __rest
   const uint32_t pmask = pass == 0 ? 0u : ~0u << (shift + 8);
   const uint32_t p0 = pass == 0 ? 0u : st.prefix[0], p1 = pass == 0 ? 0u : st.prefix[1];
   int local_nan = 0;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + t; i < m; i += (int64_t)gridDim.x * blockDim.x) {
-    const uint32_t k = keys[i];
+  auto count = [&](uint32_t k) {
     const uint32_t d = (k >> shift) & 0xffu;
     local_nan |= k == 0xffffffffu;
     if ((k & pmask) == p0) atomicAdd(&hist[wv][0][d], 1u);
     if (pass > 0 && (k & pmask) == p1) atomicAdd(&hist[wv][1][d], 1u);
+  };
+  // 8 keys per thread and round, loaded before any is counted (one memory
+  // latency per round rather than per key)
+  constexpr int kU = 8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = blockIdx.x * (int64_t)blockDim.x + t;
+  for (; i + (kU - 1) * stride < m; i += kU * stride) {
+    uint32_t k8[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) k8[u] = keys[i + u * stride];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) count(k8[u]);
   }
+  for (; i < m; i += stride) count(keys[i]);
   if (local_nan) atomicOr(&nan, 1);
   __syncthreads();
   uint32_t* out = partial_out + (int64_t)blockIdx.x * kSelStride;
