@@ -238,15 +238,18 @@ def test_tau_quantile_matches_torch(cuda_device):
         assert t2.item() == torch.quantile(scores, q).item()
 
 
-@pytest.mark.parametrize("case", ["gauss", "ties", "nan", "tiny"])
+@pytest.mark.parametrize("case", ["gauss", "ties", "nan", "tiny", "ragged"])
 def test_tau_quantile_radix_select_large(cuda_device, case):
-    """The multi-workgroup radix select equals torch.quantile over 262144 keys (ties, NaN, tiny inputs)."""
+    """The multi-workgroup radix select equals torch.quantile over 262144 keys (ties, NaN, tiny inputs) and
+    over 275561 keys (ragged: the passes' 8-keys-per-round loop plus its remainder loop)."""
     sm = _sm()
     cfg = sm.SparseLinearConfig(mask_type="unstructured", tau_sample_size=10 ** 7)
     layer = sm.SparseLinear(64, 32, sparselinear_config=cfg, bias=False).to(cuda_device)
     g = torch.Generator().manual_seed(17)
     if case == "tiny":
         scores = torch.randn(1, 3, generator=g)
+    elif case == "ragged":
+        scores = torch.randn(517, 533, generator=g)
     else:
         scores = torch.randn(512, 512, generator=g)
     if case == "ties":
