@@ -278,6 +278,7 @@ def kl_leg(torch, dev, steps: int, warmup: int = 2) -> dict:
            "ms_per_step": round(el * 1e3 / steps, 4), "bytes_per_element": 10,
            "roofline": {"bound": "hbm", "kernel": "sf_kl_forward", "achieved": round(f.rate / 1e9, 2),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(f.rate / 1e9 / PEAK_HBM_GBS, 4),
+                        "traffic": profiled_traffic().get("sf_kl_forward_bytes_per_launch"), "traffic_unit": "B/launch",
                         "avg_launch_ms": round(f.avg_ms, 4)},
            "backward": {"kernel": "sf_kl_backward", "achieved": round(b.rate / 1e9, 2), "unit": "GB/s",
                         "avg_launch_ms": round(b.avg_ms, 4)}}
