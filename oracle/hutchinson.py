@@ -49,7 +49,13 @@ def update(H: np.ndarray, hvp: np.ndarray, v: np.ndarray, beta: float) -> np.nda
     return (est.astype(np.float64) * np.float32(1 - beta) + h.astype(np.float64)).astype(np.float32)
 
 
-def quadratic_hvp(x: np.ndarray, v: np.ndarray) -> np.ndarray:
-    """HVP of 1/2 ||x (W.M)^T - y||^2 w.r.t. W along v under the STE backward: v (x^T x) (the mask drops out)."""
+def quadratic_hvp(x: np.ndarray, v: np.ndarray, E: np.ndarray | None = None, decay: float = 0.0) -> np.ndarray:
+    """HVP of 1/2 ||x (W.M)^T - y||^2 w.r.t. W along v under the STE backward: v (x^T x) (the mask drops out).
+
+    With the SR-STE term (decay != 0, legacy/sparse_modeling.py:123-125) the weight gradient also
+    holds decay * W * [E < 0.5], whose derivative along v adds decay * v * [E < 0.5]."""
     xtx = np.asarray(x, np.float64).T @ np.asarray(x, np.float64)
-    return np.asarray(v, np.float64) @ xtx
+    hvp = np.asarray(v, np.float64) @ xtx
+    if decay != 0.0:
+        hvp = hvp + decay * np.asarray(v, np.float64) * (np.asarray(E, np.float64) < 0.5)
+    return hvp

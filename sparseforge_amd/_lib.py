@@ -69,6 +69,7 @@ EFF_HARD = 2
 LAYOUT_K = 0
 LAYOUT_MN = 1
 
+
 BFMT_DENSE = 0
 BFMT_BSR16 = 1
 
@@ -291,6 +292,25 @@ def require_device(*tensors: torch.Tensor | None) -> torch.device:
             )
         if not t.is_contiguous():
             raise ValueError("sparseforge_amd: tensors must be contiguous")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"sparseforge_amd: tensors on different devices ({dev} vs {t.device})")
+    if dev is None:
+        raise ValueError("sparseforge_amd: no tensor given")
+    return dev
+
+
+def require_device_only(*tensors: torch.Tensor | None) -> torch.device:
+    """All given tensors must be ROCm tensors on one device (any strides)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"sparseforge_amd runs on the GPU only; got a tensor on {t.device} (no CPU path exists)"
+            )
         if dev is None:
             dev = t.device
         elif t.device != dev:

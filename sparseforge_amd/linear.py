@@ -192,6 +192,25 @@ def transpose_u8(E: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def decay_term(G: torch.Tensor, E: torch.Tensor | None, decay: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out (+)= decay * G * [E < 0.5] in G's dtype (E = None: nothing is pruned and the term is 0).
+
+    The derivative along G of the SR-STE term decay * W * [E < 0.5] of the weight
+    gradient (legacy/sparse_modeling.py:123-125), which is elementwise in W.  Off
+    the paper's path (its decay is 0), so it is two device elementwise ops.
+    """
+    L.require_device(G, E, out)
+    if out is None:
+        out = torch.zeros_like(G)
+    if E is None:
+        return out
+    if E.shape != G.shape or out.shape != G.shape:
+        raise ValueError("decay_term: G, E and out must have one shape")
+    pruned = (E == 0) if E.dtype == torch.uint8 else (E < 0.5)
+    out.add_(G * pruned.to(G.dtype), alpha=float(decay))
+    return out
+
+
 def _as_values(E: torch.Tensor | None, dt: torch.dtype) -> torch.Tensor | None:
     """A byte and-mask as 0/1 values of dtype dt (for epilogue products); other masks unchanged."""
     if E is not None and E.dtype == torch.uint8:
@@ -253,8 +272,6 @@ class _MaskedLinearBackward(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g_dx, g_dW, g_db, g_dP, g_dS):
         gy, x, W, P, S, E, z, dz = ctx.saved_tensors
-        if ctx.decay != 0.0 and g_dW is not None:
-            raise NotImplementedError("double backward of the SR-STE decay term")
         T, out = gy.shape
         dt = gy.dtype
         g_dx, g_dW, g_db, g_dP, g_dS = (_opt(t) for t in (g_dx, g_dW, g_db, g_dP, g_dS))
@@ -305,8 +322,11 @@ class _MaskedLinearBackward(torch.autograd.Function):
                 mm_nn(dz, g_dP, out=gx, accumulate=True)
         else:
             w = None
-        # d/dW = (gy^T gdx) . E
+        # d/dW = (gy^T gdx) . E  (+ decay gdW [E < 0.5]: the SR-STE term decay W [E < 0.5] of dW is
+        # elementwise in W, legacy/sparse_modeling.py:123-125)
         gW = mm_tn(gy, g_dx, emask=_as_values(E, W.dtype)) if g_dx is not None else None
+        if ctx.decay != 0.0 and g_dW is not None:
+            gW = decay_term(g_dW, E, ctx.decay, out=gW)
         # d/dP = dz^T gdx + (gy gdS)^T x ;  d/dS = gy^T (gdx P^T + x gdP^T)
         gP = gS = None
         if ctx.has_slorb:
@@ -332,21 +352,22 @@ class _MaskedLinear(torch.autograd.Function):
             y = mm_nt(x2, Wm, bscale=s, A2=z, B2=S, K2=P.shape[0], bias=bias)
         else:
             y = mm_nt(x2, Wm, bscale=s, bias=bias)
-        # Without a weight-scaling factor the input gradient needs the same W.E: it stays in HBM until
-        # the backward (2 B/param of bf16 weight) instead of being rebuilt there by another pass.
-        ctx.wm = Wm if (E is not None and scale == 1.0) else None
+        # Without a weight-scaling factor the input gradient needs the same W.E: it is saved for the
+        # backward (2 B/param of bf16 weight) instead of being rebuilt there by another pass.  It goes
+        # through save_for_backward, so the version counters of W and E guard it like the rest.
+        keep = E is not None and scale == 1.0
+        ctx.save_for_backward(x2, W, P, S, E, z, Wm if keep else None)
         del Wm
-        ctx.save_for_backward(x2, W, P, S, E, z)
         ctx.decay = decay
         ctx.has_bias = bias is not None
         return y
 
     @staticmethod
     def backward(ctx, gy):
-        x2, W, P, S, E, z = ctx.saved_tensors
+        x2, W, P, S, E, z, wm = ctx.saved_tensors
         gy = gy.contiguous().to(W.dtype)
-        wm, ctx.wm = ctx.wm, None
         dx, dW, db, dP, dS = _MaskedLinearBackward.apply(gy, x2, W, P, S, E, ctx.decay, ctx.has_bias, z, wm)
+        del wm
         return dx, dW, db, dP, dS, None, None, None
 
 
@@ -357,14 +378,16 @@ def _compute_dtype(x: torch.Tensor, W: torch.Tensor) -> torch.dtype:
 
 
 def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale, P=None, S=None, decay=0.0,
-                  eff=None, hard=None):
+                  eff=None, hard=None, hard_m=4):
     """y = x (W.E.s)^T + (x P^T) S^T + b with STE gradients.
 
     mask_mode: 'none' (E = 1), 'soft' (E = mask) or 'mix' (E = hx*mask + (1-hx)*hard(mask)).
     eff: a precomputed E in the compute dtype (skips the mask pass).
-    hard: a precomputed hard(mask) (block hard types); else hard_kind / hard_n project per group.
+    hard: a precomputed hard(mask) (block hard types); else hard_kind / hard_n / hard_m project
+    per group of hard_m along the input dimension.
+    Strided inputs are accepted (made contiguous before the kernels, as F.linear accepts them).
     """
-    L.require_device(x, weight, bias, mask, P, S)
+    L.require_device_only(x, weight, bias, mask, P, S, eff, hard)
     dt = _compute_dtype(x, weight)
     if dt not in (torch.float32, torch.bfloat16):
         raise TypeError(f"sparseforge_amd: unsupported compute dtype {dt}")
@@ -373,23 +396,27 @@ def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale
     if x2.dtype != dt:
         x2 = x2.to(dt)
     x2 = x2.contiguous()
-    W = weight if weight.dtype == dt else weight.to(dt)
-    b = None if bias is None else (bias if bias.dtype == dt else bias.to(dt))
+    W = (weight if weight.dtype == dt else weight.to(dt)).contiguous()
+    b = None if bias is None else (bias if bias.dtype == dt else bias.to(dt)).contiguous()
+    mask = _opt(mask)
+    hard = _opt(hard)
     if eff is None and mask_mode != "none":
         if mask_mode == "mix" and hx <= 0.0 and scale == 1.0:
             # E = hard(mask) exactly: staged as a byte and-mask (W * 1 = W, W * 0 = 0)
             eff = (effective_mask_given(mask, hard, torch.uint8, "hard", 0.0) if hard is not None
-                   else effective_mask(mask, torch.uint8, "hard", 0.0, hard_kind, hard_n))
+                   else effective_mask(mask, torch.uint8, "hard", 0.0, hard_kind, hard_n, hard_m))
         elif hard is not None and mask_mode == "mix":
             eff = effective_mask_given(mask, hard, dt, mask_mode, hx)
         else:
-            eff = effective_mask(mask, dt, mask_mode, hx, hard_kind, hard_n)
+            eff = effective_mask(mask, dt, mask_mode, hx, hard_kind, hard_n, hard_m)
     if mask_mode == "none":
         eff = None
+    eff = _opt(eff)
     Pp = Sp = None
     r = 0
     if P is not None:
         Pp, Sp, r = (P, S, P.shape[0]) if P.dtype == dt else (P.to(dt), S.to(dt), P.shape[0])
+        Pp, Sp = Pp.contiguous(), Sp.contiguous()
         if Pp.shape[0] % _vec(dt):
             Pp, Sp, r = _PadRank.apply(Pp, Sp)
     y = _MaskedLinear.apply(x2, W, b, Pp, Sp, eff, float(scale), float(decay))

@@ -11,6 +11,7 @@ never travels with them.  Functions covered (reference file:line):
   adamw_*     AdamW.step(decay=...)                legacy/adamw.py:65-176
   hutch_*     update_hessian_hutchinson            legacy/utils.py:714-869
   linear_*    FusedMaskedLinearSTE + SLoRB fwd/bwd legacy/sparse_modeling.py:56-132, :737-796
+  ste_*       FusedMaskedLinearSTE.apply, decay    legacy/sparse_modeling.py:56-132
   kl_*        Distill_Model.kl_loss                legacy/sparse_modeling.py:1749-1828
   bsr_*       convert_to_block_sparse              legacy/triton_block_sparse.py:46-103
   hardblk_*   _hard_mask_from_soft, block types    legacy/sparse_modeling.py:537-718
@@ -30,7 +31,7 @@ mask_stats samples torch.randint indices per layer; the draws are replayed
 after the same torch.manual_seed and stored with the fixture.
 
 Run:  python tests/golden/make_reference_golden.py [group ...]   (needs /root/reference;
-      groups: gate update glu adamw hutch linear kl bsr block stats harden, default all)
+      groups: gate update glu adamw hutch linear ste kl bsr block stats harden, default all)
 """
 from __future__ import annotations
 
@@ -282,6 +283,36 @@ def linear_case(ref_sm, out):
     out["linear_slorb_f32"] = rec
 
 
+def ste_cases(ref_sm, out):
+    """FusedMaskedLinearSTE.apply(x, W, b, mask, decay, scale) with decay != 0 and scale != 1
+    (:56-132): forward, backward (dW carries decay * W * [mask < 0.5]) and the Hessian-vector
+    product of a quadratic loss by double backward (the decay term is differentiated too)."""
+    for dt, tag in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        torch.manual_seed(720)
+        x = torch.randn(2, 40, 64).to(dt)
+        W = (torch.randn(48, 64) * 0.02).to(dt)
+        b = (torch.randn(48) * 0.1).to(dt)
+        mask = torch.rand(48, 64)
+        mask[:, ::7] = 0.5  # entries exactly at the decay threshold (kept: the test is mask < 0.5)
+        gy = torch.randn(2, 40, 48).to(dt)
+        t = torch.randn(2, 40, 48).to(dt)
+        v = (torch.randint(0, 2, (48, 64)) * 2 - 1).to(dt)
+        decay, scale = 0.05, 1.7
+        xr, Wr, br = x.clone().requires_grad_(True), W.clone().requires_grad_(True), b.clone().requires_grad_(True)
+        y = ref_sm.FusedMaskedLinearSTE.apply(xr, Wr, br, mask, decay, scale)
+        y.backward(gy)
+        rec = dict(x=np32(x), W=np32(W), b=np32(b), mask=np32(mask), gy=np32(gy), t=np32(t), v=np32(v),
+                   decay=np.float64(decay), scale=np.float64(scale), y=np32(y), dx=np32(xr.grad),
+                   dW=np32(Wr.grad), db=np32(br.grad))
+        Wh = W.clone().requires_grad_(True)
+        yh = ref_sm.FusedMaskedLinearSTE.apply(x, Wh, b, mask, decay, scale)
+        loss = 0.5 * ((yh.float() - t.float()) ** 2).sum()
+        (g,) = torch.autograd.grad(loss, Wh, create_graph=True)
+        (hvp,) = torch.autograd.grad((g * v).sum(), Wh)
+        rec["hvp"] = np32(hvp)
+        out[f"ste_decay_{tag}"] = rec
+
+
 def kl_case(ref_sm, out):
     torch.manual_seed(800)
     s = torch.randn(2, 37, 300) * 4
@@ -491,7 +522,7 @@ def harden_case(ref_sm, ref_utils, out):
     out["harden_f32"] = rec
 
 
-GROUPS = ("gate", "update", "glu", "adamw", "hutch", "linear", "kl", "bsr", "block", "stats", "harden")
+GROUPS = ("gate", "update", "glu", "adamw", "hutch", "linear", "ste", "kl", "bsr", "block", "stats", "harden")
 
 
 def main():
@@ -516,6 +547,8 @@ def main():
         linear_case(ref_sm, out)
     if "kl" in groups:
         kl_case(ref_sm, out)
+    if "ste" in groups:
+        ste_cases(ref_sm, out)
     if "bsr" in groups:
         bsr_case(out)
     if "block" in groups:

@@ -68,3 +68,36 @@ def test_oracle_matches_autograd_of_dense_equivalent():
 def test_weight_scale_and_flops():
     assert ol.weight_scale(0.0, 2.0) == 2.0 and ol.weight_scale(1.0, 2.0) == 1.0
     assert ol.flops_fwd_bwd(8192, 4096, 4096) == 6 * 8192 * 4096 * 4096
+
+
+def test_oracle_matches_reference_ste_decay_golden():
+    """FusedMaskedLinearSTE.apply with decay != 0 and scale != 1 (the reference's own outputs): the
+    forward carries the scale, dx does not, dW carries decay * W * [mask < 0.5] (mask exactly 0.5
+    is kept), and the Hessian-vector product by double backward adds decay * v * [mask < 0.5]."""
+    from oracle import hutchinson as oh
+
+    r = load_golden("ste_decay_f32")
+    W, b, M = r["W"], r["b"], r["mask"]
+    x = r["x"].reshape(-1, W.shape[1])
+    gy = r["gy"].reshape(-1, W.shape[0])
+    decay, scale = float(r["decay"]), float(r["scale"])
+    y = ol.forward(x, W, M, b, scale)
+    assert rel(y, r["y"].reshape(y.shape)) < 1e-5
+    g = ol.backward(x, W, M, gy, True, decay=decay)
+    assert rel(g["dx"], r["dx"].reshape(g["dx"].shape)) < 1e-5
+    assert rel(g["dW"], r["dW"]) < 1e-5
+    assert rel(g["db"], r["db"]) < 1e-5
+    # the decay term itself (about 1e-4 of dW's scale, so a relative bar on dW cannot see it): the
+    # reference's dW minus the straight-through product is decay * W * [mask < 0.5], zero at mask == 0.5
+    x64, gy64 = x.astype(np.float64), gy.astype(np.float64)
+    term = decay * W.astype(np.float64) * (M < 0.5)
+    resid = r["dW"].astype(np.float64) - gy64.T @ x64
+    tol = 1e-6 * np.abs(r["dW"]).max()
+    assert np.abs(resid - term).max() < tol
+    assert np.abs(term).max() > 100 * tol and np.all(term[M == 0.5] == 0) and np.any(M == 0.5)
+    # the reference's HVP is two chained f32 products (x^T x then along v): f32 rounding of both
+    hvp = oh.quadratic_hvp(x, r["v"], M, decay)
+    assert rel(hvp, r["hvp"]) < 3e-5
+    h_resid = r["hvp"].astype(np.float64) - oh.quadratic_hvp(x, r["v"])
+    h_tol = 2e-5 * np.abs(r["hvp"]).max()  # f32 rounding of the reference's HVP (~350) over 80 + 64 terms
+    assert np.abs(h_resid - decay * r["v"] * (M < 0.5)).max() < h_tol < decay / 5
