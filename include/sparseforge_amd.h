@@ -139,6 +139,24 @@ int sf_tau_quantile(const sf_mask_params* p, const void* W, int w_dtype, const v
                     size_t workspace_bytes, void* stream);
 
 /*
+ * sf_tau_quantile without a workspace argument: allocates nothing (no
+ * hipMalloc, no allocating library call), for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation).  No counterpart in the reference.  The scratch
+ * lives in a static device array of the library (about 4.2 MiB per GPU, held
+ * until the process ends), one copy per GPU; the device is the stream's
+ * (NULL stream: the current device).  Samples above SF_TAU_NOALLOC_MAX_SAMPLE
+ * elements are rejected with SF_ERR_INVALID.  Every call on one GPU shares
+ * that scratch: calls that overlap on one GPU (different streams without
+ * ordering between them) race and must not be issued.  Results equal
+ * sf_tau_quantile's for the same inputs.
+ */
+#define SF_TAU_NOALLOC_MAX_SAMPLE (1 << 20)
+int sf_tau_quantile_noalloc(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                            const void* aux, int aux_dtype, const float* stats, const int64_t* sample_idx,
+                            int64_t sample_size, float q, float* tau_out, void* stream);
+
+/*
  * Sample indices for the tau quantile: idx[i] uniform in [0, n) from the
  * counter-based generator (seed, i).  Replaces torch.randint at :993.
  */

@@ -69,6 +69,7 @@ EFF_HARD = 2
 LAYOUT_K = 0
 LAYOUT_MN = 1
 
+TAU_NOALLOC_MAX_SAMPLE = 1 << 20  # SF_TAU_NOALLOC_MAX_SAMPLE
 
 BFMT_DENSE = 0
 BFMT_BSR16 = 1
@@ -184,6 +185,7 @@ SIGNATURES = {
     "sf_mask_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "sf_score_stats": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _P, _SZ, _P]),
     "sf_tau_quantile": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _P, _I64, _F, _P, _P, _SZ, _P]),
+    "sf_tau_quantile_noalloc": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _P, _I64, _F, _P, _P]),
     "sf_sample_indices": (_I, [_P, _I64, _I64, ctypes.c_uint64, _P]),
     "sf_gate_target": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P]),
     "sf_update_mask": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _P]),

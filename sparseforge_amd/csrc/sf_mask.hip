@@ -16,6 +16,8 @@
 #include <initializer_list>
 #include <utility>
 
+#include <mutex>
+
 #include "sf_common.hpp"
 #include "sf_rng.hpp"
 
@@ -1063,25 +1065,31 @@ extern "C" int sf_sample_indices(int64_t* idx, int64_t sample_size, int64_t n, u
   return launch_status("sf_sample_indices");
 }
 
-extern "C" int sf_tau_quantile(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
-                               const void* aux, int aux_dtype, const float* stats, const int64_t* sample_idx,
-                               int64_t sample_size, float q, float* tau_out, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+namespace sf {
+namespace {
+// Argument checks and launches of the tau selection, over a scratch region `ws`
+// laid out as sf_mask_workspace_size describes (the caller's workspace, or the
+// library's static scratch for sf_tau_quantile_noalloc).  Every scratch word a
+// kernel reads was written earlier in the same call: nothing needs clearing.
+int tau_quantile_checks(const sf_mask_params* p, const void* W, const void* H, const void* aux, const float* stats,
+                        const int64_t* sample_idx, int64_t sample_size, float* tau_out) {
   if (int rc = check_common(p)) return rc;
   if (int rc = check_metric_operands(p, H, aux)) return rc;
   SF_CHECK_ARG(W && stats && tau_out, "null tensor");
   SF_CHECK_ARG(sample_size > 0, "empty tau sample");
   SF_CHECK_ARG(sample_idx || sample_size == p->rows * p->cols, "sample_size must equal numel without indices");
-  SF_CHECK_ARG(workspace && workspace_bytes >= sf_mask_workspace_size(p->rows, p->cols, sample_size),
-               "workspace too small");
+  return SF_OK;
+}
+
+int tau_quantile_launch(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                        const void* aux, int aux_dtype, const float* stats, const int64_t* sample_idx,
+                        int64_t sample_size, float q, float* tau_out, char* ws, hipStream_t st) {
   if (!H) h_dtype = SF_DTYPE_F32;
   ScoreSpec s = make_spec(p, w_dtype, h_dtype, aux_dtype);
-  char* ws = static_cast<char*>(workspace);
   uint32_t* keys = reinterpret_cast<uint32_t*>(ws + ws_keys_off());
   SelState* states = reinterpret_cast<SelState*>(ws + ws_state_off());
   uint32_t* parts[2] = {reinterpret_cast<uint32_t*>(ws + ws_partial_off()),
                         reinterpret_cast<uint32_t*>(ws + ws_partial_off() + ws_partial_bytes())};
-  hipStream_t st = static_cast<hipStream_t>(stream);
   tau_gather_kernel<<<elementwise_grid(sample_size, kBlock), kBlock, 0, st>>>(s, W, H, aux, p->rows, p->cols, stats,
                                                                                sample_idx, sample_size, keys);
   // pass p reads state p-2 (slot p & 1) and partials p-1, writes state p-1 (slot (p + 1) & 1) and partials p
@@ -1090,7 +1098,83 @@ extern "C" int sf_tau_quantile(const sf_mask_params* p, const void* W, int w_dty
     tau_pass_kernel<<<grid, kBlock, 0, st>>>(keys, sample_size, pass, q, &states[pass & 1], &states[(pass + 1) & 1],
                                              parts[(pass + 1) & 1], parts[pass & 1]);
   tau_final_kernel<<<1, kBlock, 0, st>>>(sample_size, q, grid, &states[0], parts[1], tau_out);
+  return SF_OK;
+}
+
+// ---- static scratch of sf_tau_quantile_noalloc -------------------------------
+// One copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel: it is a host-side stand-in, and the device address
+// of each GPU's copy comes from hipGetSymbolAddress with that GPU current.
+// Same layout as a caller's workspace (sf_mask_workspace_size) at the largest sample it accepts.
+constexpr size_t up256(size_t b) { return (b + 255) / 256 * 256; }
+constexpr size_t kNoallocScratchBytes = up256(sizeof(double) * 2 * kStatsGrid) + up256(2 * sizeof(SelState)) +
+                                        2 * up256(sizeof(uint32_t) * kSelStride * kSelGrid) +
+                                        sizeof(uint32_t) * static_cast<size_t>(SF_TAU_NOALLOC_MAX_SAMPLE);
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device` (resolved once per device, with that device current).
+int scratch_on(int device, char** out) {
+  SF_CHECK_ARG(device >= 0 && device < kMaxDevices, "device ordinal %d out of range", device);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (!g_scratch_ptr[device]) {
+    int prev = -1;
+    SF_CHECK_HIP(hipGetDevice(&prev));
+    if (prev != device) SF_CHECK_HIP(hipSetDevice(device));
+    void* addr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (prev != device) SF_CHECK_HIP(hipSetDevice(prev));
+    if (e != hipSuccess || !addr) {
+      set_error("hipGetSymbolAddress(scratch) on device %d failed: %s", device, hipGetErrorString(e));
+      return SF_ERR_HIP;
+    }
+    g_scratch_ptr[device] = static_cast<char*>(addr);
+  }
+  *out = g_scratch_ptr[device];
+  return SF_OK;
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" int sf_tau_quantile(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                               const void* aux, int aux_dtype, const float* stats, const int64_t* sample_idx,
+                               int64_t sample_size, float q, float* tau_out, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (int rc = tau_quantile_checks(p, W, H, aux, stats, sample_idx, sample_size, tau_out)) return rc;
+  SF_CHECK_ARG(workspace && workspace_bytes >= sf_mask_workspace_size(p->rows, p->cols, sample_size),
+               "workspace too small");
+  tau_quantile_launch(p, W, w_dtype, H, h_dtype, aux, aux_dtype, stats, sample_idx, sample_size, q, tau_out,
+                      static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
   return launch_status("sf_tau_quantile");
+}
+
+extern "C" int sf_tau_quantile_noalloc(const sf_mask_params* p, const void* W, int w_dtype, const void* H,
+                                       int h_dtype, const void* aux, int aux_dtype, const float* stats,
+                                       const int64_t* sample_idx, int64_t sample_size, float q, float* tau_out,
+                                       void* stream) {
+  if (int rc = tau_quantile_checks(p, W, H, aux, stats, sample_idx, sample_size, tau_out)) return rc;
+  SF_CHECK_ARG(sample_size <= SF_TAU_NOALLOC_MAX_SAMPLE,
+               "sf_tau_quantile_noalloc: tau sample of %lld elements exceeds the static scratch maximum of %d "
+               "(use sf_tau_quantile with a workspace)",
+               (long long)sample_size, SF_TAU_NOALLOC_MAX_SAMPLE);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int device = -1;
+  if (st) {
+    SF_CHECK_HIP(hipStreamGetDevice(st, &device));
+  } else {
+    SF_CHECK_HIP(hipGetDevice(&device));
+  }
+  char* ws = nullptr;
+  if (int rc = scratch_on(device, &ws)) return rc;
+  if (sf_mask_workspace_size(p->rows, p->cols, sample_size) > kNoallocScratchBytes) {
+    set_error("sf_tau_quantile_noalloc: scratch layout exceeds the static array");
+    return SF_ERR_INVALID;
+  }
+  tau_quantile_launch(p, W, w_dtype, H, h_dtype, aux, aux_dtype, stats, sample_idx, sample_size, q, tau_out, ws, st);
+  return launch_status("sf_tau_quantile_noalloc");
 }
 
 namespace sf {

@@ -137,6 +137,32 @@ def tau_quantile(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, q: flo
     return tau
 
 
+def tau_quantile_noalloc(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, q: float,
+                         sample_idx: torch.Tensor | None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """tau_quantile through sf_tau_quantile_noalloc: the library's static scratch, no workspace.
+
+    `out` (device float[1]) lets a caller that cannot allocate pass the output
+    too.  Calls that overlap on one GPU race on the shared scratch."""
+    dev = ops.device()
+    if sample_idx is not None:
+        L.require_device(sample_idx)
+        if sample_idx.dim() != 1 or sample_idx.dtype != torch.int64:
+            raise TypeError("sample indices must be a 1-D int64 tensor")
+        m = sample_idx.numel()
+    else:
+        m = p.rows * p.cols
+    if m > L.TAU_NOALLOC_MAX_SAMPLE:
+        raise ValueError(f"tau sample of {m} elements exceeds the static scratch maximum {L.TAU_NOALLOC_MAX_SAMPLE}")
+    tau = out if out is not None else torch.empty(1, dtype=torch.float32, device=dev)
+    L.check(
+        L.lib().sf_tau_quantile_noalloc(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight), L.ptr(ops.hessian),
+                                        ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux), L.ptr(stats),
+                                        L.ptr(sample_idx), m, float(q), L.ptr(tau), L.stream(dev)),
+        "sf_tau_quantile_noalloc",
+    )
+    return tau
+
+
 def gate_target(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: torch.Tensor | None,
                 g_dtype: torch.dtype) -> torch.Tensor:
     dev = ops.device()
