@@ -339,6 +339,97 @@ def sparse24_leg(torch, dev, tokens: int, steps: int, warmup: int = 2) -> dict:
     return out
 
 
+E2E_BATCH, E2E_SEQ, E2E_START = 8, 2048, 5000
+
+
+def e2e_leg(torch, dev, steps: int, warmup: int, micro: int, layers: int = 22) -> dict:
+    """cfg5: sparse retraining steps of a random-init LLaMA-architecture ~1.1B student (22 layers, hidden 2048,
+    FFN 5632, 32 heads, vocab 32000, bf16; every decoder projection a SparseLinear, unstructured soft mask with
+    the hard 2:4 projection, SLoRB rank 64, hessian_ratio + Hutchinson) distilled from a dense random-init
+    teacher of the same shape, batch 8 x seq 2048 as 8 / micro micro-batches, in the paper's schedule
+    (mask update every 10 steps after step 2000, hardening from 2000 over 15000 steps) starting at step 5000:
+    the timed window holds one mask update per 10 steps.  Each step: forward (student + teacher + CE + KL +
+    penalties), one Hutchinson probe on the last micro-batch, backward, clipping, AdamW(decay), mask update."""
+    from sparseforge_amd import sparse_modeling as sm
+    from sparseforge_amd.adamw import AdamW
+    from sparseforge_amd.llama import LlamaDecoder, LlamaShape
+    from sparseforge_amd.retrain import PHASES, RetrainConfig, RetrainStep, optimizer_groups
+    from sparseforge_amd.schedules import hardening_coefficient
+
+    if E2E_BATCH % micro:
+        raise ValueError("--e2e-micro must divide the batch of 8")
+    shape = LlamaShape(num_hidden_layers=layers)
+    cfg = sm.SparseLinearConfig(mask_type="unstructured", hard_mask_type="nm_2_4", mask_metric="hessian_ratio",
+                                sparsity_ratio=0.5, beta=0.98, mask_update_period_before=30,
+                                mask_update_period_after=10, mask_update_switch_step=2000, mask_lr=0.1,
+                                temp_init=1.0, temp_decay=0.97, temp_min=0.05, sparsity_warmup_steps=500,
+                                tau_sample_size=262144, mask_penalty_lr=0.1, mask_penalty_mode="nm_2_4",
+                                mask_hardening_start=2000, mask_hardening_duration=15000, SLoRB=True,
+                                SLoRB_init_type="sum", trainable_projection=True)
+    cfg.enable_hutchinson = True
+    g = torch.Generator(device=dev).manual_seed(21)
+    student = LlamaDecoder(shape, cfg, RANK, dev, torch.bfloat16)
+    student.init_random(g)
+    teacher = LlamaDecoder(shape, None, RANK, dev, torch.bfloat16)
+    teacher.init_random(g)
+    teacher.requires_grad_(False)
+    hx = hardening_coefficient(cfg, E2E_START - 10)
+    with torch.no_grad():  # mid-training state: soft masks from Hessian-weighted scores, hardening under way
+        for m in student.modules():
+            if isinstance(m, sm.SparseLinear):
+                m.hessian_diag.copy_(torch.rand(m.mask.shape, generator=g, device=dev) * 1e-3 + 1e-6)
+                m.mask.copy_(m.compute_gate_target(step=E2E_START - 10))
+                m.hardening_x = hx
+    n_student = sum(p.numel() for p in student.parameters() if p.requires_grad)
+    n_sparse = sum(m.weight.numel() for m in student.modules() if isinstance(m, sm.SparseLinear))
+    opt = AdamW(optimizer_groups(student, 0.1), lr=1e-4, betas=(0.9, 0.95))
+    rc = RetrainConfig(grad_accum=E2E_BATCH // micro, lr=1e-4)
+    step = RetrainStep(student, teacher, opt, rc, timed=True)
+    tok = torch.Generator(device=dev).manual_seed(22)
+
+    def batches():
+        out = []
+        for _ in range(rc.grad_accum):
+            seq = torch.randint(0, shape.vocab_size, (micro, E2E_SEQ + 1), generator=tok, device=dev)
+            out.append((seq[:, :-1].contiguous(), seq[:, 1:].contiguous()))
+        return out
+
+    data = [batches() for _ in range(steps + warmup)]
+    it = E2E_START - warmup
+    log(f"e2e: {shape.num_hidden_layers} layers, {n_student / 1e9:.3f} G trainable params "
+        f"({n_sparse / 1e9:.3f} G in SparseLinear), micro-batch {micro} x {E2E_SEQ}, {rc.grad_accum} micro-batches")
+    for k in range(warmup):
+        step(it, data[k])
+        it += 1
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    phases = {n: 0.0 for n in PHASES}
+    losses = []
+    t0 = time.perf_counter()
+    for k in range(steps):
+        r = step(it, data[warmup + k])
+        it += 1
+        losses.append(r.loss)
+        for n, ms in r.phase_ms().items():  # waits for the step's last event (the next step is not queued yet)
+            phases[n] += ms
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    tokens = E2E_BATCH * E2E_SEQ * steps
+    res = {"value": round(tokens / el, 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+           "ms_per_step": round(el * 1e3 / steps, 2), "batch": E2E_BATCH, "seq_len": E2E_SEQ, "micro_batch": micro,
+           "grad_accum": rc.grad_accum, "layers": shape.num_hidden_layers, "trainable_params": n_student,
+           "sparse_params": n_sparse, "first_iter": E2E_START, "hardening_x": round(hx, 4),
+           "mask_updates_in_window": sum(1 for i in range(E2E_START, E2E_START + steps) if i % 10 == 0),
+           "phase_ms_per_step": {n: round(v / steps, 2) for n, v in phases.items()},
+           "peak_mem_gib": round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 1),
+           "loss_first_last": [round(losses[0], 4), round(losses[-1], 4)],
+           "data": "synthetic token ids uniform over the vocabulary; random-init student and teacher"}
+    log(f"e2e: {res['ms_per_step']:.0f} ms/step, {res['value']:.0f} tokens/s; phases {res['phase_ms_per_step']}; "
+        f"peak {res['peak_mem_gib']} GiB")
+    del step, opt, student, teacher, data
+    return res
+
+
 def mfma_sustained(torch, dev, iters: int = 4000, blocks: int = 1024, reps: int = 6) -> float:
     """TFLOP/s of sf_mfma_probe (MFMA-only loop, bf16 register operands distributed like the GEMM's):
     the rate this GPU sustains on the bf16 MFMA pipe alone, best of `reps` after a clock ramp-up."""
@@ -481,6 +572,12 @@ def main(argv=None) -> int:
     ap.add_argument("--kl-steps", type=int, default=10, help="steps of the distillation-KL leg (0 skips it)")
     ap.add_argument("--s24-steps", type=int, default=10,
                     help="steps of the 2:4 packed inference-forward leg (0 skips it)")
+    ap.add_argument("--e2e-steps", type=int, default=10,
+                    help="timed steps of the end-to-end 1.1B retraining leg (0 skips it)")
+    ap.add_argument("--e2e-warmup", type=int, default=2)
+    ap.add_argument("--e2e-micro", type=int, default=2, help="micro-batch of the end-to-end leg (divides 8)")
+    ap.add_argument("--e2e-layers", type=int, default=22)
+    ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--calib", action="store_true",
                     help="first run one plain 256 MiB device copy (a known-size reference for HBM byte counters)")
@@ -504,6 +601,10 @@ def main(argv=None) -> int:
     L.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if a.e2e_only:
+        print(json.dumps({"e2e_1p1b": e2e_leg(torch, dev, a.e2e_steps, a.e2e_warmup, a.e2e_micro, a.e2e_layers)}),
+              flush=True)
+        return 0
     if a.calib:
         src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -582,7 +683,7 @@ def main(argv=None) -> int:
     mstats_gbs = msk.rate / 1e9
     log(f"mask statistics: sf_mask_stats {mstats_gbs:.0f} GB/s over {len(arena)} masks")
     # ---- mask-aware AdamW leg (same arena: W is the bf16 copy, M the mask) ---
-    from sparseforge_amd.adamw import adamw_step_
+    from sparseforge_amd.adamw import TensorStep, adamw_step_multi_
 
     log("building AdamW state (f32 master, bf16 grad, f32 m / v)")
     gen = torch.Generator(device=dev).manual_seed(2)
@@ -594,9 +695,11 @@ def main(argv=None) -> int:
         opt_state.append((master, grad, torch.zeros_like(master), torch.zeros_like(master), M, W))
     torch.cuda.synchronize()
 
+    items = [TensorStep(master, grad, m, v, None, M, W) for master, grad, m, v, M, W in opt_state]
+
     def adamw_leg_step(k):
-        for master, grad, m, v, M, W in opt_state:
-            adamw_step_(master, grad, m, v, None, M, k, 1e-4, (0.9, 0.95), 1e-8, 0.1, decay=6e-5, bf16_copy=W)
+        # the whole arena in one sf_adamw_step_multi call (a launch per 40 tensors)
+        adamw_step_multi_(items, k, 1e-4, (0.9, 0.95), 1e-8, 0.1, decay=6e-5)
 
     adamw_leg_step(1)  # warmup
     torch.cuda.synchronize()
@@ -607,11 +710,11 @@ def main(argv=None) -> int:
             adamw_leg_step(k + 2)
         torch.cuda.synchronize()
         ael = time.perf_counter() - t0
-    as_ = at.summary()["sf_adamw_step"]
+    as_ = at.summary()["sf_adamw_step_multi"]
     adamw_gbs = ADAMW_BYTES_PER_PARAM * n_params * a.adamw_steps / ael / 1e9
     log(f"adamw: {ael * 1e3 / a.adamw_steps:.2f} ms/step of the arena, {adamw_gbs:.0f} GB/s; "
-        f"sf_adamw_step {as_.rate / 1e9:.0f} GB/s over kernel time")
-    del arena, opt_state
+        f"sf_adamw_step_multi {as_.rate / 1e9:.0f} GB/s over kernel time")
+    del arena, opt_state, items
     torch.cuda.empty_cache()
 
     # ---- block-sparse-16 leg (gate/up shape, block densities 0.5 and 0.25) ----
@@ -620,6 +723,8 @@ def main(argv=None) -> int:
 
     kl = kl_leg(torch, dev, a.kl_steps) if a.kl_steps > 0 else None
     s24 = sparse24_leg(torch, dev, a.tokens, a.s24_steps) if a.s24_steps > 0 else None
+    e2e = e2e_leg(torch, dev, a.e2e_steps, a.e2e_warmup, a.e2e_micro, a.e2e_layers) if a.e2e_steps > 0 else None
+    torch.cuda.empty_cache()
     sustained = mfma_sustained(torch, dev)
     copy_gbs = copy_sustained(torch, dev)
     torch.cuda.empty_cache()
@@ -680,6 +785,8 @@ def main(argv=None) -> int:
         out["distill_kl"] = kl
     if s24:
         out["sparse24_forward"] = s24
+    if e2e:
+        out["e2e_1p1b"] = e2e
     if not a.no_cpu:
         log("timing CPU baseline (numpy oracle)")
         out["cpu_baseline"] = cpu_baseline()

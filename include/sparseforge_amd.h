@@ -488,6 +488,36 @@ int sf_adamw_step(void* param, int param_dtype, const void* grad, int grad_dtype
                   void* max_exp_avg_sq, int state_dtype, const void* mask, int mask_dtype, void* param_bf16_copy,
                   int64_t n, const sf_adamw_params* hp, void* stream);
 
+/*
+ * One tensor of a multi-tensor AdamW step (the per-parameter operands of
+ * sf_adamw_step).  apply_l1: the parameter is >= 2-D (the L1 term also needs
+ * a mask).  Tensors with n == 0 are skipped.
+ */
+typedef struct sf_adamw_tensor {
+  void* param;             /* [n] param_dtype, updated in place           */
+  const void* grad;        /* [n] grad_dtype                               */
+  void* exp_avg;           /* [n] state_dtype                              */
+  void* exp_avg_sq;        /* [n] state_dtype                              */
+  void* max_exp_avg_sq;    /* [n] state_dtype when amsgrad, else NULL      */
+  const void* mask;        /* [n] mask_dtype (the parameter's `mask`) or NULL */
+  void* param_bf16_copy;   /* [n] bf16 copy of the updated parameter or NULL */
+  int64_t n;
+  int grad_dtype, mask_dtype;
+  int apply_l1;
+  int reserved;
+} sf_adamw_tensor;
+
+/*
+ * The AdamW step of a whole parameter list in one pass over HBM
+ * (AdamW.step's loop over parameters, legacy/adamw.py:79-174, fused): the
+ * per-element arithmetic of sf_adamw_step for every tensor of `tensors` (a
+ * HOST array of `count` entries that share param_dtype, state_dtype and the
+ * hyper-parameters, including step).  The list travels in the kernel
+ * arguments: one launch per 40 tensors, nothing allocated or copied.
+ */
+int sf_adamw_step_multi(const sf_adamw_tensor* tensors, int count, int param_dtype, int state_dtype,
+                        const sf_adamw_params* hp, void* stream);
+
 /* ---- Hutchinson Hessian diagonal (update_hessian_hutchinson, legacy/utils.py:710-869) ----
  * Probe v(seed, i) = +-1 from bit i % 64 of output i / 64 of the SplitMix64
  * stream seeded with `seed`: a pure function, regenerated wherever needed.  It

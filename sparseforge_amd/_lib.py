@@ -151,6 +151,25 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+class AdamwTensor(ctypes.Structure):
+    """Mirror of ``sf_adamw_tensor``."""
+
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("exp_avg", ctypes.c_void_p),
+        ("exp_avg_sq", ctypes.c_void_p),
+        ("max_exp_avg_sq", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("param_bf16_copy", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+        ("grad_dtype", ctypes.c_int),
+        ("mask_dtype", ctypes.c_int),
+        ("apply_l1", ctypes.c_int),
+        ("reserved", ctypes.c_int),
+    ]
+
+
 class AdamwParams(ctypes.Structure):
     """Mirror of ``sf_adamw_params``."""
 
@@ -210,6 +229,7 @@ SIGNATURES = {
     "sf_gemm_workspace_size": (_SZ, [ctypes.POINTER(GemmDesc)]),
     "sf_column_sum": (_I, [_P, _I, _I64, _I64, _P, _I, _P]),
     "sf_adamw_step": (_I, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _P, _I64, ctypes.POINTER(AdamwParams), _P]),
+    "sf_adamw_step_multi": (_I, [ctypes.POINTER(AdamwTensor), _I, _I, _I, ctypes.POINTER(AdamwParams), _P]),
     "sf_bsr_count": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _P, _P, _P]),
     "sf_bsr_scan": (_I, [_P, _I64, _P, _P]),
     "sf_bsr_fill": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _P, _P, _P, _P, _I, _P, _P]),

@@ -1,4 +1,4 @@
-"""Drop-in AdamW with the mask-aware decay, one fused HIP kernel per parameter.
+"""Drop-in AdamW with the mask-aware decay: one fused pass over all parameters of a step.
 
 Mirrors legacy/adamw.py of liuhanzuo/SparseForge: the same constructor
 (``AdamW(params, lr, betas, eps, weight_decay, amsgrad, srste_decay,
@@ -10,8 +10,11 @@ the two.  The masked decay finds the mask through the parameter's ``mask``
 attribute, which SparseLinear aliases to its mask (sparse_modeling.py:372).
 
 Each parameter's whole update (decoupled weight decay, masked decay,
-moments, bias corrections, AMSGrad, adaptive L1) is one pass of
-``sf_adamw_step``; parameters must live on the GPU (there is no CPU path).
+moments, bias corrections, AMSGrad, adaptive L1) is one elementwise pass;
+``step`` updates all parameters that share dtypes and hyper-parameters with
+one ``sf_adamw_step_multi`` call (a launch per 40 tensors, the tensor table
+in the kernel arguments).  Parameters must live on the GPU (there is no CPU
+path).
 """
 from __future__ import annotations
 
@@ -55,6 +58,60 @@ def adamw_step_(p: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor, exp_
                                       L.byref(hp), L.stream(dev)), "sf_adamw_step")
 
 
+class TensorStep:
+    """Operands of one tensor in a multi-tensor step (see adamw_step_multi_)."""
+
+    __slots__ = ("param", "grad", "exp_avg", "exp_avg_sq", "max_exp_avg_sq", "mask", "bf16_copy", "apply_l1")
+
+    def __init__(self, param, grad, exp_avg, exp_avg_sq, max_exp_avg_sq=None, mask=None, bf16_copy=None,
+                 apply_l1=None):
+        self.param, self.grad, self.exp_avg, self.exp_avg_sq = param, grad, exp_avg, exp_avg_sq
+        self.max_exp_avg_sq, self.mask, self.bf16_copy = max_exp_avg_sq, mask, bf16_copy
+        self.apply_l1 = param.dim() >= 2 if apply_l1 is None else bool(apply_l1)
+
+
+def adamw_step_multi_(items, step: int, lr: float, betas, eps: float, weight_decay: float, decay: float = 0.0,
+                      l1: float = 0.0, amsgrad: bool = False) -> None:
+    """In-place fused AdamW step of every TensorStep in `items` (one parameter dtype, one state dtype,
+    one step count): one sf_adamw_step_multi call, one launch per 40 tensors."""
+    items = [t for t in items if t.param.numel() > 0]
+    if not items:
+        return
+    dev = L.require_device(items[0].param)
+    pdt, sdt = items[0].param.dtype, items[0].exp_avg.dtype
+    arr = (L.AdamwTensor * len(items))()
+    nbytes = 0
+    for e, t in zip(arr, items):
+        L.require_device(t.param, t.grad, t.exp_avg, t.exp_avg_sq, t.max_exp_avg_sq, t.mask, t.bf16_copy)
+        n = t.param.numel()
+        if t.param.device != dev or t.param.dtype != pdt or t.exp_avg.dtype != sdt or t.exp_avg_sq.dtype != sdt:
+            raise TypeError("adamw: a multi-tensor step needs one device, one parameter dtype and one state dtype")
+        for name, x in (("grad", t.grad), ("exp_avg", t.exp_avg), ("exp_avg_sq", t.exp_avg_sq),
+                        ("max_exp_avg_sq", t.max_exp_avg_sq), ("mask", t.mask), ("bf16_copy", t.bf16_copy)):
+            if x is not None and x.numel() != n:
+                raise ValueError(f"adamw: {name} has {x.numel()} elements, the parameter {n}")
+        if amsgrad and (t.max_exp_avg_sq is None or t.max_exp_avg_sq.dtype != sdt):
+            raise TypeError("adamw: amsgrad needs max_exp_avg_sq in the state dtype")
+        if t.bf16_copy is not None and t.bf16_copy.dtype != torch.bfloat16:
+            raise TypeError("adamw: the parameter copy must be bfloat16")
+        e.param, e.grad, e.exp_avg, e.exp_avg_sq = L.ptr(t.param), L.ptr(t.grad), L.ptr(t.exp_avg), L.ptr(t.exp_avg_sq)
+        e.max_exp_avg_sq = L.ptr(t.max_exp_avg_sq) if amsgrad else None
+        e.mask, e.param_bf16_copy, e.n = L.ptr(t.mask), L.ptr(t.bf16_copy), n
+        e.grad_dtype = _code(t.grad)
+        e.mask_dtype = _code(t.mask) if t.mask is not None else L.DT_F32
+        e.apply_l1 = int(t.apply_l1)
+        nbytes += n * (2 * t.param.element_size() + t.grad.element_size() + 4 * t.exp_avg.element_size()
+                       + (2 * t.exp_avg.element_size() if amsgrad else 0)
+                       + (t.mask.element_size() if t.mask is not None else 0) + (2 if t.bf16_copy is not None else 0))
+    hp = L.AdamwParams()
+    hp.lr, hp.weight_decay, hp.beta1, hp.beta2, hp.eps = float(lr), float(weight_decay), float(betas[0]), \
+        float(betas[1]), float(eps)
+    hp.decay, hp.l1, hp.amsgrad, hp.step, hp.apply_l1 = float(decay), float(l1), int(bool(amsgrad)), int(step), 0
+    with _prof.region("sf_adamw_step_multi", nbytes, "B", dev):
+        L.check(L.lib().sf_adamw_step_multi(arr, len(items), L.dtype_code(items[0].param), L.dtype_code(items[0].exp_avg),
+                                            L.byref(hp), L.stream(dev)), "sf_adamw_step_multi")
+
+
 class AdamW(torch.optim.Optimizer):
     """AdamW with SR-STE masked decay and adaptive L1 decay (legacy/adamw.py:13-176)."""
 
@@ -80,12 +137,19 @@ class AdamW(torch.optim.Optimizer):
 
     @torch.no_grad()
     def step(self, closure=None, decay=None):
+        """One step of every parameter with a gradient (:65-176).
+
+        Parameters that share a device, dtypes, hyper-parameters and step count
+        are updated by one sf_adamw_step_multi call (one pass over HBM for the
+        whole group) instead of one kernel per parameter."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
         if decay is not None:
             self.decay = decay
+        groups: dict = {}
+        keep = []  # temporaries (contiguous gradient copies, mask views) alive until their launch
         for group in self.param_groups:
             lr, betas, eps, wd, amsgrad = group["lr"], group["betas"], group["eps"], group["weight_decay"], \
                 group["amsgrad"]
@@ -119,9 +183,16 @@ class AdamW(torch.optim.Optimizer):
                 if amsgrad and "max_exp_avg_sq" not in state:
                     state["max_exp_avg_sq"] = torch.zeros_like(p)
                 state["step"] += 1
-                l1 = self.adaptive_l1_decay if (self.adaptive_l1_decay > 0.0 and p.dim() >= 2) else 0.0
-                adamw_step_(p.data, grad.contiguous(), state["exp_avg"],
-                            state["exp_avg_sq"], state.get("max_exp_avg_sq") if amsgrad else None,
-                            mask.detach().contiguous() if mask is not None else None, state["step"], lr, betas, eps, wd,
-                            decay=float(self.decay) if mask is not None else 0.0, l1=l1, amsgrad=amsgrad)
+                g = grad.contiguous()
+                m = mask.detach().contiguous() if mask is not None else None
+                keep.extend(t for t in (g, m) if t is not None)
+                key = (p.device, p.dtype, state["exp_avg"].dtype, state["step"], float(lr), tuple(map(float, betas)),
+                       float(eps), float(wd), bool(amsgrad))
+                groups.setdefault(key, []).append(
+                    TensorStep(p.data, g, state["exp_avg"], state["exp_avg_sq"],
+                               state.get("max_exp_avg_sq") if amsgrad else None, m, apply_l1=p.dim() >= 2))
+        for (_dev, _pdt, _sdt, step, lr, betas, eps, wd, amsgrad), items in groups.items():
+            adamw_step_multi_(items, step, lr, betas, eps, wd, decay=float(self.decay),
+                              l1=float(self.adaptive_l1_decay), amsgrad=amsgrad)
+        del keep
         return loss

@@ -104,3 +104,47 @@ def test_adamw_rejects_bad_hyperparameters():
         AdamW(p, lr=-1)
     with pytest.raises(ValueError, match="beta parameter at index 1"):
         AdamW(p, betas=(0.9, 1.0))
+
+
+@pytest.mark.parametrize("amsgrad,l1,sdt", [(False, 0.0, torch.float32), (True, 2e-3, torch.float32),
+                                           (False, 1e-3, torch.bfloat16)])
+def test_multi_tensor_step_equals_per_tensor_step(cuda_device, amsgrad, l1, sdt):
+    """sf_adamw_step_multi over 97 tensors (three launches of at most 40) equals sf_adamw_step per
+    tensor bit for bit: ragged sizes, an empty tensor, unaligned views (vector accesses off), f32 and
+    bf16 gradients and masks, tensors without a mask, 1-D tensors (no L1 term), bf16 copies."""
+    from sparseforge_amd.adamw import TensorStep, adamw_step_, adamw_step_multi_
+
+    g = torch.Generator(device=cuda_device).manual_seed(41)
+    dev = cuda_device
+    sizes = [0, 1, 3, 4, 5, 1023, 1024, 1025, 4099, 65537, 300_001] + [int(x) for x in
+                                                                       torch.randint(1, 20000, (86,), generator=g,
+                                                                                     device=dev).cpu()]
+
+    def make(k, n):
+        off = 1 if k % 5 == 3 else 0  # an unaligned view: element offset 1
+        mk = lambda dt, s=1.0: (torch.randn(n + off, generator=g, device=dev) * s).to(dt)[off:]  # noqa: E731
+        p = mk(torch.float32, 0.05)
+        gr = mk(torch.bfloat16 if k % 2 else torch.float32, 1e-3)
+        m = mk(sdt, 1e-3)
+        v = mk(sdt, 1e-3).abs()
+        vmax = (v.float() * 1.5).to(sdt) if amsgrad else None
+        mask = None if k % 7 == 0 else mk(torch.bfloat16 if k % 3 else torch.float32).sigmoid()
+        copy = torch.empty(n, dtype=torch.bfloat16, device=dev) if k % 4 == 1 else None
+        return dict(p=p, g=gr, m=m, v=v, vmax=vmax, mask=mask, copy=copy, l1=(k % 6 != 5))
+
+    tensors = [make(k, n) for k, n in enumerate(sizes)]
+    clones = [{k: (x.clone() if isinstance(x, torch.Tensor) else x) for k, x in t.items()} for t in tensors]
+    hp = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, decay=6e-5, l1=l1, amsgrad=amsgrad)
+    for t in clones:
+        if t["p"].numel():
+            adamw_step_(t["p"], t["g"], t["m"], t["v"], t["vmax"], t["mask"], 3, hp["lr"], hp["betas"], hp["eps"],
+                        hp["weight_decay"], decay=hp["decay"] if t["mask"] is not None else 0.0, l1=l1,
+                        amsgrad=amsgrad, apply_l1=t["l1"], bf16_copy=t["copy"])
+    items = [TensorStep(t["p"], t["g"], t["m"], t["v"], t["vmax"], t["mask"], t["copy"], apply_l1=t["l1"])
+             for t in tensors]
+    adamw_step_multi_(items, 3, **hp)
+    torch.cuda.synchronize()
+    for k, (a, b) in enumerate(zip(tensors, clones)):
+        for key in ("p", "m", "v", "vmax", "copy"):
+            if a[key] is not None:
+                assert torch.equal(a[key], b[key]), (k, key, sizes[k])
