@@ -42,17 +42,54 @@ class _KL(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         s2, t2, lse, scale = ctx.saved_tensors
+        # a Function of its own, so that torch.autograd.grad(..., create_graph=True) (the Hutchinson
+        # Hessian-vector product) differentiates the KL gradient as the reference's torch ops are
+        gs = _KLGrad.apply(s2, t2, lse, scale, g, ctx.temperature)
+        return gs, None, None, None
+
+
+class _KLGrad(torch.autograd.Function):
+    """gs = g * c_r * (q - p) inside the clamp range (sf_kl_backward), differentiable once more.
+
+    With q = softmax(clamp(s) / T) per row, m = [-100 <= s <= 100] and c_r the row scale
+    (T / rows, or 0 for a skipped chunk): d gs_i / d s_j = m_i m_j (g c_r / T) q_i (delta_ij - q_j),
+    so the vector-Jacobian product with u = ggs * m is
+        s_bar_j = m_j (g c_r / T) q_j (u_j - sum_i u_i q_i),
+    and d gs / d g = c_r m (q - p) gives g_bar = sum ggs * c_r * m * (q - p).  These run as float32
+    device elementwise ops and row sums (they are needed once per Hutchinson probe)."""
+
+    @staticmethod
+    def forward(ctx, s2, t2, lse, scale, g, temperature: float):
         dev = s2.device
-        g = g.contiguous()
-        if g.dtype not in (torch.float32, torch.bfloat16):
-            g = g.float()
+        gg = g.detach().contiguous()
+        if gg.dtype not in (torch.float32, torch.bfloat16):
+            gg = gg.float()
         gs = torch.empty_like(s2)
         rows, vocab = s2.shape
         with _prof.region("sf_kl_backward", 3 * s2.numel() * s2.element_size(), "B", dev):
-            L.check(L.lib().sf_kl_backward(L.ptr(s2), L.ptr(t2), L.dtype_code(s2), rows, vocab, ctx.temperature,
-                                           L.ptr(lse), L.ptr(scale), L.ptr(g), L.dtype_code(g), L.ptr(gs),
+            L.check(L.lib().sf_kl_backward(L.ptr(s2), L.ptr(t2), L.dtype_code(s2), rows, vocab, float(temperature),
+                                           L.ptr(lse), L.ptr(scale), L.ptr(gg), L.dtype_code(gg), L.ptr(gs),
                                            L.stream(dev)), "sf_kl_backward")
-        return gs, None, None, None
+        ctx.save_for_backward(s2, t2, lse, scale, g)
+        ctx.temperature = float(temperature)
+        return gs
+
+    @staticmethod
+    def backward(ctx, ggs):
+        s2, t2, lse, scale, g = ctx.saved_tensors
+        T = ctx.temperature
+        s = s2.float()
+        inside = (s >= -100.0) & (s <= 100.0)
+        q = torch.exp(s.clamp(-100.0, 100.0) / T - lse[:, 0:1].float())
+        u = ggs.float() * inside
+        dot = (u * q).sum(dim=1, keepdim=True)
+        coef = (g.float() * scale / T)[:, None]
+        s_bar = (coef * q * (u - dot) * inside).to(s2.dtype)
+        g_bar = None
+        if ctx.needs_input_grad[4]:
+            p = torch.exp(t2.float().clamp(-100.0, 100.0) / T - lse[:, 1:2].float())
+            g_bar = (u * (q - p) * scale[:, None]).sum().to(g.dtype).reshape(g.shape)
+        return s_bar, None, None, None, g_bar, None
 
 
 def chunked_kl_loss(student_logits: torch.Tensor, teacher_logits: torch.Tensor, temperature=2) -> torch.Tensor:

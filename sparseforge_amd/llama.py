@@ -1,0 +1,191 @@
+"""A LLaMA-architecture decoder for the end-to-end sparse retraining step.
+
+The reference retrains HuggingFace's LlamaForCausalLM with every nn.Linear
+inside the decoder stack (`model.model`) swapped for SparseLinear, keeping
+the embedding, the final norm and lm_head dense (legacy/model_llama.py:18-57),
+and it needs eager attention so that Hutchinson's double backward works
+(legacy/model_llama.py:108-123, legacy/utils.py:796-801).  This module builds
+that architecture directly, with the drop-in SparseLinear for the student's
+projections and plain nn.Linear for the dense teacher:
+
+    h = embed(tokens)
+    per layer:  h = h + o(attn(rope(q(n1(h))), rope(k(n1(h))), v(n1(h))))
+                h = h + down(silu(gate(n2(h))) * up(n2(h)))
+    logits = lm_head(norm(h))
+
+* RMSNorm: x * rsqrt(mean(x^2) + eps) in float32, scaled by a learned
+  weight after the cast back to the input dtype.
+* Rotary embedding: the half-split form (pairs (i, i + d/2) rotate by
+  position * theta^(-2i/d)).
+* Attention: causal softmax attention written with differentiable torch ops
+  in float32 (the Hessian-vector product differentiates it twice; float32
+  batched products also stay clear of bf16 batched products on transposed
+  operands).
+* forward(idx, targets) returns (logits, loss, None) like the reference's
+  LlamaSparse.forward (legacy/model_llama.py:59-85): loss is the
+  cross-entropy of the logits against already shifted targets,
+  ignore_index=-1.
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+from torch.nn import functional as F
+
+from .sparse_modeling import SparseLinear, SparseLinearConfig
+
+
+@dataclass
+class LlamaShape:
+    """Architecture of the decoder (the fields of a LLaMA config this build uses)."""
+
+    vocab_size: int = 32000
+    hidden_size: int = 2048
+    intermediate_size: int = 5632
+    num_hidden_layers: int = 22
+    num_attention_heads: int = 32
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    output_hidden_state: bool = False  # set by Distill_Model
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float, device=None, dtype=None):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return self.weight * xf.to(x.dtype)
+
+
+def rotary_tables(seq: int, head_dim: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos, sin [seq, head_dim] (float32) of the half-split rotary embedding."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
+    ang = torch.arange(seq, device=device, dtype=torch.float32)[:, None] * inv[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos(), ang.sin()
+
+
+def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    swapped = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+    return x * cos + swapped * sin
+
+
+def causal_attention(q, k, v, cos, sin) -> torch.Tensor:
+    """q, k, v [B, S, H, D] -> [B, S, H * D] in q's dtype; float32 arithmetic, causal mask."""
+    B, S, H, D = q.shape
+    # autocast would recast these float32 products to bf16: keep it off for the attention math
+    with torch.autocast(q.device.type, enabled=False):
+        qf = _rotate(q.float().transpose(1, 2), cos, sin)                  # [B, H, S, D]
+        kf = _rotate(k.float().transpose(1, 2), cos, sin)
+        vf = v.float().transpose(1, 2).contiguous()
+        scores = torch.matmul(qf, kf.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(D))
+        future = torch.ones(S, S, dtype=torch.bool, device=q.device).triu_(1)
+        probs = torch.softmax(scores.masked_fill(future, float("-inf")), dim=-1)
+        out = torch.matmul(probs, vf)                                      # [B, H, S, D]
+    return out.transpose(1, 2).reshape(B, S, H * D).to(q.dtype)
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, shape: LlamaShape, make_linear, device=None, dtype=None):
+        super().__init__()
+        h, f = shape.hidden_size, shape.intermediate_size
+        self.input_layernorm = RMSNorm(h, shape.rms_norm_eps, device=device, dtype=dtype)
+        self.post_attention_layernorm = RMSNorm(h, shape.rms_norm_eps, device=device, dtype=dtype)
+        self.self_attn = nn.Module()
+        for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            setattr(self.self_attn, name, make_linear(h, h))
+        self.mlp = nn.Module()
+        self.mlp.gate_proj = make_linear(h, f)
+        self.mlp.up_proj = make_linear(h, f)
+        self.mlp.down_proj = make_linear(f, h)
+        self.heads = shape.num_attention_heads
+
+    def forward(self, x, cos, sin):
+        B, S, Hd = x.shape
+        a = self.self_attn
+        n = self.input_layernorm(x)
+        q = a.q_proj(n).view(B, S, self.heads, -1)
+        k = a.k_proj(n).view(B, S, self.heads, -1)
+        v = a.v_proj(n).view(B, S, self.heads, -1)
+        x = x + a.o_proj(causal_attention(q, k, v, cos, sin))
+        n = self.post_attention_layernorm(x)
+        m = self.mlp
+        return x + m.down_proj(F.silu(m.gate_proj(n)) * m.up_proj(n))
+
+
+class LlamaDecoder(nn.Module):
+    """Student (SparseLinear projections, `sparse_config` given) or dense teacher (nn.Linear)."""
+
+    def __init__(self, shape: LlamaShape, sparse_config: SparseLinearConfig | None = None, slorb_rank: int = 64,
+                 device=None, dtype=torch.bfloat16):
+        super().__init__()
+        self.config = dataclasses.replace(shape)
+
+        def make_linear(fin, fout):
+            if sparse_config is None:
+                return nn.Linear(fin, fout, bias=False, device=device, dtype=dtype)
+            cfg = sparse_config
+            if cfg.SLoRB:
+                if fin % slorb_rank:
+                    raise ValueError(f"in_features {fin} is not a multiple of the SLoRB rank {slorb_rank}")
+                cfg = dataclasses.replace(cfg, SLoRB_k=fin // slorb_rank)  # rank = in / k
+            for key, val in vars(sparse_config).items():  # attributes set outside the dataclass fields
+                if not hasattr(cfg, key):
+                    setattr(cfg, key, val)
+            return SparseLinear(fin, fout, sparselinear_config=cfg, bias=False, device=device, dtype=dtype)
+
+        self.embed_tokens = nn.Embedding(shape.vocab_size, shape.hidden_size, device=device, dtype=dtype)
+        self.layers = nn.ModuleList(DecoderLayer(shape, make_linear, device, dtype)
+                                    for _ in range(shape.num_hidden_layers))
+        self.norm = RMSNorm(shape.hidden_size, shape.rms_norm_eps, device=device, dtype=dtype)
+        self.lm_head = nn.Linear(shape.hidden_size, shape.vocab_size, bias=False, device=device, dtype=dtype)
+        self._rope = {}
+
+    @torch.no_grad()
+    def init_random(self, generator: torch.Generator, std: float = 0.02, slorb_std: float = 0.01) -> None:
+        """Random init: N(0, std) projections / embedding / lm_head, unit norms; SparseLinear masks at
+        one (initialize), SLoRB projection the block-sum matrix (init_SLoRB), SLoRB weights N(0, slorb_std)."""
+        def normal_(t, s):
+            t.copy_(torch.randn(t.shape, generator=generator, device=t.device, dtype=torch.float32) * s)
+
+        normal_(self.embed_tokens.weight, std)
+        normal_(self.lm_head.weight, std)
+        for mod in self.modules():
+            if isinstance(mod, SparseLinear):
+                normal_(mod.weight, std)
+                mod.initialize()
+                if mod.SLoRB:
+                    mod.init_SLoRB()
+                    normal_(mod.SLoRB_Weight, slorb_std)
+            elif isinstance(mod, nn.Linear) and mod is not self.lm_head:
+                normal_(mod.weight, std)
+
+    def _tables(self, seq: int, device):
+        key = (seq, str(device))
+        if key not in self._rope:
+            self._rope[key] = rotary_tables(seq, self.config.head_dim, self.config.rope_theta, device)
+        return self._rope[key]
+
+    def forward(self, idx: torch.Tensor, targets: torch.Tensor | None = None):
+        cos, sin = self._tables(idx.shape[1], idx.device)
+        h = self.embed_tokens(idx)
+        for layer in self.layers:
+            h = layer(h, cos, sin)
+        logits = self.lm_head(self.norm(h))
+        loss = None
+        if targets is not None:
+            loss = F.cross_entropy(logits.view(-1, logits.size(-1)), targets.view(-1), ignore_index=-1)
+        return logits, loss, None

@@ -112,3 +112,35 @@ def test_distill_model_returns_kl(cuda_device):
                                rtol=2e-6)
     (task + kl).backward()
     assert student.head.weight.grad is not None and teacher.head.weight.grad is None
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_kl_second_derivative_matches_float64_autograd(cuda_device, dtype, tol):
+    """The distillation KL is twice differentiable (the Hutchinson probe differentiates its gradient):
+    the Hessian-vector product of the device KL along a random direction equals the float64 double
+    backward of the reference formula (oracle/retrain.kl_loss), with clamped logits and a second,
+    non-constant outer gradient (d/dg of g * dKL/ds)."""
+    from oracle import retrain as orc
+    from sparseforge_amd.distill import chunked_kl_loss
+
+    g = torch.Generator().manual_seed(23)
+    s = torch.randn(3, 70, 257, generator=g) * 4
+    t = torch.randn(3, 70, 257, generator=g) * 4
+    s[0, 2, 5] = 180.0  # clamped: no gradient there
+    d = torch.randn(3, 70, 257, generator=g)
+    w = torch.tensor(1.7)
+    s64 = s.double().requires_grad_(True)
+    (gs64,) = torch.autograd.grad(orc.kl_loss(s64, t.double()) * w.double(), s64, create_graph=True)
+    (h64,) = torch.autograd.grad((gs64 * d.double()).sum(), s64)
+    sd = s.to(dtype).to(cuda_device).requires_grad_(True)
+    wd = w.to(cuda_device).requires_grad_(True)
+    kl = chunked_kl_loss(sd, t.to(dtype).to(cuda_device), 2) * wd.to(dtype)
+    (gs,) = torch.autograd.grad(kl, sd, create_graph=True)
+    hv, hw = torch.autograd.grad((gs.float() * d.to(cuda_device)).sum(), (sd, wd))
+    assert float((hv.double().cpu() - h64).abs().max() / h64.abs().max()) < tol
+    assert hv[0, 2, 5].item() == 0.0
+    # d/dw of <dKL/ds * w, d> = <dKL/ds, d>: a sum whose terms largely cancel, so its error is bounded
+    # relative to the sum of their magnitudes (bf16 rounds every gradient entry before the sum)
+    terms = gs64.detach() / w.double() * d.double()
+    ref_w = float(terms.sum())
+    assert abs(hw.item() - ref_w) <= tol * float(terms.abs().sum())
