@@ -1,9 +1,9 @@
 """GPU checks at the benchmark's full sizes, through size-independent properties and torch's
 own float32 GPU results (the float64 CPU oracle would take minutes at these sizes).
 
-* SparseLinear fwd / dX / dW at the gate / down shapes of a LLaMA-2-7B layer (T = 8192) with
-  the hard 2:4 mask: against torch float32 products of the same bf16 operands, rtol 2e-2
-  (bf16) relative to the output scale.
+* SparseLinear fwd / dX / dW / dP / dS at the q/k/v/o, gate/up and down shapes of a
+  LLaMA-2-7B layer (T = 8192) with the hard 2:4 mask and SLoRB rank 64: against torch
+  float32 products of the same bf16 operands, rtol 2e-2 (bf16) relative to the output scale.
 * the fused mask update over a full [11008, 4096] layer: the new mask stays in [0, 1], its
   hard 2:4 projection keeps exactly two of every four, and the flip count equals the number
   of changed hard-mask entries counted independently.
@@ -21,27 +21,61 @@ def rel_err(got, ref):
     return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
 
 
-@pytest.mark.parametrize("in_f,out_f", [(4096, 11008), (11008, 4096)])
+def within_bf16_rounding(got, ref, extra=None) -> float:
+    """Largest ratio of |got - ref| to the elementwise bound 2^-7 |ref| + 2^-12 max|ref|: a bf16 result
+    of a float32 accumulation is within half an ulp (2^-9 relative) of the exact value; a dropped 8-wide
+    k chunk at K = 4096 moves an element by about 4e-2 of the output scale, 160 times the absolute term.
+    `extra`: the elementwise effect of one ulp (2^-7 relative at most) of a bf16 intermediate, whose two
+    float32 accumulations may round to neighbouring bf16 values."""
+    got, ref = got.detach().float(), ref.detach().float()
+    bound = ref.abs() * 2.0 ** -7 + ref.abs().max() * 2.0 ** -12
+    if extra is not None:
+        bound = bound + extra
+    return float(((got - ref).abs() / bound).max())
+
+
+@pytest.mark.parametrize("in_f,out_f", [(4096, 4096), (4096, 11008), (11008, 4096)])
 def test_sparse_linear_full_shape(cuda_device, in_f, out_f):
+    """The seven cfg2 shapes (q/k/v/o, gate/up, down) with SLoRB at rank 64 (the block-sum projection of
+    init_SLoRB, k = in / 64): forward, dX, dW, dP, dS against torch float32 products."""
     from sparseforge_amd import _lib as L
     from sparseforge_amd import kernels as K
     from sparseforge_amd.linear import masked_linear
 
-    print(f"[fullsize] linear {in_f}->{out_f}", flush=True)
-    T = 8192
+    print(f"[fullsize] linear {in_f}->{out_f} + SLoRB r=64", flush=True)
+    T, R = 8192, 64
+    k = in_f // R
     g = torch.Generator(device=cuda_device).manual_seed(in_f + out_f)
     x = torch.randn(T, in_f, generator=g, device=cuda_device).to(torch.bfloat16).requires_grad_(True)
     W = (torch.randn(out_f, in_f, generator=g, device=cuda_device) * 0.02).to(torch.bfloat16).requires_grad_(True)
+    P = torch.zeros(R, in_f, device=cuda_device)
+    P[torch.arange(R, device=cuda_device)[:, None], torch.arange(R, device=cuda_device)[:, None] * k
+      + torch.arange(k, device=cuda_device)] = 1.0
+    P = P.to(torch.bfloat16).requires_grad_(True)
+    S = (torch.randn(out_f, R, generator=g, device=cuda_device) * 0.01).to(torch.bfloat16).requires_grad_(True)
     soft = torch.rand(out_f, in_f, generator=g, device=cuda_device)
-    y = masked_linear(x, W, None, soft, "mix", 0.0, L.HARD_NM_TAIL_KEEP, 2, 1.0)
+    y = masked_linear(x, W, None, soft, "mix", 0.0, L.HARD_NM_TAIL_KEEP, 2, 1.0, P=P, S=S)
     gy = torch.randn(T, out_f, generator=g, device=cuda_device).to(torch.bfloat16)
     y.backward(gy)
     E = K.hard_mask(soft, L.HARD_NM_TAIL_KEEP, 2, 4).float()
     Wm = W.detach().float() * E
-    xf, gyf = x.detach().float(), gy.float()
-    assert rel_err(y, xf @ Wm.t()) < 2e-2
-    assert rel_err(x.grad, gyf @ Wm) < 2e-2                  # dX = dY (W . M)
+    xf, gyf, Pf, Sf = x.detach().float(), gy.float(), P.detach().float(), S.detach().float()
+    z = xf @ Pf.t()
+    dz = gyf @ Sf
+    assert rel_err(y, xf @ Wm.t() + z @ Sf.t()) < 2e-2
+    assert rel_err(x.grad, gyf @ Wm + dz @ Pf) < 2e-2         # dX = dY (W . M) + (dY S) P
     assert rel_err(W.grad, gyf.t() @ xf) < 2e-2              # dW = dY^T X (straight-through, unmasked)
+    assert rel_err(P.grad, dz.t() @ xf) < 2e-2               # dP = (dY S)^T X
+    assert rel_err(S.grad, gyf.t() @ z) < 2e-2               # dS = dY^T (X P^T)
+    # elementwise: each bf16 result within rounding of the float32 product, the SLoRB intermediates z and
+    # dz rounded to bf16 first as the bf16 path (and the reference under autocast) stores them
+    zb, dzb = z.bfloat16().float(), dz.bfloat16().float()
+    ulp = 2.0 ** -7
+    checks = ((y, xf @ Wm.t() + zb @ Sf.t(), (zb.abs() @ Sf.abs().t()) * ulp),
+              (x.grad, gyf @ Wm + dzb @ Pf, (dzb.abs() @ Pf.abs()) * ulp),
+              (W.grad, gyf.t() @ xf, None))
+    for got, ref, extra in checks:
+        assert within_bf16_rounding(got, ref, extra) <= 1.0
 
 
 def test_update_mask_full_layer_properties(cuda_device):

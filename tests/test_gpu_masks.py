@@ -30,6 +30,25 @@ def _K():
     return L, K
 
 
+def _hard_parity(got: np.ndarray, ref: np.ndarray, tol: float, gpu_flips: int, ref_flips: int, tag: str) -> int:
+    """Hard 2:4 projections of the GPU's soft mask and of the oracle's own soft mask agree except in
+    groups whose decision is a genuine near-tie: there the oracle's 2nd and 3rd largest values lie within
+    2 * tol (the two soft masks may each sit tol from the true value).  The flip counts differ by at most
+    four positions per such group.  Returns the count of such groups (printed)."""
+    hg, hr = om.hard_mask_from_soft(got, "nm_2_4"), om.hard_mask_from_soft(ref, "nm_2_4")
+    full = (ref.shape[1] // 4) * 4
+    diff = (hg[:, :full] != hr[:, :full]).reshape(ref.shape[0], -1, 4).any(-1)
+    assert np.array_equal(hg[:, full:], hr[:, full:]), "tail columns are kept by both"
+    rows, grps = np.nonzero(diff)
+    srt = -np.sort(-ref[:, :full].reshape(ref.shape[0], -1, 4)[rows, grps].astype(np.float64), axis=-1)
+    gap = srt[:, 1] - srt[:, 2] if len(rows) else np.zeros(0)
+    assert np.all(gap <= 2 * tol), (tag, gap.max(initial=0.0))
+    assert abs(gpu_flips - ref_flips) <= 4 * len(rows), (tag, gpu_flips, ref_flips, len(rows))
+    print(f"[{tag}] groups {diff.size}, hard decisions differing from the oracle's own mask: {len(rows)} "
+          f"(all near-ties, max gap {gap.max(initial=0.0):.2e}); flips gpu {gpu_flips} oracle {ref_flips}")
+    return len(rows)
+
+
 def _tie_heavy(rng, shape):
     vals = np.array([0.0, 1.0, 0.5, 0.25, 0.75, 1.0, 0.0], dtype=np.float32)
     return vals[rng.integers(0, len(vals), size=shape)]
@@ -190,11 +209,11 @@ def test_update_mask_cfg1_shape_matches_oracle(cuda_device, wdt):
     got = layer.mask.float().cpu().numpy()
     tol = 1e-6 if odt == F32 else 2 ** -8
     np.testing.assert_allclose(got, new, rtol=0, atol=tol)
-    if odt == F32:
-        # near-ties within the tolerance may flip a hard decision; everywhere else the count matches exactly
-        assert abs(int(layer.weight.flipped_mask) - flips) <= max(2, flips // 10000)
+    # the device projection of the GPU mask is the oracle's projection of it, bit for bit
     hard_gpu = layer._hard_mask_from_soft(layer.mask).float().cpu().numpy()
     assert np.array_equal(hard_gpu, om.hard_mask_from_soft(got, "nm_2_4"))
+    # against the oracle's own mask: only genuine near-ties may differ
+    _hard_parity(got, new, tol, int(layer.weight.flipped_mask), flips, f"cfg1 {odt}")
 
 
 def test_update_mask_multi_stride_ragged(cuda_device):
@@ -218,9 +237,9 @@ def test_update_mask_multi_stride_ragged(cuda_device):
     layer.update_mask(3, lambda_mid=0.05, sample_idx=idx.to(cuda_device))
     new, _, flips, _ = om.layer_update_mask(om.full_config(**kw), 3, W.numpy(), H.numpy(), M0.numpy(), None,
                                             idx.numpy(), 0.05)
-    np.testing.assert_allclose(layer.mask.cpu().numpy(), new, rtol=0, atol=1e-6)
-    # near-ties within the tolerance may flip a hard decision
-    assert abs(int(layer.weight.flipped_mask) - flips) <= max(2, flips // 10000)
+    got = layer.mask.cpu().numpy()
+    np.testing.assert_allclose(got, new, rtol=0, atol=1e-6)
+    _hard_parity(got, new, 1e-6, int(layer.weight.flipped_mask), flips, "ragged f32")
 
 
 def test_tau_quantile_matches_torch(cuda_device):
