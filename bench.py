@@ -7,9 +7,13 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
 * ``value`` -- one step = forward + backward of the seven SparseLinear layers
   of a LLaMA-2-7B decoder layer (q/k/v/o [4096, 4096], gate/up
   [11008, 4096], down [4096, 11008]) over T = 8192 tokens in bf16, with the
-  hard 2:4 mask of the layer's soft mask (hardening_x = 0) applied inside the
-  GEMMs and the SLoRB bypass at rank 64.  Throughput counts the algorithmic
-  6 T in out + 6 T r (in + out) FLOPs per linear.
+  hard 2:4 mask of the layer's soft mask (hardening_x = 0) and the SLoRB
+  bypass at rank 64.  The forward writes W * E with one elementwise pass and
+  keeps it for the input gradient; the GEMMs then read it.  Throughput counts
+  the algorithmic 6 T in out + 6 T r (in + out) FLOPs per linear;
+  ``per_linear`` times each linear alone.
+* ``hutchinson_probe_layer`` -- one Hutchinson probe of the same seven linears
+  (create_graph gradients, probe dot, double backward, accumulator updates).
 * ``mask_update`` -- one step = the periodic mask update of every linear of
   the 7B model (32 layers x 7 linears, 6.48 G params; bf16 W, fp32
   Hutchinson accumulator and soft mask): score statistics, tau quantile over
@@ -17,9 +21,13 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
   temperature taken from a 1.0 -> 0.01 geometric schedule over 10 steps.
   GB/s counts 20 B per parameter (stats pass: W 2 + H 4; update pass: W 2 +
   H 4 + mask read 4 + mask write 4).
+* ``hutchinson`` -- the accumulator update of every linear of the 7B arena
+  (f32 accumulator read and written, bf16 Hessian-vector product, probe
+  regenerated): 10 B per parameter.
 * ``adamw`` -- one step = the fused mask-aware AdamW update of every masked
   linear of the 7B model (f32 master weight, bf16 gradient, f32 moments and
-  soft mask, bf16 working copy written back): 32 B per parameter.
+  soft mask, bf16 working copy written back) in one multi-tensor call: 32 B
+  per parameter.
 * ``block_sparse`` -- fwd + dx + SDDMM dW of a block-sparse-16 linear at the
   gate/up shape, block densities 0.5 and 0.25, kept-block FLOPs.
 * ``distill_kl`` -- the fused distillation KL of Distill_Model: forward and
@@ -28,19 +36,21 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
 * ``sparse24_forward`` -- inference forward of a finalized decoder layer: the
   seven linears with hard 2:4 weights packed (kept values + 2-bit indices)
   through gfx950's sparse MFMA, beside the dense forward of the same weights;
-  dense-equivalent 2 T in out FLOPs.
+  dense-equivalent 2 T in out FLOPs against the 2:4-sparse MFMA peak.
+* ``e2e_1p1b`` -- cfg5: sparse retraining steps of a random-init
+  LLaMA-architecture 1.1B model (batch 8 x 2048) with distillation, one
+  Hutchinson probe, mask-aware AdamW and the periodic mask update; tokens/s
+  and a per-phase breakdown.
 * ``roofline`` -- the dominant kernel (the sf_gemm MFMA GEMM): algorithmic
   FLOPs of the step over the summed device time of its sf_gemm launches,
-  timed with HIP events on the launch stream inside the timed region.  ``peak`` is the published dense bf16 figure; ``mfma_sustained`` is what
-  an MFMA-only loop (sf_mfma_probe, operands distributed like the GEMM's, no
-  memory traffic)
-  sustains on the same GPU, the practical ceiling under that figure.  The
-  HBM legs' roofline objects carry ``copy_sustained``, the rate of a plain
-  1 GiB device-to-device copy on the same GPU (read + written bytes), and
-  their fraction of it.
-* ``cpu_baseline`` -- the numpy oracle (oracle/linear.py, a CPU restatement of
-  the reference's FusedMaskedLinearSTE + SLoRB path) on the host cores, on a
-  bounded token sample of the same seven shapes (rank 0, N = 1 only).
+  timed with HIP events on the launch stream inside the timed region.
+  ``peak`` is the published dense bf16 figure; ``mfma_sustained`` is what an
+  MFMA-only loop (sf_mfma_probe, operands distributed like the GEMM's, no
+  memory traffic) sustains on the same GPU.
+* ``cpu_baseline`` -- the numpy oracle on the host cores: the linear leg's
+  products through the BLAS threads on a bounded token sample, the HBM legs
+  as one worker process per core (up to 16) each on its own slice, timed
+  before the GPU is initialised (rank 0, N = 1 only).
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 """
@@ -63,9 +73,12 @@ LINEARS = [("q_proj", HIDDEN, HIDDEN), ("k_proj", HIDDEN, HIDDEN), ("v_proj", HI
            ("o_proj", HIDDEN, HIDDEN), ("gate_proj", HIDDEN, FFN), ("up_proj", HIDDEN, FFN),
            ("down_proj", FFN, HIDDEN)]
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_BF16_SPARSE_TFLOPS = 5000.0  # MI355X 2:4-sparse bf16 MFMA (dense-equivalent FLOPs: twice the dense rate)
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 MASK_BYTES_PER_PARAM = 20   # stats pass 6 B + update pass 14 B
 ADAMW_BYTES_PER_PARAM = 32  # master r/w 8, grad 2, m r/w 8, v r/w 8, mask 4, bf16 copy 2
+ALL_LEGS = ("linear", "mask", "hutch", "adamw", "bsr", "kl", "s24", "e2e")
+HUTCH_BYTES_PER_PARAM = 10  # accumulator f32 r/w 8, Hessian-vector product bf16 2 (probe regenerated)
 
 
 def log(msg: str) -> None:
@@ -330,9 +343,10 @@ def sparse24_leg(torch, dev, tokens: int, steps: int, warmup: int = 2) -> dict:
            "dense_forward": {"value": round(flops * steps / del_ / 1e12, 3), "kernel_tflops": round(dtf, 3),
                              "ms_per_step": round(del_ * 1e3 / steps, 4)},
            "speedup_vs_dense": round(del_ / el, 3),
-           "roofline": {"bound": "mfma", "kernel": "sf_gemm_2to4 (gemm24_kernel, v_smfmac_f32_32x32x32_bf16)",
-                        "achieved": round(ktf, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s dense-equivalent",
-                        "frac": round(ktf / PEAK_BF16_TFLOPS, 4), "launches": k.launches,
+           "roofline": {"bound": "mfma (2:4 sparse)", "kernel": "sf_gemm_2to4 (gemm24_kernel, v_smfmac_f32_32x32x32_bf16)",
+                        "achieved": round(ktf, 3), "peak": PEAK_BF16_SPARSE_TFLOPS,
+                        "unit": "TFLOP/s dense-equivalent", "frac": round(ktf / PEAK_BF16_SPARSE_TFLOPS, 4),
+                        "frac_of_dense_peak": round(ktf / PEAK_BF16_TFLOPS, 4), "launches": k.launches,
                         "avg_launch_ms": round(k.avg_ms, 4)}}
     log(f"2:4 forward: {out['value']:.0f} TFLOP/s dense-equivalent ({out['ms_per_step']:.3f} ms), dense "
         f"{out['dense_forward']['value']:.0f} TFLOP/s, x{out['speedup_vs_dense']:.2f}")
@@ -451,26 +465,6 @@ def mfma_sustained(torch, dev, iters: int = 4000, blocks: int = 1024, reps: int 
     return best
 
 
-def copy_sustained(torch, dev, mib: int = 1024, reps: int = 5) -> float:
-    """GB/s (read + written bytes) of a plain 1 GiB device-to-device copy (torch copy_, the runtime's copy
-    kernel): the streaming rate this GPU's HBM sustains in practice, best of `reps` after a warm-up."""
-    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
-    dst = torch.empty_like(src)
-    st = torch.cuda.current_stream(dev)
-    best = 0.0
-    for r in range(reps + 2):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        dst.copy_(src)
-        e1.record(st)
-        e1.synchronize()
-        if r >= 2:
-            best = max(best, 2.0 * src.numel() * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9)
-    del src, dst
-    log(f"device copy: {best:.0f} GB/s sustained (1 GiB f32, read + write)")
-    return best
-
-
 def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
     import numpy as np
 
@@ -510,13 +504,30 @@ def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
                       f"tokens (full shapes, SLoRB rank {RANK}), {reps} reps in {el:.1f} s"}
 
 
-def cpu_adamw_baseline(budget_s: float = 6.0) -> dict:
+def cpu_pool_size() -> int:
+    """Worker processes of the CPU baselines: the host cores, at most 16 (one GPU's CPU share on the box)."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def _single_thread_blas():
+    try:
+        from threadpoolctl import threadpool_limits
+
+        threadpool_limits(1)
+    except Exception:
+        pass
+
+
+def _adamw_worker(args):
+    """One core: oracle AdamW steps over its own 4 M-parameter slice until the budget runs out."""
+    seed, budget_s = args
     import numpy as np
 
     from oracle import adamw as oa
 
-    rng = np.random.default_rng(2)
-    n = 1 << 22  # 4 M params
+    _single_thread_blas()
+    rng = np.random.default_rng(seed)
+    n = 1 << 22
     p = (rng.standard_normal(n, dtype=np.float32) * 0.02)
     g = (rng.standard_normal(n, dtype=np.float32) * 1e-3)
     mask = rng.random(n, dtype=np.float32)
@@ -526,19 +537,21 @@ def cpu_adamw_baseline(budget_s: float = 6.0) -> dict:
         p, m, v, _ = oa.step(p, g, m, v, None, mask, reps + 1, 1e-4, (0.9, 0.95), 1e-8, 0.1, decay=6e-5)
         reps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 20:
-            break
-    return {"value": round(ADAMW_BYTES_PER_PARAM * n * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port", "sample": f"numpy oracle (oracle/adamw.py) on {n} params, {reps} steps in {el:.1f} s"}
+        if el >= budget_s:
+            return n * reps / el
 
 
-def cpu_mask_baseline(budget_s: float = 8.0) -> dict:
+def _mask_worker(args):
+    """One core: oracle mask updates (stats, tau quantile, gate, penalty, EMA, flips) of its own
+    [1024, 4096] slice of a linear until the budget runs out."""
+    seed, budget_s = args
     import numpy as np
 
     from oracle import masks as om
 
-    rng = np.random.default_rng(1)
-    rows, cols = 1024, HIDDEN  # a slice of one linear: 4 M params
+    _single_thread_blas()
+    rng = np.random.default_rng(seed)
+    rows, cols = 1024, HIDDEN
     W = om.round_bf16(rng.standard_normal((rows, cols), dtype=np.float32) * 0.02)
     H = rng.random((rows, cols), dtype=np.float32) * 1e-3 + 1e-6
     M = rng.random((rows, cols), dtype=np.float32)
@@ -550,15 +563,123 @@ def cpu_mask_baseline(budget_s: float = 8.0) -> dict:
         M = om.layer_update_mask(c, 1 + reps, W, H, M, None, idx, 0.0, w_dt="bf16")[0]
         reps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 20:
-            break
-    gbs = MASK_BYTES_PER_PARAM * rows * cols * reps / el / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle (oracle/masks.py layer_update_mask) on a [{rows}, {cols}] slice, {reps} updates "
-                      f"in {el:.1f} s"}
+        if el >= budget_s:
+            return rows * cols * reps / el
+
+
+def _hutch_worker(args):
+    """One core: oracle Hutchinson accumulator updates (probe regenerated, clamp, EMA) of 4 M elements."""
+    seed, budget_s = args
+    import numpy as np
+
+    from oracle import hutchinson as oh
+
+    _single_thread_blas()
+    rng = np.random.default_rng(seed)
+    n = 1 << 22
+    H = rng.random(n, dtype=np.float32) * 1e-3
+    hvp = rng.standard_normal(n, dtype=np.float32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        H = oh.update(H, hvp, oh.rademacher(seed * 1000 + reps, n), 0.98)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            return n * reps / el
+
+
+def cpu_parallel_baseline(worker, bytes_per_param: int, budget_s: float, what: str) -> dict:
+    """Run `worker` on every pool core at once (each on its own slice); the aggregate rate in GB/s.
+    Called before the GPU is initialised: worker processes are forked from a process without a GPU context."""
+    import multiprocessing as mp
+
+    n = cpu_pool_size()
+    with mp.get_context("fork").Pool(n) as pool:
+        rates = pool.map(worker, [(7 + i, budget_s) for i in range(n)])
+    params_per_s = float(sum(rates))
+    return {"value": round(bytes_per_param * params_per_s / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+            "sample": f"{what}: {n} processes, one per core, each on its own slice for {budget_s:.0f} s; "
+                      f"{bytes_per_param} B/param"}
 
 
 # ---------------------------------------------------------------------------
+def per_linear_times(torch, mods, xs, gys, reps: int = 5) -> list:
+    """cfg2's per-linear figure: fwd + bwd of each linear alone (device events around each repetition)."""
+    from oracle.linear import flops_fwd_bwd
+
+    out = []
+    for (name, fin, fout), lin, x, gy in zip(LINEARS, mods, xs, gys):
+        for _ in range(2):
+            linear_step([lin], [x], [gy])
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in ev:
+            e0.record()
+            linear_step([lin], [x], [gy])
+            e1.record()
+        torch.cuda.synchronize()
+        ms = min(e0.elapsed_time(e1) for e0, e1 in ev)
+        fl = flops_fwd_bwd(x.shape[0], fin, fout, RANK)
+        out.append({"linear": name, "in": fin, "out": fout, "ms": round(ms, 4),
+                    "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 2)})
+    return out
+
+
+def hvp_layer_leg(torch, mods, xs, reps: int = 3) -> dict:
+    """Hutchinson probe of one decoder layer's seven linears at T = 8192 (hard 2:4, SLoRB): the
+    update_hessian_hutchinson call after a forward (first-order gradients with create_graph, the probe
+    dot, the double backward, the seven accumulator updates), on a quadratic loss sum 1/2 ||y||^2."""
+    from sparseforge_amd import utils as U
+
+    model = torch.nn.ModuleList(mods)
+    times = []
+    for r in range(reps + 1):
+        ys = [lin(x) for lin, x in zip(mods, xs)]
+        loss = sum(0.5 * (y.float() ** 2).sum() for y in ys)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        U.update_hessian_hutchinson(model, loss)
+        e1.record()
+        torch.cuda.synchronize()
+        del ys, loss
+        if r:
+            times.append(e0.elapsed_time(e1))
+    for lin, x in zip(mods, xs):
+        lin.weight.grad = lin.x_proj.grad = lin.SLoRB_Weight.grad = x.grad = None
+    ms = min(times)
+    log(f"hutchinson probe of one decoder layer (7 linears, T={xs[0].shape[0]}): {ms:.2f} ms")
+    return {"ms_per_layer": round(ms, 3), "linears": len(mods), "tokens": xs[0].shape[0],
+            "what": "update_hessian_hutchinson after a forward: create_graph gradients, probe dot, double "
+                    "backward, accumulator updates; quadratic loss"}
+
+
+def hutch_arena_leg(torch, arena, steps: int) -> dict:
+    """The accumulator update of every linear of the 7B arena: H (f32) <- beta H + (1 - beta) clamp(hvp v, 0)
+    with a bf16 Hessian-vector product and the probe regenerated from the seed: 10 B per parameter."""
+    from sparseforge_amd import profiling as prof
+    from sparseforge_amd import utils as U
+
+    n = sum(W.numel() for W, _, _ in arena)
+    for k, (W, H, _M) in enumerate(arena):  # warmup
+        U.hutchinson_update_(H, W, 0.98, seed=k)
+    torch.cuda.synchronize()
+    with prof.kernel_timer() as kt:
+        t0 = time.perf_counter()
+        for s_ in range(steps):
+            for k, (W, H, _M) in enumerate(arena):  # the arena's bf16 W stands in for the bf16 hvp
+                U.hutchinson_update_(H, W, 0.98, seed=(s_ + 1) * 1000 + k)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+    k_ = kt.summary()["sf_hutchinson_update"]
+    gbs = HUTCH_BYTES_PER_PARAM * n * steps / el / 1e9
+    log(f"hutchinson update: {el * 1e3 / steps:.2f} ms over the arena, {gbs:.0f} GB/s; kernel {k_.rate / 1e9:.0f} GB/s")
+    return {"value": round(gbs, 2), "unit": "GB/s", "params": n, "steps": steps,
+            "ms_per_step": round(el * 1e3 / steps, 3), "bytes_per_param": HUTCH_BYTES_PER_PARAM,
+            "roofline": {"bound": "hbm", "kernel": "sf_hutchinson_update (hutch_update_vec_kernel)",
+                         "achieved": round(k_.rate / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(k_.rate / 1e9 / PEAK_HBM_GBS, 4), "launches": k_.launches,
+                         "avg_launch_ms": round(k_.avg_ms, 4)}}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -568,6 +689,7 @@ def main(argv=None) -> int:
     ap.add_argument("--mask-layers", type=int, default=LAYERS, help="decoder layers in the mask-update arena")
     ap.add_argument("--mask-steps", type=int, default=10)
     ap.add_argument("--adamw-steps", type=int, default=5)
+    ap.add_argument("--hutch-steps", type=int, default=5, help="updates of the Hutchinson accumulator leg")
     ap.add_argument("--bsr-steps", type=int, default=5, help="steps of the block-sparse leg (0 skips it)")
     ap.add_argument("--kl-steps", type=int, default=10, help="steps of the distillation-KL leg (0 skips it)")
     ap.add_argument("--s24-steps", type=int, default=10,
@@ -579,6 +701,8 @@ def main(argv=None) -> int:
     ap.add_argument("--e2e-layers", type=int, default=22)
     ap.add_argument("--e2e-only", action="store_true", help="run only the end-to-end leg")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--legs", default=",".join(ALL_LEGS),
+                    help=f"comma-separated GPU legs to run (default all: {','.join(ALL_LEGS)}); profiling runs pick one")
     ap.add_argument("--calib", action="store_true",
                     help="first run one plain 256 MiB device copy (a known-size reference for HBM byte counters)")
     a = ap.parse_args(argv)
@@ -587,6 +711,23 @@ def main(argv=None) -> int:
     if a.gpus != 1 or world != 1:
         print("bench.py: this build measures one MI355X only (no multi-GPU path); run with --gpus 1", file=sys.stderr)
         return 2
+
+    legs = set(a.legs.split(","))
+    unknown = legs - set(ALL_LEGS)
+    if unknown:
+        print(f"bench.py: unknown legs {sorted(unknown)}", file=sys.stderr)
+        return 2
+    # CPU baselines first: their worker processes are forked before anything touches the GPU
+    cpu = {}
+    if not a.no_cpu and not a.e2e_only and "linear" in legs:
+        log(f"timing CPU baselines (numpy oracle, {cpu_pool_size()} worker processes for the HBM legs)")
+        cpu["linear"] = cpu_baseline()
+        cpu["mask"] = cpu_parallel_baseline(_mask_worker, MASK_BYTES_PER_PARAM, 8.0,
+                                            "oracle/masks.py layer_update_mask on [1024, 4096] slices")
+        cpu["adamw"] = cpu_parallel_baseline(_adamw_worker, ADAMW_BYTES_PER_PARAM, 6.0,
+                                             "oracle/adamw.py step on 4 M-parameter slices")
+        cpu["hutch"] = cpu_parallel_baseline(_hutch_worker, HUTCH_BYTES_PER_PARAM, 4.0,
+                                             "oracle/hutchinson.py update (probe regenerated) on 4 M-element slices")
 
     import torch
 
@@ -613,6 +754,41 @@ def main(argv=None) -> int:
         del src, dst
 
     # ---- SparseLinear leg ---------------------------------------------------
+    out = {"metric": "SparseLinear fwd+bwd TFLOP/s @7B shapes; 2:4 mask-update HBM GB/s"}
+    if "linear" in legs:
+        out.update(linear_leg(torch, sm, prof, dev, a))
+    if legs & {"mask", "hutch", "adamw"}:
+        arena_legs(torch, L, K, prof, dev, a, legs, out)
+    # ---- block-sparse-16 leg (gate/up shape, block densities 0.5 and 0.25) ----
+    if "bsr" in legs and a.bsr_steps > 0:
+        out["block_sparse"] = [bsr_leg(torch, dev, a.tokens, d, a.bsr_steps, 2) for d in (0.5, 0.25)]
+        torch.cuda.empty_cache()
+    if "kl" in legs and a.kl_steps > 0:
+        out["distill_kl"] = kl_leg(torch, dev, a.kl_steps)
+    if "s24" in legs and a.s24_steps > 0:
+        out["sparse24_forward"] = sparse24_leg(torch, dev, a.tokens, a.s24_steps)
+    torch.cuda.empty_cache()
+    if "e2e" in legs and a.e2e_steps > 0:
+        out["e2e_1p1b"] = e2e_leg(torch, dev, a.e2e_steps, a.e2e_warmup, a.e2e_micro, a.e2e_layers)
+    torch.cuda.empty_cache()
+    if "linear" in legs:
+        sustained = mfma_sustained(torch, dev)
+        out["roofline"]["mfma_sustained"] = round(sustained, 1)
+        out["roofline"]["frac_of_sustained"] = round(out["roofline"]["achieved"] / sustained, 4)
+    if cpu:
+        out["cpu_baseline"] = cpu["linear"]
+        if "mask_update" in out:
+            out["mask_update"]["cpu_baseline"] = cpu["mask"]
+        if "adamw" in out:
+            out["adamw"]["cpu_baseline"] = cpu["adamw"]
+        if "hutchinson" in out:
+            out["hutchinson"]["cpu_baseline"] = cpu["hutch"]
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def linear_leg(torch, sm, prof, dev, a) -> dict:
+    """The headline leg: fwd + bwd of the seven 7B-layer linears; the fields of the bench line."""
     log(f"building decoder layer (T={a.tokens}, bf16, SLoRB rank {RANK})")
     mods, xs, gys = build_layer(torch, sm, dev, a.tokens)
     for _ in range(a.warmup):
@@ -636,102 +812,13 @@ def main(argv=None) -> int:
         f"avg {g.avg_ms:.3f} ms, {gemm_tflops:.1f} TFLOP/s over GEMM time")
     other = {n: {"launches": s.launches, "avg_ms": round(s.avg_ms, 4), "total_ms": round(s.total_ms, 3)}
              for n, s in ks.items()}
+    per_linear = per_linear_times(torch, mods, xs, gys)
+    log("per linear: " + ", ".join(f"{r['linear']} {r['ms']:.3f} ms" for r in per_linear))
+    hvp = hvp_layer_leg(torch, mods, xs)
     del mods, xs, gys
     torch.cuda.empty_cache()
-
-    # ---- mask-update leg ----------------------------------------------------
-    log(f"building mask arena ({a.mask_layers} layers x 7 linears)")
-    arena = build_arena(torch, dev, a.mask_layers)
-    n_params = sum(W.numel() for W, _, _ in arena)
-    flips = torch.zeros(1, dtype=torch.int64, device=dev)
-    sample_idx = {}
-    for W, _, _ in arena:
-        key = tuple(W.shape)
-        if key not in sample_idx:
-            sample_idx[key] = K.sample_indices(262144, W.numel(), 1234 + len(sample_idx), dev)
-    mask_step(torch, L, K, arena, 0, flips, sample_idx)  # warmup
-    torch.cuda.synchronize()
-    log(f"mask arena: {n_params / 1e9:.3f} G params; timing {a.mask_steps} updates")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(a.mask_steps):
-        mask_step(torch, L, K, arena, s, flips, sample_idx)
-    torch.cuda.synchronize()
-    mel = time.perf_counter() - t0
-    # per-kernel launch times from one more update with the layers one after another: overlapping
-    # kernels share the GPU and their individual durations would not describe either kernel
-    with prof.kernel_timer() as mt:
-        mask_step(torch, L, K, arena, a.mask_steps, flips, sample_idx, overlap=False)
-    ms_ = mt.summary()
-    mask_gbs = MASK_BYTES_PER_PARAM * n_params * a.mask_steps / mel / 1e9
-    up = ms_["sf_update_mask"]
-    up_gbs = up.rate / 1e9
-    st_gbs = ms_["sf_score_stats"].rate / 1e9
-    log(f"mask update: {mel * 1e3 / a.mask_steps:.2f} ms/update of the arena, {mask_gbs:.0f} GB/s; "
-        f"sf_update_mask {up_gbs:.0f} GB/s, sf_score_stats {st_gbs:.0f} GB/s")
-    # mask statistics / penalties of the whole model: one fused sf_mask_stats pass per soft mask (4 B/param)
-    srows = torch.empty((len(arena), L.MSTAT_COUNT), dtype=torch.float64, device=dev)
-    sws = K.mask_stats_workspace(dev)
-    for i, (_W, _H, M) in enumerate(arena):
-        K.mask_stats(M, srows[i], 0, 1e-8, sws)
-    torch.cuda.synchronize()
-    with prof.kernel_timer() as mst:
-        for i, (_W, _H, M) in enumerate(arena):
-            K.mask_stats(M, srows[i], 0, 1e-8, sws)
-        torch.cuda.synchronize()
-    msk = mst.summary()["sf_mask_stats"]
-    mstats_gbs = msk.rate / 1e9
-    log(f"mask statistics: sf_mask_stats {mstats_gbs:.0f} GB/s over {len(arena)} masks")
-    # ---- mask-aware AdamW leg (same arena: W is the bf16 copy, M the mask) ---
-    from sparseforge_amd.adamw import TensorStep, adamw_step_multi_
-
-    log("building AdamW state (f32 master, bf16 grad, f32 m / v)")
-    gen = torch.Generator(device=dev).manual_seed(2)
-    opt_state = []
-    arena = [(W, M) for W, _H, M in arena]  # the Hutchinson accumulator is not an AdamW operand: free it
-    for W, M in arena:
-        master = W.float()
-        grad = (torch.randn(W.shape, generator=gen, device=dev) * 1e-3).to(torch.bfloat16)
-        opt_state.append((master, grad, torch.zeros_like(master), torch.zeros_like(master), M, W))
-    torch.cuda.synchronize()
-
-    items = [TensorStep(master, grad, m, v, None, M, W) for master, grad, m, v, M, W in opt_state]
-
-    def adamw_leg_step(k):
-        # the whole arena in one sf_adamw_step_multi call (a launch per 40 tensors)
-        adamw_step_multi_(items, k, 1e-4, (0.9, 0.95), 1e-8, 0.1, decay=6e-5)
-
-    adamw_leg_step(1)  # warmup
-    torch.cuda.synchronize()
-    with prof.kernel_timer() as at:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(a.adamw_steps):
-            adamw_leg_step(k + 2)
-        torch.cuda.synchronize()
-        ael = time.perf_counter() - t0
-    as_ = at.summary()["sf_adamw_step_multi"]
-    adamw_gbs = ADAMW_BYTES_PER_PARAM * n_params * a.adamw_steps / ael / 1e9
-    log(f"adamw: {ael * 1e3 / a.adamw_steps:.2f} ms/step of the arena, {adamw_gbs:.0f} GB/s; "
-        f"sf_adamw_step_multi {as_.rate / 1e9:.0f} GB/s over kernel time")
-    del arena, opt_state, items
-    torch.cuda.empty_cache()
-
-    # ---- block-sparse-16 leg (gate/up shape, block densities 0.5 and 0.25) ----
-    bsr = [bsr_leg(torch, dev, a.tokens, d, a.bsr_steps, 2) for d in (0.5, 0.25)] if a.bsr_steps > 0 else []
-    torch.cuda.empty_cache()
-
-    kl = kl_leg(torch, dev, a.kl_steps) if a.kl_steps > 0 else None
-    s24 = sparse24_leg(torch, dev, a.tokens, a.s24_steps) if a.s24_steps > 0 else None
-    e2e = e2e_leg(torch, dev, a.e2e_steps, a.e2e_warmup, a.e2e_micro, a.e2e_layers) if a.e2e_steps > 0 else None
-    torch.cuda.empty_cache()
-    sustained = mfma_sustained(torch, dev)
-    copy_gbs = copy_sustained(torch, dev)
-    torch.cuda.empty_cache()
-
     traffic = profiled_traffic()
-    out = {
-        "metric": "SparseLinear fwd+bwd TFLOP/s @7B shapes; 2:4 mask-update HBM GB/s",
+    return {
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -751,49 +838,120 @@ def main(argv=None) -> int:
                      "traffic": traffic.get("sf_gemm_bytes_per_launch"), "traffic_unit": "B/launch",
                      "traffic_source": TRAFFIC_SUMMARY,
                      "kernel": "sf_gemm (gemm_bf16_kernel)", "launches": g.launches,
-                     "mfma_sustained": round(sustained, 1), "frac_of_sustained": round(gemm_tflops / sustained, 4),
                      "avg_launch_ms": round(g.avg_ms, 4)},
+        "per_linear": per_linear,
+        "hutchinson_probe_layer": hvp,
         "kernels": other,
-        "mask_update": {
+    }
+
+
+def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
+    """The 7B-arena HBM legs: mask update (+ mask statistics), Hutchinson accumulator, AdamW."""
+    log(f"building mask arena ({a.mask_layers} layers x 7 linears)")
+    arena = build_arena(torch, dev, a.mask_layers)
+    n_params = sum(W.numel() for W, _, _ in arena)
+    traffic = profiled_traffic()
+    if "mask" in legs:
+        flips = torch.zeros(1, dtype=torch.int64, device=dev)
+        sample_idx = {}
+        for W, _, _ in arena:
+            key = tuple(W.shape)
+            if key not in sample_idx:
+                sample_idx[key] = K.sample_indices(262144, W.numel(), 1234 + len(sample_idx), dev)
+        mask_step(torch, L, K, arena, 0, flips, sample_idx)  # warmup
+        torch.cuda.synchronize()
+        log(f"mask arena: {n_params / 1e9:.3f} G params; timing {a.mask_steps} updates")
+        t0 = time.perf_counter()
+        for s in range(a.mask_steps):
+            mask_step(torch, L, K, arena, s, flips, sample_idx)
+        torch.cuda.synchronize()
+        mel = time.perf_counter() - t0
+        # per-kernel launch times from one more update with the layers one after another: overlapping
+        # kernels share the GPU and their individual durations would not describe either kernel
+        with prof.kernel_timer() as mt:
+            mask_step(torch, L, K, arena, a.mask_steps, flips, sample_idx, overlap=False)
+        ms_ = mt.summary()
+        mask_gbs = MASK_BYTES_PER_PARAM * n_params * a.mask_steps / mel / 1e9
+        up = ms_["sf_update_mask"]
+        up_gbs = up.rate / 1e9
+        st_gbs = ms_["sf_score_stats"].rate / 1e9
+        log(f"mask update: {mel * 1e3 / a.mask_steps:.2f} ms/update of the arena, {mask_gbs:.0f} GB/s; "
+            f"sf_update_mask {up_gbs:.0f} GB/s, sf_score_stats {st_gbs:.0f} GB/s")
+        # mask statistics / penalties of the whole model: one fused sf_mask_stats pass per soft mask (4 B/param)
+        srows = torch.empty((len(arena), L.MSTAT_COUNT), dtype=torch.float64, device=dev)
+        sws = K.mask_stats_workspace(dev)
+        for i, (_W, _H, M) in enumerate(arena):
+            K.mask_stats(M, srows[i], 0, 1e-8, sws)
+        torch.cuda.synchronize()
+        with prof.kernel_timer() as mst:
+            for i, (_W, _H, M) in enumerate(arena):
+                K.mask_stats(M, srows[i], 0, 1e-8, sws)
+            torch.cuda.synchronize()
+        msk = mst.summary()["sf_mask_stats"]
+        mstats_gbs = msk.rate / 1e9
+        log(f"mask statistics: sf_mask_stats {mstats_gbs:.0f} GB/s over {len(arena)} masks")
+        out["mask_update"] = {
             "value": round(mask_gbs, 2), "unit": "GB/s", "params": n_params, "updates": a.mask_steps,
             "ms_per_update": round(mel * 1e3 / a.mask_steps, 3), "bytes_per_param": MASK_BYTES_PER_PARAM,
             "roofline": {"bound": "hbm", "kernel": "sf_update_mask", "achieved": round(up_gbs, 2),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(up_gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic.get("sf_update_mask_bytes_per_launch"), "traffic_unit": "B/launch",
-                         "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4),
-                         "copy_sustained": round(copy_gbs, 1), "frac_of_copy": round(up_gbs / copy_gbs, 4)},
+                         "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4)},
             "score_stats_gbs": round(st_gbs, 2),
             "mask_stats": {"kernel": "sf_mask_stats", "GB/s": round(mstats_gbs, 2), "bytes_per_param": 4,
                            "frac": round(mstats_gbs / PEAK_HBM_GBS, 4), "launches": msk.launches,
                            "avg_launch_ms": round(msk.avg_ms, 4)},
             "kernels": {n: {"launches": s.launches, "avg_ms": round(s.avg_ms, 4), "total_ms": round(s.total_ms, 3)}
                         for n, s in ms_.items()},
-        },
-    }
+        }
+    if "hutch" in legs and a.hutch_steps > 0:
+        out["hutchinson"] = hutch_arena_leg(torch, arena, a.hutch_steps)
+    if "adamw" not in legs:
+        del arena
+        torch.cuda.empty_cache()
+        return
+    # ---- mask-aware AdamW leg (same arena: W is the bf16 copy, M the mask) ---
+    from sparseforge_amd.adamw import TensorStep, adamw_step_multi_
+
+    log("building AdamW state (f32 master, bf16 grad, f32 m / v)")
+    gen = torch.Generator(device=dev).manual_seed(2)
+    opt_state = []
+    arena = [(W, M) for W, _H, M in arena]  # the Hutchinson accumulator is not an AdamW operand: free it
+    for W, M in arena:
+        master = W.float()
+        grad = (torch.randn(W.shape, generator=gen, device=dev) * 1e-3).to(torch.bfloat16)
+        opt_state.append((master, grad, torch.zeros_like(master), torch.zeros_like(master), M, W))
+    torch.cuda.synchronize()
+    items = [TensorStep(master, grad, m, v, None, M, W) for master, grad, m, v, M, W in opt_state]
+
+    def adamw_leg_step(k):
+        # the whole arena in one sf_adamw_step_multi call (a launch per 40 tensors)
+        adamw_step_multi_(items, k, 1e-4, (0.9, 0.95), 1e-8, 0.1, decay=6e-5)
+
+    adamw_leg_step(1)  # warmup
+    torch.cuda.synchronize()
+    with prof.kernel_timer() as at:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(a.adamw_steps):
+            adamw_leg_step(k + 2)
+        torch.cuda.synchronize()
+        ael = time.perf_counter() - t0
+    as_ = at.summary()["sf_adamw_step_multi"]
+    adamw_gbs = ADAMW_BYTES_PER_PARAM * n_params * a.adamw_steps / ael / 1e9
+    log(f"adamw: {ael * 1e3 / a.adamw_steps:.2f} ms/step of the arena, {adamw_gbs:.0f} GB/s; "
+        f"sf_adamw_step_multi {as_.rate / 1e9:.0f} GB/s over kernel time")
     out["adamw"] = {
         "value": round(adamw_gbs, 2), "unit": "GB/s", "params": n_params, "steps": a.adamw_steps,
         "ms_per_step": round(ael * 1e3 / a.adamw_steps, 3), "bytes_per_param": ADAMW_BYTES_PER_PARAM,
-        "roofline": {"bound": "hbm", "kernel": "sf_adamw_step", "achieved": round(as_.rate / 1e9, 2),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(as_.rate / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": traffic.get("sf_adamw_step_bytes_per_launch"), "traffic_unit": "B/launch",
-                     "avg_launch_ms": round(as_.avg_ms, 4), "copy_sustained": round(copy_gbs, 1),
-                     "frac_of_copy": round(as_.rate / 1e9 / copy_gbs, 4)},
+        "roofline": {"bound": "hbm", "kernel": "sf_adamw_step_multi (adamw_multi_kernel)",
+                     "achieved": round(as_.rate / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(as_.rate / 1e9 / PEAK_HBM_GBS, 4),
+                     "traffic": traffic.get("sf_adamw_step_multi_bytes_per_launch"), "traffic_unit": "B/launch",
+                     "launches": as_.launches, "avg_launch_ms": round(as_.avg_ms, 4)},
     }
-    if bsr:
-        out["block_sparse"] = bsr
-    if kl:
-        out["distill_kl"] = kl
-    if s24:
-        out["sparse24_forward"] = s24
-    if e2e:
-        out["e2e_1p1b"] = e2e
-    if not a.no_cpu:
-        log("timing CPU baseline (numpy oracle)")
-        out["cpu_baseline"] = cpu_baseline()
-        out["mask_update"]["cpu_baseline"] = cpu_mask_baseline()
-        out["adamw"]["cpu_baseline"] = cpu_adamw_baseline()
-    print(json.dumps(out), flush=True)
-    return 0
+    del arena, opt_state, items
+    torch.cuda.empty_cache()
 
 
 if __name__ == "__main__":

@@ -28,12 +28,13 @@ def test_rademacher_matches_oracle(cuda_device):
         assert np.array_equal(vb, oh.rademacher(seed, n))
 
 
-def test_probe_dot_and_update_bit_exact(cuda_device):
+@pytest.mark.parametrize("n", [300_007, 300_008, 4096 * 1027])
+def test_probe_dot_and_update_bit_exact(cuda_device, n):
+    """n % 4 == 0 takes the vectorised update (one hash per 4 elements), the others the scalar one."""
     from oracle import hutchinson as oh
     from sparseforge_amd import utils
 
     rng = np.random.default_rng(8)
-    n = 300_007
     g = rng.standard_normal(n).astype(np.float32)
     hvp = rng.standard_normal(n).astype(np.float32)
     H = (rng.random(n) * 1e-3).astype(np.float32)
@@ -149,3 +150,22 @@ def test_hvp_with_slorb_and_mixed_mask(cuda_device, autocast, tol):
     for name, got, ref in zip(("W", "P", "S"), hvps, h64):
         err = float((got.double().cpu() - ref).abs().max() / ref.abs().max())
         assert err < tol, (name, err)
+
+
+@pytest.mark.parametrize("hdt,vdt", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16),
+                                     (torch.bfloat16, torch.float32)])
+def test_vector_update_equals_scalar_update(cuda_device, hdt, vdt):
+    """The vectorised update (probe regenerated, n % 4 == 0) equals the scalar one fed the materialised
+    probe, bit for bit, for bf16 accumulators and bf16 Hessian-vector products."""
+    from sparseforge_amd import utils
+
+    n = 4096 * 515
+    g = torch.Generator(device=cuda_device).manual_seed(4)
+    H = (torch.rand(n, generator=g, device=cuda_device) * 1e-3).to(hdt)
+    hvp = torch.randn(n, generator=g, device=cuda_device).to(vdt)
+    seed = 12345
+    a, b = H.clone(), H.clone()
+    utils.hutchinson_update_(a, hvp, 0.98, seed=seed)
+    v = utils.rademacher((n,), hvp.dtype, cuda_device, seed)
+    utils.hutchinson_update_(b, hvp, 0.98, v=v)
+    assert torch.equal(a, b)
