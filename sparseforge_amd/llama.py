@@ -19,8 +19,8 @@ projections and plain nn.Linear for the dense teacher:
   position * theta^(-2i/d)).
 * Attention: causal softmax attention written with differentiable torch ops
   in float32 (the Hessian-vector product differentiates it twice; float32
-  batched products also stay clear of bf16 batched products on transposed
-  operands).
+  batched products with contiguous operands also stay clear of bf16 batched
+  products on transposed operands).
 * forward(idx, targets) returns (logits, loss, None) like the reference's
   LlamaSparse.forward (legacy/model_llama.py:59-85): loss is the
   cross-entropy of the logits against already shifted targets,
@@ -83,19 +83,33 @@ def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tens
     return x * cos + swapped * sin
 
 
+_CAUSAL_BIAS: dict = {}
+
+
+def causal_bias(S: int, device) -> torch.Tensor:
+    """[1, S, S] float32: 0 on and below the diagonal, -inf above (cached per size and device)."""
+    key = (S, str(device))
+    if key not in _CAUSAL_BIAS:
+        _CAUSAL_BIAS[key] = torch.full((S, S), float("-inf"), device=device).triu_(1)[None]
+    return _CAUSAL_BIAS[key]
+
+
 def causal_attention(q, k, v, cos, sin) -> torch.Tensor:
-    """q, k, v [B, S, H, D] -> [B, S, H * D] in q's dtype; float32 arithmetic, causal mask."""
+    """q, k, v [B, S, H, D] -> [B, S, H * D] in q's dtype; float32 arithmetic, causal mask.
+
+    The 1/sqrt(D) scale goes into q and the causal mask into the product's bias
+    (one baddbmm writes the masked scores), so the [B H, S, S] scores make one
+    write, one softmax pass and one read."""
     B, S, H, D = q.shape
     # autocast would recast these float32 products to bf16: keep it off for the attention math
     with torch.autocast(q.device.type, enabled=False):
-        qf = _rotate(q.float().transpose(1, 2), cos, sin)                  # [B, H, S, D]
+        qf = _rotate(q.float().transpose(1, 2), cos, sin) * (1.0 / math.sqrt(D))   # [B, H, S, D]
         kf = _rotate(k.float().transpose(1, 2), cos, sin)
-        vf = v.float().transpose(1, 2).contiguous()
-        scores = torch.matmul(qf, kf.transpose(-2, -1).contiguous()) * (1.0 / math.sqrt(D))
-        future = torch.ones(S, S, dtype=torch.bool, device=q.device).triu_(1)
-        probs = torch.softmax(scores.masked_fill(future, float("-inf")), dim=-1)
-        out = torch.matmul(probs, vf)                                      # [B, H, S, D]
-    return out.transpose(1, 2).reshape(B, S, H * D).to(q.dtype)
+        vf = v.float().transpose(1, 2).reshape(B * H, S, D).contiguous()
+        kt = kf.transpose(-2, -1).reshape(B * H, D, S).contiguous()
+        scores = torch.baddbmm(causal_bias(S, q.device).to(qf.dtype), qf.reshape(B * H, S, D).contiguous(), kt)
+        out = torch.bmm(torch.softmax(scores, dim=-1), vf)                          # [B H, S, D]
+    return out.view(B, H, S, D).transpose(1, 2).reshape(B, S, H * D).to(q.dtype)
 
 
 class DecoderLayer(nn.Module):
