@@ -1503,6 +1503,182 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int elem
   }
 }
 
+// ---------------------------------------------------------------------------
+// Block-sparse-16 products on bf16 operands (the BSR layout of
+// convert_to_block_sparse plus its block map), DMA-staged like gemm_bf16_kernel.
+//
+// bsr_mm_kernel<DX>: C[T, n_out] = A[T, n_red] . B^T with B block-sparse.
+//   forward (DX = 0):    A = x [T, in],  C = y [T, out];   B = W: block (o, r) of
+//                        the tile is W block (row o, col r), read as stored.
+//   input grad (DX = 1): A = dy [T, out], C = dx [T, in]; B = W^T: block (o, r)
+//                        is W block (row r, col o), read transposed with
+//                        ds_read_b64_tr_b16.
+// A 256 x 256 tile (16 output blocks) over stages of 64 reduction values (4
+// reduction blocks).  A is staged whole (the K-contiguous swizzled DMA tile of
+// the dense kernel); of B only the present blocks are copied (an absent
+// block's lanes read past the resource: zeros, no memory traffic) into 64
+// slots of 512 B, slot o * 4 + r.  MFMAs are v_mfma_f32_32x32x16_bf16 with one
+// reduction block per MFMA: the 32 output columns of a wave fragment are two
+// adjacent output blocks, and the fragment's MFMAs run only when one of the two
+// is present (a wave-uniform branch on a ballot of the block map); the other
+// half then reads zeros.
+// ---------------------------------------------------------------------------
+template <int DX>
+__global__ void __launch_bounds__(kThreads, 1) bsr_mm_kernel(GemmArgs g) {
+  constexpr uint32_t ABUF = 32768u, BBUF = 32768u;
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* const As = smem;
+  unsigned char* const Bs = smem + 2 * ABUF;
+  const uint32_t As_l = lds_addr(As), Bs_l = lds_addr(Bs);
+  int64_t tm, tn;
+  tile_coords(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = tm * kTileM, n0 = tn * kTileN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t ob0 = n0 / 16;                 // first output block of the tile
+  const int64_t nk = ceil_div(g.K1, 64);       // reduction stages
+  const int64_t out_blocks = DX ? g.b_map_cols : g.b_map_rows;
+  const int64_t red_blocks = DX ? g.b_map_rows : g.b_map_cols;
+  const int64_t nblocks = g.b_map_rows * g.b_map_cols;  // upper bound of block indices (extent of the blocks array)
+
+  f32x16_t acc[kFragM * kFragN];
+#pragma unroll
+  for (int i = 0; i < kFragM * kFragN; ++i) acc[i] = f32x16_t{};
+
+  // block index of tile slot (o, r) at stage s, or -1
+  auto block_at = [&](int o, int r, int64_t s) -> int {
+    const int64_t ob = ob0 + o, rb = s * 4 + r;
+    if (ob >= out_blocks || rb >= red_blocks) return -1;
+    return DX ? g.b_map[rb * g.b_map_cols + ob] : g.b_map[ob * g.b_map_cols + rb];
+  };
+  // DMA of B: wave w copies slots [16 w, 16 w + 16), two per instruction (lanes 0-31, 32-63).
+  // The forward's blocks land with the 16-byte halves of rows 8..15 swapped, so that the
+  // 16-byte fragment reads of rows 0..15 at one half fall in distinct banks.
+  const int half = lane >> 5, part = lane & 31;
+  const uint32_t chunk_off = DX ? (uint32_t)part * 16
+                                : (uint32_t)((part >> 1) * 32 + (((part & 1) ^ ((part >> 4) & 1)) << 4));
+  const Rsrc rsb = make_rsrc(g.B1, nblocks * 512);
+  int nidx[8];
+  auto load_idx = [&](int64_t s) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int slot = 16 * wave + 2 * i + half;
+      nidx[i] = s < nk ? block_at(slot >> 2, slot & 3, s) : -1;
+    }
+  };
+  auto issue_b = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t voff = nidx[i] >= 0 ? (uint32_t)nidx[i] * 512u + chunk_off : kOob;
+      dma16(rsb, Bs_l + buf * BBUF + (uint32_t)(16 * wave + 2 * i) * 512u, voff, 0);
+    }
+  };
+  // presence of this wave's output blocks 8 wn .. 8 wn + 7 at the 4 reduction blocks of a stage:
+  // bit (o - 8 wn) * 4 + r of the ballot
+  int pidx;
+  auto load_pres = [&](int64_t s) { pidx = (s < nk && lane < 32) ? block_at(8 * wn + (lane >> 2), lane & 3, s) : -1; };
+
+  DmaLoader dak;
+  dak.init(g.A1, g.lda1, m0, g.M, g.K1);
+  using Tail = std::integral_constant<bool, true>;
+
+  // fragment offsets: A as the dense kernel's K-contiguous tile; B per wave fragment j (output
+  // blocks 8 wn + 2 j, + 1) at reduction block 0 (block r adds r * 512)
+  uint32_t aoff[4][kFragM], boff[kFragN];
+#pragma unroll
+  for (int i = 0; i < kFragM; ++i) {
+    const uint32_t base = frag_base<true>(wm * kWaveM + i * 32 + (lane & 31));
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) aoff[kk][i] = frag_at<true>(base, kk);
+  }
+#pragma unroll
+  for (int j = 0; j < kFragN; ++j) {
+    if constexpr (!DX) {
+      const int o = 8 * wn + 2 * j + ((lane & 31) >> 4), row = lane & 15;
+      boff[j] = (uint32_t)(o * 4 * 512 + row * 32 + ((half ^ (row >> 3)) << 4));
+    } else {
+      // ds_read_b64_tr_b16: lane 4q + c of a 16-lane group gets the c-th value of the 4-element rows
+      // addressed by lanes q, q + 4, q + 8, q + 12.  Group G covers output columns 16 (G & 1) .. + 16
+      // (block 8 wn + 2 j + (G & 1)) and reduction rows 8 (G >> 1) .. + 4 (the second read: + 4)
+      const int G = lane >> 4, L = lane & 15;
+      const int o = 8 * wn + 2 * j + (G & 1);
+      boff[j] = (uint32_t)(o * 4 * 512 + (8 * (G >> 1) + (L >> 2)) * 32 + (L & 3) * 8);
+    }
+  }
+  auto read_b = [&](int buf, int r, int j) -> bf16x8_t {
+    const unsigned char* p = Bs + buf * BBUF + boff[j] + r * 512;
+    if constexpr (!DX) {
+      return *reinterpret_cast<const bf16x8_t*>(p);
+    } else {
+      typedef __attribute__((address_space(3))) v4i16_t lds_v4;
+      const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(p));
+      const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(p + 128));
+      return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+
+  // Fragments are double-buffered over the 4 reduction blocks of a stage: the reads of block
+  // r + 1 are issued before the MFMAs of block r, and the reads of the next stage's block 0 right
+  // after the barrier that publishes it, before the MFMAs of block 3.  B fragments are read
+  // whether or not their blocks are present (an absent block reads zeros); only the MFMAs branch.
+  bf16x8_t fa[2][kFragM], fb[2][kFragN];
+  auto load_frags = [&](int slot, int buf, int r) {
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8_t*>(As + buf * ABUF + aoff[r][i]);
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j) fb[slot][j] = read_b(buf, r, j);
+  };
+  auto mfmas = [&](int slot, int r, uint32_t pm) {
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j) {
+      if ((pm >> (8 * j + r)) & 0x11u) {
+#pragma unroll
+        for (int i = 0; i < kFragM; ++i)
+          acc[i * kFragN + j] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], 0, 0, 0);
+      }
+    }
+  };
+
+  // prologue: stage 0 into buffer 0; block indices of stage 1
+  load_idx(0);
+  load_pres(0);
+  if (nk > 0) {
+    dak.issue<true>(As_l, 0);
+    issue_b(0);
+  }
+  int pres_cur = pidx;
+  load_idx(1);
+  load_pres(1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (nk > 0) load_frags(0, 0, 0);
+  for (int64_t s = 0; s < nk; ++s) {
+    const int cur = static_cast<int>(s & 1);
+    const uint32_t pmask = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)__ballot(pres_cur >= 0));
+    const int pres_next = pidx;
+    if (s + 1 < nk) {
+      dak.issue<true>(As_l + (cur ^ 1) * ABUF, (s + 1) * 64);
+      issue_b(cur ^ 1);
+      load_idx(s + 2);
+      load_pres(s + 2);
+    }
+    load_frags(1, cur, 1);
+    mfmas(0, 0, pmask);
+    load_frags(0, cur, 2);
+    mfmas(1, 1, pmask);
+    load_frags(1, cur, 3);
+    mfmas(0, 2, pmask);
+    // the next stage's copies (and index loads) landed; every wave's reads of this stage are in registers
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (s + 1 < nk) load_frags(0, cur ^ 1, 0);
+    mfmas(1, 3, pmask);
+    pres_cur = pres_next;
+  }
+  gemm_epilogue<uint16_t>(g, acc, smem, m0, n0, 0);
+}
+
 template <typename T>
 constexpr size_t smem_bytes() {
   return sizeof(T) * 2ull * (kTileM + kTileN) * Tr<T>::PITCH + 2 * 16 * (Tr<T>::BK / 16);
@@ -1560,9 +1736,34 @@ int launch_gemm(const GemmArgs& g, hipStream_t st) {
   return SF_OK;
 }
 
+// The bf16 block-sparse kernels (one 256 x 256 tile per workgroup, no split K).
+constexpr size_t smem_bytes_bsr() {
+  constexpr size_t ops = 4ull * 32768;
+  constexpr size_t epi = 4ull * 64 * kEpiPitch * sizeof(float);
+  return ops > epi ? ops : epi;
+}
+template <typename K>
+int launch_bsr_kernel(K kern, bool& attr, const GemmArgs& g, hipStream_t st, const char* what) {
+  const size_t smem = smem_bytes_bsr();
+  if (int rc = set_smem(kern, smem, attr)) return rc;
+  const int64_t tiles = g.tiles_m * g.tiles_n;
+  if (tiles == 0) return SF_OK;
+  SF_CHECK_ARG(tiles < (1ll << 31), "GEMM grid too large");
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), smem, st, g);
+  return launch_status(what);
+}
+
 template <typename T, int MASK>
 int dispatch_layouts(const sf_gemm_desc* d, const GemmArgs& g, hipStream_t st) {
   if constexpr (MASK == kMaskNone) {
+    if constexpr (sizeof(T) == 2) {
+      if (d->b_format == SF_BFMT_BSR16 && g.splits == 1) {
+        static bool attr_f = false, attr_t = false;
+        return d->b_layout == SF_LAYOUT_K
+                   ? launch_bsr_kernel(bsr_mm_kernel<0>, attr_f, g, st, "sf_gemm (block-sparse)")
+                   : launch_bsr_kernel(bsr_mm_kernel<1>, attr_t, g, st, "sf_gemm (block-sparse, transposed)");
+      }
+    }
     if (d->b_format == SF_BFMT_BSR16)
       return d->b_layout == SF_LAYOUT_K ? launch_gemm<T, 0, 2, MASK>(g, st) : launch_gemm<T, 0, 3, MASK>(g, st);
   }
@@ -1629,6 +1830,8 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
     SF_CHECK_ARG(!d->bmask && d->K2 == 0, "block-sparse B takes no effective mask and no second K segment");
     SF_CHECK_ARG(d->K1 % 16 == 0, "block-sparse B: K (%lld) must be a multiple of 16", (long long)d->K1);
     SF_CHECK_ARG(d->K1 == 0 || (d->B1 && al16(d->B1)), "block-sparse B: blocks must be 16-byte aligned");
+    SF_CHECK_ARG(d->b_map_rows * d->b_map_cols * 512 < (int64_t(1) << 31),
+                 "block-sparse B: block arrays of 2 GiB or more are not supported");
   }
   if (d->bmask_kmajor) {
     SF_CHECK_ARG(d->bmask && d->bmask_bytes && d->b_layout == SF_LAYOUT_MN && d->dtype == SF_DTYPE_BF16,

@@ -123,3 +123,34 @@ def test_distill_kl_full_logits(cuda_device):
     # the loss comes back in the logits' dtype (bf16 here), as the reference returns it
     want = float(torch.tensor(ref, dtype=torch.float32).to(loss.dtype))
     assert float(loss) == pytest.approx(want, rel=8e-3)  # within one bf16 ulp of the rounded float32 value
+
+
+@pytest.mark.parametrize("density", [0.5, 0.25])
+def test_block_sparse_full_shape(cuda_device, density):
+    """cfg4: the block-sparse-16 forward, input gradient and SDDMM weight gradient at W [11008, 4096],
+    x [8192, 4096] (bf16), against torch float32 products of the dense masked weight; each bf16 result
+    within rounding of the float32 product, elementwise."""
+    from sparseforge_amd import block_sparse as bs
+
+    print(f"[fullsize] block-sparse d={density}", flush=True)
+    out_f, in_f, T = 11008, 4096, 8192
+    bm = torch.rand(out_f // 16, in_f // 16, generator=torch.Generator().manual_seed(1)) < density
+    g = torch.Generator(device=cuda_device).manual_seed(3)
+    W = (torch.randn(out_f, in_f, generator=g, device=cuda_device) * 0.02).to(torch.bfloat16)
+    M = bm.to(cuda_device).repeat_interleave(16, 0).repeat_interleave(16, 1).to(torch.bfloat16)
+    x = torch.randn(T, in_f, generator=g, device=cuda_device).to(torch.bfloat16)
+    gy = torch.randn(T, out_f, generator=g, device=cuda_device).to(torch.bfloat16)
+    blocks, rp, ci, bmap = bs.convert_to_block_sparse(W, M, return_block_map=True)
+    nnz = ci.numel()
+    y = bs._bsr_gemm(x, blocks, bmap, out_f, False, torch.bfloat16)
+    dx = bs._bsr_gemm(gy, blocks, bmap, in_f, True, torch.bfloat16)
+    dwb = bs.bsr_sddmm(gy, x, bmap, nnz, torch.bfloat16)
+    Wm = (W * M).float()
+    xf, gyf = x.float(), gy.float()
+    assert within_bf16_rounding(y, xf @ Wm.t()) <= 1.0
+    assert within_bf16_rounding(dx, gyf @ Wm) <= 1.0
+    dW = gyf.t() @ xf
+    # the kept blocks of dW in CSR order (row-major over block rows, ascending columns)
+    rows = torch.repeat_interleave(torch.arange(out_f // 16, device=cuda_device), (rp[1:] - rp[:-1]).long())
+    ref_blocks = dW.view(out_f // 16, 16, in_f // 16, 16).permute(0, 2, 1, 3)[rows, ci.long()]
+    assert within_bf16_rounding(dwb[:nnz], ref_blocks) <= 1.0
