@@ -18,8 +18,10 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
   the 7B model (32 layers x 7 linears, 6.48 G params; bf16 W, fp32
   Hutchinson accumulator and soft mask): score statistics, tau quantile over
   a 262 144-element sample, then the fused gate + EMA + flip-count pass, at a
-  temperature taken from a 1.0 -> 0.01 geometric schedule over 10 steps.
-  GB/s counts 20 B per parameter (stats pass: W 2 + H 4; update pass: W 2 +
+  temperature taken from a 1.0 -> 0.01 geometric schedule over 10 steps;
+  the 224 layers share their parameters, so the update is batched as
+  calculate_model_mask batches it (sf_update_mask_multi, 28 layers per
+  launch).  GB/s counts 20 B per parameter (stats pass: W 2 + H 4; update pass: W 2 +
   H 4 + mask read 4 + mask write 4).
 * ``hutchinson`` -- the accumulator update of every linear of the 7B arena
   (f32 accumulator read and written, bf16 Hessian-vector product, probe
@@ -179,24 +181,25 @@ def mask_params(L, rows, cols, temperature):
     return p
 
 
-def mask_step(torch, L, K, arena, step: int, flips, sample_idx, overlap: bool = True):
-    """One mask update of every linear of the arena.  overlap: the layers' chains run on side
-    streams (the LayerPipeline that calculate_model_mask uses); otherwise one after another on the
-    current stream (used to time each kernel alone)."""
-    import contextlib
+def mask_jobs(torch, K, arena, sample_idx):
+    """The arena's layers as batched-update jobs (per-layer stats / tau / flip outputs)."""
+    dev = arena[0][0].device
+    n = len(arena)
+    stats = torch.empty((n, 2), dtype=torch.float32, device=dev)
+    tau = torch.empty(n, dtype=torch.float32, device=dev)
+    flips = torch.zeros(n, dtype=torch.int64, device=dev)
+    jobs = [K.MaskJob(K.MaskOperands(weight=W, mask=M, hessian=H), sample_idx[tuple(W.shape)], stats[i],
+                      tau[i:i + 1], flips[i:i + 1]) for i, (W, H, M) in enumerate(arena)]
+    return jobs, K.multi_workspace(jobs, dev)
 
+
+def mask_step(L, K, jobs, ws, step: int, stages=None):
+    """One mask update of every linear of the arena: what calculate_model_mask does for layers that share
+    their parameters, sf_update_mask_multi over the whole arena (stats, tau select and fused update of
+    28 layers per launch).  stages: run only these stages (SF_MULTI_*), to time each alone."""
     temperature = 1.0 * (0.01 ** (min(step, 9) / 9.0))
-    pipe = K.LayerPipeline(arena[0][0].device) if overlap else None
-    for W, H, M in arena:
-        rows, cols = W.shape
-        p = mask_params(L, rows, cols, temperature)
-        ops = K.MaskOperands(weight=W, mask=M, hessian=H)
-        with pipe.next() if pipe else contextlib.nullcontext():
-            stats = K.score_stats(p, ops)
-            tau = K.tau_quantile(p, ops, stats, 0.5, sample_idx[(rows, cols)])
-            K.update_mask(p, ops, stats, tau, flips)
-    if pipe:
-        pipe.join()
+    p = mask_params(L, 0, 0, temperature)
+    K.update_mask_multi(p, 0.5, jobs, L.MULTI_ALL if stages is None else stages, ws)
 
 
 # ---------------------------------------------------------------------------
@@ -852,31 +855,33 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
     n_params = sum(W.numel() for W, _, _ in arena)
     traffic = profiled_traffic()
     if "mask" in legs:
-        flips = torch.zeros(1, dtype=torch.int64, device=dev)
         sample_idx = {}
         for W, _, _ in arena:
             key = tuple(W.shape)
             if key not in sample_idx:
                 sample_idx[key] = K.sample_indices(262144, W.numel(), 1234 + len(sample_idx), dev)
-        mask_step(torch, L, K, arena, 0, flips, sample_idx)  # warmup
+        jobs, mws = mask_jobs(torch, K, arena, sample_idx)
+        mask_step(L, K, jobs, mws, 0)  # warmup
         torch.cuda.synchronize()
         log(f"mask arena: {n_params / 1e9:.3f} G params; timing {a.mask_steps} updates")
         t0 = time.perf_counter()
         for s in range(a.mask_steps):
-            mask_step(torch, L, K, arena, s, flips, sample_idx)
+            mask_step(L, K, jobs, mws, s)
         torch.cuda.synchronize()
         mel = time.perf_counter() - t0
-        # per-kernel launch times from one more update with the layers one after another: overlapping
-        # kernels share the GPU and their individual durations would not describe either kernel
-        with prof.kernel_timer() as mt:
-            mask_step(torch, L, K, arena, a.mask_steps, flips, sample_idx, overlap=False)
-        ms_ = mt.summary()
+        # each stage alone over the arena (HIP events around each batched call): the statistics pass
+        # (6 B/param), the tau selection, the fused update (14 B/param)
+        stage_ms = {}
+        for name, stg in (("stats", L.MULTI_STATS), ("tau", L.MULTI_TAU), ("update", L.MULTI_UPDATE)):
+            with prof.kernel_timer() as mt:
+                mask_step(L, K, jobs, mws, a.mask_steps, stg)
+            stage_ms[name] = mt.summary()["sf_update_mask_multi"]
         mask_gbs = MASK_BYTES_PER_PARAM * n_params * a.mask_steps / mel / 1e9
-        up = ms_["sf_update_mask"]
+        up = stage_ms["update"]
         up_gbs = up.rate / 1e9
-        st_gbs = ms_["sf_score_stats"].rate / 1e9
+        st_gbs = stage_ms["stats"].rate / 1e9
         log(f"mask update: {mel * 1e3 / a.mask_steps:.2f} ms/update of the arena, {mask_gbs:.0f} GB/s; "
-            f"sf_update_mask {up_gbs:.0f} GB/s, sf_score_stats {st_gbs:.0f} GB/s")
+            f"update stage {up_gbs:.0f} GB/s, stats stage {st_gbs:.0f} GB/s, tau {stage_ms['tau'].total_ms:.2f} ms")
         # mask statistics / penalties of the whole model: one fused sf_mask_stats pass per soft mask (4 B/param)
         srows = torch.empty((len(arena), L.MSTAT_COUNT), dtype=torch.float64, device=dev)
         sws = K.mask_stats_workspace(dev)
@@ -893,16 +898,17 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
         out["mask_update"] = {
             "value": round(mask_gbs, 2), "unit": "GB/s", "params": n_params, "updates": a.mask_steps,
             "ms_per_update": round(mel * 1e3 / a.mask_steps, 3), "bytes_per_param": MASK_BYTES_PER_PARAM,
-            "roofline": {"bound": "hbm", "kernel": "sf_update_mask", "achieved": round(up_gbs, 2),
-                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(up_gbs / PEAK_HBM_GBS, 4),
+            "roofline": {"bound": "hbm", "kernel": "sf_update_mask_multi (update stage, update_mask_multi_kernel)",
+                         "achieved": round(up_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(up_gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic.get("sf_update_mask_bytes_per_launch"), "traffic_unit": "B/launch",
                          "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4)},
+            "arena_frac": round(mask_gbs / PEAK_HBM_GBS, 4),
             "score_stats_gbs": round(st_gbs, 2),
+            "stage_ms": {k: round(v.total_ms, 3) for k, v in stage_ms.items()},
             "mask_stats": {"kernel": "sf_mask_stats", "GB/s": round(mstats_gbs, 2), "bytes_per_param": 4,
                            "frac": round(mstats_gbs / PEAK_HBM_GBS, 4), "launches": msk.launches,
                            "avg_launch_ms": round(msk.avg_ms, 4)},
-            "kernels": {n: {"launches": s.launches, "avg_ms": round(s.avg_ms, 4), "total_ms": round(s.total_ms, 3)}
-                        for n, s in ms_.items()},
         }
     if "hutch" in legs and a.hutch_steps > 0:
         out["hutchinson"] = hutch_arena_leg(torch, arena, a.hutch_steps)

@@ -187,6 +187,50 @@ int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtype, const vo
                    void* stream);
 
 /*
+ * One layer of sf_update_mask_multi: its operands (as sf_update_mask takes
+ * them) and its outputs.
+ */
+typedef struct sf_mask_layer {
+  int64_t rows, cols;
+  const void* W;
+  const void* H;              /* hessian_diag, or NULL */
+  const void* aux;            /* scaler_row / grad_ema, or NULL */
+  void* mask;
+  void* frozen;               /* frozen flags (when p->has_frozen), or NULL */
+  const int64_t* sample_idx;  /* tau sample indices, or NULL for every element */
+  int64_t sample_size;        /* tau sample size (rows * cols when sample_idx is NULL) */
+  float* stats;               /* out: device float[2] {mu, sigma} */
+  float* tau;                 /* out: device float[1] (unstructured gate), else may be NULL */
+  int64_t* flips;             /* device int64[1], incremented, or NULL */
+} sf_mask_layer;
+
+/*
+ * Workspace bytes of sf_update_mask_multi over these layers.
+ */
+size_t sf_update_mask_multi_workspace_size(const sf_mask_layer* layers, int count);
+
+/*
+ * The mask update of every SparseLinear of a model in a handful of launches:
+ * calculate_model_mask (legacy/utils.py:184-310) calls update_mask
+ * (legacy/sparse_modeling.py:1242-1666) layer after layer, and each call here
+ * would be sf_score_stats + sf_tau_quantile(q) (unstructured gate) +
+ * sf_update_mask.  For layers whose parameters are equal but for their shape
+ * (p->rows / p->cols are ignored: each layer brings its own), this runs all
+ * three stages of up to 28 layers per launch, and every output (stats, tau,
+ * mask, frozen flags, flip counts) equals that of the three single-layer
+ * calls bit for bit.  Empty layers are skipped.  `stages` (SF_MULTI_*) picks
+ * the stages to run: a stage run alone reads what earlier calls wrote to the
+ * layers' stats / tau.
+ */
+#define SF_MULTI_STATS 1  /* sf_score_stats: layers' stats */
+#define SF_MULTI_TAU 2    /* sf_tau_quantile (unstructured gate only): layers' tau */
+#define SF_MULTI_UPDATE 4 /* sf_update_mask: masks, frozen flags, flips */
+#define SF_MULTI_ALL 7
+int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_mask_layer* layers, int count,
+                         int stages, int w_dtype, int h_dtype, int aux_dtype, int mask_dtype,
+                         int frozen_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Count of positions whose hard projection differs between two soft masks
  * (legacy/sparse_modeling.py:1659-1661).  flips: device int64[1], incremented.
  */

@@ -55,6 +55,10 @@ PENALTY_TARGET = 4
 BLOCK_MEAN = 0
 BLOCK_RMS = 1
 
+# stages of sf_update_mask_multi
+MULTI_STATS, MULTI_TAU, MULTI_UPDATE = 1, 2, 4
+MULTI_ALL = 7
+
 # sums of sf_mask_stats (one row of MSTAT_COUNT doubles per mask)
 MSTAT_SUM, MSTAT_SUM2, MSTAT_ENTROPY = 0, 1, 2
 MSTAT_LT05, MSTAT_LT01, MSTAT_LT001, MSTAT_GT90, MSTAT_GT99, MSTAT_GT05 = 3, 4, 5, 6, 7, 8
@@ -170,6 +174,25 @@ class AdamwTensor(ctypes.Structure):
     ]
 
 
+class MaskLayer(ctypes.Structure):
+    """Mirror of ``sf_mask_layer`` (one layer of sf_update_mask_multi)."""
+
+    _fields_ = [
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("W", ctypes.c_void_p),
+        ("H", ctypes.c_void_p),
+        ("aux", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("frozen", ctypes.c_void_p),
+        ("sample_idx", ctypes.c_void_p),
+        ("sample_size", ctypes.c_int64),
+        ("stats", ctypes.c_void_p),
+        ("tau", ctypes.c_void_p),
+        ("flips", ctypes.c_void_p),
+    ]
+
+
 class AdamwParams(ctypes.Structure):
     """Mirror of ``sf_adamw_params``."""
 
@@ -208,6 +231,8 @@ SIGNATURES = {
     "sf_sample_indices": (_I, [_P, _I64, _I64, ctypes.c_uint64, _P]),
     "sf_gate_target": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P]),
     "sf_update_mask": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _P]),
+    "sf_update_mask_multi_workspace_size": (_SZ, [ctypes.POINTER(MaskLayer), _I]),
+    "sf_update_mask_multi": (_I, [_MP, _F, ctypes.POINTER(MaskLayer), _I, _I, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "sf_hard_flip_count": (_I, [_P, _P, _I, _I64, _I64, _I, _I, _I, _P, _P]),
     "sf_joint_scores": (_I, [_MP, _P, _P, _P, _MP, _P, _P, _P, _I, _I, _I, _P, _I, _P]),
     "sf_glu_update_masks": (_I, [_MP, _P, _I, _P, _P, _I, _P, _I, _P, _P, _I, _I, _P, _P, _P]),

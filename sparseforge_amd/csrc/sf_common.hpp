@@ -228,9 +228,13 @@ struct GroupWalk {
   int64_t sdiv, smod;      // stride = sdiv * gpr + smod
   int64_t estep, ewrap;    // element step per stride, correction when gc wraps
   __device__ __forceinline__ GroupWalk(int64_t groups_, int64_t cols_, int64_t gpr_)
+      : GroupWalk(groups_, cols_, gpr_, blockIdx.x, gridDim.x) {}
+  // The walk of workgroup `block` of a grid of `nblocks` (a multi-layer kernel
+  // runs each layer's grid as a range of its own workgroups).
+  __device__ __forceinline__ GroupWalk(int64_t groups_, int64_t cols_, int64_t gpr_, int64_t block, int64_t nblocks)
       : groups(groups_), gpr(gpr_), cols(cols_) {
-    gi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    stride = (int64_t)gridDim.x * blockDim.x;
+    gi = block * (int64_t)blockDim.x + threadIdx.x;
+    stride = nblocks * (int64_t)blockDim.x;
     row = gi / gpr;
     gc = gi - row * gpr;
     elem = row * cols + gc * 4;

@@ -344,14 +344,15 @@ __device__ __forceinline__ void block_sum2_f64(double a, double b, double* out_a
   }
 }
 
-// VEC: every group full and vector-loadable (as in update_mask_kernel).
+// Partial sums of workgroup `blk` of the kStatsGrid-workgroup grid over one
+// layer.  VEC: every group full and vector-loadable (as in update_mask_kernel).
 template <int WD, int HD, bool VEC>
-__global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, const void* __restrict__ W,
-                                                               const void* __restrict__ H, const void* __restrict__ aux,
-                                                               int64_t cols, int64_t groups, int64_t gpr, bool vec,
-                                                               double* partial) {
+__device__ __forceinline__ void stats_partial_block(const ScoreSpec& s, const void* __restrict__ W,
+                                                    const void* __restrict__ H, const void* __restrict__ aux,
+                                                    int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                    double* partial, int blk) {
   double sum = 0.0, sq = 0.0;
-  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+  for (GroupWalk w(groups, cols, gpr, blk, kStatsGrid); w.live(); w.next()) {
     Group g = w.group();
     if constexpr (VEC) {
       g.n = 4;
@@ -367,11 +368,20 @@ __global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, cons
         sq += d * d;
       }
   }
-  block_sum2_f64(sum, sq, &partial[2 * blockIdx.x], &partial[2 * blockIdx.x + 1]);
+  block_sum2_f64(sum, sq, &partial[2 * blk], &partial[2 * blk + 1]);
 }
 
-__global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __restrict__ partial, int nparts,
-                                                             int64_t n, float* stats) {
+template <int WD, int HD, bool VEC>
+__global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, const void* __restrict__ W,
+                                                               const void* __restrict__ H, const void* __restrict__ aux,
+                                                               int64_t cols, int64_t groups, int64_t gpr, bool vec,
+                                                               double* partial) {
+  stats_partial_block<WD, HD, VEC>(s, W, H, aux, cols, groups, gpr, vec, partial, blockIdx.x);
+}
+
+// Fold of one layer's kStatsGrid partials by one workgroup, in a fixed order.
+__device__ __forceinline__ void stats_final_block(const double* __restrict__ partial, int nparts, int64_t n,
+                                                  float* stats) {
   // 8 partials per thread and round, their loads issued together: the partials
   // were just written by workgroups on every XCD, so each round costs a memory
   // latency, and a one-at-a-time loop paid it 16 times
@@ -416,6 +426,11 @@ __global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __res
   }
 }
 
+__global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __restrict__ partial, int nparts,
+                                                             int64_t n, float* stats) {
+  stats_final_block(partial, nparts, n, stats);
+}
+
 // ---------------------------------------------------------------------------
 // tau quantile: z at the sample indices as order-preserving uint32 keys
 // (a wide gather kernel: the reads are random), then one 1024-thread
@@ -426,18 +441,26 @@ __global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __res
 // per-wave copies keep atomic contention low), reading keys 16 bytes at a
 // time; pass 0 also flags NaN (torch.quantile then takes the last rank).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void tau_gather_block(const ScoreSpec& s, const void* __restrict__ W,
+                                                 const void* __restrict__ H, const void* __restrict__ aux,
+                                                 int64_t rows, int64_t cols, const float* __restrict__ stats,
+                                                 const int64_t* __restrict__ idx, int64_t m,
+                                                 uint32_t* __restrict__ keys, int64_t blk, int64_t nblk) {
+  const float mu = stats[0], sigma = stats[1];
+  const int64_t n = cols * rows;
+  for (int64_t i = blk * (int64_t)blockDim.x + threadIdx.x; i < m; i += nblk * blockDim.x) {
+    int64_t e = idx ? idx[i] : i;
+    e = e < 0 ? 0 : (e >= n ? n - 1 : e);  // indices outside the layer are clamped, never dereferenced
+    keys[i] = ordered_key(znorm(score_at(s, W, H, aux, e, cols), mu, sigma, s.score_dtype));
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) tau_gather_kernel(ScoreSpec s, const void* __restrict__ W,
                                                             const void* __restrict__ H, const void* __restrict__ aux,
                                                             int64_t rows, int64_t cols, const float* __restrict__ stats,
                                                             const int64_t* __restrict__ idx, int64_t m,
                                                             uint32_t* __restrict__ keys) {
-  const float mu = stats[0], sigma = stats[1];
-  const int64_t n = cols * rows;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < m; i += (int64_t)gridDim.x * blockDim.x) {
-    int64_t e = idx ? idx[i] : i;
-    e = e < 0 ? 0 : (e >= n ? n - 1 : e);  // indices outside the layer are clamped, never dereferenced
-    keys[i] = ordered_key(znorm(score_at(s, W, H, aux, e, cols), mu, sigma, s.score_dtype));
-  }
+  tau_gather_block(s, W, H, aux, rows, cols, stats, idx, m, keys, blockIdx.x, gridDim.x);
 }
 
 __device__ __forceinline__ float key_to_float(uint32_t k) {
@@ -533,11 +556,11 @@ __device__ void advance_state(SelState& st, const uint32_t* __restrict__ partial
 // waits for another), then histograms the current digit of the keys that
 // match each statistic's prefix into per-wave LDS histograms and publishes
 // the sum.  Workgroup 0 publishes the state the next pass starts from.
-__global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __restrict__ keys, int64_t m, int pass, float q,
-                                                          const SelState* __restrict__ state_in,
-                                                          SelState* __restrict__ state_out,
-                                                          const uint32_t* __restrict__ partial_in,
-                                                          uint32_t* __restrict__ partial_out) {
+// Workgroup `blk` of the pass over a grid of `nblk` workgroups.
+__device__ __forceinline__ void tau_pass_block(const uint32_t* __restrict__ keys, int64_t m, int pass, float q,
+                                               const SelState* __restrict__ state_in, SelState* __restrict__ state_out,
+                                               const uint32_t* __restrict__ partial_in,
+                                               uint32_t* __restrict__ partial_out, int blk, int nblk) {
   constexpr int kWaves = kBlock / 64;
   __shared__ uint32_t hist[kWaves][2][256];
   __shared__ SelState st;
@@ -546,8 +569,8 @@ __global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __rest
   if (pass >= 2 && t == 0) st = *state_in;
   if (t == 0) nan = 0;
   __syncthreads();
-  if (pass >= 1) advance_state(st, partial_in, gridDim.x, pass - 1, m, q);
-  if (pass >= 1 && blockIdx.x == 0 && t == 0) *state_out = st;
+  if (pass >= 1) advance_state(st, partial_in, nblk, pass - 1, m, q);
+  if (pass >= 1 && blk == 0 && t == 0) *state_out = st;
   for (int i = t; i < kWaves * 2 * 256; i += kBlock) (&hist[0][0][0])[i] = 0u;
   __syncthreads();
   const int wv = t >> 6;
@@ -564,8 +587,8 @@ __global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __rest
   // 8 keys per thread and round, loaded before any is counted (one memory
   // latency per round rather than per key)
   constexpr int kU = 8;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = blockIdx.x * (int64_t)blockDim.x + t;
+  const int64_t stride = (int64_t)nblk * blockDim.x;
+  int64_t i = blk * (int64_t)blockDim.x + t;
   for (; i + (kU - 1) * stride < m; i += kU * stride) {
     uint32_t k8[kU];
 #pragma unroll
@@ -576,7 +599,7 @@ __global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __rest
   for (; i < m; i += stride) count(keys[i]);
   if (local_nan) atomicOr(&nan, 1);
   __syncthreads();
-  uint32_t* out = partial_out + (int64_t)blockIdx.x * kSelStride;
+  uint32_t* out = partial_out + (int64_t)blk * kSelStride;
   for (int i = t; i < 2 * 256; i += kBlock) {
     uint32_t c = 0;
 #pragma unroll
@@ -586,12 +609,18 @@ __global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __rest
   if (t == 0) out[2 * 256] = nan;
 }
 
+__global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __restrict__ keys, int64_t m, int pass, float q,
+                                                          const SelState* __restrict__ state_in,
+                                                          SelState* __restrict__ state_out,
+                                                          const uint32_t* __restrict__ partial_in,
+                                                          uint32_t* __restrict__ partial_out) {
+  tau_pass_block(keys, m, pass, q, state_in, state_out, partial_in, partial_out, blockIdx.x, gridDim.x);
+}
+
 // After pass 3: fix its digit and lerp the two order statistics (torch.lerp:
 // small weight -> a + w (b - a), else b - (b - a)(1 - w), each op rounded).
-__global__ void __launch_bounds__(kBlock) tau_final_kernel(int64_t m, float q, int nparts,
-                                                           const SelState* __restrict__ state_in,
-                                                           const uint32_t* __restrict__ partial_in,
-                                                           float* __restrict__ tau) {
+__device__ __forceinline__ void tau_final_block(int64_t m, float q, int nparts, const SelState* __restrict__ state_in,
+                                                const uint32_t* __restrict__ partial_in, float* __restrict__ tau) {
   __shared__ SelState st;
   if (threadIdx.x == 0) st = *state_in;
   __syncthreads();
@@ -602,6 +631,13 @@ __global__ void __launch_bounds__(kBlock) tau_final_kernel(int64_t m, float q, i
     const float dlt = __fsub_rn(hi, lo);
     *tau = fabsf(w) < 0.5f ? __fadd_rn(lo, __fmul_rn(w, dlt)) : __fsub_rn(hi, __fmul_rn(dlt, __fsub_rn(1.0f, w)));
   }
+}
+
+__global__ void __launch_bounds__(kBlock) tau_final_kernel(int64_t m, float q, int nparts,
+                                                           const SelState* __restrict__ state_in,
+                                                           const uint32_t* __restrict__ partial_in,
+                                                           float* __restrict__ tau) {
+  tau_final_block(m, q, nparts, state_in, partial_in, tau);
 }
 
 __global__ void __launch_bounds__(kBlock) sample_indices_kernel(int64_t* idx, int64_t m, uint64_t n, uint64_t seed) {
@@ -807,18 +843,19 @@ __device__ __forceinline__ int flips_of(const float a[4], const float b[4], cons
 
 // VEC: cols % 4 == 0 and every operand 16-byte aligned, so every group is a
 // full, vector-loadable group of 4 (known at compile time: no tail branches).
+// Workgroup `blk` of a grid of `nblk` over one layer.
 template <int WD, int HD, int MD, int SD, bool VEC>
-__global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, const void* __restrict__ W,
-                                                             const void* __restrict__ H, const void* __restrict__ aux,
-                                                             void* __restrict__ mask, void* __restrict__ frozen,
-                                                             const float* __restrict__ stats,
-                                                             const float* __restrict__ tau_p, int64_t cols,
-                                                             int64_t groups, int64_t gpr, bool vec, int64_t* flips) {
+__device__ __forceinline__ void update_mask_block(const UpdateSpec& us, const void* __restrict__ W,
+                                                  const void* __restrict__ H, const void* __restrict__ aux,
+                                                  void* __restrict__ mask, void* __restrict__ frozen,
+                                                  const float* __restrict__ stats, const float* __restrict__ tau_p,
+                                                  int64_t cols, int64_t groups, int64_t gpr, bool vec, int64_t* flips,
+                                                  int64_t blk, int64_t nblk) {
   const GateSpec& gs = us.gs;
   const float mu = stats[0], sigma = stats[1], rsigma = 1.0f / sigma;
   const float tau = tau_p ? *tau_p : 0.0f;
   int64_t cnt = 0;
-  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+  for (GroupWalk w(groups, cols, gpr, blk, nblk); w.live(); w.next()) {
     Group g = w.group();
     if constexpr (VEC) {
       g.n = 4;
@@ -838,6 +875,115 @@ __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, cons
     if (flips) cnt += flips_of(mp, mn, g, us.hard_kind, us.hard_n);
   }
   if (flips) block_add_i64(cnt, flips);
+}
+
+template <int WD, int HD, int MD, int SD, bool VEC>
+__global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, const void* __restrict__ W,
+                                                             const void* __restrict__ H, const void* __restrict__ aux,
+                                                             void* __restrict__ mask, void* __restrict__ frozen,
+                                                             const float* __restrict__ stats,
+                                                             const float* __restrict__ tau_p, int64_t cols,
+                                                             int64_t groups, int64_t gpr, bool vec, int64_t* flips) {
+  update_mask_block<WD, HD, MD, SD, VEC>(us, W, H, aux, mask, frozen, stats, tau_p, cols, groups, gpr, vec, flips,
+                                         blockIdx.x, gridDim.x);
+}
+
+// ---------------------------------------------------------------------------
+// Multi-layer mask update: the score statistics, tau selection and fused
+// update of up to kMultiLayers layers that share every parameter but their
+// shape, as a handful of launches.  Each layer runs exactly the workgroup
+// grid its single-layer launch would (the statistics' kStatsGrid partials
+// fold in the same order, the update walks the same groups), laid end to end
+// in one grid, so every output equals the single-layer entry points' bit for
+// bit.  The layer table travels in the kernel arguments.
+// ---------------------------------------------------------------------------
+constexpr int kMultiLayers = 28;
+
+struct MultiLayer {
+  const void* W;
+  const void* H;
+  const void* aux;
+  void* mask;
+  void* frozen;
+  float* stats;
+  float* tau;
+  int64_t* flips;
+  const int64_t* idx;  // tau sample indices (null: every element)
+  int64_t rows, cols;
+  int64_t m;           // tau sample size
+  int64_t keys_off;    // first key of the layer's sample in the keys buffer
+  int32_t nblk;        // workgroups of the layer's update grid
+  int32_t vec;         // vector-loadable groups
+  int32_t nsel;        // workgroups of the layer's radix passes
+  int32_t pad;
+};
+
+struct MultiArgs {
+  UpdateSpec us;
+  int32_t count;
+  int32_t first[kMultiLayers + 1];  // update grid: layer l owns workgroups [first[l], first[l + 1])
+  MultiLayer l[kMultiLayers];
+};
+static_assert(sizeof(MultiArgs) <= 4000, "multi-layer table exceeds the kernel argument budget");
+
+// Layer of workgroup b of the update grid (first[0] == 0, first[count] == grid).
+__device__ __forceinline__ int multi_layer_of(const MultiArgs& a, int b) {
+  int l = 0;
+#pragma unroll
+  for (int i = 1; i < kMultiLayers; ++i) l += (i < a.count && a.first[i] <= b) ? 1 : 0;
+  return l;
+}
+
+// Statistics partials: kStatsGrid workgroups per layer, layer = blockIdx.x / kStatsGrid.
+template <int WD, int HD, bool VEC>
+__global__ void __launch_bounds__(kBlock) stats_partial_multi_kernel(MultiArgs a, double* partial) {
+  const int l = blockIdx.x / kStatsGrid, blk = blockIdx.x - l * kStatsGrid;
+  const MultiLayer& L = a.l[l];
+  const int64_t gpr = ceil_div(L.cols, 4);
+  stats_partial_block<WD, HD, VEC>(a.us.gs.s, L.W, L.H, L.aux, L.cols, L.rows * gpr, gpr, L.vec != 0,
+                                   partial + (int64_t)l * 2 * kStatsGrid, blk);
+}
+
+__global__ void __launch_bounds__(kBlock) stats_final_multi_kernel(MultiArgs a, const double* partial) {
+  const int l = blockIdx.x;
+  stats_final_block(partial + (int64_t)l * 2 * kStatsGrid, kStatsGrid, a.l[l].rows * a.l[l].cols, a.l[l].stats);
+}
+
+// tau: grid (x, layer); each layer's gather strides over gridDim.x workgroups,
+// its radix passes use its own nsel of them.
+__global__ void __launch_bounds__(kBlock) tau_gather_multi_kernel(MultiArgs a, uint32_t* keys) {
+  const MultiLayer& L = a.l[blockIdx.y];
+  tau_gather_block(a.us.gs.s, L.W, L.H, L.aux, L.rows, L.cols, L.stats, L.idx, L.m, keys + L.keys_off, blockIdx.x,
+                   gridDim.x);
+}
+
+__global__ void __launch_bounds__(kBlock) tau_pass_multi_kernel(MultiArgs a, const uint32_t* keys, int pass, float q,
+                                                                SelState* states, uint32_t* parts0, uint32_t* parts1) {
+  const int l = blockIdx.y;
+  const MultiLayer& L = a.l[l];
+  if ((int)blockIdx.x >= L.nsel) return;  // the whole workgroup: no barrier is skipped
+  // pass p reads state p-2 (slot p & 1) and partials p-1, writes state p-1 (slot (p + 1) & 1) and partials p
+  SelState* st = states + 2 * l;
+  const int64_t pstride = (int64_t)kSelStride * kSelGrid;
+  uint32_t* part[2] = {parts0 + l * pstride, parts1 + l * pstride};
+  tau_pass_block(keys + L.keys_off, L.m, pass, q, &st[pass & 1], &st[(pass + 1) & 1], part[(pass + 1) & 1],
+                 part[pass & 1], blockIdx.x, L.nsel);
+}
+
+__global__ void __launch_bounds__(kBlock) tau_final_multi_kernel(MultiArgs a, float q, const SelState* states,
+                                                                 const uint32_t* parts1) {
+  const int l = blockIdx.x;
+  const MultiLayer& L = a.l[l];
+  tau_final_block(L.m, q, L.nsel, &states[2 * l], parts1 + l * (int64_t)kSelStride * kSelGrid, L.tau);
+}
+
+template <int WD, int HD, int MD, int SD, bool VEC>
+__global__ void __launch_bounds__(kBlock) update_mask_multi_kernel(MultiArgs a) {
+  const int l = multi_layer_of(a, blockIdx.x);
+  const MultiLayer& L = a.l[l];
+  const int64_t gpr = ceil_div(L.cols, 4);
+  update_mask_block<WD, HD, MD, SD, VEC>(a.us, L.W, L.H, L.aux, L.mask, L.frozen, L.stats, L.tau, L.cols,
+                                         L.rows * gpr, gpr, L.vec != 0, L.flips, blockIdx.x - a.first[l], L.nblk);
 }
 
 // ---------------------------------------------------------------------------
@@ -1325,6 +1471,200 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
   }
 #undef SF_LAUNCH_UPD
   return launch_status("sf_update_mask");
+}
+
+namespace sf {
+namespace {
+// Multi-layer workspace: [stats partials | select states | 2 x partial histograms | keys], per batch of
+// kMultiLayers layers (the batches run one after another on the stream and reuse it).
+size_t multi_partial_bytes() { return align256(sizeof(double) * 2 * kStatsGrid * kMultiLayers); }
+size_t multi_states_bytes() { return align256(sizeof(SelState) * 2 * kMultiLayers); }
+size_t multi_hist_bytes() { return align256(sizeof(uint32_t) * kSelStride * kSelGrid * kMultiLayers); }
+size_t multi_keys_off() { return multi_partial_bytes() + multi_states_bytes() + 2 * multi_hist_bytes(); }
+
+bool layer_empty(const sf_mask_layer& l) { return l.rows == 0 || l.cols == 0; }
+
+// Calls f(first, end, keys) for each batch: up to kMultiLayers non-empty layers of [first, end), and the
+// keys their tau samples need.
+template <typename F>
+void for_each_batch(const sf_mask_layer* layers, int count, F&& f) {
+  int i = 0;
+  while (i < count) {
+    while (i < count && layer_empty(layers[i])) ++i;
+    if (i == count) break;
+    const int first = i;
+    int taken = 0;
+    int64_t keys = 0;
+    while (i < count && taken < kMultiLayers) {
+      if (!layer_empty(layers[i])) {
+        keys += layers[i].sample_size;
+        ++taken;
+      }
+      ++i;
+    }
+    f(first, i, keys);
+  }
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" size_t sf_update_mask_multi_workspace_size(const sf_mask_layer* layers, int count) {
+  int64_t keys = 0;
+  if (layers && count > 0)
+    for_each_batch(layers, count, [&](int, int, int64_t k) { keys = k > keys ? k : keys; });
+  return multi_keys_off() + sizeof(uint32_t) * static_cast<size_t>(keys);
+}
+
+extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_mask_layer* layers, int count,
+                                    int stages, int w_dtype, int h_dtype, int aux_dtype, int mask_dtype,
+                                    int frozen_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_common(p)) return rc;
+  SF_CHECK_ARG(count >= 0 && (count == 0 || layers), "bad layer table (count %d)", count);
+  SF_CHECK_ARG(stages > 0 && (stages & ~SF_MULTI_ALL) == 0, "bad stage mask %d", stages);
+  SF_CHECK_ARG(dtype_ok(w_dtype) && dtype_ok(mask_dtype), "bad dtype");
+  SF_CHECK_ARG(p->penalty >= SF_PENALTY_NONE && p->penalty <= SF_PENALTY_STRUCTURED_TOPN, "bad penalty %d", p->penalty);
+  SF_CHECK_ARG(p->hard_kind >= SF_HARD_NONE && p->hard_kind <= SF_HARD_NM_STRICT, "bad hard kind %d", p->hard_kind);
+  SF_CHECK_ARG(p->gate != SF_GATE_ZSCORE, "the z-score gate form is an output of sf_gate_target only");
+  const bool unstructured = p->gate == SF_GATE_UNSTRUCTURED;
+  bool any_h = false, any_aux = false, any_flips = false;
+  for (int i = 0; i < count; ++i) {
+    const sf_mask_layer& l = layers[i];
+    SF_CHECK_ARG(l.rows >= 0 && l.cols >= 0, "layer %d: negative shape", i);
+    if (layer_empty(l)) continue;
+    if (int rc = check_metric_operands(p, l.H, l.aux)) return rc;
+    SF_CHECK_ARG(l.W && l.mask && l.stats, "layer %d: null tensor", i);
+    SF_CHECK_ARG(!unstructured || l.tau, "layer %d: unstructured gate needs tau", i);
+    SF_CHECK_ARG(!p->has_frozen || l.frozen, "layer %d: has_frozen without frozen flags", i);
+    if (unstructured) {
+      SF_CHECK_ARG(l.sample_size > 0, "layer %d: empty tau sample", i);
+      SF_CHECK_ARG(l.sample_idx || l.sample_size == l.rows * l.cols,
+                   "layer %d: sample_size must equal numel without indices", i);
+    }
+    any_h = any_h || l.H;
+    any_aux = any_aux || l.aux;
+    any_flips = any_flips || l.flips;
+  }
+  SF_CHECK_ARG(!any_h || dtype_ok(h_dtype), "bad hessian dtype");
+  SF_CHECK_ARG(!any_aux || dtype_ok(aux_dtype), "bad aux dtype");
+  if (!any_h) h_dtype = SF_DTYPE_F32;
+  // every layer's shape passes the single-layer checks; the spec itself does not depend on the shape
+  UpdateSpec us;
+  bool have_spec = false;
+  for (int i = 0; i < count; ++i) {
+    if (layer_empty(layers[i])) continue;
+    sf_mask_params pl = *p;
+    pl.rows = layers[i].rows;
+    pl.cols = layers[i].cols;
+    if (int rc = make_update_spec(&pl, w_dtype, h_dtype, aux_dtype, mask_dtype, frozen_dtype, any_flips, &us))
+      return rc;
+    have_spec = true;
+  }
+  if (!have_spec) return SF_OK;
+  SF_CHECK_ARG(workspace && workspace_bytes >= sf_update_mask_multi_workspace_size(layers, count),
+               "workspace too small");
+  char* ws = static_cast<char*>(workspace);
+  double* partial = reinterpret_cast<double*>(ws);
+  SelState* states = reinterpret_cast<SelState*>(ws + multi_partial_bytes());
+  uint32_t* parts0 = reinterpret_cast<uint32_t*>(ws + multi_partial_bytes() + multi_states_bytes());
+  uint32_t* parts1 = reinterpret_cast<uint32_t*>(ws + multi_partial_bytes() + multi_states_bytes() + multi_hist_bytes());
+  uint32_t* keys = reinterpret_cast<uint32_t*>(ws + multi_keys_off());
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool sf32 = p->score_dtype == SF_DTYPE_F32;
+  int rc_all = SF_OK;
+  for_each_batch(layers, count, [&](int first, int end, int64_t) {
+    if (rc_all != SF_OK) return;
+    MultiArgs a;
+    memset(&a, 0, sizeof(a));
+    a.us = us;
+    int n = 0, gather_grid = 1;
+    bool all_vec = true;
+    int64_t koff = 0;
+    a.first[0] = 0;
+    for (int i = first; i < end; ++i) {
+      const sf_mask_layer& l = layers[i];
+      if (layer_empty(l)) continue;
+      MultiLayer& L = a.l[n];
+      L.W = l.W;
+      L.H = l.H;
+      L.aux = l.aux;
+      L.mask = l.mask;
+      L.frozen = l.frozen;
+      L.stats = l.stats;
+      L.tau = l.tau;
+      L.flips = l.flips;
+      L.idx = l.sample_idx;
+      L.rows = l.rows;
+      L.cols = l.cols;
+      const int64_t groups = l.rows * ceil_div(l.cols, 4);
+      L.nblk = elementwise_grid(groups, kBlock);
+      // the single-layer update's vector test (it implies the statistics' one)
+      L.vec = vec_ok(l.cols, {{l.W, w_dtype}, {l.H, h_dtype}, {l.mask, mask_dtype},
+                              {p->has_frozen ? l.frozen : nullptr, frozen_dtype}}) &&
+              (!l.aux || aligned(l.aux, 4 * esize(aux_dtype)));
+      all_vec = all_vec && L.vec;
+      if (unstructured) {
+        L.m = l.sample_size;
+        L.nsel = static_cast<int32_t>(ceil_div(l.sample_size, kBlock) < kSelGrid ? ceil_div(l.sample_size, kBlock)
+                                                                                   : kSelGrid);
+        L.keys_off = koff;
+        koff += l.sample_size;
+        const int gg = elementwise_grid(l.sample_size, kBlock);
+        gather_grid = gg > gather_grid ? gg : gather_grid;
+      }
+      a.first[n + 1] = a.first[n] + L.nblk;
+      ++n;
+    }
+    a.count = n;
+    const int total = a.first[n];
+    // statistics
+    if (stages & SF_MULTI_STATS) {
+      if (all_vec)
+        SF_DISPATCH_WH(w_dtype, h_dtype,
+                       stats_partial_multi_kernel<WD_, HD_, true><<<n * kStatsGrid, kBlock, 0, st>>>(a, partial));
+      else
+        SF_DISPATCH_WH(w_dtype, h_dtype,
+                       stats_partial_multi_kernel<WD_, HD_, false><<<n * kStatsGrid, kBlock, 0, st>>>(a, partial));
+      stats_final_multi_kernel<<<n, kBlock, 0, st>>>(a, partial);
+    }
+    // tau
+    if (unstructured && (stages & SF_MULTI_TAU)) {
+      tau_gather_multi_kernel<<<dim3(gather_grid, n), kBlock, 0, st>>>(a, keys);
+      for (int pass = 0; pass < 4; ++pass)
+        tau_pass_multi_kernel<<<dim3(kSelGrid, n), kBlock, 0, st>>>(a, keys, pass, q, states, parts0, parts1);
+      tau_final_multi_kernel<<<n, kBlock, 0, st>>>(a, q, states, parts1);
+    }
+    // update
+    if (stages & SF_MULTI_UPDATE) {
+#define SF_LAUNCH_UPDM(MDT, SDT)                                                                                  \
+  do {                                                                                                            \
+    if (all_vec)                                                                                                  \
+      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                            \
+                     update_mask_multi_kernel<WD_, HD_, MDT, SDT, true><<<total, kBlock, 0, st>>>(a));            \
+    else                                                                                                          \
+      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                            \
+                     update_mask_multi_kernel<WD_, HD_, MDT, SDT, false><<<total, kBlock, 0, st>>>(a));           \
+  } while (0)
+      if (mask_dtype == SF_DTYPE_F32) {
+        if (sf32)
+          SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_F32);
+        else
+          SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_BF16);
+      } else {
+        if (sf32)
+          SF_LAUNCH_UPDM(SF_DTYPE_BF16, SF_DTYPE_F32);
+        else
+          SF_LAUNCH_UPDM(SF_DTYPE_BF16, SF_DTYPE_BF16);
+      }
+#undef SF_LAUNCH_UPDM
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      set_error("sf_update_mask_multi: launch failed: %s", hipGetErrorString(e));
+      rc_all = SF_ERR_HIP;
+    }
+  });
+  if (rc_all != SF_OK) return rc_all;
+  return launch_status("sf_update_mask_multi");
 }
 
 extern "C" int sf_joint_scores(const sf_mask_params* gate_p, const void* gate_W, const void* gate_H,

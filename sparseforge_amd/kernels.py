@@ -194,6 +194,77 @@ def update_mask(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: to
         )
 
 
+@dataclass
+class MaskJob:
+    """One layer of a batched mask update: operands, tau sample and the device outputs."""
+
+    ops: MaskOperands
+    sample_idx: torch.Tensor | None  # tau sample indices (None: every element)
+    stats: torch.Tensor              # f32 [2], written
+    tau: torch.Tensor | None         # f32 [1], written (unstructured gate)
+    flips: torch.Tensor | None       # int64 [1], incremented
+
+
+def multi_workspace(jobs: list[MaskJob], device: torch.device) -> torch.Tensor:
+    table = _layer_table(jobs)
+    return _ws(L.lib().sf_update_mask_multi_workspace_size(table, len(jobs)), device)
+
+
+def _layer_table(jobs: list[MaskJob]):
+    table = (L.MaskLayer * max(len(jobs), 1))()
+    for i, j in enumerate(jobs):
+        o = j.ops
+        rows, cols = o.weight.shape
+        e = table[i]
+        e.rows, e.cols = rows, cols
+        e.W, e.H, e.aux = L.ptr(o.weight), L.ptr(o.hessian), L.ptr(o.aux)
+        e.mask, e.frozen = L.ptr(o.mask), L.ptr(o.frozen)
+        e.sample_idx = L.ptr(j.sample_idx)
+        e.sample_size = j.sample_idx.numel() if j.sample_idx is not None else rows * cols
+        e.stats, e.tau, e.flips = L.ptr(j.stats), L.ptr(j.tau), L.ptr(j.flips)
+    return table
+
+
+def update_mask_multi(p: L.MaskParams, q: float, jobs: list[MaskJob], stages: int = L.MULTI_ALL,
+                      workspace: torch.Tensor | None = None) -> None:
+    """sf_score_stats + sf_tau_quantile(q) + sf_update_mask of many layers whose parameters differ only in
+    shape (p.rows / p.cols are ignored), in a few launches per 28 layers; outputs equal the single-layer
+    calls' bit for bit.  Every layer's tensors share one dtype per operand."""
+    if not jobs:
+        return
+    dev = jobs[0].ops.device()
+    first = jobs[0].ops
+    dts = [first.dt(t) for t in (first.weight, first.hessian, first.aux, first.mask, first.frozen)]
+    nbytes = 0
+    for j in jobs:
+        o = j.ops
+        if o.device() != dev:
+            raise ValueError("update_mask_multi: every layer must live on one device")
+        for t, want, name in ((o.weight, dts[0], "weight"), (o.hessian, dts[1], "hessian_diag"),
+                              (o.aux, dts[2], "aux"), (o.mask, dts[3], "mask"), (o.frozen, dts[4], "frozen")):
+            if t is not None and o.dt(t) != want:
+                raise ValueError(f"update_mask_multi: {name} dtypes differ between layers")
+        L.require_device(o.weight, j.stats, j.tau, j.flips, j.sample_idx)
+        if j.sample_idx is not None and (j.sample_idx.dim() != 1 or j.sample_idx.dtype != torch.int64):
+            raise TypeError("sample indices must be a 1-D int64 tensor")
+        # algorithmic bytes: the statistics read the score operands, the update reads them again and
+        # reads + writes the mask (and the frozen flags when freezing)
+        if stages & L.MULTI_STATS:
+            nbytes += o.score_bytes()
+        if stages & L.MULTI_UPDATE:
+            nbytes += o.score_bytes() + 2 * o.mask.numel() * o.mask.element_size()
+            if o.frozen is not None and p.apply_freeze:
+                nbytes += 2 * o.frozen.numel() * o.frozen.element_size()
+    table = _layer_table(jobs)
+    ws = workspace if workspace is not None else _ws(L.lib().sf_update_mask_multi_workspace_size(table, len(jobs)), dev)
+    with _prof.region("sf_update_mask_multi", nbytes, "B", dev):
+        L.check(
+            L.lib().sf_update_mask_multi(ctypes.byref(p), float(q), table, len(jobs), int(stages), *dts, L.ptr(ws),
+                                         ws.numel(), L.stream(dev)),
+            "sf_update_mask_multi",
+        )
+
+
 # ---------------------------------------------------------------------------
 # block hard types and block_sparse masks (sparse_modeling.py:460-507, :537-718,
 # :1100-1158, :1237, :1298-1529, :1598-1601)

@@ -144,10 +144,44 @@ def calculate_model_mask(model, step=0, lambda_mid: float = 0.0):
     for gate_name, up_name in pairs.items():
         with pipe.next() if pipe else _nullctx():
             _update_glu_joint_mask(mods[gate_name], mods[up_name], step, lambda_mid)
+    # Layers on the fused update path whose parameters differ only in shape update together
+    # (sf_update_mask_multi: a few launches per 28 layers, results equal to one update_mask per
+    # layer); the block hard types and block penalty modes keep their multi-pass update.
+    batches: dict = {}
     for name, m in mods.items():
-        if name not in handled:
+        if name in handled:
+            continue
+        prep = m._prepare_update(step, lambda_mid)
+        if prep is None:
+            continue
+        ops, p, code = prep
+        if m._staged_update(p):
             with pipe.next() if pipe else _nullctx():
-                m.update_mask(step, lambda_mid=lambda_mid)
+                stats, tau = m._gate_inputs(step, ops, code, p)
+                flips = torch.zeros(1, dtype=torch.int64, device=m.mask.device)
+                m._update_mask_staged(step, ops, p, stats, tau, flips)
+                m._finish_update(step, flips)
+            continue
+        q = float(m._effective_sparsity(step)) if p.gate == L.GATE_UNSTRUCTURED else 0.0
+        shape_free = L.MaskParams.from_buffer_copy(p)
+        shape_free.rows = shape_free.cols = 0
+        key = (ops.device(), tuple(ops.dt(t) if t is not None else -1
+                                   for t in (ops.weight, ops.hessian, ops.aux, ops.mask, ops.frozen)),
+               bytes(shape_free), q)
+        batches.setdefault(key, []).append((m, ops, p))
+    for (dev, _dts, _pb, q), items in batches.items():
+        n = len(items)
+        stats = torch.empty((n, 2), dtype=torch.float32, device=dev)
+        tau = torch.empty(n, dtype=torch.float32, device=dev)
+        flips = torch.zeros(n, dtype=torch.int64, device=dev)
+        jobs = []
+        for i, (m, ops, p) in enumerate(items):
+            # the tau sample of each layer, drawn in layer order as update_mask draws it
+            idx = m._sample_indices(ops.weight.numel(), dev) if p.gate == L.GATE_UNSTRUCTURED else None
+            jobs.append(K.MaskJob(ops, idx, stats[i], tau[i:i + 1], flips[i:i + 1]))
+        K.update_mask_multi(items[0][2], q, jobs)
+        for i, (m, _ops, _p) in enumerate(items):
+            m._finish_update(step, flips[i:i + 1])
     if pipe:
         pipe.join()
 
