@@ -119,6 +119,23 @@ __device__ __forceinline__ float rndc(float x) {
     return x;
 }
 
+// RN(sqrt(x)).  For x in [2^-96, 2^127) the hardware square root (within
+// 1 ulp) is corrected by the signs of its two neighbours' residuals x - y' y
+// (exact with an FMA) -- the correctly rounded expansion the compiler emits,
+// without its range scaling and special-value handling, which that range
+// does not need; other x (zero, subnormal, huge, negative, inf, NaN) take
+// sqrtf under a branch that is almost never taken.
+__device__ __forceinline__ float sqrt_rn(float x) {
+  const float y = __builtin_amdgcn_sqrtf(x);
+  const float dn = __int_as_float(__float_as_int(y) - 1), up = __int_as_float(__float_as_int(y) + 1);
+  float r = fmaf(-dn, y, x) <= 0.0f ? dn : y;
+  r = fmaf(-up, y, x) > 0.0f ? up : r;
+  float alt = 0.0f;
+  const bool odd = !(x >= 0x1p-96f && x < 0x1p127f);
+  if (__builtin_expect(odd, 0)) alt = sqrtf(x);
+  return odd ? alt : r;
+}
+
 template <int WD, int HD>
 __device__ __forceinline__ float score_of(const ScoreSpec& s, float w, float h, float a) {
   constexpr int PWH = (WD == SF_DTYPE_F32 || HD == SF_DTYPE_F32) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
@@ -130,7 +147,7 @@ __device__ __forceinline__ float score_of(const ScoreSpec& s, float w, float h, 
     }
     case SF_METRIC_HESSIAN_RATIO: {  // |W| / sqrt(H + eps)
       float hp = rndc<HD>(h + s.eps);
-      float sq = rndc<HD>(sqrtf(hp));
+      float sq = rndc<HD>(sqrt_rn(hp));
       return rndc<PWH>(fabsf(w) / sq);
     }
     case SF_METRIC_HESSIAN:
@@ -158,19 +175,30 @@ __device__ __forceinline__ float score_of_rt(const ScoreSpec& s, float w, float 
                                    : score_of<SF_DTYPE_BF16, SF_DTYPE_BF16>(s, w, h, a);
 }
 
-// Gather the operands of a group and compute the 4 scores.
+// The score operands of one group (W, H, aux widened to f32).
+struct GroupOps {
+  float w[4], h[4], a[4];
+};
+
 template <int WD, int HD>
-__device__ __forceinline__ void group_scores(const ScoreSpec& s, const void* W, const void* H, const void* aux,
-                                             const Group& g, bool vec, int64_t cols, float sc[4]) {
-  float w[4], h[4] = {0, 0, 0, 0}, a[4] = {0, 0, 0, 0};
-  load4<WD>(W, g.elem, g.n, vec, w);
-  if (H) load4<HD>(H, g.elem, g.n, vec, h);
+__device__ __forceinline__ void load_group_ops(const ScoreSpec& s, const void* W, const void* H, const void* aux,
+                                               const Group& g, bool vec, GroupOps& o) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o.h[j] = o.a[j] = 0.0f;
+  load4<WD>(W, g.elem, g.n, vec, o.w);
+  if (H) load4<HD>(H, g.elem, g.n, vec, o.h);
   if (aux) {
     if (s.metric == SF_METRIC_WANDA)
-      load4_any(aux, s.aux_dtype, g.col, g.n, vec, a);  // scaler_row [cols]
+      load4_any(aux, s.aux_dtype, g.col, g.n, vec, o.a);  // scaler_row [cols]
     else
-      load4_any(aux, s.aux_dtype, g.elem, g.n, vec, a);  // grad_ema [rows, cols]
+      load4_any(aux, s.aux_dtype, g.elem, g.n, vec, o.a);  // grad_ema [rows, cols]
   }
+}
+
+// The 4 scores of a group from its operands.
+template <int WD, int HD>
+__device__ __forceinline__ void scores_of_ops(const ScoreSpec& s, const GroupOps& o, const Group& g, float sc[4]) {
+  const float *w = o.w, *h = o.h, *a = o.a;
   // one switch per group, the element loop inside each case
   switch (s.metric) {
 #define SF_SCORES_CASE(M)                                                                            \
@@ -190,6 +218,15 @@ __device__ __forceinline__ void group_scores(const ScoreSpec& s, const void* W, 
 #pragma unroll
       for (int j = 0; j < 4; ++j) sc[j] = j < g.n ? fabsf(w[j]) : 0.0f;
   }
+}
+
+// Gather the operands of a group and compute the 4 scores.
+template <int WD, int HD>
+__device__ __forceinline__ void group_scores(const ScoreSpec& s, const void* W, const void* H, const void* aux,
+                                             const Group& g, bool vec, int64_t cols, float sc[4]) {
+  GroupOps o;
+  load_group_ops<WD, HD>(s, W, H, aux, g, vec, o);
+  scores_of_ops<WD, HD>(s, o, g, sc);
 }
 
 __device__ __forceinline__ float score_at(const ScoreSpec& s, const void* W, const void* H, const void* aux,
@@ -346,20 +383,22 @@ __device__ __forceinline__ void block_sum2_f64(double a, double b, double* out_a
 
 // Partial sums of workgroup `blk` of the kStatsGrid-workgroup grid over one
 // layer.  VEC: every group full and vector-loadable (as in update_mask_kernel).
-template <int WD, int HD, bool VEC>
-__device__ __forceinline__ void stats_partial_block(const ScoreSpec& s, const void* __restrict__ W,
-                                                    const void* __restrict__ H, const void* __restrict__ aux,
+// RATIO: the metric is hessian_ratio (|W| / sqrt(H + eps), no aux operand), fixed at compile time.
+template <int WD, int HD, bool VEC, bool RATIO = false>
+__device__ __forceinline__ void stats_partial_block(const ScoreSpec& s_in, const void* __restrict__ W,
+                                                    const void* __restrict__ H, const void* __restrict__ aux_in,
                                                     int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                     double* partial, int blk) {
+  ScoreSpec s = s_in;
+  const void* aux = aux_in;
+  if constexpr (RATIO) {
+    s.metric = SF_METRIC_HESSIAN_RATIO;
+    aux = nullptr;
+  }
   double sum = 0.0, sq = 0.0;
-  for (GroupWalk w(groups, cols, gpr, blk, kStatsGrid); w.live(); w.next()) {
-    Group g = w.group();
-    if constexpr (VEC) {
-      g.n = 4;
-      g.full = true;
-    }
+  auto add = [&](const Group& g, const GroupOps& o) {
     float sc[4];
-    group_scores<WD, HD>(s, W, H, aux, g, VEC || (vec && g.full), cols, sc);
+    scores_of_ops<WD, HD>(s, o, g, sc);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (j < g.n) {
@@ -367,16 +406,46 @@ __device__ __forceinline__ void stats_partial_block(const ScoreSpec& s, const vo
         sum += d;
         sq += d * d;
       }
+  };
+  GroupWalk w(groups, cols, gpr, blk, kStatsGrid);
+  if constexpr (VEC) {
+    // two groups per round, both loaded before either is used (the sums keep the walk's order)
+    while (w.live()) {
+      Group g0 = w.group();
+      g0.n = 4;
+      g0.full = true;
+      w.next();
+      const bool two = w.live();
+      Group g1 = g0;
+      if (two) {
+        g1 = w.group();
+        g1.n = 4;
+        g1.full = true;
+        w.next();
+      }
+      GroupOps o0, o1;
+      load_group_ops<WD, HD>(s, W, H, aux, g0, true, o0);
+      if (two) load_group_ops<WD, HD>(s, W, H, aux, g1, true, o1);
+      add(g0, o0);
+      if (two) add(g1, o1);
+    }
+  } else {
+    for (; w.live(); w.next()) {
+      const Group g = w.group();
+      GroupOps o;
+      load_group_ops<WD, HD>(s, W, H, aux, g, vec && g.full, o);
+      add(g, o);
+    }
   }
   block_sum2_f64(sum, sq, &partial[2 * blk], &partial[2 * blk + 1]);
 }
 
-template <int WD, int HD, bool VEC>
+template <int WD, int HD, bool VEC, bool RATIO>
 __global__ void __launch_bounds__(kBlock) stats_partial_kernel(ScoreSpec s, const void* __restrict__ W,
                                                                const void* __restrict__ H, const void* __restrict__ aux,
                                                                int64_t cols, int64_t groups, int64_t gpr, bool vec,
                                                                double* partial) {
-  stats_partial_block<WD, HD, VEC>(s, W, H, aux, cols, groups, gpr, vec, partial, blockIdx.x);
+  stats_partial_block<WD, HD, VEC, RATIO>(s, W, H, aux, cols, groups, gpr, vec, partial, blockIdx.x);
 }
 
 // Fold of one layer's kStatsGrid partials by one workgroup, in a fixed order.
@@ -432,35 +501,39 @@ __global__ void __launch_bounds__(kBlock) stats_final_kernel(const double* __res
 }
 
 // ---------------------------------------------------------------------------
-// tau quantile: z at the sample indices as order-preserving uint32 keys
-// (a wide gather kernel: the reads are random), then one 1024-thread
-// workgroup runs a 4 x 8-bit radix select of the two order statistics around
-// rank q * (n - 1) and torch.lerp between them.  Each pass histograms the
-// current digit of the keys that match each statistic's prefix into 16
-// per-wave LDS histograms (z-scores crowd into a few exponent bins, so
-// per-wave copies keep atomic contention low), reading keys 16 bytes at a
-// time; pass 0 also flags NaN (torch.quantile then takes the last rank).
+// tau quantile: the scores at the sample indices as order-preserving uint32
+// keys (a wide gather kernel: the reads are random), then a 4 x 8-bit radix
+// select of the two order statistics around rank q * (n - 1) over a few
+// workgroups per pass, and torch.lerp between their z-scores.  The select
+// runs on the raw scores: z = RN((s - mu) / sigma) in the score dtype is
+// non-decreasing in s (sigma > 0; every op rounds monotonically), so the k-th
+// smallest z is the z of the k-th smallest score, and the gather needs no
+// statistics (a multi-layer update runs it beside the statistics pass).  NaN
+// scores make z NaN as well, and NaN statistics make every z NaN: both give a
+// NaN tau, as torch.quantile does.  Each pass histograms the current digit of
+// the keys that match each statistic's prefix into per-wave LDS histograms
+// (scores crowd into a few exponent bins, so per-wave copies keep atomic
+// contention low); pass 0 also flags NaN (torch.quantile then takes the last
+// rank).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void tau_gather_block(const ScoreSpec& s, const void* __restrict__ W,
                                                  const void* __restrict__ H, const void* __restrict__ aux,
-                                                 int64_t rows, int64_t cols, const float* __restrict__ stats,
-                                                 const int64_t* __restrict__ idx, int64_t m,
-                                                 uint32_t* __restrict__ keys, int64_t blk, int64_t nblk) {
-  const float mu = stats[0], sigma = stats[1];
+                                                 int64_t rows, int64_t cols, const int64_t* __restrict__ idx,
+                                                 int64_t m, uint32_t* __restrict__ keys, int64_t blk, int64_t nblk) {
   const int64_t n = cols * rows;
   for (int64_t i = blk * (int64_t)blockDim.x + threadIdx.x; i < m; i += nblk * blockDim.x) {
     int64_t e = idx ? idx[i] : i;
     e = e < 0 ? 0 : (e >= n ? n - 1 : e);  // indices outside the layer are clamped, never dereferenced
-    keys[i] = ordered_key(znorm(score_at(s, W, H, aux, e, cols), mu, sigma, s.score_dtype));
+    keys[i] = ordered_key(score_at(s, W, H, aux, e, cols));
   }
 }
 
 __global__ void __launch_bounds__(kBlock) tau_gather_kernel(ScoreSpec s, const void* __restrict__ W,
                                                             const void* __restrict__ H, const void* __restrict__ aux,
-                                                            int64_t rows, int64_t cols, const float* __restrict__ stats,
+                                                            int64_t rows, int64_t cols,
                                                             const int64_t* __restrict__ idx, int64_t m,
                                                             uint32_t* __restrict__ keys) {
-  tau_gather_block(s, W, H, aux, rows, cols, stats, idx, m, keys, blockIdx.x, gridDim.x);
+  tau_gather_block(s, W, H, aux, rows, cols, idx, m, keys, blockIdx.x, gridDim.x);
 }
 
 __device__ __forceinline__ float key_to_float(uint32_t k) {
@@ -617,16 +690,21 @@ __global__ void __launch_bounds__(kBlock) tau_pass_kernel(const uint32_t* __rest
   tau_pass_block(keys, m, pass, q, state_in, state_out, partial_in, partial_out, blockIdx.x, gridDim.x);
 }
 
-// After pass 3: fix its digit and lerp the two order statistics (torch.lerp:
-// small weight -> a + w (b - a), else b - (b - a)(1 - w), each op rounded).
+// After pass 3: fix its digit, z-normalise the two order statistics and lerp
+// them (torch.lerp: small weight -> a + w (b - a), else b - (b - a)(1 - w),
+// each op rounded).
 __device__ __forceinline__ void tau_final_block(int64_t m, float q, int nparts, const SelState* __restrict__ state_in,
-                                                const uint32_t* __restrict__ partial_in, float* __restrict__ tau) {
+                                                const uint32_t* __restrict__ partial_in,
+                                                const float* __restrict__ stats, int score_dtype,
+                                                float* __restrict__ tau) {
   __shared__ SelState st;
   if (threadIdx.x == 0) st = *state_in;
   __syncthreads();
   advance_state(st, partial_in, nparts, 3, m, q);
   if (threadIdx.x == 0) {
-    const float lo = key_to_float(st.prefix[0]), hi = key_to_float(st.prefix[1]);
+    const float mu = stats[0], sigma = stats[1];
+    const float lo = znorm(key_to_float(st.prefix[0]), mu, sigma, score_dtype);
+    const float hi = znorm(key_to_float(st.prefix[1]), mu, sigma, score_dtype);
     const float w = st.wgt;
     const float dlt = __fsub_rn(hi, lo);
     *tau = fabsf(w) < 0.5f ? __fadd_rn(lo, __fmul_rn(w, dlt)) : __fsub_rn(hi, __fmul_rn(dlt, __fsub_rn(1.0f, w)));
@@ -636,8 +714,9 @@ __device__ __forceinline__ void tau_final_block(int64_t m, float q, int nparts, 
 __global__ void __launch_bounds__(kBlock) tau_final_kernel(int64_t m, float q, int nparts,
                                                            const SelState* __restrict__ state_in,
                                                            const uint32_t* __restrict__ partial_in,
+                                                           const float* __restrict__ stats, int score_dtype,
                                                            float* __restrict__ tau) {
-  tau_final_block(m, q, nparts, state_in, partial_in, tau);
+  tau_final_block(m, q, nparts, state_in, partial_in, stats, score_dtype, tau);
 }
 
 __global__ void __launch_bounds__(kBlock) sample_indices_kernel(int64_t* idx, int64_t m, uint64_t n, uint64_t seed) {
@@ -841,51 +920,129 @@ __device__ __forceinline__ int flips_of(const float a[4], const float b[4], cons
   return __popc((hard_bits(a, g, kind, n) ^ hard_bits(b, g, kind, n)) & ((1u << g.n) - 1u));
 }
 
+// Specialisations of the fused update for the configurations training runs
+// spend their time in: kFastPlain = hessian_ratio scores, unstructured gate,
+// no penalty, binarisation, frozen flags, freezing or structural mix, 2:4 flip
+// count; kFastNm24 = the same with the nm_2_4 penalty.  The spec's fields are
+// fixed to those values, so the compiler drops every other branch (the
+// arithmetic is the generic path's, operation for operation).
+constexpr int kFastNone = 0, kFastPlain = 1, kFastNm24 = 2;
+
+template <int FAST>
+__device__ __forceinline__ UpdateSpec fast_spec(const UpdateSpec& in) {
+  UpdateSpec us = in;
+  if constexpr (FAST != kFastNone) {
+    us.gs.s.metric = SF_METRIC_HESSIAN_RATIO;
+    us.gs.gate = SF_GATE_UNSTRUCTURED;
+    us.gs.beta_struct = 0.0f;
+    us.gs.has_frozen = 0;
+    us.apply_freeze = 0;
+    us.binarize = 0;
+    us.penalty = FAST == kFastNm24 ? SF_PENALTY_NM_2_4 : SF_PENALTY_NONE;
+    us.pen_n = 2;
+    us.hard_kind = SF_HARD_NM_TAIL_KEEP;
+    us.hard_n = 2;
+  }
+  return us;
+}
+
+// Workgroups of an update grid: 8 groups per thread (each workgroup's set-up --
+// the statistics and tau loads, 1 / sigma -- and its flip-count reduction
+// amortised over 8 rounds; measured faster than the capped elementwise grid).
+int update_grid(int64_t groups) {
+  const int64_t g = ceil_div(groups, 8 * kBlock);
+  return static_cast<int>(g < 1 ? 1 : g);
+}
+
+// The specialisation a spec qualifies for (kFastNone: the generic kernel).
+int fast_kind(const UpdateSpec& us) {
+  const GateSpec& gs = us.gs;
+  if (gs.s.metric != SF_METRIC_HESSIAN_RATIO || gs.gate != SF_GATE_UNSTRUCTURED || gs.beta_struct != 0.0f ||
+      gs.has_frozen || us.apply_freeze || us.binarize || us.hard_kind != SF_HARD_NM_TAIL_KEEP || us.hard_n != 2)
+    return kFastNone;
+  if (us.penalty == SF_PENALTY_NONE) return kFastPlain;
+  if (us.penalty == SF_PENALTY_NM_2_4 && us.pen_n == 2) return kFastNm24;
+  return kFastNone;
+}
+
 // VEC: cols % 4 == 0 and every operand 16-byte aligned, so every group is a
 // full, vector-loadable group of 4 (known at compile time: no tail branches).
 // Workgroup `blk` of a grid of `nblk` over one layer.
-template <int WD, int HD, int MD, int SD, bool VEC>
-__device__ __forceinline__ void update_mask_block(const UpdateSpec& us, const void* __restrict__ W,
+template <int WD, int HD, int MD, int SD, bool VEC, int FAST = kFastNone>
+__device__ __forceinline__ void update_mask_block(const UpdateSpec& us_in, const void* __restrict__ W,
                                                   const void* __restrict__ H, const void* __restrict__ aux,
                                                   void* __restrict__ mask, void* __restrict__ frozen,
                                                   const float* __restrict__ stats, const float* __restrict__ tau_p,
                                                   int64_t cols, int64_t groups, int64_t gpr, bool vec, int64_t* flips,
                                                   int64_t blk, int64_t nblk) {
+  const UpdateSpec us = fast_spec<FAST>(us_in);
   const GateSpec& gs = us.gs;
   const float mu = stats[0], sigma = stats[1], rsigma = 1.0f / sigma;
   const float tau = tau_p ? *tau_p : 0.0f;
   int64_t cnt = 0;
-  for (GroupWalk w(groups, cols, gpr, blk, nblk); w.live(); w.next()) {
-    Group g = w.group();
-    if constexpr (VEC) {
-      g.n = 4;
-      g.full = true;
-    }
-    const bool v = VEC || (vec && g.full);
-    float sc[4], mp[4], fz[4] = {0, 0, 0, 0}, G[4];
-    group_scores<WD, HD>(gs.s, W, H, aux, g, v, cols, sc);
+  auto load = [&](const Group& g, bool v, GroupOps& o, float mp[4], float fz[4]) {
+    load_group_ops<WD, HD>(gs.s, W, H, aux, g, v, o);
     load4<MD>(mask, g.elem, g.n, v, mp);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fz[j] = 0.0f;
     if (gs.has_frozen) load4_any(frozen, gs.frozen_dtype, g.elem, g.n, v, fz);
+  };
+  auto finish = [&](const Group& g, bool v, const GroupOps& o, const float mp[4], const float fz[4]) {
+    float sc[4], G[4], mn[4];
+    scores_of_ops<WD, HD>(gs.s, o, g, sc);
     gate_of_group<SD>(gs, sc, g, mu, sigma, rsigma, tau, mp, fz, G);
     pull_and_push<MD, SD>(us, g, mp, G);
-    float mn[4];
     ema_of<MD>(us, mp, G, mn);
     if (us.apply_freeze) freeze_group(us, g, v, mn, fz, frozen);
     store4<MD>(mask, g.elem, g.n, v, mn);
     if (flips) cnt += flips_of(mp, mn, g, us.hard_kind, us.hard_n);
+  };
+  GroupWalk w(groups, cols, gpr, blk, nblk);
+  if constexpr (VEC) {
+    // two groups per round, every load of both issued before either is used: one memory
+    // latency per two groups
+    while (w.live()) {
+      Group g0 = w.group();
+      g0.n = 4;
+      g0.full = true;
+      w.next();
+      const bool two = w.live();
+      Group g1 = g0;
+      if (two) {
+        g1 = w.group();
+        g1.n = 4;
+        g1.full = true;
+        w.next();
+      }
+      GroupOps o0, o1;
+      float m0[4], m1[4], f0[4], f1[4];
+      load(g0, true, o0, m0, f0);
+      if (two) load(g1, true, o1, m1, f1);
+      finish(g0, true, o0, m0, f0);
+      if (two) finish(g1, true, o1, m1, f1);
+    }
+  } else {
+    for (; w.live(); w.next()) {
+      const Group g = w.group();
+      const bool v = vec && g.full;
+      GroupOps o;
+      float mp[4], fz[4];
+      load(g, v, o, mp, fz);
+      finish(g, v, o, mp, fz);
+    }
   }
   if (flips) block_add_i64(cnt, flips);
 }
 
-template <int WD, int HD, int MD, int SD, bool VEC>
+template <int WD, int HD, int MD, int SD, bool VEC, int FAST>
 __global__ void __launch_bounds__(kBlock) update_mask_kernel(UpdateSpec us, const void* __restrict__ W,
                                                              const void* __restrict__ H, const void* __restrict__ aux,
                                                              void* __restrict__ mask, void* __restrict__ frozen,
                                                              const float* __restrict__ stats,
                                                              const float* __restrict__ tau_p, int64_t cols,
                                                              int64_t groups, int64_t gpr, bool vec, int64_t* flips) {
-  update_mask_block<WD, HD, MD, SD, VEC>(us, W, H, aux, mask, frozen, stats, tau_p, cols, groups, gpr, vec, flips,
-                                         blockIdx.x, gridDim.x);
+  update_mask_block<WD, HD, MD, SD, VEC, FAST>(us, W, H, aux, mask, frozen, stats, tau_p, cols, groups, gpr, vec,
+                                               flips, blockIdx.x, gridDim.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -935,13 +1092,25 @@ __device__ __forceinline__ int multi_layer_of(const MultiArgs& a, int b) {
 }
 
 // Statistics partials: kStatsGrid workgroups per layer, layer = blockIdx.x / kStatsGrid.
-template <int WD, int HD, bool VEC>
-__global__ void __launch_bounds__(kBlock) stats_partial_multi_kernel(MultiArgs a, double* partial) {
-  const int l = blockIdx.x / kStatsGrid, blk = blockIdx.x - l * kStatsGrid;
+// The first n * gather workgroups gather the layers' tau samples (gather per
+// layer; 0 when the tau stage runs on its own), the rest are the statistics
+// grids.  The gather's random reads go first and overlap the statistics pass,
+// whose cost is its arithmetic.
+template <int WD, int HD, bool VEC, bool RATIO>
+__global__ void __launch_bounds__(kBlock) stats_partial_multi_kernel(MultiArgs a, double* partial, int gather,
+                                                                     uint32_t* keys) {
+  int b = blockIdx.x;
+  if (b < a.count * gather) {
+    const MultiLayer& L = a.l[b / gather];
+    tau_gather_block(a.us.gs.s, L.W, L.H, L.aux, L.rows, L.cols, L.idx, L.m, keys + L.keys_off, b % gather, gather);
+    return;
+  }
+  b -= a.count * gather;
+  const int l = b / kStatsGrid, blk = b - l * kStatsGrid;
   const MultiLayer& L = a.l[l];
   const int64_t gpr = ceil_div(L.cols, 4);
-  stats_partial_block<WD, HD, VEC>(a.us.gs.s, L.W, L.H, L.aux, L.cols, L.rows * gpr, gpr, L.vec != 0,
-                                   partial + (int64_t)l * 2 * kStatsGrid, blk);
+  stats_partial_block<WD, HD, VEC, RATIO>(a.us.gs.s, L.W, L.H, L.aux, L.cols, L.rows * gpr, gpr, L.vec != 0,
+                                          partial + (int64_t)l * 2 * kStatsGrid, blk);
 }
 
 __global__ void __launch_bounds__(kBlock) stats_final_multi_kernel(MultiArgs a, const double* partial) {
@@ -953,7 +1122,7 @@ __global__ void __launch_bounds__(kBlock) stats_final_multi_kernel(MultiArgs a, 
 // its radix passes use its own nsel of them.
 __global__ void __launch_bounds__(kBlock) tau_gather_multi_kernel(MultiArgs a, uint32_t* keys) {
   const MultiLayer& L = a.l[blockIdx.y];
-  tau_gather_block(a.us.gs.s, L.W, L.H, L.aux, L.rows, L.cols, L.stats, L.idx, L.m, keys + L.keys_off, blockIdx.x,
+  tau_gather_block(a.us.gs.s, L.W, L.H, L.aux, L.rows, L.cols, L.idx, L.m, keys + L.keys_off, blockIdx.x,
                    gridDim.x);
 }
 
@@ -974,16 +1143,18 @@ __global__ void __launch_bounds__(kBlock) tau_final_multi_kernel(MultiArgs a, fl
                                                                  const uint32_t* parts1) {
   const int l = blockIdx.x;
   const MultiLayer& L = a.l[l];
-  tau_final_block(L.m, q, L.nsel, &states[2 * l], parts1 + l * (int64_t)kSelStride * kSelGrid, L.tau);
+  tau_final_block(L.m, q, L.nsel, &states[2 * l], parts1 + l * (int64_t)kSelStride * kSelGrid, L.stats,
+                  a.us.gs.s.score_dtype, L.tau);
 }
 
-template <int WD, int HD, int MD, int SD, bool VEC>
+template <int WD, int HD, int MD, int SD, bool VEC, int FAST>
 __global__ void __launch_bounds__(kBlock) update_mask_multi_kernel(MultiArgs a) {
   const int l = multi_layer_of(a, blockIdx.x);
   const MultiLayer& L = a.l[l];
   const int64_t gpr = ceil_div(L.cols, 4);
-  update_mask_block<WD, HD, MD, SD, VEC>(a.us, L.W, L.H, L.aux, L.mask, L.frozen, L.stats, L.tau, L.cols,
-                                         L.rows * gpr, gpr, L.vec != 0, L.flips, blockIdx.x - a.first[l], L.nblk);
+  update_mask_block<WD, HD, MD, SD, VEC, FAST>(a.us, L.W, L.H, L.aux, L.mask, L.frozen, L.stats, L.tau, L.cols,
+                                               L.rows * gpr, gpr, L.vec != 0, L.flips, blockIdx.x - a.first[l],
+                                               L.nblk);
 }
 
 // ---------------------------------------------------------------------------
@@ -1189,14 +1360,18 @@ extern "C" int sf_score_stats(const sf_mask_params* p, const void* W, int w_dtyp
                    (!aux || p->metric != SF_METRIC_WANDA || aligned(aux, 4 * esize(aux_dtype)));
   double* partial = static_cast<double*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (vec)
+  if (vec && p->metric == SF_METRIC_HESSIAN_RATIO)
     SF_DISPATCH_WH(w_dtype, h_dtype,
-                   stats_partial_kernel<WD_, HD_, true><<<kStatsGrid, kBlock, 0, st>>>(s, W, H, aux, p->cols, groups,
-                                                                                      gpr, vec, partial));
+                   stats_partial_kernel<WD_, HD_, true, true><<<kStatsGrid, kBlock, 0, st>>>(
+                       s, W, H, aux, p->cols, groups, gpr, vec, partial));
+  else if (vec)
+    SF_DISPATCH_WH(w_dtype, h_dtype,
+                   stats_partial_kernel<WD_, HD_, true, false><<<kStatsGrid, kBlock, 0, st>>>(
+                       s, W, H, aux, p->cols, groups, gpr, vec, partial));
   else
     SF_DISPATCH_WH(w_dtype, h_dtype,
-                   stats_partial_kernel<WD_, HD_, false><<<kStatsGrid, kBlock, 0, st>>>(s, W, H, aux, p->cols, groups,
-                                                                                       gpr, vec, partial));
+                   stats_partial_kernel<WD_, HD_, false, false><<<kStatsGrid, kBlock, 0, st>>>(
+                       s, W, H, aux, p->cols, groups, gpr, vec, partial));
   stats_final_kernel<<<1, kBlock, 0, st>>>(partial, kStatsGrid, n, stats_out);
   return launch_status("sf_score_stats");
 }
@@ -1236,14 +1411,14 @@ int tau_quantile_launch(const sf_mask_params* p, const void* W, int w_dtype, con
   SelState* states = reinterpret_cast<SelState*>(ws + ws_state_off());
   uint32_t* parts[2] = {reinterpret_cast<uint32_t*>(ws + ws_partial_off()),
                         reinterpret_cast<uint32_t*>(ws + ws_partial_off() + ws_partial_bytes())};
-  tau_gather_kernel<<<elementwise_grid(sample_size, kBlock), kBlock, 0, st>>>(s, W, H, aux, p->rows, p->cols, stats,
+  tau_gather_kernel<<<elementwise_grid(sample_size, kBlock), kBlock, 0, st>>>(s, W, H, aux, p->rows, p->cols,
                                                                                sample_idx, sample_size, keys);
   // pass p reads state p-2 (slot p & 1) and partials p-1, writes state p-1 (slot (p + 1) & 1) and partials p
   const int grid = static_cast<int>(ceil_div(sample_size, kBlock) < kSelGrid ? ceil_div(sample_size, kBlock) : kSelGrid);
   for (int pass = 0; pass < 4; ++pass)
     tau_pass_kernel<<<grid, kBlock, 0, st>>>(keys, sample_size, pass, q, &states[pass & 1], &states[(pass + 1) & 1],
                                              parts[(pass + 1) & 1], parts[pass & 1]);
-  tau_final_kernel<<<1, kBlock, 0, st>>>(sample_size, q, grid, &states[0], parts[1], tau_out);
+  tau_final_kernel<<<1, kBlock, 0, st>>>(sample_size, q, grid, &states[0], parts[1], stats, s.score_dtype, tau_out);
   return SF_OK;
 }
 
@@ -1445,21 +1620,26 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
                                     {p->has_frozen ? frozen : nullptr, frozen_dtype}}) &&
                    (!aux || aligned(aux, 4 * esize(aux_dtype)));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int grid = elementwise_grid(groups, kBlock);
+  const int grid = update_grid(groups);
+#define SF_LAUNCH_UPD_V(MDT, SDT, VEC, FAST)                                                                \
+  SF_DISPATCH_WH(w_dtype, h_dtype,                                                                          \
+                 update_mask_kernel<WD_, HD_, MDT, SDT, VEC, FAST><<<grid, kBlock, 0, st>>>(                \
+                     us, W, H, aux, mask, frozen, stats, tau, p->cols, groups, gpr, vec, flips))
 #define SF_LAUNCH_UPD(MDT, SDT)                                                                             \
   do {                                                                                                      \
     if (vec)                                                                                                \
-      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                      \
-                     update_mask_kernel<WD_, HD_, MDT, SDT, true><<<grid, kBlock, 0, st>>>(                 \
-                         us, W, H, aux, mask, frozen, stats, tau, p->cols, groups, gpr, vec, flips));       \
+      SF_LAUNCH_UPD_V(MDT, SDT, true, kFastNone);                                                           \
     else                                                                                                    \
-      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                      \
-                     update_mask_kernel<WD_, HD_, MDT, SDT, false><<<grid, kBlock, 0, st>>>(                \
-                         us, W, H, aux, mask, frozen, stats, tau, p->cols, groups, gpr, vec, flips));       \
+      SF_LAUNCH_UPD_V(MDT, SDT, false, kFastNone);                                                          \
   } while (0)
   const bool sf32 = p->score_dtype == SF_DTYPE_F32;
+  const int fk = vec ? fast_kind(us) : kFastNone;
   if (mask_dtype == SF_DTYPE_F32) {
-    if (sf32)
+    if (sf32 && fk == kFastPlain)
+      SF_LAUNCH_UPD_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastPlain);
+    else if (sf32 && fk == kFastNm24)
+      SF_LAUNCH_UPD_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastNm24);
+    else if (sf32)
       SF_LAUNCH_UPD(SF_DTYPE_F32, SF_DTYPE_F32);
     else
       SF_LAUNCH_UPD(SF_DTYPE_F32, SF_DTYPE_BF16);
@@ -1470,6 +1650,7 @@ extern "C" int sf_update_mask(const sf_mask_params* p, const void* W, int w_dtyp
       SF_LAUNCH_UPD(SF_DTYPE_BF16, SF_DTYPE_BF16);
   }
 #undef SF_LAUNCH_UPD
+#undef SF_LAUNCH_UPD_V
   return launch_status("sf_update_mask");
 }
 
@@ -1596,7 +1777,7 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
       L.rows = l.rows;
       L.cols = l.cols;
       const int64_t groups = l.rows * ceil_div(l.cols, 4);
-      L.nblk = elementwise_grid(groups, kBlock);
+      L.nblk = update_grid(groups);
       // the single-layer update's vector test (it implies the statistics' one)
       L.vec = vec_ok(l.cols, {{l.W, w_dtype}, {l.H, h_dtype}, {l.mask, mask_dtype},
                               {p->has_frozen ? l.frozen : nullptr, frozen_dtype}}) &&
@@ -1617,35 +1798,49 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
     a.count = n;
     const int total = a.first[n];
     // statistics
+    const bool want_tau = unstructured && (stages & SF_MULTI_TAU);
+    // the tau gather rides in the statistics launch when both stages run
+    const bool fused_gather = want_tau && (stages & SF_MULTI_STATS);
     if (stages & SF_MULTI_STATS) {
-      if (all_vec)
+      const int g = fused_gather ? gather_grid : 0;
+      const int grid = n * g + n * kStatsGrid;
+      if (all_vec && p->metric == SF_METRIC_HESSIAN_RATIO)
         SF_DISPATCH_WH(w_dtype, h_dtype,
-                       stats_partial_multi_kernel<WD_, HD_, true><<<n * kStatsGrid, kBlock, 0, st>>>(a, partial));
+                       stats_partial_multi_kernel<WD_, HD_, true, true><<<grid, kBlock, 0, st>>>(a, partial, g, keys));
+      else if (all_vec)
+        SF_DISPATCH_WH(w_dtype, h_dtype,
+                       stats_partial_multi_kernel<WD_, HD_, true, false><<<grid, kBlock, 0, st>>>(a, partial, g, keys));
       else
         SF_DISPATCH_WH(w_dtype, h_dtype,
-                       stats_partial_multi_kernel<WD_, HD_, false><<<n * kStatsGrid, kBlock, 0, st>>>(a, partial));
+                       stats_partial_multi_kernel<WD_, HD_, false, false><<<grid, kBlock, 0, st>>>(a, partial, g,
+                                                                                                   keys));
       stats_final_multi_kernel<<<n, kBlock, 0, st>>>(a, partial);
     }
     // tau
-    if (unstructured && (stages & SF_MULTI_TAU)) {
-      tau_gather_multi_kernel<<<dim3(gather_grid, n), kBlock, 0, st>>>(a, keys);
+    if (want_tau) {
+      if (!fused_gather) tau_gather_multi_kernel<<<dim3(gather_grid, n), kBlock, 0, st>>>(a, keys);
       for (int pass = 0; pass < 4; ++pass)
         tau_pass_multi_kernel<<<dim3(kSelGrid, n), kBlock, 0, st>>>(a, keys, pass, q, states, parts0, parts1);
       tau_final_multi_kernel<<<n, kBlock, 0, st>>>(a, q, states, parts1);
     }
     // update
     if (stages & SF_MULTI_UPDATE) {
-#define SF_LAUNCH_UPDM(MDT, SDT)                                                                                  \
-  do {                                                                                                            \
-    if (all_vec)                                                                                                  \
-      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                            \
-                     update_mask_multi_kernel<WD_, HD_, MDT, SDT, true><<<total, kBlock, 0, st>>>(a));            \
-    else                                                                                                          \
-      SF_DISPATCH_WH(w_dtype, h_dtype,                                                                            \
-                     update_mask_multi_kernel<WD_, HD_, MDT, SDT, false><<<total, kBlock, 0, st>>>(a));           \
+#define SF_LAUNCH_UPDM_V(MDT, SDT, VEC, FAST) \
+  SF_DISPATCH_WH(w_dtype, h_dtype, update_mask_multi_kernel<WD_, HD_, MDT, SDT, VEC, FAST><<<total, kBlock, 0, st>>>(a))
+#define SF_LAUNCH_UPDM(MDT, SDT)                            \
+  do {                                                      \
+    if (all_vec)                                            \
+      SF_LAUNCH_UPDM_V(MDT, SDT, true, kFastNone);          \
+    else                                                    \
+      SF_LAUNCH_UPDM_V(MDT, SDT, false, kFastNone);         \
   } while (0)
+      const int fk = all_vec ? fast_kind(us) : kFastNone;
       if (mask_dtype == SF_DTYPE_F32) {
-        if (sf32)
+        if (sf32 && fk == kFastPlain)
+          SF_LAUNCH_UPDM_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastPlain);
+        else if (sf32 && fk == kFastNm24)
+          SF_LAUNCH_UPDM_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastNm24);
+        else if (sf32)
           SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_F32);
         else
           SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_BF16);
@@ -1656,6 +1851,7 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
           SF_LAUNCH_UPDM(SF_DTYPE_BF16, SF_DTYPE_BF16);
       }
 #undef SF_LAUNCH_UPDM
+#undef SF_LAUNCH_UPDM_V
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
