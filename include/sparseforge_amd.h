@@ -238,6 +238,18 @@ int sf_hard_flip_count(const void* prev, const void* now, int dtype, int64_t row
                        int kind, int n_keep, int m_group, int64_t* flips, void* stream);
 
 /*
+ * Importance scores of one layer (_compute_importance_scores,
+ * legacy/utils.py:482-533; the score half of compute_gate_target,
+ * legacy/sparse_modeling.py:1041-1079): magnitude |W|, hessian_obd
+ * (H + eps) W^2, hessian_ratio |W| / sqrt(H + eps), hessian H, wanda
+ * |W| sqrt(scaler + eps), movement |W g| / max(temperature, eps), each
+ * reference op rounded to its result dtype, the result rounded to s_dtype.
+ * S: [rows, cols].
+ */
+int sf_importance_scores(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                         const void* aux, int aux_dtype, void* S, int s_dtype, void* stream);
+
+/*
  * Joint importance score of a GLU gate/up pair: S = score(gate) + score(up),
  * each from its own layer's metric, eps and operands
  * (_compute_importance_scores, legacy/utils.py:480-533, summed at :415-420),

@@ -534,6 +534,26 @@ def layer_update_mask(c: dict, step: int, W, H, mask, frozen, sample_idx, lambda
     return new, new_frozen, flips, hx
 
 
+def joint_gate_target(c: dict, step: int, S, mask, frozen, sample_idx, m_dt=F32) -> np.ndarray:
+    """_compute_joint_gate_target(module, scores, step) (utils.py:536-613) for a module of config c:
+    z = ((S - mu) / sigma) in the mask dtype, the gate form (a mask_type other than structured behaves as
+    unstructured; tau = quantile of z over the sample), the beta structural mix, the frozen override."""
+    S = np.asarray(S, np.float32)
+    if S.size == 0:
+        return np.asarray(mask, np.float32)
+    mu, sigma = score_stats(S)
+    z = znorm(S, mu, sigma, m_dt)
+    sch = layer_schedule(c, step)
+    mtype = "structured" if c["mask_type"] == "structured" else "unstructured"
+    N, M = int(c["N"]), int(c["M"])
+    tau = None
+    if mtype == "unstructured":
+        flat = z.ravel()
+        sample = flat[np.asarray(sample_idx)] if sample_idx is not None else flat
+        tau = quantile_linear(sample, sch["sparsity"])
+    return gate_target(z, m_dt, mtype, sch["T"], tau, N, M, bool(c["structured_exact"]), sch["beta_s"], mask, frozen)
+
+
 def glu_joint_update(c: dict, step: int, Wg, Hg, Mg, Wu, Hu, Mu, frozen_g, sample_idx, lambda_mid: float,
                      w_dt=F32, h_dt=F32, m_dt=F32, aux_g=None, aux_u=None, aux_dt=F32):
     """_update_glu_joint_mask (utils.py:363-479) for one gate/up pair sharing config c (the gate's).
@@ -558,17 +578,9 @@ def glu_joint_update(c: dict, step: int, Wg, Hg, Mg, Wu, Hu, Mu, frozen_g, sampl
     sg = scores(Wg, Hg, aux_g, metric, w_dt, h_dt, aux_dt, temperature=c["temperature"])
     su = scores(Wu, Hu, aux_u, metric, w_dt, h_dt, aux_dt, temperature=c["temperature"])
     S = rnd(sg + su, sdt)
-    mu, sigma = score_stats(S)
-    z = znorm(S, mu, sigma, m_dt)
     sch = layer_schedule(c, step)
-    mtype = "structured" if c["mask_type"] == "structured" else "unstructured"
     N, M = int(c["N"]), int(c["M"])
-    tau = None
-    if mtype == "unstructured":
-        flat = z.ravel()
-        sample = flat[np.asarray(sample_idx)] if sample_idx is not None else flat
-        tau = quantile_linear(sample, sch["sparsity"])
-    G = gate_target(z, m_dt, mtype, sch["T"], tau, N, M, bool(c["structured_exact"]), sch["beta_s"], Mg, frozen_g)
+    G = joint_gate_target(c, step, S, Mg, frozen_g, sample_idx, m_dt)
     Mg = np.asarray(Mg, np.float32)
     rows, cols = Mg.shape
     lam = float(lambda_mid or 0.0)

@@ -234,6 +234,7 @@ SIGNATURES = {
     "sf_update_mask_multi_workspace_size": (_SZ, [ctypes.POINTER(MaskLayer), _I]),
     "sf_update_mask_multi": (_I, [_MP, _F, ctypes.POINTER(MaskLayer), _I, _I, _I, _I, _I, _I, _I, _P, _SZ, _P]),
     "sf_hard_flip_count": (_I, [_P, _P, _I, _I64, _I64, _I, _I, _I, _P, _P]),
+    "sf_importance_scores": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P]),
     "sf_joint_scores": (_I, [_MP, _P, _P, _P, _MP, _P, _P, _P, _I, _I, _I, _P, _I, _P]),
     "sf_glu_update_masks": (_I, [_MP, _P, _I, _P, _P, _I, _P, _I, _P, _P, _I, _I, _P, _P, _P]),
     "sf_effective_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _F, _I, _I, _I, _P]),

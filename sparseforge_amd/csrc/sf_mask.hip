@@ -1185,6 +1185,27 @@ __global__ void __launch_bounds__(kBlock) joint_scores_kernel(ScoreSpec sg, cons
   }
 }
 
+// One layer's importance scores, rounded to s_dtype (_compute_importance_scores).
+template <int WD, int HD>
+__global__ void __launch_bounds__(kBlock) importance_scores_kernel(ScoreSpec sp, const void* __restrict__ W,
+                                                                   const void* __restrict__ H,
+                                                                   const void* __restrict__ aux, void* __restrict__ S,
+                                                                   int s_dtype, int64_t cols, int64_t groups,
+                                                                   int64_t gpr, bool vec) {
+  for (GroupWalk w(groups, cols, gpr); w.live(); w.next()) {
+    Group g = w.group();
+    const bool v = vec && g.full;
+    float a[4], o[4];
+    group_scores<WD, HD>(sp, W, H, aux, g, v, cols, a);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = rnd(a[j], s_dtype);
+    if (s_dtype == SF_DTYPE_F32)
+      store4<SF_DTYPE_F32>(S, g.elem, g.n, v, o);
+    else
+      store4<SF_DTYPE_BF16>(S, g.elem, g.n, v, o);
+  }
+}
+
 template <int SD, int MD>
 __global__ void __launch_bounds__(kBlock) glu_update_kernel(UpdateSpec us, const void* __restrict__ S,
                                                             void* __restrict__ mask_g, void* __restrict__ mask_u,
@@ -1861,6 +1882,27 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
   });
   if (rc_all != SF_OK) return rc_all;
   return launch_status("sf_update_mask_multi");
+}
+
+extern "C" int sf_importance_scores(const sf_mask_params* p, const void* W, int w_dtype, const void* H, int h_dtype,
+                                    const void* aux, int aux_dtype, void* S, int s_dtype, void* stream) {
+  if (int rc = check_common(p)) return rc;
+  if (int rc = check_metric_operands(p, H, aux)) return rc;
+  SF_CHECK_ARG(dtype_ok(w_dtype) && dtype_ok(s_dtype), "bad dtype");
+  SF_CHECK_ARG(!H || dtype_ok(h_dtype), "bad hessian dtype");
+  SF_CHECK_ARG(!aux || dtype_ok(aux_dtype), "bad aux dtype");
+  if (p->rows == 0 || p->cols == 0) return SF_OK;
+  SF_CHECK_ARG(W && S, "null tensor");
+  if (!H) h_dtype = SF_DTYPE_F32;
+  const ScoreSpec sp = make_spec(p, w_dtype, h_dtype, aux_dtype);
+  const int64_t cols = p->cols, gpr = ceil_div(cols, 4), groups = p->rows * gpr;
+  const bool vec = vec_ok(cols, {{W, w_dtype}, {H, h_dtype}, {aux, aux_dtype}, {S, s_dtype}});
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int grid = elementwise_grid(groups, kBlock);
+  SF_DISPATCH_WH(w_dtype, h_dtype,
+                 importance_scores_kernel<WD_, HD_><<<grid, kBlock, 0, st>>>(sp, W, H, aux, S, s_dtype, cols, groups,
+                                                                             gpr, vec));
+  return launch_status("sf_importance_scores");
 }
 
 extern "C" int sf_joint_scores(const sf_mask_params* gate_p, const void* gate_W, const void* gate_H,

@@ -351,6 +351,18 @@ def freeze_mask(p: L.MaskParams, mask: torch.Tensor, frozen: torch.Tensor | None
 # ---------------------------------------------------------------------------
 # GLU gate/up joint update (legacy/utils.py:363-643)
 # ---------------------------------------------------------------------------
+def importance_scores(p: L.MaskParams, ops: MaskOperands, s_dtype: torch.dtype) -> torch.Tensor:
+    """One layer's importance scores in s_dtype (sf_importance_scores)."""
+    dev = ops.device()
+    S = torch.empty(ops.weight.shape, dtype=s_dtype, device=dev)
+    with _prof.region("sf_importance_scores", ops.score_bytes() + S.numel() * S.element_size(), "B", dev):
+        L.check(L.lib().sf_importance_scores(ctypes.byref(p), L.ptr(ops.weight), ops.dt(ops.weight),
+                                             L.ptr(ops.hessian), ops.dt(ops.hessian), L.ptr(ops.aux), ops.dt(ops.aux),
+                                             L.ptr(S), L.dtype_code(S), L.stream(dev)),
+                "sf_importance_scores")
+    return S
+
+
 def joint_scores(pg: L.MaskParams, gate: MaskOperands, pu: L.MaskParams, up: MaskOperands,
                  s_dtype: torch.dtype) -> torch.Tensor:
     """S = score(gate) + score(up), rounded in s_dtype."""

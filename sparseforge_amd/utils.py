@@ -195,6 +195,48 @@ def _update_glu_joint_mask(gate_module, up_module, step, lambda_mid, sample_idx=
 
 
 @torch.no_grad()
+def _compute_importance_scores(module):
+    """A SparseLinear's importance scores (:482-533), in the dtype the reference's torch ops produce
+    (the promotion of W and the metric's operand), on the device (sf_importance_scores)."""
+    from .glu import _score_only_params
+
+    ops = module._mask_operands()
+    code = module._metric_code(ops)
+    if code == -1:  # hessian_obd without H: the reference takes W * W
+        raise NotImplementedError("hessian_obd without a hessian_diag tensor")
+    p = _score_only_params(module, ops, code)
+    dt = torch.bfloat16 if p.score_dtype == L.DT_BF16 else torch.float32
+    return K.importance_scores(p, ops, dt)
+
+
+@torch.no_grad()
+def _compute_joint_gate_target(module, scores, step, sample_idx=None):
+    """Gate target G of `module` from precomputed (joint) scores (:536-613): z-scores in the mask
+    dtype, the module's gate form at the step's temperature (unstructured tau over a sample of z,
+    structured top-N), the beta structural mix and the frozen override.  `sample_idx` optionally
+    injects the tau sample (the reference draws it with torch.randint, :993)."""
+    from .glu import _joint_params
+
+    if scores.numel() == 0:
+        return module.mask
+    S = scores.detach().contiguous()
+    if S.shape != module.mask.shape:
+        raise ValueError(f"scores shape {tuple(S.shape)} != mask shape {tuple(module.mask.shape)}")
+    mask = module.mask.data
+    frozen = module._mask_operands().frozen
+    rows, cols = S.shape
+    p = _joint_params(module, step, rows, cols, mask.dtype, frozen is not None, 0.0)
+    ops = K.MaskOperands(weight=S, mask=mask, hessian=S, frozen=frozen)
+    stats = K.score_stats(p, ops)
+    tau = None
+    if p.gate == L.GATE_UNSTRUCTURED:
+        if sample_idx is None:
+            sample_idx = module._sample_indices(S.numel(), S.device)
+        tau = K.tau_quantile(p, ops, stats, module._effective_sparsity(step), sample_idx)
+    return K.gate_target(p, ops, stats, tau, mask.dtype)
+
+
+@torch.no_grad()
 def calculate_flip_rate(model):
     """(flipped, ratio, init_flipped, init_ratio) summed over SparseLinear layers (:692-704)."""
     flipped = init_flipped = total = 0

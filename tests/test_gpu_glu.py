@@ -149,3 +149,66 @@ def test_calculate_model_mask_routes_glu_pairs(cuda_device):
     np.testing.assert_allclose(f(gm.mask), ref[0], rtol=0, atol=1e-6)
     np.testing.assert_allclose(f(um.mask), ref[1], rtol=0, atol=1e-6)
     np.testing.assert_allclose(f(dm.mask), ref_d[0], rtol=0, atol=1e-6)
+
+
+def _layer(cfg_kw, W, H, M, tdt, dev, aux=None):
+    sm = _sm()
+    cfg = sm.SparseLinearConfig(**cfg_kw)
+    cfg.enable_hutchinson = True
+    layer = sm.SparseLinear(W.shape[1], W.shape[0], sparselinear_config=cfg, bias=False).to(tdt).to(dev)
+    with torch.no_grad():
+        layer.weight.copy_(torch.as_tensor(W).to(tdt))
+        layer.hessian_diag.copy_(torch.as_tensor(H).to(tdt))
+        layer.mask.copy_(torch.as_tensor(M).to(tdt))
+    return layer
+
+
+@pytest.mark.parametrize("metric", ["hessian_ratio", "hessian_obd", "hessian", "magnitude"])
+@pytest.mark.parametrize("tdt", [torch.float32, torch.bfloat16])
+def test_compute_importance_scores_bit_exact(cuda_device, metric, tdt):
+    """utils._compute_importance_scores (legacy/utils.py:482-533) against oracle.masks.scores, bit for bit,
+    with the reference's result dtype (ragged cols: a tail group)."""
+    from sparseforge_amd import utils as U
+
+    rng = np.random.default_rng(4)
+    W = (rng.standard_normal((40, 70)) * 0.02).astype(np.float32)
+    H = (rng.random((40, 70)) * 1e-3 + 1e-7).astype(np.float32)
+    M = rng.random((40, 70)).astype(np.float32)
+    layer = _layer(dict(mask_metric=metric), W, H, M, tdt, cuda_device)
+    S = U._compute_importance_scores(layer)
+    dt = F32 if tdt == torch.float32 else BF16
+    Wd, Hd = (layer.weight.detach().float().cpu().numpy(), layer.hessian_diag.float().cpu().numpy())
+    ref = om.scores(Wd, Hd, None, metric, dt, dt)
+    assert S.dtype == tdt
+    np.testing.assert_array_equal(S.float().cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("kw", [dict(mask_type="unstructured"), dict(mask_type="structured"),
+                                dict(mask_type="unstructured", beta_structural_start=0, beta_structural_end=10)])
+@pytest.mark.parametrize("tdt", [torch.float32, torch.bfloat16])
+def test_compute_joint_gate_target_matches_oracle(cuda_device, kw, tdt):
+    """utils._compute_joint_gate_target (legacy/utils.py:536-613) on the summed scores of a gate/up pair,
+    with frozen flags, against oracle.masks.joint_gate_target: within 1e-6 (f32) / one bf16 ulp."""
+    from sparseforge_amd import utils as U
+
+    rng = np.random.default_rng(9)
+    shape = (64, 128)
+    Wg, Wu = [(rng.standard_normal(shape) * 0.02).astype(np.float32) for _ in range(2)]
+    Hg, Hu = [(rng.random(shape) * 1e-3 + 1e-6).astype(np.float32) for _ in range(2)]
+    Mg = rng.random(shape).astype(np.float32)
+    cfg_kw = dict(mask_metric="hessian_ratio", sparsity_warmup_steps=0, freeze_low=0.01, **kw)
+    gate = _layer(cfg_kw, Wg, Hg, Mg, tdt, cuda_device)
+    up = _layer(cfg_kw, Wu, Hu, Mg, tdt, cuda_device)
+    F = (rng.random(shape) < 0.1).astype(np.float32)
+    with torch.no_grad():
+        gate.frozen_mask_flags.copy_(torch.as_tensor(F).to(tdt))
+    S = U._compute_importance_scores(gate) + U._compute_importance_scores(up)
+    idx = torch.as_tensor(rng.integers(0, S.numel(), 3000)).to(cuda_device)
+    G = U._compute_joint_gate_target(gate, S, 7, sample_idx=idx)
+    dt = F32 if tdt == torch.float32 else BF16
+    ref = om.joint_gate_target(om.full_config(**cfg_kw), 7, S.float().cpu().numpy(), gate.mask.float().cpu().numpy(),
+                               F, idx.cpu().numpy(), dt)
+    assert G.dtype == tdt and G.shape == S.shape
+    tol = 1e-6 if dt == F32 else 2 ** -8
+    np.testing.assert_allclose(G.float().cpu().numpy(), ref, rtol=0, atol=tol)
+    np.testing.assert_array_equal(G.float().cpu().numpy()[F > 0], gate.mask.float().cpu().numpy()[F > 0])

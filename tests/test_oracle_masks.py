@@ -262,3 +262,26 @@ def test_block_update_matches_reference_golden(case):
         assert flips == int(r[f"flips{j}"])
         assert hx == float(r[f"hx{j}"])
         mask = r[f"mask{j}"].copy()
+
+
+@pytest.mark.parametrize("kw", [dict(mask_type="unstructured"), dict(mask_type="structured"),
+                                dict(mask_type="unstructured", beta_structural_start=0, beta_structural_end=10),
+                                dict(mask_type="structured", structured_exact=True)])
+def test_joint_gate_target_on_a_layers_own_scores_is_its_gate_target(kw):
+    """_compute_joint_gate_target(module, _compute_importance_scores(module), step) is
+    compute_gate_target(step) for an f32 layer (utils.py:482-613 vs sparse_modeling.py:1018-1239), which
+    the reference's own gate goldens pin; with frozen flags the override copies the current mask."""
+    rng = np.random.default_rng(11)
+    W = (rng.standard_normal((48, 64)) * 0.02).astype(np.float32)
+    H = (rng.random((48, 64)) * 1e-3 + 1e-6).astype(np.float32)
+    M = rng.random((48, 64)).astype(np.float32)
+    F = (rng.random((48, 64)) < 0.1).astype(np.float32)
+    idx = rng.integers(0, W.size, 500)
+    c = om.full_config(mask_metric="hessian_ratio", sparsity_warmup_steps=0, **kw)
+    S = om.scores(W, H, None, "hessian_ratio")
+    for frozen in (None, F):
+        a = om.joint_gate_target(c, 7, S, M, frozen, idx)
+        b = om.layer_gate_target(c, 7, W, H, M, frozen, idx)
+        np.testing.assert_array_equal(a, b)
+        if frozen is not None:
+            np.testing.assert_array_equal(a[F > 0], M[F > 0])
