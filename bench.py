@@ -12,6 +12,9 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
   keeps it for the input gradient; the GEMMs then read it.  Throughput counts
   the algorithmic 6 T in out + 6 T r (in + out) FLOPs per linear;
   ``per_linear`` times each linear alone.
+* ``gemm_vs_hipblaslt`` -- the three big products (fwd, dx, dW) of each 7B
+  linear shape through sf_gemm and through torch.matmul (hipBLASLt), and the
+  layer's 21 products summed.
 * ``hutchinson_probe_layer`` -- one Hutchinson probe of the same seven linears
   (create_graph gradients, probe dot, double backward, accumulator updates).
 * ``mask_update`` -- one step = the periodic mask update of every linear of
@@ -22,7 +25,8 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
   the 224 layers share their parameters, so the update is batched as
   calculate_model_mask batches it (sf_update_mask_multi, 28 layers per
   launch).  GB/s counts 20 B per parameter (stats pass: W 2 + H 4; update pass: W 2 +
-  H 4 + mask read 4 + mask write 4).
+  H 4 + mask read 4 + mask write 4).  ``hbm_sustained`` is what a stream of
+  the same traffic with token arithmetic sustains (sf_hbm_probe).
 * ``hutchinson`` -- the accumulator update of every linear of the 7B arena
   (f32 accumulator read and written, bf16 Hessian-vector product, probe
   regenerated): 10 B per parameter.
@@ -79,7 +83,7 @@ PEAK_BF16_SPARSE_TFLOPS = 5000.0  # MI355X 2:4-sparse bf16 MFMA (dense-equivalen
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 MASK_BYTES_PER_PARAM = 20   # stats pass 6 B + update pass 14 B
 ADAMW_BYTES_PER_PARAM = 32  # master r/w 8, grad 2, m r/w 8, v r/w 8, mask 4, bf16 copy 2
-ALL_LEGS = ("linear", "mask", "hutch", "adamw", "bsr", "kl", "s24", "e2e")
+ALL_LEGS = ("linear", "blas", "mask", "hutch", "adamw", "bsr", "kl", "s24", "e2e")
 HUTCH_BYTES_PER_PARAM = 10  # accumulator f32 r/w 8, Hessian-vector product bf16 2 (probe regenerated)
 
 
@@ -100,7 +104,7 @@ def profiled_traffic() -> dict:
                 if line.startswith("bench-traffic:"):
                     for kv in line.split(":", 1)[1].split():
                         k, v = kv.split("=")
-                        out[k] = int(v)
+                        out[k] = float(v) if "." in v else int(v)
     except OSError:
         pass
     return out
@@ -468,6 +472,86 @@ def mfma_sustained(torch, dev, iters: int = 4000, blocks: int = 1024, reps: int 
     return best
 
 
+def blas_leg(torch, dev, tokens: int, reps: int = 20) -> dict:
+    """The three GEMM products of each distinct 7B linear shape (fwd x W^T, dx = gy W, dW = gy^T x; bf16,
+    no mask, no SLoRB) through sf_gemm and through torch.matmul (hipBLASLt), and the layer's 21 products
+    weighted by how many linears share each shape."""
+    from sparseforge_amd import linear as lin
+
+    def timeit(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    rows, tot = {}, {"sf_gemm": 0.0, "hipblaslt": 0.0}
+    count = {}
+    for _name, fin, fout in LINEARS:
+        count[(fin, fout)] = count.get((fin, fout), 0) + 1
+    flops_layer = 0.0
+    for (fin, fout), k in count.items():
+        x = torch.randn(tokens, fin, generator=g, device=dev).to(torch.bfloat16)
+        W = (torch.randn(fout, fin, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        gy = torch.randn(tokens, fout, generator=g, device=dev).to(torch.bfloat16)
+        fl = 2.0 * tokens * fin * fout
+        prods = {"fwd": (lambda: lin.mm_nt(x, W), lambda: x @ W.t()),
+                 "dx": (lambda: lin.mm_nn(gy, W), lambda: gy @ W),
+                 "dw": (lambda: lin.mm_tn(gy, x), lambda: gy.t() @ x)}
+        row = {}
+        for pname, (f_sf, f_bl) in prods.items():
+            a, b = timeit(f_sf), timeit(f_bl)
+            row[pname] = {"sf_gemm_TFLOP/s": round(fl / a / 1e9, 1), "hipblaslt_TFLOP/s": round(fl / b / 1e9, 1)}
+            tot["sf_gemm"] += k * a
+            tot["hipblaslt"] += k * b
+            flops_layer += k * fl
+        rows[f"{fout}x{fin}"] = row
+        del x, W, gy
+    torch.cuda.empty_cache()
+    out = {"tokens": tokens, "products": rows,
+           "layer_21_products_ms": {k: round(v, 3) for k, v in tot.items()},
+           "layer_21_products_TFLOP/s": {k: round(flops_layer / v / 1e9, 1) for k, v in tot.items()}}
+    log("GEMM vs hipBLASLt, the layer's 21 products: " + ", ".join(
+        f"{k} {v:.2f} ms" for k, v in out["layer_21_products_ms"].items()))
+    return out
+
+
+def hbm_sustained(torch, dev, n: int = 180 * (1 << 20), reps: int = 5) -> dict:
+    """GB/s of sf_hbm_probe's streams (token arithmetic) over n elements, best over grid sizes and reps:
+    what this GPU's HBM sustains for the fused mask update's traffic (read W bf16, H f32, M f32, write M:
+    14 B/elem), the score statistics' (read W, H: 6 B/elem) and a plain copy (8 B/elem)."""
+    from sparseforge_amd import _lib as L
+
+    W = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    H = torch.zeros(n, dtype=torch.float32, device=dev)
+    M = torch.zeros(n, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    out = {}
+    for name, pattern, nbytes in (("update_pattern", 0, 14), ("stats_pattern", 1, 6), ("copy", 2, 8)):
+        best = 0.0
+        for blocks in (2048, 4096, 16384):
+            for r in range(reps + 2):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(st)
+                L.check(L.lib().sf_hbm_probe(pattern, L.ptr(W), L.ptr(H), L.ptr(M), n, blocks, L.stream(dev)),
+                        "sf_hbm_probe")
+                e1.record(st)
+                e1.synchronize()
+                if r >= 2:
+                    best = max(best, nbytes * n / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+        out[name] = round(best, 1)
+    del W, H, M
+    torch.cuda.empty_cache()
+    log("HBM probe: " + ", ".join(f"{k} {v:.0f} GB/s" for k, v in out.items()))
+    return out
+
+
 def cpu_baseline(budget_s: float = 15.0, tokens: int = 512) -> dict:
     import numpy as np
 
@@ -680,7 +764,9 @@ def hutch_arena_leg(torch, arena, steps: int) -> dict:
             "roofline": {"bound": "hbm", "kernel": "sf_hutchinson_update (hutch_update_vec_kernel)",
                          "achieved": round(k_.rate / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(k_.rate / 1e9 / PEAK_HBM_GBS, 4), "launches": k_.launches,
-                         "avg_launch_ms": round(k_.avg_ms, 4)}}
+                         "avg_launch_ms": round(k_.avg_ms, 4),
+                         "traffic": profiled_traffic().get("sf_hutch_bytes_per_param"), "traffic_unit": "B/param",
+                         "traffic_source": TRAFFIC_SUMMARY}}
 
 
 def main(argv=None) -> int:
@@ -760,6 +846,8 @@ def main(argv=None) -> int:
     out = {"metric": "SparseLinear fwd+bwd TFLOP/s @7B shapes; 2:4 mask-update HBM GB/s"}
     if "linear" in legs:
         out.update(linear_leg(torch, sm, prof, dev, a))
+    if "blas" in legs:
+        out["gemm_vs_hipblaslt"] = blas_leg(torch, dev, a.tokens)
     if legs & {"mask", "hutch", "adamw"}:
         arena_legs(torch, L, K, prof, dev, a, legs, out)
     # ---- block-sparse-16 leg (gate/up shape, block densities 0.5 and 0.25) ----
@@ -877,6 +965,7 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
                 mask_step(L, K, jobs, mws, a.mask_steps, stg)
             stage_ms[name] = mt.summary()["sf_update_mask_multi"]
         mask_gbs = MASK_BYTES_PER_PARAM * n_params * a.mask_steps / mel / 1e9
+        sustained = hbm_sustained(torch, dev)
         up = stage_ms["update"]
         up_gbs = up.rate / 1e9
         st_gbs = stage_ms["stats"].rate / 1e9
@@ -901,9 +990,15 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
             "roofline": {"bound": "hbm", "kernel": "sf_update_mask_multi (update stage, update_mask_multi_kernel)",
                          "achieved": round(up_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(up_gbs / PEAK_HBM_GBS, 4),
-                         "traffic": traffic.get("sf_update_mask_bytes_per_launch"), "traffic_unit": "B/launch",
-                         "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4)},
+                         "traffic": traffic.get("sf_update_mask_bytes_per_param"), "traffic_unit": "B/param",
+                         "bytes_per_param": 14, "avg_launch_ms": round(up.avg_ms, 4),
+                         "frac_of_sustained": round(up_gbs / sustained["update_pattern"], 4)},
             "arena_frac": round(mask_gbs / PEAK_HBM_GBS, 4),
+            "hbm_sustained": sustained,
+            # the arena's best time at the sustained rates of its two streams (update 14 B, statistics 6 B per
+            # param, the tau select free) against the measured update
+            "arena_frac_of_sustained": round(
+                (14 / sustained["update_pattern"] + 6 / sustained["stats_pattern"]) * mask_gbs / 20, 4),
             "score_stats_gbs": round(st_gbs, 2),
             "stage_ms": {k: round(v.total_ms, 3) for k, v in stage_ms.items()},
             "mask_stats": {"kernel": "sf_mask_stats", "GB/s": round(mstats_gbs, 2), "bytes_per_param": 4,
@@ -953,7 +1048,7 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
         "roofline": {"bound": "hbm", "kernel": "sf_adamw_step_multi (adamw_multi_kernel)",
                      "achieved": round(as_.rate / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(as_.rate / 1e9 / PEAK_HBM_GBS, 4),
-                     "traffic": traffic.get("sf_adamw_step_multi_bytes_per_launch"), "traffic_unit": "B/launch",
+                     "traffic": traffic.get("sf_adamw_bytes_per_param"), "traffic_unit": "B/param",
                      "launches": as_.launches, "avg_launch_ms": round(as_.avg_ms, 4)},
     }
     del arena, opt_state, items

@@ -716,6 +716,17 @@ int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const void* vals, c
  */
 int sf_mfma_probe(int iters, int blocks, float* out, void* stream);
 
+/*
+ * Sustained HBM rate probe, a measurement aid with no counterpart in the
+ * reference (bench.py reports the rates beside the mask kernels' GB/s): a
+ * grid-stride stream over n elements (n % 4 == 0, 16-byte aligned operands)
+ * with a token FMA per element.  pattern 0: the fused mask update's traffic
+ * (read W bf16, H f32, M f32; write M f32: 14 B / element); 1: the score
+ * statistics' (read W, H: 6 B / element; M receives blocks * 256 floats);
+ * 2: a copy (read H, write M: 8 B / element).
+ */
+int sf_hbm_probe(int pattern, const void* W, const void* H, void* M, int64_t n, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,7 +78,49 @@ __global__ void __launch_bounds__(256, 1) mfma_probe_kernel(int iters, float* __
   out[t] = s;
 }
 }  // namespace
+// Streaming patterns of the HBM probe (n elements, vector of 4 per thread and round):
+//   0: the fused mask update's traffic: read W (bf16), H (f32), M (f32), write M (14 B / element)
+//   1: the score statistics' traffic: read W (bf16), H (f32) (6 B / element), one f32 per thread to M
+//   2: a copy: read H (f32), write M (f32) (8 B / element)
+// The arithmetic is a token FMA per element, so only the memory system limits it.
+__global__ void __launch_bounds__(256) hbm_probe_kernel(int pattern, const uint2* __restrict__ W,
+                                                        const float4* __restrict__ H, float4* __restrict__ M,
+                                                        int64_t n4) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  float acc = 0.0f;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const float4 h = H[i];
+    if (pattern == 2) {
+      M[i] = h;
+      continue;
+    }
+    const uint2 w = W[i];
+    const float a = __uint_as_float(w.x << 16), b = __uint_as_float(w.x & 0xffff0000u);
+    const float c = __uint_as_float(w.y << 16), d = __uint_as_float(w.y & 0xffff0000u);
+    if (pattern == 1) {
+      acc += a * h.x + b * h.y + c * h.z + d * h.w;
+      continue;
+    }
+    float4 m = M[i];
+    m.x = fmaf(a, h.x, m.x * 0.9f);
+    m.y = fmaf(b, h.y, m.y * 0.9f);
+    m.z = fmaf(c, h.z, m.z * 0.9f);
+    m.w = fmaf(d, h.w, m.w * 0.9f);
+    M[i] = m;
+  }
+  if (pattern == 1) reinterpret_cast<float*>(M)[blockIdx.x * (int64_t)blockDim.x + threadIdx.x] = acc;
+}
 }  // namespace sf
+
+extern "C" int sf_hbm_probe(int pattern, const void* W, const void* H, void* M, int64_t n, int blocks, void* stream) {
+  SF_CHECK_ARG(pattern >= 0 && pattern <= 2, "bad probe pattern %d", pattern);
+  SF_CHECK_ARG(n > 0 && n % 4 == 0 && blocks > 0, "bad probe size (n %lld, blocks %d)", (long long)n, blocks);
+  SF_CHECK_ARG((pattern == 2 || W) && H && M, "null tensor");
+  SF_CHECK_ARG(pattern != 1 || (int64_t)blocks * 256 <= n, "pattern 1 writes one float per thread to M");
+  sf::hbm_probe_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      pattern, static_cast<const uint2*>(W), static_cast<const float4*>(H), static_cast<float4*>(M), n / 4);
+  return sf::launch_status("sf_hbm_probe");
+}
 
 // out: device float[blocks * 256] (checksums).  FLOPs = blocks * 4 * iters * 16 * 32768.
 extern "C" int sf_mfma_probe(int iters, int blocks, float* out, void* stream) {
