@@ -746,22 +746,22 @@ def hutch_arena_leg(torch, arena, steps: int) -> dict:
     from sparseforge_amd import utils as U
 
     n = sum(W.numel() for W, _, _ in arena)
-    for k, (W, H, _M) in enumerate(arena):  # warmup
-        U.hutchinson_update_(H, W, 0.98, seed=k)
+    # the whole arena in one multi-tensor call, as update_hessian_hutchinson issues it (the arena's bf16 W
+    # stands in for the bf16 Hessian-vector product)
+    U.hutchinson_update_multi_([(H, W, 0.98, k) for k, (W, H, _M) in enumerate(arena)])  # warmup
     torch.cuda.synchronize()
     with prof.kernel_timer() as kt:
         t0 = time.perf_counter()
         for s_ in range(steps):
-            for k, (W, H, _M) in enumerate(arena):  # the arena's bf16 W stands in for the bf16 hvp
-                U.hutchinson_update_(H, W, 0.98, seed=(s_ + 1) * 1000 + k)
+            U.hutchinson_update_multi_([(H, W, 0.98, (s_ + 1) * 1000 + k) for k, (W, H, _M) in enumerate(arena)])
         torch.cuda.synchronize()
         el = time.perf_counter() - t0
-    k_ = kt.summary()["sf_hutchinson_update"]
+    k_ = kt.summary()["sf_hutchinson_update_multi"]
     gbs = HUTCH_BYTES_PER_PARAM * n * steps / el / 1e9
     log(f"hutchinson update: {el * 1e3 / steps:.2f} ms over the arena, {gbs:.0f} GB/s; kernel {k_.rate / 1e9:.0f} GB/s")
     return {"value": round(gbs, 2), "unit": "GB/s", "params": n, "steps": steps,
             "ms_per_step": round(el * 1e3 / steps, 3), "bytes_per_param": HUTCH_BYTES_PER_PARAM,
-            "roofline": {"bound": "hbm", "kernel": "sf_hutchinson_update (hutch_update_vec_kernel)",
+            "roofline": {"bound": "hbm", "kernel": "sf_hutchinson_update_multi (hutch_update_multi_kernel)",
                          "achieved": round(k_.rate / 1e9, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": round(k_.rate / 1e9 / PEAK_HBM_GBS, 4), "launches": k_.launches,
                          "avg_launch_ms": round(k_.avg_ms, 4),

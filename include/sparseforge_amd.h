@@ -601,6 +601,23 @@ int sf_rademacher_dot(const void* g, int g_dtype, const void* v, int v_dtype, in
 int sf_hutchinson_update(void* H, int h_dtype, const void* hvp, int hvp_dtype, const void* v, int v_dtype, int64_t n,
                          uint64_t seed, double beta, void* stream);
 
+/* One tensor of sf_hutchinson_update_multi (probe regenerated from its seed). */
+typedef struct sf_hutch_tensor {
+  void* H;          /* hessian_diag, updated in place */
+  const void* hvp;  /* the Hessian-vector product */
+  int64_t n;        /* elements, a multiple of 4; H and hvp 4-element aligned */
+  uint64_t seed;
+  double beta;
+} sf_hutch_tensor;
+
+/*
+ * sf_hutchinson_update over many tensors (the per-weight loop of
+ * update_hessian_hutchinson, legacy/utils.py:806-868), 48 tensors per
+ * launch; every element gets the value sf_hutchinson_update gives it.
+ */
+int sf_hutchinson_update_multi(const sf_hutch_tensor* tensors, int count, int h_dtype, int hvp_dtype,
+                               void* stream);
+
 /* ---------------------------------------------------------------------------
  * Mask statistics and penalties: one fused pass per mask tensor
  * (legacy/utils.py mid_penalty :876-938, sparsity_penalty :942-1025,

@@ -193,6 +193,18 @@ class MaskLayer(ctypes.Structure):
     ]
 
 
+class HutchTensor(ctypes.Structure):
+    """Mirror of ``sf_hutch_tensor``."""
+
+    _fields_ = [
+        ("H", ctypes.c_void_p),
+        ("hvp", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
+        ("seed", ctypes.c_uint64),
+        ("beta", ctypes.c_double),
+    ]
+
+
 class AdamwParams(ctypes.Structure):
     """Mirror of ``sf_adamw_params``."""
 
@@ -263,6 +275,7 @@ SIGNATURES = {
     "sf_rademacher": (_I, [_P, _I, _I64, ctypes.c_uint64, _P]),
     "sf_rademacher_dot_workspace_size": (_SZ, []),
     "sf_rademacher_dot": (_I, [_P, _I, _P, _I, _I64, ctypes.c_uint64, _P, _P, _SZ, _P]),
+    "sf_hutchinson_update_multi": (_I, [ctypes.POINTER(HutchTensor), _I, _I, _I, _P]),
     "sf_hutchinson_update": (_I, [_P, _I, _P, _I, _P, _I, _I64, ctypes.c_uint64, ctypes.c_double, _P]),
     "sf_mask_stats_workspace_size": (_SZ, []),
     "sf_mask_stats": (_I, [_P, _I, _I64, _I64, _I64, _F, _P, _P, _SZ, _P]),

@@ -145,6 +145,61 @@ __global__ void __launch_bounds__(kBlock) hutch_update_vec_kernel(void* __restri
   }
 }
 
+// Multi-tensor accumulator update: one launch covers up to kHutchMulti
+// tensors (table in the kernel arguments).  Tensor i owns workgroups
+// [first[i], first[i + 1]), grid-striding over its float4s like the single
+// kernel with its own workgroup count, so every element gets the single
+// kernel's value (the probe bit depends only on (seed, element index)).
+constexpr int kHutchMulti = 48;
+struct HutchEntry {
+  void* H;
+  const void* hvp;
+  int64_t n4;
+  uint64_t seed;
+  float beta, omb;
+};
+struct HutchArgs {
+  int count, h_dtype, hvp_dtype, est_dtype;
+  int32_t first[kHutchMulti + 1];
+  HutchEntry t[kHutchMulti];
+};
+static_assert(sizeof(HutchArgs) <= 4000, "Hutchinson table exceeds the kernel argument budget");
+
+template <int HD>
+__global__ void __launch_bounds__(kBlock) hutch_update_multi_kernel(HutchArgs a) {
+  const int b = blockIdx.x;
+  int i = 0;
+#pragma unroll
+  for (int k = 1; k < kHutchMulti; ++k) i += (k < a.count && a.first[k] <= b) ? 1 : 0;
+  const HutchEntry& e = a.t[i];
+  const int64_t nblk = a.first[i + 1] - a.first[i];
+  const int64_t stride = nblk * kBlock;
+  for (int64_t j = (b - a.first[i]) * (int64_t)kBlock + threadIdx.x; j < e.n4; j += stride) {
+    float h[4], x[4];
+    ld4v<float>(e.H, 4 * j, HD, h);
+    ld4v<float>(e.hvp, 4 * j, a.hvp_dtype, x);
+    const int64_t i0 = 4 * j;
+    const uint64_t word = counter_hash(e.seed, static_cast<uint64_t>(i0) >> 6);
+    float out[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float v = ((word >> ((i0 + q) & 63)) & 1ull) ? 1.0f : -1.0f;
+      float est = rnd(x[q] * v, a.est_dtype);
+      est = est < 0.0f ? 0.0f : est;
+      const float hb = rnd(h[q] * e.beta, HD);
+      out[q] = rnd(fmaf(est, e.omb, hb), HD);
+    }
+    if (HD == SF_DTYPE_F32) {
+      *reinterpret_cast<float4*>(static_cast<float*>(e.H) + i0) = make_float4(out[0], out[1], out[2], out[3]);
+    } else {
+      uint2 o;
+      o.x = static_cast<uint32_t>(f32_to_bf16(out[0])) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
+      o.y = static_cast<uint32_t>(f32_to_bf16(out[2])) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.H) + i0) = o;
+    }
+  }
+}
+
 bool dt_ok(int d) { return d == SF_DTYPE_F32 || d == SF_DTYPE_BF16; }
 
 }  // namespace
@@ -200,4 +255,54 @@ extern "C" int sf_hutchinson_update(void* H, int h_dtype, const void* hvp, int h
     hutch_update_kernel<SF_DTYPE_BF16><<<grid, kBlock, 0, st>>>(H, hvp, hvp_dtype, v, v_dtype, est_dtype, n, seed, b,
                                                                 omb);
   return launch_status("sf_hutchinson_update");
+}
+
+extern "C" int sf_hutchinson_update_multi(const sf_hutch_tensor* tensors, int count, int h_dtype, int hvp_dtype,
+                                          void* stream) {
+  SF_CHECK_ARG(count >= 0 && (count == 0 || tensors), "bad tensor table (count %d)", count);
+  SF_CHECK_ARG(dt_ok(h_dtype) && dt_ok(hvp_dtype), "bad dtype");
+  auto al = [](const void* q, int dt) { return (reinterpret_cast<uintptr_t>(q) % (dt == SF_DTYPE_F32 ? 16 : 8)) == 0; };
+  for (int i = 0; i < count; ++i) {
+    const sf_hutch_tensor& t = tensors[i];
+    SF_CHECK_ARG(t.n >= 0 && t.n % 4 == 0, "tensor %d: n = %lld is not a multiple of 4", i, (long long)t.n);
+    if (t.n == 0) continue;
+    SF_CHECK_ARG(t.H && t.hvp, "tensor %d: null tensor", i);
+    SF_CHECK_ARG(al(t.H, h_dtype) && al(t.hvp, hvp_dtype), "tensor %d: operands not 4-element aligned", i);
+  }
+  const int est_dtype = hvp_dtype == SF_DTYPE_F32 ? SF_DTYPE_F32 : SF_DTYPE_BF16;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  HutchArgs a;
+  int i = 0;
+  while (i < count) {
+    memset(&a, 0, sizeof(a));
+    a.h_dtype = h_dtype;
+    a.hvp_dtype = hvp_dtype;
+    a.est_dtype = est_dtype;
+    int n = 0;
+    int64_t blocks = 0;
+    for (; i < count && n < kHutchMulti; ++i) {
+      const sf_hutch_tensor& t = tensors[i];
+      if (t.n == 0) continue;
+      HutchEntry& e = a.t[n];
+      e.H = t.H;
+      e.hvp = t.hvp;
+      e.n4 = t.n / 4;
+      e.seed = t.seed;
+      e.beta = static_cast<float>(t.beta);
+      e.omb = static_cast<float>(1.0 - t.beta);
+      a.first[n] = static_cast<int32_t>(blocks);
+      // the single kernel's grid for this tensor (its workgroups stride over it the same way)
+      blocks += elementwise_grid((e.n4 + 1) / 2, kBlock);
+      ++n;
+    }
+    if (n == 0) break;
+    a.count = n;
+    a.first[n] = static_cast<int32_t>(blocks);
+    if (h_dtype == SF_DTYPE_F32)
+      hutch_update_multi_kernel<SF_DTYPE_F32><<<static_cast<int>(blocks), kBlock, 0, st>>>(a);
+    else
+      hutch_update_multi_kernel<SF_DTYPE_BF16><<<static_cast<int>(blocks), kBlock, 0, st>>>(a);
+    if (int rc = launch_status("sf_hutchinson_update_multi")) return rc;
+  }
+  return SF_OK;
 }

@@ -8,6 +8,7 @@ hot-path helpers:
   calculate_model_mask (with the GLU gate/up joint update)         (:184-643)
   calculate_flip_rate                                              (:692-704)
   _rademacher_like, update_hessian_hutchinson                      (:710-869)
+  _compute_importance_scores, _compute_joint_gate_target           (:482-613)
   update_mask_penalty_lr                                           (:142-180)
   mid_penalty, sparsity_penalty, nm_2_4_tile_stats, harden_fraction (:876-1276)
   mask_stats, log_mask_stats                                       (:2069-2335)
@@ -138,7 +139,7 @@ def calculate_model_mask(model, step=0, lambda_mid: float = 0.0):
     handled = set(pairs) | set(pairs.values())
     for m in mods.values():
         m._in_summon_context = False
-    # layers are independent: their update chains run on a few side streams and overlap
+    # GLU pairs and the staged block-type updates run on a few side streams and overlap
     devs = {m.mask.device for m in mods.values()}
     pipe = K.LayerPipeline(next(iter(devs))) if len(devs) == 1 and next(iter(devs)).type == "cuda" else None
     for gate_name, up_name in pairs.items():
@@ -301,6 +302,34 @@ def hutchinson_update_(H: torch.Tensor, hvp: torch.Tensor, beta: float, seed: in
                 "sf_hutchinson_update")
 
 
+def hutchinson_update_multi_(items) -> None:
+    """hutchinson_update_ over many (H, hvp, beta, seed) with regenerated probes in a few launches
+    (sf_hutchinson_update_multi: 48 tensors per launch); every element gets the single call's value.
+    Items whose sizes are not multiples of 4 take the single call."""
+    groups: dict = {}
+    for H, hvp, beta, seed in items:
+        hvp = hvp.contiguous()
+        L.require_device(H, hvp)
+        if hvp.numel() != H.numel():
+            raise ValueError("hutchinson: hvp / hessian_diag sizes differ")
+        if H.numel() % 4 or H.data_ptr() % 16 or hvp.data_ptr() % 16:
+            hutchinson_update_(H, hvp, beta, seed=seed)
+            continue
+        groups.setdefault((H.device, H.dtype, hvp.dtype), []).append((H, hvp, beta, seed))
+    for (dev, hdt, gdt), grp in groups.items():
+        table = (L.HutchTensor * len(grp))()
+        nbytes = 0
+        for i, (H, hvp, beta, seed) in enumerate(grp):
+            e = table[i]
+            e.H, e.hvp, e.n = L.ptr(H), L.ptr(hvp), H.numel()
+            e.seed, e.beta = seed & ((1 << 64) - 1), float(beta)
+            nbytes += H.numel() * (2 * H.element_size() + hvp.element_size())
+        with _prof.region("sf_hutchinson_update_multi", nbytes, "B", dev):
+            L.check(L.lib().sf_hutchinson_update_multi(table, len(grp), L.dtype_code(grp[0][0]),
+                                                       L.dtype_code(grp[0][1]), L.stream(dev)),
+                    "sf_hutchinson_update_multi")
+
+
 def update_hessian_hutchinson(model, loss, probes=None):
     """Hutchinson update of every SparseLinear's hessian_diag (:714-869); call before loss.backward().
 
@@ -341,10 +370,14 @@ def update_hessian_hutchinson(model, loss, probes=None):
     except Exception:
         world = 1
     with torch.no_grad():
+        batched = []  # probes regenerated from their seeds: one multi-tensor update
         for m, hvp, seed, v in zip(owners, hvps, seeds, vs):
             if hvp is None or seed is None or m._is_placeholder("hessian_diag"):
                 continue
             beta = float(getattr(m.cfg, "beta", 0.99))
+            if world == 1 and v is None:
+                batched.append((m.hessian_diag.data, hvp.detach(), beta, seed))
+                continue
             if world > 1:
                 # data-parallel ranks average their estimates before the EMA (:863-865)
                 vv = v if v is not None else rademacher(hvp.shape, hvp.dtype, hvp.device, seed)
@@ -354,6 +387,8 @@ def update_hessian_hutchinson(model, loss, probes=None):
                 hutchinson_update_(m.hessian_diag.data, est, beta, v=torch.ones_like(est))
             else:
                 hutchinson_update_(m.hessian_diag.data, hvp.detach(), beta, seed=seed, v=v)
+        if batched:
+            hutchinson_update_multi_(batched)
 
 
 # ---------------------------------------------------------------------------

@@ -169,3 +169,27 @@ def test_vector_update_equals_scalar_update(cuda_device, hdt, vdt):
     v = utils.rademacher((n,), hvp.dtype, cuda_device, seed)
     utils.hutchinson_update_(b, hvp, 0.98, v=v)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("hdt,vdt", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.bfloat16),
+                                     (torch.float32, torch.float32)])
+def test_multi_tensor_update_equals_single_updates(cuda_device, hdt, vdt):
+    """hutchinson_update_multi_ (sf_hutchinson_update_multi, 48 tensors per launch) equals one
+    hutchinson_update_ per tensor bit for bit: 53 tensors (two launches) of mixed sizes, one not a
+    multiple of 4 (it takes the single call), different seeds and betas."""
+    from sparseforge_amd import utils
+
+    g = torch.Generator(device=cuda_device).manual_seed(8)
+    sizes = [4096 * (1 + (k * 37) % 300) for k in range(52)] + [4099]
+    items_a, items_b = [], []
+    for k, n in enumerate(sizes):
+        H = (torch.rand(n, generator=g, device=cuda_device) * 1e-3).to(hdt)
+        hvp = torch.randn(n, generator=g, device=cuda_device).to(vdt)
+        beta = 0.98 if k % 3 else 0.9
+        items_a.append((H.clone(), hvp, beta, 1000 + k))
+        items_b.append((H.clone(), hvp, beta, 1000 + k))
+    utils.hutchinson_update_multi_(items_a)
+    for H, hvp, beta, seed in items_b:
+        utils.hutchinson_update_(H, hvp, beta, seed=seed)
+    for (a, *_), (b, *_) in zip(items_a, items_b):
+        assert torch.equal(a, b)
