@@ -1753,6 +1753,266 @@ int launch_bsr_kernel(K kern, bool& attr, const GemmArgs& g, hipStream_t st, con
   return launch_status(what);
 }
 
+// ---------------------------------------------------------------------------
+// Skinny products: one side of C at most 64 wide (the SLoRB terms z = x P^T,
+// dz = dy S, dP = dz^T x, dS = dy^T z at rank 64).  On the 256 x 256 tile
+// three quarters of every MFMA would multiply padding, so these run on a
+// 128 x 64 tile: C' [M', N' <= 64] = A' B'^T, 4 waves of 32 long-side rows by
+// the 64 short-side columns (2 v_mfma_f32_32x32x16_bf16 per 16-k step), 64-k
+// stages double-buffered in LDS through registers (the M/N-contiguous layouts
+// are transposed while they are written to LDS), split-K over enough
+// workgroups to fill the GPU, f32 partials reduced by splitk_reduce_kernel
+// (which applies the output epilogue).  When C's short side is its rows
+// (M <= 64) the roles swap (A' = B, B' = A) and so do the MFMA operands, so
+// the accumulators come out in C's orientation and the partial stores stay
+// coalesced.
+// ---------------------------------------------------------------------------
+constexpr int kSkM = 128, kSkN = 64, kSkK = 64, kSkPitch = kSkK + 8;  // LDS row: 64 bf16 + 16 B of padding
+
+struct SkinnyArgs {
+  const uint16_t* A;  // A' (long side M'): layout AL
+  const uint16_t* B;  // B' (short side N' <= 64): layout BL
+  int64_t lda, ldb;
+  int64_t M, N, K;    // M' (long), N' (short), K
+  int64_t split_stages;
+  float* partial;     // [splits][C rows][C cols]
+};
+
+template <int AL, int BL, bool TOUT>
+__global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs g) {
+  __shared__ __align__(16) uint16_t As[2][kSkM][kSkPitch];  // [m][k]
+  __shared__ __align__(16) uint16_t Bs[2][kSkN][kSkPitch];  // [n][k]
+  const int64_t tiles = ceil_div(g.M, kSkM);
+  const int64_t kz = blockIdx.x / tiles;
+  const int64_t m0 = (blockIdx.x - kz * tiles) * kSkM;
+  const int64_t nk = ceil_div(g.K, kSkK);
+  const int64_t s0 = kz * g.split_stages;
+  const int64_t s1 = s0 + g.split_stages < nk ? s0 + g.split_stages : nk;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+  // Register stage of one K step.  K layout: 16-byte chunks of rows, stored as they are.
+  // MN layout: A' as a 4 (k) x 8 (m) block per thread (k fastest over the threads), B' as
+  // a 2 (k) x 8 (n) block; both are transposed in registers, so every LDS write is one
+  // 8- or 4-byte word and both the writes and the MFMA operand reads are free of bank
+  // conflicts at the 144-byte row pitch.
+  struct Stage {
+    uint4 a[4], b[2];
+  };
+  // Loads are unconditional, so the compiler's wait counts stay exact and two steps stay in
+  // flight: a lane outside the split's K range or outside M' / N' reads the operand's first
+  // chunk, and the store to LDS (where the data is first needed) replaces it with zeros.
+  const int64_t kend = s1 * kSkK < g.K ? s1 * kSkK : g.K;
+  auto a_ok = [&](int64_t k0, int i) {
+    if constexpr (AL == 0) {
+      const int c = t + 256 * i;
+      return m0 + (c >> 3) < g.M && k0 + (c & 7) * 8 < kend;
+    } else {
+      return k0 + (t & 15) * 4 + i < kend && m0 + (t >> 4) * 8 < g.M;
+    }
+  };
+  auto b_ok = [&](int64_t k0, int i) {
+    if constexpr (BL == 0) {
+      const int c = t + 256 * i;
+      return (c >> 3) < g.N && k0 + (c & 7) * 8 < kend;
+    } else {
+      return k0 + (t & 31) * 2 + i < kend && (t >> 5) * 8 < g.N;
+    }
+  };
+  auto gload = [&](Stage& r, int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // A' tile: 128 rows x 64 k
+      int64_t off;
+      if constexpr (AL == 0) {
+        const int c = t + 256 * i;
+        off = (m0 + (c >> 3)) * g.lda + k0 + (c & 7) * 8;
+      } else {
+        off = (k0 + (t & 15) * 4 + i) * g.lda + m0 + (t >> 4) * 8;
+      }
+      r.a[i] = *reinterpret_cast<const uint4*>(g.A + (a_ok(k0, i) ? off : 0));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // B' tile: 64 rows x 64 k
+      int64_t off;
+      if constexpr (BL == 0) {
+        const int c = t + 256 * i;
+        off = (c >> 3) * g.ldb + k0 + (c & 7) * 8;
+      } else {
+        off = (k0 + (t & 31) * 2 + i) * g.ldb + (t >> 5) * 8;
+      }
+      r.b[i] = *reinterpret_cast<const uint4*>(g.B + (b_ok(k0, i) ? off : 0));
+    }
+  };
+  auto zap = [](const uint4& v, bool ok) {
+    return make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
+  };
+  // (lo16(x), lo16(y)) or (hi16(x), hi16(y)) packed into one word: element i of two rows.
+  auto pair = [](uint32_t x, uint32_t y, int i) {
+    return __builtin_amdgcn_perm(y, x, (i & 1) ? 0x07060302u : 0x05040100u);
+  };
+  auto word = [](const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; };
+  auto sstore = [&](int buf, const Stage& raw, int64_t k0) {
+    Stage r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.a[i] = zap(raw.a[i], a_ok(k0, i));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) r.b[i] = zap(raw.b[i], b_ok(k0, i));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (AL == 0) {
+        const int c = t + 256 * i;
+        *reinterpret_cast<uint4*>(&As[buf][c >> 3][(c & 7) * 8]) = r.a[i];
+      }
+    }
+    if constexpr (AL != 0) {
+      const int kq = (t & 15) * 4, mb = (t >> 4) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // row m = mb + i: k-values kq .. kq + 3
+        const uint32_t lo = pair(word(r.a[0], i >> 1), word(r.a[1], i >> 1), i);
+        const uint32_t hi = pair(word(r.a[2], i >> 1), word(r.a[3], i >> 1), i);
+        *reinterpret_cast<uint2*>(&As[buf][mb + i][kq]) = make_uint2(lo, hi);
+      }
+    }
+    if constexpr (BL == 0) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int c = t + 256 * i;
+        *reinterpret_cast<uint4*>(&Bs[buf][c >> 3][(c & 7) * 8]) = r.b[i];
+      }
+    } else {
+      const int kq = (t & 31) * 2, nb = (t >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)  // row n = nb + i: k-values kq, kq + 1
+        *reinterpret_cast<uint32_t*>(&Bs[buf][nb + i][kq]) = pair(word(r.b[0], i >> 1), word(r.b[1], i >> 1), i);
+    }
+  };
+  f32x16_t acc[2] = {f32x16_t{}, f32x16_t{}};
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < kSkK / 16; ++kk) {
+      const int kofs = kk * 16 + (lane >> 5) * 8;
+      const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&As[buf][wave * 32 + (lane & 31)][kofs]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const bf16x8_t b = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][j * 32 + (lane & 31)][kofs]);
+        if constexpr (TOUT)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, acc[j], 0, 0, 0);  // rows n', columns m'
+        else
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[j], 0, 0, 0);  // rows m', columns n'
+      }
+    }
+  };
+  // Two K steps of loads in flight: while step s is multiplied out of LDS buffer (s - s0) & 1,
+  // step s + 1 waits in one register stage and step s + 2 is being fetched into the other.
+  // The split runs an even number of steps; a step past kend loads zeros.
+  Stage r0, r1;
+  const int64_t se = s0 + ((s1 - s0 + 1) & ~int64_t(1));
+  gload(r0, s0 * kSkK);
+  gload(r1, (s0 + 1) * kSkK);
+  sstore(0, r0, s0 * kSkK);
+  __syncthreads();
+  auto step = [&](int64_t s, Stage& next, Stage& ahead) {
+    const int buf = static_cast<int>((s - s0) & 1);
+    gload(ahead, (s + 2) * kSkK);
+    compute(buf);
+    sstore(buf ^ 1, next, (s + 1) * kSkK);
+    __syncthreads();
+  };
+  for (int64_t s = s0; s < se; s += 2) {
+    step(s, r1, r0);
+    step(s + 1, r0, r1);
+  }
+  // 32x32 accumulator layout: lane holds column (lane % 32) and rows (e / 4) * 8 + (lane / 32) * 4 + e % 4
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      int64_t row, col, rows, cols;  // in C's coordinates
+      if constexpr (TOUT) {
+        row = j * 32 + r;
+        col = m0 + wave * 32 + (lane & 31);
+        rows = g.N;
+        cols = g.M;
+      } else {
+        row = m0 + wave * 32 + r;
+        col = j * 32 + (lane & 31);
+        rows = g.M;
+        cols = g.N;
+      }
+      if (row < rows && col < cols) g.partial[(kz * rows + row) * cols + col] = acc[j][e];
+    }
+}
+
+// Splits of a skinny product.  A CU moves about the same bytes per unit time with one
+// workgroup as with two, so the time of a split count is the number of workgroups on the
+// busiest CU times the K steps each runs, plus about four steps of fixed cost (the first
+// loads, the partial write); the count (1 .. 16) that minimises it wins.
+int skinny_splits(int64_t long_side, int64_t K) {
+  const int64_t tiles = ceil_div(long_side, kSkM), stages = ceil_div(K, kSkK);
+  int64_t best = 1, best_cost = -1;
+  for (int64_t sp = 1; sp <= 16 && sp <= stages; ++sp) {
+    const int64_t cost = ceil_div(tiles * sp, 256) * (ceil_div(stages, sp) + 4);
+    if (best_cost < 0 || cost < best_cost) {
+      best = sp;
+      best_cost = cost;
+    }
+  }
+  return static_cast<int>(best);
+}
+
+// A product the skinny kernel takes: bf16, dense B, no effective mask, one K segment, dense C, a side of at most 64.
+bool skinny_ok(const sf_gemm_desc* d) {
+  return d->dtype == SF_DTYPE_BF16 && d->b_format == SF_BFMT_DENSE && !d->bmask && d->K2 == 0 && !d->c_blocks &&
+         d->K1 > 0 && (d->N <= kSkN || d->M <= kSkN);
+}
+
+size_t skinny_workspace(const sf_gemm_desc* d) {
+  const bool tout = d->N > kSkN;
+  const int sp = skinny_splits(tout ? d->N : d->M, d->K1);
+  return static_cast<size_t>(sp) * d->M * d->N * sizeof(float);
+}
+
+int launch_skinny(const sf_gemm_desc* d, GemmArgs g, hipStream_t st) {
+  const bool tout = d->N > kSkN;  // C's short side is its rows: A' = B, B' = A
+  SkinnyArgs a;
+  a.A = static_cast<const uint16_t*>(tout ? d->B1 : d->A1);
+  a.B = static_cast<const uint16_t*>(tout ? d->A1 : d->B1);
+  a.lda = tout ? d->ldb1 : d->lda1;
+  a.ldb = tout ? d->lda1 : d->ldb1;
+  a.M = tout ? d->N : d->M;
+  a.N = tout ? d->M : d->N;
+  a.K = d->K1;
+  const int al = tout ? d->b_layout : d->a_layout, bl = tout ? d->a_layout : d->b_layout;
+  const int sp = skinny_splits(a.M, a.K);
+  a.split_stages = ceil_div(ceil_div(a.K, kSkK), sp);
+  a.partial = static_cast<float*>(d->workspace);
+  const int64_t grid = ceil_div(a.M, kSkM) * sp;
+  SF_CHECK_ARG(grid < (1ll << 31), "GEMM grid too large");
+  const dim3 gd(static_cast<unsigned>(grid)), bd(256);
+#define SF_SKINNY(AL_, BL_)                                                      \
+  do {                                                                           \
+    if (tout)                                                                    \
+      hipLaunchKernelGGL((skinny_kernel<AL_, BL_, true>), gd, bd, 0, st, a);     \
+    else                                                                         \
+      hipLaunchKernelGGL((skinny_kernel<AL_, BL_, false>), gd, bd, 0, st, a);    \
+  } while (0)
+  if (al == SF_LAYOUT_K && bl == SF_LAYOUT_K)
+    SF_SKINNY(0, 0);
+  else if (al == SF_LAYOUT_K)
+    SF_SKINNY(0, 1);
+  else if (bl == SF_LAYOUT_K)
+    SF_SKINNY(1, 0);
+  else
+    SF_SKINNY(1, 1);
+#undef SF_SKINNY
+  if (int rc = launch_status("sf_gemm (skinny)")) return rc;
+  g.splits = sp;
+  g.partial = a.partial;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(static_cast<unsigned>(elementwise_grid(g.M * g.N, 256))), dim3(256), 0,
+                     st, g, SF_DTYPE_BF16);
+  return launch_status("sf_gemm (skinny reduce)");
+}
+
 template <typename T, int MASK>
 int dispatch_layouts(const sf_gemm_desc* d, const GemmArgs& g, hipStream_t st) {
   if constexpr (MASK == kMaskNone) {
@@ -1796,6 +2056,7 @@ using namespace sf;
 extern "C" size_t sf_gemm_workspace_size(const sf_gemm_desc* d) {
   if (!d || d->M <= 0 || d->N <= 0 || d->K1 <= 0) return 0;
   if (d->dtype != SF_DTYPE_BF16 && d->dtype != SF_DTYPE_F32) return 0;
+  if (skinny_ok(d)) return skinny_workspace(d);
   const int sp = choose_splits(d);
   return sp > 1 ? static_cast<size_t>(sp) * d->M * d->N * sizeof(float) : 0;
 }
@@ -1925,6 +2186,8 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   // the weight-scaling factor is applied together with a multiplicative mask
   SF_CHECK_ARG(!g.has_scale || (g.bmask && !d->bmask_bytes), "bscale != 1 needs a multiplicative effective mask");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (skinny_ok(d) && d->workspace && d->workspace_bytes >= skinny_workspace(d) && al16(d->workspace))
+    return launch_skinny(d, g, st);
   const bool bf = d->dtype == SF_DTYPE_BF16;
   if (g.bmask && d->bmask_bytes)
     return bf ? dispatch_layouts<uint16_t, kMaskByte>(d, g, st) : dispatch_layouts<float, kMaskByte>(d, g, st);
