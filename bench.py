@@ -8,10 +8,12 @@ Metric (the reference's headline benchmark): SparseLinear fwd+bwd TFLOP/s at LLa
   of a LLaMA-2-7B decoder layer (q/k/v/o [4096, 4096], gate/up
   [11008, 4096], down [4096, 11008]) over T = 8192 tokens in bf16, with the
   hard 2:4 mask of the layer's soft mask (hardening_x = 0) and the SLoRB
-  bypass at rank 64.  The forward writes W * E with one elementwise pass and
-  keeps it for the input gradient; the GEMMs then read it.  Throughput counts
-  the algorithmic 6 T in out + 6 T r (in + out) FLOPs per linear;
-  ``per_linear`` times each linear alone.
+  bypass at rank 64.  The forward writes W * E and its packed 2:4 form with
+  one elementwise pass, keeps W * E for the input gradient and runs its
+  product on the 2:4 sparse MFMA (``sparse_forward``); the gradient products
+  and the SLoRB products run on sf_gemm (``roofline``: its own FLOPs over its
+  own device time).  Throughput counts the algorithmic (dense) 6 T in out +
+  6 T r (in + out) FLOPs per linear; ``per_linear`` times each linear alone.
 * ``gemm_vs_hipblaslt`` -- the three big products (fwd, dx, dW) of each 7B
   linear shape through sf_gemm and through torch.matmul (hipBLASLt), and the
   layer's 21 products summed.
@@ -897,10 +899,15 @@ def linear_leg(torch, sm, prof, dev, a) -> dict:
     flops = step_flops(a.tokens)
     ms_per_step = el * 1e3 / a.steps
     tflops = flops * a.steps / el / 1e12
+    # sf_gemm: the dense products (input and weight gradients, the SLoRB products); its own FLOPs over
+    # its own device time.  The hardening_x = 0 forward runs on the 2:4 sparse MFMA (sf_gemm_2to4),
+    # reported against the sparse peak in dense-equivalent FLOPs.
     g = ks["sf_gemm"]
-    gemm_tflops = flops * a.steps / (g.total_ms * 1e-3) / 1e12
+    gemm_tflops = g.rate / 1e12
+    s24 = ks.get("sf_gemm_2to4")
     log(f"linear: {ms_per_step:.2f} ms/step, {tflops:.1f} TFLOP/s; sf_gemm {g.launches} launches, "
-        f"avg {g.avg_ms:.3f} ms, {gemm_tflops:.1f} TFLOP/s over GEMM time")
+        f"avg {g.avg_ms:.3f} ms, {gemm_tflops:.1f} TFLOP/s" +
+        (f"; sf_gemm_2to4 {s24.launches} launches, {s24.rate / 1e12:.1f} TFLOP/s dense-equivalent" if s24 else ""))
     other = {n: {"launches": s.launches, "avg_ms": round(s.avg_ms, 4), "total_ms": round(s.total_ms, 3)}
              for n, s in ks.items()}
     per_linear = per_linear_times(torch, mods, xs, gys)
@@ -928,8 +935,13 @@ def linear_leg(torch, sm, prof, dev, a) -> dict:
                      "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic.get("sf_gemm_bytes_per_launch"), "traffic_unit": "B/launch",
                      "traffic_source": TRAFFIC_SUMMARY,
-                     "kernel": "sf_gemm (gemm_bf16_kernel)", "launches": g.launches,
+                     "kernel": "sf_gemm (gemm_bf16_kernel, skinny_kernel)", "launches": g.launches,
                      "avg_launch_ms": round(g.avg_ms, 4)},
+        "sparse_forward": None if s24 is None else {
+            "kernel": "sf_gemm_2to4 (gemm24_kernel, v_smfmac_f32_32x32x32_bf16)", "launches": s24.launches,
+            "avg_launch_ms": round(s24.avg_ms, 4), "achieved": round(s24.rate / 1e12, 3),
+            "unit": "TFLOP/s dense-equivalent", "peak": PEAK_BF16_SPARSE_TFLOPS,
+            "frac": round(s24.rate / 1e12 / PEAK_BF16_SPARSE_TFLOPS, 4)},
         "per_linear": per_linear,
         "hutchinson_probe_layer": hvp,
         "kernels": other,

@@ -724,6 +724,32 @@ int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const void* vals, c
                  void* stream);
 
 /*
+ * The training forward of a SparseLinear whose effective mask is a 2:4 hard
+ * mask (hardening_x = 0 in legacy/sparse_modeling.py:56-81
+ * FusedMaskedLinearSTE.forward, with E from _hard_mask_from_soft :578-603 /
+ * :720-735 and the SLoRB pair of :790-794), on the sparse MFMA.
+ *
+ * sf_apply_mask_2to4: Wm = W * mask (W bf16 [out, in], mask a byte and-mask,
+ * 0 = pruned; the elementwise product sf_apply_mask writes, which the input
+ * gradient reuses) and the packed vals / idx of Wm in one pass.  Groups with
+ * more than two kept columns are added to *bad_groups (device uint64,
+ * accumulated); a mask from the N:M hard projection with N = 2, M = 4 has none.
+ * Pruned columns do not enter the packed product, so a non-finite weight there
+ * does not reach y (the dense product of Wm would carry its NaN).
+ *
+ * sf_gemm_2to4_lowrank: sf_gemm_2to4 plus the low-rank term z S^T
+ * (z [tokens, rank] row pitch ldz, S [out, rank] row pitch lds, bf16,
+ * rank % 8 == 0; rank 0: none) accumulated in f32 before the output rounding,
+ * i.e. y = x Wm^T + z S^T (+ bias) as the dense forward computes it.
+ */
+int sf_apply_mask_2to4(const void* W, const void* mask, int64_t out_features, int64_t in_features, void* Wm,
+                       void* vals, void* idx, unsigned long long* bad_groups, void* stream);
+int sf_gemm_2to4_lowrank(const void* x, int64_t ldx, int64_t tokens, const void* vals, const void* idx,
+                         int64_t out_features, int64_t in_features, const void* z, int64_t ldz, const void* S,
+                         int64_t lds, int64_t rank, const void* bias, int bias_dtype, void* y, int y_dtype,
+                         int64_t ldy, void* stream);
+
+/*
  * Sustained MFMA rate probe, a measurement aid with no counterpart in the
  * reference (bench.py reports the rate beside the published dense peak):
  * `blocks` workgroups of 4 waves, each wave iters x 16

@@ -285,6 +285,9 @@ SIGNATURES = {
     "sf_pack_2to4": (_I, [_P, _I, _P, _I, _I64, _I64, _P, _P, _P, _P]),
     "sf_unpack_2to4": (_I, [_P, _P, _I64, _I64, _P, _I, _P]),
     "sf_gemm_2to4": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I, _P, _I, _I64, _P]),
+    "sf_apply_mask_2to4": (_I, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "sf_gemm_2to4_lowrank": (_I, [_P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P, _I64, _I64, _P, _I, _P, _I,
+                                  _I64, _P]),
     "sf_mfma_probe": (_I, [_I, _I, _P, _P]),
     "sf_hbm_probe": (_I, [_I, _P, _P, _P, _I64, _I, _P]),
 }

@@ -2267,6 +2267,10 @@ struct Gemm24Args {
   int64_t ldy;
   int64_t tiles_m, tiles_n;
   int y_aligned;
+  // optional dense second segment y^T += A2 . B2^T: A2 [M, K2] and B2 [N, K2] bf16, K-contiguous
+  const void* A2;
+  const void* B2;
+  int64_t lda2, ldb2, K2;
 };
 
 constexpr int kEpi24Pitch = 68;  // f32 pitch of the transposed staging: 128 token rows x 64 out columns per wave
@@ -2393,6 +2397,41 @@ __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
     mfmas1(1, ix);
   }
 
+  // Segment 2 (dense, 64 k a stage through the first 64 KB of LDS): the low-rank term
+  // A2 . B2^T accumulated into the same tile with v_mfma_f32_32x32x16_bf16, operands
+  // in the swizzled K-contiguous layout of the dense kernel.
+  if (g.K2 > 0) {
+    DmaLoader d2a, d2b;
+    d2a.init(g.A2, g.lda2, m0, g.M, g.K2);
+    d2b.init(g.B2, g.ldb2, n0, g.N, g.K2);
+    uint32_t a2[kFragM], b2[kFragN];
+#pragma unroll
+    for (int i = 0; i < kFragM; ++i) a2[i] = frag_base<true>(wm * kWaveM + i * 32 + (lane & 31));
+#pragma unroll
+    for (int j = 0; j < kFragN; ++j) b2[j] = 32768u + frag_base<true>(wn * kWaveN + j * 32 + (lane & 31));
+    const int64_t nk2 = ceil_div(g.K2, 64);
+    for (int64_t s2 = 0; s2 < nk2; ++s2) {
+      __syncthreads();  // every wave is done with the buffers
+      d2a.issue<true>(base_l, s2 * 64);
+      d2b.issue<true>(base_l + 32768u, s2 * 64);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        bf16x8_t a[kFragM], b[kFragN];
+#pragma unroll
+        for (int i = 0; i < kFragM; ++i) a[i] = *reinterpret_cast<const bf16x8_t*>(smem + frag_at<true>(a2[i], kk));
+#pragma unroll
+        for (int j = 0; j < kFragN; ++j) b[j] = *reinterpret_cast<const bf16x8_t*>(smem + frag_at<true>(b2[j], kk));
+#pragma unroll
+        for (int j = 0; j < kFragN; ++j)
+#pragma unroll
+          for (int i = 0; i < kFragM; ++i)
+            acc[i * kFragN + j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i * kFragN + j], 0, 0, 0);
+      }
+    }
+  }
+
   // Epilogue: acc block (i, j) holds y^T rows (out) m = i * 32 + (e / 4) * 8 +
   // (lane / 32) * 4 + e % 4 and column (token) n = j * 32 + lane % 32.  Each
   // wave stages 64 out columns x its 128 tokens transposed, then every lane
@@ -2513,6 +2552,69 @@ __global__ void __launch_bounds__(256) pack24_kernel(const void* __restrict__ W,
   if (nbad) atomicAdd(bad, nbad);
 }
 
+// The hx = 0 training forward's weight pass: Wm = round(W * E) for a byte and-mask E (W
+// bf16; the elementwise product of sf_apply_mask, kept for the input gradient) and, from
+// the same loads, the packed 2:4 form of Wm (the kept bf16 values exactly, the index bits
+// of pack24_kernel).  One thread per (row, 16 columns).
+__global__ void __launch_bounds__(256) apply_pack24_kernel(const uint16_t* __restrict__ W, const uint8_t* __restrict__ E,
+                                                           int64_t M, int64_t K, uint16_t* __restrict__ Wm,
+                                                           uint16_t* __restrict__ vals, uint16_t* __restrict__ idx,
+                                                           unsigned long long* __restrict__ bad) {
+  const int64_t per_row = K / 16, total = M * per_row, nk = K / 64;
+  unsigned long long nbad = 0;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = t / per_row, c16 = t - row * per_row;
+    const int64_t e0 = row * K + c16 * 16;
+    const uint4 wa = *reinterpret_cast<const uint4*>(W + e0), wb = *reinterpret_cast<const uint4*>(W + e0 + 8);
+    const uint4 mb = *reinterpret_cast<const uint4*>(E + e0);
+    const uint32_t ww[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    const uint32_t mw[4] = {mb.x, mb.y, mb.z, mb.w};
+    uint32_t om[8], ov[4], bits = 0;
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      uint16_t kept[2] = {0, 0};
+      int pos[2] = {-1, -1}, n = 0;
+      uint16_t prod[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int e = grp * 4 + c;
+        const uint16_t wbits = static_cast<uint16_t>(ww[e >> 1] >> (16 * (e & 1)));
+        const bool keep = ((mw[grp] >> (8 * c)) & 0xffu) != 0;
+        prod[c] = f32_to_bf16(bf16_to_f32(wbits) * (keep ? 1.0f : 0.0f));
+        if (keep) {
+          if (n < 2) {
+            pos[n] = c;
+            kept[n] = prod[c];
+          }
+          ++n;
+        }
+      }
+      if (n > 2) ++nbad;
+      for (int c = 0; c < 4 && (pos[0] < 0 || pos[1] < 0); ++c) {  // pad to two distinct columns, zero values
+        if (c == pos[0] || c == pos[1]) continue;
+        if (pos[0] < 0) pos[0] = c;
+        else pos[1] = c;
+      }
+      if (pos[1] < pos[0]) {
+        const int tp = pos[0]; pos[0] = pos[1]; pos[1] = tp;
+        const uint16_t tv = kept[0]; kept[0] = kept[1]; kept[1] = tv;
+      }
+      om[2 * grp] = prod[0] | (static_cast<uint32_t>(prod[1]) << 16);
+      om[2 * grp + 1] = prod[2] | (static_cast<uint32_t>(prod[3]) << 16);
+      ov[grp] = kept[0] | (static_cast<uint32_t>(kept[1]) << 16);
+      bits |= (uint32_t)pos[0] << (4 * grp);
+      bits |= (uint32_t)pos[1] << (4 * grp + 2);
+    }
+    *reinterpret_cast<uint4*>(Wm + e0) = make_uint4(om[0], om[1], om[2], om[3]);
+    *reinterpret_cast<uint4*>(Wm + e0 + 8) = make_uint4(om[4], om[5], om[6], om[7]);
+    *reinterpret_cast<uint4*>(vals + row * (K / 2) + c16 * 8) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+    const int64_t q64 = c16 >> 2, sub = c16 & 3;
+    const int64_t word = (((row >> 5) * nk + q64) * 2 + (sub & 1)) * 32 + (row & 31);
+    idx[word * 2 + (sub >> 1)] = static_cast<uint16_t>(bits);
+  }
+  if (nbad) atomicAdd(bad, nbad);
+}
+
 __global__ void __launch_bounds__(256) unpack24_kernel(const uint16_t* __restrict__ vals, const uint16_t* __restrict__ idx,
                                                        int64_t M, int64_t K, void* __restrict__ W, int w_dtype) {
   const int64_t per_row = K / 16, total = M * per_row, nk = K / 64;
@@ -2575,12 +2677,14 @@ extern "C" int sf_unpack_2to4(const void* vals, const void* idx, int64_t out_fea
   return launch_status("sf_unpack_2to4");
 }
 
-extern "C" int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const void* vals, const void* idx,
-                            int64_t out_features, int64_t in_features, const void* bias, int bias_dtype, void* y,
-                            int y_dtype, int64_t ldy, void* stream) {
+namespace sf {
+namespace {
+int launch_gemm24(const void* x, int64_t ldx, int64_t tokens, const void* vals, const void* idx, int64_t out_features,
+                  int64_t in_features, const void* z, int64_t ldz, const void* S, int64_t lds, int64_t rank,
+                  const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy, void* stream, const char* what) {
   SF_CHECK_ARG(y_dtype == SF_DTYPE_F32 || y_dtype == SF_DTYPE_BF16, "bad output dtype");
   SF_CHECK_ARG(!bias || bias_dtype == SF_DTYPE_F32 || bias_dtype == SF_DTYPE_BF16, "bad bias dtype");
-  SF_CHECK_ARG(tokens >= 0 && out_features > 0 && in_features > 0, "bad shape");
+  SF_CHECK_ARG(tokens >= 0 && out_features > 0 && in_features > 0 && rank >= 0, "bad shape");
   SF_CHECK_ARG(out_features % 32 == 0 && in_features % 64 == 0,
                "2:4 product needs out %% 32 == 0 and in %% 64 == 0 (got %lld x %lld)", (long long)out_features,
                (long long)in_features);
@@ -2591,6 +2695,13 @@ extern "C" int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const vo
   SF_CHECK_ARG(ldy >= out_features, "ldy < out_features");
   SF_CHECK_ARG(tokens * ldx * 2 < (int64_t(1) << 31) && out_features * in_features < (int64_t(1) << 31),
                "2:4 product: operands of 2 GiB or more are not supported");
+  if (rank > 0) {
+    SF_CHECK_ARG(z && S, "null low-rank operand");
+    SF_CHECK_ARG(rank % 8 == 0 && ldz >= rank && lds >= rank && ldz % 8 == 0 && lds % 8 == 0 && al16(z) && al16(S),
+                 "low-rank operands: rank, ldz and lds must be multiples of 8 with 16-byte aligned rows");
+    SF_CHECK_ARG(tokens * ldz * 2 < (int64_t(1) << 31) && out_features * lds * 2 < (int64_t(1) << 31),
+                 "2:4 product: low-rank operands of 2 GiB or more are not supported");
+  }
   Gemm24Args g;
   g.x = x;
   g.ldx = ldx;
@@ -2607,11 +2718,50 @@ extern "C" int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const vo
   g.tiles_m = ceil_div(out_features, kTileM);
   g.tiles_n = ceil_div(tokens, kTileN);
   g.y_aligned = al16(y);
+  g.A2 = S;
+  g.B2 = z;
+  g.lda2 = lds;
+  g.ldb2 = ldz;
+  g.K2 = rank > 0 ? rank : 0;
   static bool attr = false;
   if (int rc = set_smem(gemm24_kernel, smem24_bytes(), attr)) return rc;
   const int64_t tiles = g.tiles_m * g.tiles_n;
   SF_CHECK_ARG(tiles < (1ll << 31), "grid too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(gemm24_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), smem24_bytes(), st, g);
-  return launch_status("sf_gemm_2to4");
+  return launch_status(what);
+}
+}  // namespace
+}  // namespace sf
+
+extern "C" int sf_gemm_2to4(const void* x, int64_t ldx, int64_t tokens, const void* vals, const void* idx,
+                            int64_t out_features, int64_t in_features, const void* bias, int bias_dtype, void* y,
+                            int y_dtype, int64_t ldy, void* stream) {
+  return sf::launch_gemm24(x, ldx, tokens, vals, idx, out_features, in_features, nullptr, 0, nullptr, 0, 0, bias,
+                           bias_dtype, y, y_dtype, ldy, stream, "sf_gemm_2to4");
+}
+
+extern "C" int sf_gemm_2to4_lowrank(const void* x, int64_t ldx, int64_t tokens, const void* vals, const void* idx,
+                                    int64_t out_features, int64_t in_features, const void* z, int64_t ldz,
+                                    const void* S, int64_t lds, int64_t rank, const void* bias, int bias_dtype,
+                                    void* y, int y_dtype, int64_t ldy, void* stream) {
+  return sf::launch_gemm24(x, ldx, tokens, vals, idx, out_features, in_features, z, ldz, S, lds, rank, bias,
+                           bias_dtype, y, y_dtype, ldy, stream, "sf_gemm_2to4_lowrank");
+}
+
+extern "C" int sf_apply_mask_2to4(const void* W, const void* mask, int64_t out_features, int64_t in_features,
+                                  void* Wm, void* vals, void* idx, unsigned long long* bad_groups, void* stream) {
+  SF_CHECK_ARG(out_features > 0 && in_features > 0, "empty weight");
+  SF_CHECK_ARG(out_features % 32 == 0 && in_features % 64 == 0,
+               "2:4 packing needs out %% 32 == 0 and in %% 64 == 0 (got %lld x %lld)", (long long)out_features,
+               (long long)in_features);
+  SF_CHECK_ARG(W && mask && Wm && vals && idx && bad_groups, "null tensor");
+  SF_CHECK_ARG(al16(W) && al16(mask) && al16(Wm) && al16(vals), "W, mask, Wm and vals must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t work = out_features * (in_features / 16);
+  hipLaunchKernelGGL(apply_pack24_kernel, dim3(static_cast<unsigned>(elementwise_grid(work, 256))), dim3(256), 0, st,
+                     static_cast<const uint16_t*>(W), static_cast<const uint8_t*>(mask), out_features, in_features,
+                     static_cast<uint16_t*>(Wm), static_cast<uint16_t*>(vals), static_cast<uint16_t*>(idx),
+                     bad_groups);
+  return launch_status("sf_apply_mask_2to4");
 }

@@ -180,6 +180,46 @@ def apply_mask(W: torch.Tensor, E: torch.Tensor, scale: float = 1.0) -> torch.Te
     return out
 
 
+_BAD24: dict = {}
+
+
+def apply_mask_2to4(W: torch.Tensor, E: torch.Tensor):
+    """Wm = W * E for a bf16 W and a byte and-mask E that keeps two of every four columns, plus
+    the packed 2:4 form of Wm (values, index words), in one pass (sf_apply_mask_2to4).  Groups
+    keeping more than two columns are only counted in a per-device device counter, never read
+    here: the N:M hard projection with N = 2, M = 4 produces none."""
+    dev = L.require_device(W, E)
+    out_f, in_f = W.shape
+    Wm = torch.empty_like(W)
+    vals = torch.empty(out_f, in_f // 2, dtype=torch.bfloat16, device=dev)
+    idx = torch.empty(out_f * in_f // 8, dtype=torch.uint8, device=dev)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    bad = _BAD24.get(key)
+    if bad is None:
+        bad = _BAD24[key] = torch.zeros(1, dtype=torch.int64, device=dev)
+    with _prof.region("sf_apply_mask_2to4", W.numel() * 5 + vals.numel() * 2 + idx.numel(), "B", dev):
+        L.check(L.lib().sf_apply_mask_2to4(L.ptr(W), L.ptr(E), out_f, in_f, L.ptr(Wm), L.ptr(vals), L.ptr(idx),
+                                           L.ptr(bad), L.stream(dev)), "sf_apply_mask_2to4")
+    return Wm, vals, idx
+
+
+def gemm_2to4(x2: torch.Tensor, vals: torch.Tensor, idx: torch.Tensor, out_features: int, z=None, S=None,
+              bias=None) -> torch.Tensor:
+    """y [T, out] bf16 = x2 Wm^T (+ z S^T) (+ bias) with Wm packed 2:4 (sf_gemm_2to4_lowrank)."""
+    dev = L.require_device(x2, vals, idx, z, S, bias)
+    T, in_f = x2.shape
+    y = torch.empty(T, out_features, dtype=torch.bfloat16, device=dev)
+    r = 0 if z is None else z.shape[1]
+    flops = 2.0 * T * out_features * (in_f + r)
+    with _prof.region("sf_gemm_2to4", flops, "FLOP", dev):
+        L.check(L.lib().sf_gemm_2to4_lowrank(L.ptr(x2), x2.stride(0), T, L.ptr(vals), L.ptr(idx), out_features,
+                                             in_f, L.ptr(z), 0 if z is None else z.stride(0), L.ptr(S),
+                                             0 if S is None else S.stride(0), r, L.ptr(bias),
+                                             L.dtype_code(bias) if bias is not None else 0, L.ptr(y),
+                                             L.dtype_code(y), y.stride(0), L.stream(dev)), "sf_gemm_2to4_lowrank")
+    return y
+
+
 def transpose_u8(E: torch.Tensor) -> torch.Tensor:
     """[rows, cols] uint8 -> its transpose [cols, rows] (sf_transpose_u8)."""
     dev = L.require_device(E)
@@ -343,15 +383,24 @@ class _MaskedLinearBackward(torch.autograd.Function):
 
 class _MaskedLinear(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x2, W, bias, P, S, E, scale, decay):
+    def forward(ctx, x2, W, bias, P, S, E, scale, decay, nm24=False):
         z = None
-        # y = x (W.E.s)^T: one elementwise pass writes the masked weight, the GEMM runs unmasked
-        Wm, s = (apply_mask(W, E, scale), 1.0) if E is not None else (W, scale)
-        if P is not None:
-            z = mm_nt(x2, P)
-            y = mm_nt(x2, Wm, bscale=s, A2=z, B2=S, K2=P.shape[0], bias=bias)
+        if nm24:
+            # E is a 2:4 hard mask: the pass that writes W.E also packs it, and the product runs on
+            # the sparse MFMA (the SLoRB term as a dense second segment of the same kernel)
+            Wm, vals, idx = apply_mask_2to4(W, E)
+            if P is not None:
+                z = mm_nt(x2, P)
+            y = gemm_2to4(x2, vals, idx, W.shape[0], z=z, S=S, bias=bias)
+            del vals, idx
         else:
-            y = mm_nt(x2, Wm, bscale=s, bias=bias)
+            # y = x (W.E.s)^T: one elementwise pass writes the masked weight, the GEMM runs unmasked
+            Wm, s = (apply_mask(W, E, scale), 1.0) if E is not None else (W, scale)
+            if P is not None:
+                z = mm_nt(x2, P)
+                y = mm_nt(x2, Wm, bscale=s, A2=z, B2=S, K2=P.shape[0], bias=bias)
+            else:
+                y = mm_nt(x2, Wm, bscale=s, bias=bias)
         # Without a weight-scaling factor the input gradient needs the same W.E: it is saved for the
         # backward (2 B/param of bf16 weight) instead of being rebuilt there by another pass.  It goes
         # through save_for_backward, so the version counters of W and E guard it like the rest.
@@ -368,7 +417,7 @@ class _MaskedLinear(torch.autograd.Function):
         gy = gy.contiguous().to(W.dtype)
         dx, dW, db, dP, dS = _MaskedLinearBackward.apply(gy, x2, W, P, S, E, ctx.decay, ctx.has_bias, z, wm)
         del wm
-        return dx, dW, db, dP, dS, None, None, None
+        return dx, dW, db, dP, dS, None, None, None, None
 
 
 def _compute_dtype(x: torch.Tensor, W: torch.Tensor) -> torch.dtype:
@@ -400,6 +449,7 @@ def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale
     b = None if bias is None else (bias if bias.dtype == dt else bias.to(dt)).contiguous()
     mask = _opt(mask)
     hard = _opt(hard)
+    own_hard_bytes = eff is None and hard is None and mask_mode == "mix" and hx <= 0.0 and scale == 1.0
     if eff is None and mask_mode != "none":
         if mask_mode == "mix" and hx <= 0.0 and scale == 1.0:
             # E = hard(mask) exactly: staged as a byte and-mask (W * 1 = W, W * 0 = 0)
@@ -419,7 +469,13 @@ def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale
         Pp, Sp = Pp.contiguous(), Sp.contiguous()
         if Pp.shape[0] % _vec(dt):
             Pp, Sp, r = _PadRank.apply(Pp, Sp)
-    y = _MaskedLinear.apply(x2, W, b, Pp, Sp, eff, float(scale), float(decay))
+    # A 2:4 hard mask along the input dimension (both N:M kinds keep exactly two of every four
+    # columns when in % 4 == 0) runs the forward product on the sparse MFMA.
+    nm24 = (own_hard_bytes and eff is not None and hard_kind in (L.HARD_NM_TAIL_KEEP, L.HARD_NM_STRICT)
+            and hard_n == 2 and hard_m == 4 and dt == torch.bfloat16 and W.shape[0] % 32 == 0
+            and W.shape[1] % 64 == 0 and x2.shape[0] * W.shape[1] * 2 < 2 ** 31
+            and W.shape[0] * W.shape[1] < 2 ** 31)
+    y = _MaskedLinear.apply(x2, W, b, Pp, Sp, eff, float(scale), float(decay), nm24)
     return y.view(*lead, y.shape[-1])
 
 
