@@ -2373,43 +2373,56 @@ __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
             __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], (int)ix[i], 0, 1);
   };
 
-  // Stage s in buffer s & 1: k-step 1 fragments read during the k-step 0
-  // products; one barrier a stage publishes stage s + 1 and frees buffer
-  // s & 1 for the copy of stage s + 2.
+  // Three-buffer ring, stage s in buffer s % 3.  One barrier a stage (between its k-steps):
+  // before it, this wave's copies of stage s + 1 have landed (the copies of stage s + 2,
+  // issued a stage later, may still be in flight: 14 copy instructions a stage per wave);
+  // after it, every wave holds stage s's last fragments in registers, so buffer s % 3 takes
+  // the copies of stage s + 3, which then have two stages' products to land.
   if (nk > 0) issue(0, 0);
   if (nk > 1) issue(1, 1);
-  __builtin_amdgcn_s_waitcnt(0);
+  if (nk > 2) issue(2, 2);
+  if (nk > 2)
+    asm volatile("s_waitcnt vmcnt(28)" ::: "memory");
+  else if (nk > 1)
+    asm volatile("s_waitcnt vmcnt(14)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (nk > 0) read_frags(0, 0, 0);
   for (int64_t s = 0; s < nk; ++s) {
-    const int b = static_cast<int>(s & 1);
+    const int b = static_cast<int>(s % 3);
     uint32_t ix[kFragM];
 #pragma unroll
     for (int i = 0; i < kFragM; ++i) ix[i] = fi[i];
     read_frags(1, b, 1);
     mfmas0(0);
     if (s + 1 < nk) {
-      __builtin_amdgcn_s_waitcnt(0);
+      if (s + 2 < nk)
+        asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
       __syncthreads();
-      if (s + 2 < nk) issue(b, s + 2);
-      read_frags(0, b ^ 1, 0);
+      if (s + 3 < nk) issue(b, s + 3);
+      read_frags(0, b == 2 ? 0 : b + 1, 0);
     }
     mfmas1(1, ix);
   }
 
   // Segment 2 (dense, 64 k a stage through the first 64 KB of LDS): the low-rank term
-  // A2 . B2^T accumulated into the same tile with v_mfma_f32_32x32x16_bf16, operands
-  // in the swizzled K-contiguous layout of the dense kernel.
+  // A2 . B2^T accumulated into the same tile, operands in the swizzled K-contiguous layout of
+  // the dense kernel.  It runs on the sparse instruction too (dense and sparse MFMAs on the
+  // same accumulators do not fit the register file).  The 16 dense k of a k-step are the
+  // kept values of 32 sparse k keeping columns 0 and 1 of every group of four: sparse k p
+  // holds dense k 2 (p / 4) + p % 4.  The A fragment (lane half h: dense k [8 h, 8 h + 8),
+  // sparse k [16 h, 16 h + 16)) is the dense one with index bits 0x4444; the B fragment
+  // (lane half h: sparse k [8 h, 8 h + 8) and [16 + 8 h, 24 + 8 h)) takes dense k
+  // [4 h, 4 h + 4) and [8 + 4 h, 12 + 4 h), each pair followed by two zeros.
   if (g.K2 > 0) {
     DmaLoader d2a, d2b;
     d2a.init(g.A2, g.lda2, m0, g.M, g.K2);
     d2b.init(g.B2, g.ldb2, n0, g.N, g.K2);
-    uint32_t a2[kFragM], b2[kFragN];
-#pragma unroll
-    for (int i = 0; i < kFragM; ++i) a2[i] = frag_base<true>(wm * kWaveM + i * 32 + (lane & 31));
-#pragma unroll
-    for (int j = 0; j < kFragN; ++j) b2[j] = 32768u + frag_base<true>(wn * kWaveN + j * 32 + (lane & 31));
     const int64_t nk2 = ceil_div(g.K2, 64);
+    const int hl = lane >> 5;
     for (int64_t s2 = 0; s2 < nk2; ++s2) {
       __syncthreads();  // every wave is done with the buffers
       d2a.issue<true>(base_l, s2 * 64);
@@ -2418,16 +2431,25 @@ __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
       __syncthreads();
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        bf16x8_t a[kFragM], b[kFragN];
+        bf16x8_t a[kFragM];
 #pragma unroll
-        for (int i = 0; i < kFragM; ++i) a[i] = *reinterpret_cast<const bf16x8_t*>(smem + frag_at<true>(a2[i], kk));
+        for (int i = 0; i < kFragM; ++i)
+          a[i] = *reinterpret_cast<const bf16x8_t*>(
+              smem + frag_at<true>(frag_base<true>(wm * kWaveM + i * 32 + (lane & 31)), kk));
 #pragma unroll
-        for (int j = 0; j < kFragN; ++j) b[j] = *reinterpret_cast<const bf16x8_t*>(smem + frag_at<true>(b2[j], kk));
-#pragma unroll
-        for (int j = 0; j < kFragN; ++j)
+        for (int j = 0; j < kFragN; ++j) {
+          const int r = wn * kWaveN + j * 32 + (lane & 31), sw = (r ^ (r >> 3)) & 7;
+          const unsigned char* row = smem + 32768u + r * kRowSw + hl * 8;
+          const uint2 p0 = *reinterpret_cast<const uint2*>(row + (((2 * kk) ^ sw) << 4));
+          const uint2 p1 = *reinterpret_cast<const uint2*>(row + (((2 * kk + 1) ^ sw) << 4));
+          const uint4 lo = make_uint4(p0.x, 0u, p0.y, 0u), hi = make_uint4(p1.x, 0u, p1.y, 0u);
+          const bf16x16_t b = __builtin_shufflevector(__builtin_bit_cast(bf16x8_t, lo), __builtin_bit_cast(bf16x8_t, hi),
+                                                      0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
 #pragma unroll
           for (int i = 0; i < kFragM; ++i)
-            acc[i * kFragN + j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i * kFragN + j], 0, 0, 0);
+            acc[i * kFragN + j] =
+                __builtin_amdgcn_smfmac_f32_32x32x32_bf16(a[i], b, acc[i * kFragN + j], 0x4444, 0, 0);
+        }
       }
     }
   }
@@ -2492,7 +2514,7 @@ __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
 }
 
 constexpr size_t smem24_bytes() {
-  constexpr size_t ops = 2ull * k24Stage, epi = 4ull * 128 * kEpi24Pitch * sizeof(float);
+  constexpr size_t ops = 3ull * k24Stage, epi = 4ull * 128 * kEpi24Pitch * sizeof(float);
   return ops > epi ? ops : epi;
 }
 
