@@ -304,18 +304,24 @@ int sf_block_stat(const void* x, int x_dtype, int64_t rows, int64_t cols, int bs
  * keep[i] = 1.0f for the k largest entries of v[n] (device floats), else 0.0f:
  * the torch.topk(flat, k) + scatter of the block_sparse hard mask
  * (legacy/sparse_modeling.py:641-655, :699-713) and penalty target
- * (:1441-1451).  NaN ranks largest; among equal values the higher index is
- * kept first (torch's CPU order for all-equal input, e.g. the initial all-ones
- * mask; torch leaves other tie orders unspecified).  k <= 0: all 0; k >= n: all 1.
+ * (:1441-1451).  NaN ranks largest, -0 == +0.  Equal values are kept exactly
+ * as torch.topk's CPU kernel keeps them: its selection (std::nth_element, or
+ * std::partial_sort when k * 64 <= n, over (value, index) pairs compared by
+ * value; GCC libstdc++'s introselect / heap select) is reproduced step for
+ * step.  k <= 0: all 0; k >= n: all 1.  workspace: device memory of
+ * sf_topk_keep_workspace_size(n) bytes, 16-byte aligned (contents undefined
+ * on entry and exit).
  */
-int sf_topk_keep(const float* v, int64_t n, int64_t k, float* keep, void* stream);
+size_t sf_topk_keep_workspace_size(int64_t n);
+int sf_topk_keep(const float* v, int64_t n, int64_t k, float* keep, void* workspace, size_t workspace_bytes,
+                 void* stream);
 
 /*
  * block16 projection: in each 16 x 16 tile of the core of x [rows, cols] the k
  * largest elements become 1 and the rest 0; elements outside the core become
  * 1 (legacy/sparse_modeling.py:537-575 for the hard mask, :1318-1341 for the
- * block16 penalty target).  Ties as sf_topk_keep, by position inside the tile
- * (row-major).  bs must be 16.  out: [rows, cols] in out_dtype.
+ * block16 penalty target).  Ties as sf_topk_keep over the tile's 256 entries
+ * in row-major order (torch.topk along the flattened tile).  bs must be 16.  out: [rows, cols] in out_dtype.
  */
 int sf_tile_topk(const void* x, int x_dtype, int64_t rows, int64_t cols, int bs, int64_t k, void* out,
                  int out_dtype, void* stream);

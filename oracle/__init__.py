@@ -17,6 +17,9 @@ sign or index, or a transposed operand):
                 (tests/golden/make_reference_golden.py) and against closed-form
                 invariants (2nd-largest of a group gets G = 0.5 exactly,
                 G in (0, 1), exactly N ones per full group).
+  select.py     torch.topk's CPU selection (libstdc++ introselect / heap
+                select): against torch.topk itself on tie-heavy inputs with NaN
+                and -0 through both branches (tests/test_oracle_select.py).
   quantile      against torch.quantile (linear interpolation).
   adamw.py      against torch.optim.AdamW(foreach=False) for decay = 0 and
                 l1 = 0, and against reference golden vectors for decay != 0,

@@ -14,6 +14,7 @@ import os
 import numpy as np
 
 from .numerics import BF16, F32, ordered_keys, promote, rnd, round_bf16, sigmoid_f32
+from .select import topk_keep as select_topk_keep
 
 _TIES_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "tests", "golden",
                           "topk_ties_m4.json")
@@ -95,20 +96,9 @@ def block_rms(x: np.ndarray, bs: int) -> np.ndarray:
 
 
 def topk_keep_desc(v: np.ndarray, k: int) -> np.ndarray:
-    """Boolean mask of the k largest entries of the last axis (torch.topk, NaN largest).
-
-    torch.topk leaves the order of equal values unspecified; here the higher index wins,
-    which is what torch's CPU kernel does when all values are equal (the all-ones initial
-    mask).  Other tie patterns are not pinned to torch."""
-    v = np.asarray(v, dtype=np.float32)
-    n = v.shape[-1]
-    keys = ordered_keys(v).astype(np.int64)
-    idx = np.broadcast_to(np.arange(n, dtype=np.int64), v.shape)
-    comp = keys * (n + 1) + idx  # key first, then the higher index
-    order = np.argsort(-comp, axis=-1, kind="stable")
-    keep = np.zeros(v.shape, dtype=bool)
-    np.put_along_axis(keep, order[..., :k], True, axis=-1)
-    return keep
+    """Boolean mask of the entries torch.topk(v, k, dim=-1) keeps (CPU kernel, NaN largest), per row
+    of the last axis, equal values included exactly as torch's selection leaves them (oracle.select)."""
+    return select_topk_keep(v, k)
 
 
 def keep_count(frac_kept: float, total: int) -> int:

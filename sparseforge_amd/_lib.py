@@ -252,7 +252,8 @@ SIGNATURES = {
     "sf_effective_mask": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _F, _I, _I, _I, _P]),
     "sf_effective_mask_given": (_I, [_P, _I, _P, _I, _P, _I, _I64, _I64, _I, _F, _P]),
     "sf_block_stat": (_I, [_P, _I, _I64, _I64, _I, _I, _P, _P]),
-    "sf_topk_keep": (_I, [_P, _I64, _I64, _P, _P]),
+    "sf_topk_keep_workspace_size": (_SZ, [_I64]),
+    "sf_topk_keep": (_I, [_P, _I64, _I64, _P, _P, _SZ, _P]),
     "sf_tile_topk": (_I, [_P, _I, _I64, _I64, _I, _I64, _P, _I, _P]),
     "sf_block_fill": (_I, [_P, _I64, _I64, _I, _P, _F, _P, _I, _I, _F, _P, _I, _P, _I, _P]),
     "sf_apply_gate": (_I, [_MP, _P, _P, _I, _P, _I, _P, _I, _I, _P]),

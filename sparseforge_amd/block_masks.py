@@ -8,9 +8,10 @@ and the mask blockify after the EMA (:1598-1601).
 
 Blocks are the bs x bs tiles of the fully covered core
 [:rows // bs * bs, :cols // bs * bs]; elements outside it are left alone by
-blockify and are 1 in hard masks, penalty targets and the block gate.  Ties of
-torch.topk (unspecified by torch) resolve toward the higher index, torch's CPU
-order for all-equal values such as the initial all-ones mask.
+blockify and are 1 in hard masks, penalty targets and the block gate.  Equal
+values are kept exactly as torch.topk's CPU kernel keeps them (its libstdc++
+nth_element / partial_sort selection, reproduced step for step by
+sf_topk_keep and sf_tile_topk), e.g. for the initial all-ones mask.
 """
 from __future__ import annotations
 

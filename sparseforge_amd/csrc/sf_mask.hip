@@ -2226,131 +2226,358 @@ __global__ void __launch_bounds__(kBlock) block_stat_kernel(const void* __restri
   }
 }
 
-// keep[i] = 1 for the k largest v (ordered keys: NaN largest, -0 == +0); among
-// equal values the higher index is kept first.  One workgroup: an MSB-first
-// radix select of the k-th largest key (4 passes of 8 bits over an LDS
-// histogram), then one pass in descending index order that keeps the keys
-// above it and the first `want` keys equal to it.
+// ---------------------------------------------------------------------------
+// torch.topk's CPU selection, which fixes which of several equal values are
+// kept.  torch (ATen native/TopKImpl.h, topk_impl_loop) compares (value, index)
+// pairs by value only -- ordered_key: NaN largest, -0 == +0 -- and runs
+// std::partial_sort(first, first + k, last) when k * 64 <= n, else
+// std::nth_element(first, first + k - 1, last); the first k pairs are kept.
+// Both are GCC libstdc++'s algorithms (bits/stl_algo.h __introselect with a
+// median-of-three pivot, __unguarded_partition and __insertion_sort below four
+// elements; bits/stl_heap.h __heap_select / __make_heap / __adjust_heap /
+// __push_heap for partial_sort and when the depth limit 2 lg n runs out),
+// restated here on pairs packed as (key << 32) | index; `a before b` is
+// key(a) > key(b).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pair_key(uint64_t v) { return static_cast<uint32_t>(v >> 32); }
+
+// Pairs in global memory (one array of keys, one of indices).
+struct SelGlobal {
+  uint32_t* K;
+  int32_t* I;
+  __device__ uint32_t key(int64_t a) const { return K[a]; }
+  __device__ uint64_t get(int64_t a) const { return (static_cast<uint64_t>(K[a]) << 32) | static_cast<uint32_t>(I[a]); }
+  __device__ void put(int64_t a, uint64_t v) const {
+    K[a] = pair_key(v);
+    I[a] = static_cast<int32_t>(static_cast<uint32_t>(v));
+  }
+  __device__ void swap(int64_t a, int64_t b) const {
+    const uint64_t t = get(a);
+    put(a, get(b));
+    put(b, t);
+  }
+};
+
+// One thread's pairs in LDS, element a at a * kSelTileThreads (indices fit a byte).
+constexpr int kSelTileThreads = 32;
+struct SelTile {
+  uint32_t* K;
+  uint8_t* I;
+  __device__ uint32_t key(int64_t a) const { return K[a * kSelTileThreads]; }
+  __device__ uint64_t get(int64_t a) const {
+    return (static_cast<uint64_t>(K[a * kSelTileThreads]) << 32) | I[a * kSelTileThreads];
+  }
+  __device__ void put(int64_t a, uint64_t v) const {
+    K[a * kSelTileThreads] = pair_key(v);
+    I[a * kSelTileThreads] = static_cast<uint8_t>(v);
+  }
+  __device__ void swap(int64_t a, int64_t b) const {
+    const uint64_t t = get(a);
+    put(a, get(b));
+    put(b, t);
+  }
+};
+
+template <class A>
+__device__ void sel_move_median_to_first(const A& s, int64_t result, int64_t a, int64_t b, int64_t c) {
+  const uint32_t ka = s.key(a), kb = s.key(b), kc = s.key(c);
+  if (ka > kb) {
+    if (kb > kc) s.swap(result, b);
+    else if (ka > kc) s.swap(result, c);
+    else s.swap(result, a);
+  } else if (ka > kc) {
+    s.swap(result, a);
+  } else if (kb > kc) {
+    s.swap(result, c);
+  } else {
+    s.swap(result, b);
+  }
+}
+
+// __unguarded_partition(first, last, pivot): the median-of-three leaves an
+// element on each side that stops the scans.
+// The range checks never fire under that invariant; they only keep every scan inside
+// [pivot, last) whatever the data.
+template <class A>
+__device__ int64_t sel_unguarded_partition(const A& s, int64_t first, int64_t last, int64_t pivot) {
+  const uint32_t kp = s.key(pivot);
+  const int64_t hi = last - 1;
+  while (true) {
+    while (first < hi && s.key(first) > kp) ++first;
+    --last;
+    while (last > pivot && kp > s.key(last)) --last;
+    if (!(first < last)) return first;
+    s.swap(first, last);
+    ++first;
+  }
+}
+
+template <class A>
+__device__ void sel_insertion_sort(const A& s, int64_t first, int64_t last) {
+  if (first == last) return;
+  for (int64_t i = first + 1; i < last; ++i) {
+    const uint64_t val = s.get(i);
+    if (pair_key(val) > s.key(first)) {
+      for (int64_t j = i; j > first; --j) s.put(j, s.get(j - 1));
+      s.put(first, val);
+    } else {
+      int64_t j = i, nxt = i - 1;
+      while (nxt >= first && pair_key(val) > s.key(nxt)) {
+        s.put(j, s.get(nxt));
+        j = nxt;
+        --nxt;
+      }
+      s.put(j, val);
+    }
+  }
+}
+
+template <class A>
+__device__ void sel_adjust_heap(const A& s, int64_t first, int64_t hole, int64_t len, uint64_t value) {
+  const int64_t top = hole;
+  int64_t second = hole;
+  while (second < (len - 1) / 2) {
+    second = 2 * (second + 1);
+    if (s.key(first + second) > s.key(first + second - 1)) --second;
+    s.put(first + hole, s.get(first + second));
+    hole = second;
+  }
+  if ((len & 1) == 0 && second == (len - 2) / 2) {
+    second = 2 * (second + 1);
+    s.put(first + hole, s.get(first + second - 1));
+    hole = second - 1;
+  }
+  int64_t parent = (hole - 1) / 2;  // __push_heap
+  while (hole > top && s.key(first + parent) > pair_key(value)) {
+    s.put(first + hole, s.get(first + parent));
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  s.put(first + hole, value);
+}
+
+template <class A>
+__device__ void sel_heap_select(const A& s, int64_t first, int64_t middle, int64_t last) {
+  const int64_t len = middle - first;
+  if (len >= 2) {  // __make_heap
+    for (int64_t parent = (len - 2) / 2;; --parent) {
+      sel_adjust_heap(s, first, parent, len, s.get(first + parent));
+      if (parent == 0) break;
+    }
+  }
+  for (int64_t i = middle; i < last; ++i) {
+    if (s.key(i) > s.key(first)) {  // __pop_heap(first, middle, i)
+      const uint64_t value = s.get(i);
+      s.put(i, s.get(first));
+      sel_adjust_heap(s, first, 0, len, value);
+    }
+  }
+}
+
+__device__ __forceinline__ int floor_log2(int64_t n) { return 63 - __clzll(static_cast<unsigned long long>(n)); }
+
+// The first k pairs of [0, n) become torch's kept set (sequential; 1 <= k < n).
+template <class A>
+__device__ void sel_topk_seq(const A& s, int64_t n, int64_t k) {
+  if (k * 64 <= n) {
+    sel_heap_select(s, 0, k, n);
+    return;
+  }
+  const int64_t nth = k - 1;
+  int64_t first = 0, last = n;
+  int depth = 2 * floor_log2(n);
+  while (last - first > 3) {
+    if (depth == 0) {
+      sel_heap_select(s, first, nth + 1, last);
+      s.swap(first, nth);
+      return;
+    }
+    --depth;
+    sel_move_median_to_first(s, first, first + 1, first + (last - first) / 2, last - 1);
+    const int64_t cut = sel_unguarded_partition(s, first + 1, last, first);
+    if (cut <= nth) first = cut;
+    else last = cut;
+  }
+  sel_insertion_sort(s, first, last);
+}
+
+// keep[i] = 1 for the entries torch.topk(v, k) keeps, else 0.  One workgroup;
+// the partition of each introselect step runs data-parallel: the left scan
+// stops at keys <= the pivot's, the right scan at keys >= it; the i-th left
+// stop (ascending) swaps with the i-th right stop (descending) while it lies
+// before it (m pairs), and the scans end at min(left stop m + 1, right stop m).
+// That is the permutation the sequential scans make (they pass only untouched
+// positions and stop at swapped ones).  Median-of-three, the final insertion
+// sort and the heap selections run on thread 0.  Workspace: keys, indices and
+// the two stop lists, n entries each.
 constexpr int kTopkBlock = 1024;
 __global__ void __launch_bounds__(kTopkBlock) topk_keep_kernel(const float* __restrict__ v, int64_t n, int64_t k,
-                                                               float* __restrict__ keep) {
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t s_prefix, s_want;
-  __shared__ uint32_t wave_cnt[kTopkBlock / 64];
-  __shared__ uint32_t s_run;
+                                                               float* __restrict__ keep, uint32_t* __restrict__ K,
+                                                               int32_t* __restrict__ I, int32_t* __restrict__ PL,
+                                                               int32_t* __restrict__ PR, int* __restrict__ status) {
+  __shared__ int64_t s_first, s_last, s_cut;
+  __shared__ int s_depth, s_end;  // s_end: 0 running, 1 insertion sort due, 2 done
+  __shared__ int s_scl[kTopkBlock / 64], s_scr[kTopkBlock / 64];
+  __shared__ int s_tot[2];
   const int tid = threadIdx.x;
   if (k <= 0 || k >= n) {
     for (int64_t i = tid; i < n; i += blockDim.x) keep[i] = k > 0 ? 1.0f : 0.0f;
     return;
   }
-  if (tid == 0) {
-    s_prefix = 0u;
-    s_want = static_cast<uint32_t>(k);
-    s_run = 0u;
+  for (int64_t i = tid; i < n; i += blockDim.x) {
+    K[i] = ordered_key(v[i]);
+    I[i] = static_cast<int32_t>(i);
   }
-  uint32_t mask_hi = 0u;
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    for (int i = tid; i < 256; i += blockDim.x) hist[i] = 0u;
-    __syncthreads();
-    const uint32_t prefix = s_prefix;
-    for (int64_t i = tid; i < n; i += blockDim.x) {
-      const uint32_t key = ordered_key(v[i]);
-      if ((key & mask_hi) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+  __syncthreads();
+  const SelGlobal sg{K, I};
+  if (k * 64 <= n) {
+    if (tid == 0) sel_heap_select(sg, 0, k, n);
+  } else {
+    const int64_t nth = k - 1;
+    if (tid == 0) {
+      s_first = 0;
+      s_last = n;
+      s_depth = 2 * floor_log2(n);
+      s_end = 0;
     }
     __syncthreads();
-    if (tid == 0) {
-      uint32_t want = s_want, cum = 0u;
-      int bin = 255;
-      for (; bin > 0; --bin) {
-        if (cum + hist[bin] >= want) break;
-        cum += hist[bin];
+    while (true) {
+      const int64_t first = s_first, last = s_last;
+      const int depth = s_depth;
+      __syncthreads();  // every thread has read the state before thread 0 changes it
+      if (last - first <= 3) {
+        if (tid == 0) sel_insertion_sort(sg, first, last);
+        break;
       }
-      s_want = want - cum;
-      s_prefix = prefix | (static_cast<uint32_t>(bin) << shift);
+      if (depth == 0) {
+        if (tid == 0) {
+          sel_heap_select(sg, first, nth + 1, last);
+          sg.swap(first, nth);
+        }
+        break;
+      }
+      if (tid == 0) {
+        s_depth = depth - 1;
+        sel_move_median_to_first(sg, first, first + 1, first + (last - first) / 2, last - 1);
+      }
+      __syncthreads();
+      const uint32_t piv = K[first];
+      const int64_t len = last - first, chunk = (len + kTopkBlock - 1) / kTopkBlock;
+      const int64_t c0 = first + tid * chunk < last ? first + tid * chunk : last;
+      const int64_t c1 = c0 + chunk < last ? c0 + chunk : last;
+      int cl = 0, cr = 0;
+      for (int64_t p = c0; p < c1; ++p) {
+        const uint32_t kp = K[p];
+        cl += (p > first && kp <= piv) ? 1 : 0;
+        cr += kp >= piv ? 1 : 0;
+      }
+      // exclusive scans of cl and cr over the threads: inside each wave by shuffles, then over
+      // the 16 wave totals
+      const int lane = tid & 63, wv = tid >> 6;
+      int il = cl, ir = cr;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int tl = __shfl_up(il, off, 64), tr = __shfl_up(ir, off, 64);
+        if (lane >= off) {
+          il += tl;
+          ir += tr;
+        }
+      }
+      if (lane == 63) {
+        s_scl[wv] = il;
+        s_scr[wv] = ir;
+      }
+      __syncthreads();
+      int bl = 0, br = 0, nl = 0, nr = 0;
+      for (int w2 = 0; w2 < kTopkBlock / 64; ++w2) {
+        if (w2 < wv) {
+          bl += s_scl[w2];
+          br += s_scr[w2];
+        }
+        nl += s_scl[w2];
+        nr += s_scr[w2];
+      }
+      int rl = bl + il - cl, rr = br + ir - cr;
+      for (int64_t p = c0; p < c1; ++p) {
+        const uint32_t kp = K[p];
+        if (p > first && kp <= piv) PL[rl++] = static_cast<int32_t>(p);
+        if (kp >= piv) PR[nr - 1 - rr++] = static_cast<int32_t>(p);
+      }
+      if (tid == 0) {
+        s_tot[0] = 0;
+      }
+      __syncthreads();
+      const int nmin = nl < nr ? nl : nr;
+      int cnt = 0;
+      for (int i = tid; i < nmin; i += kTopkBlock) cnt += PL[i] < PR[i] ? 1 : 0;
+      if (cnt) atomicAdd(&s_tot[0], cnt);
+      __syncthreads();
+      const int m = s_tot[0];  // the pairs that are swapped form a prefix: PL rises, PR falls
+      if (tid == 0) {
+        int64_t cut = m < nl ? PL[m] : last;
+        if (m >= 1 && PR[m - 1] < cut) cut = PR[m - 1];
+        if (!(cut > first && cut < last)) {  // not reachable for a median-of-three pivot
+          *status = 1;
+          cut = -1;
+        }
+        s_cut = cut;
+      }
+      __syncthreads();
+      const int64_t cut = s_cut;
+      if (cut < 0) break;
+      for (int i = tid; i < m; i += kTopkBlock) sg.swap(PL[i], PR[i]);
+      __syncthreads();
+      if (tid == 0) {
+        if (cut <= nth) s_first = cut;
+        else s_last = cut;
+      }
+      __syncthreads();
     }
-    mask_hi |= 255u << shift;
-    __syncthreads();
   }
-  const uint32_t kth = s_prefix, want = s_want;  // keep keys > kth, and `want` keys == kth
-  const int lane = tid & 63, wv = tid >> 6;
-  for (int64_t c0 = 0; c0 < n; c0 += blockDim.x) {
-    const int64_t i = n - 1 - (c0 + tid);
-    uint32_t key = 0u;
-    bool eq = false;
-    if (i >= 0) {
-      key = ordered_key(v[i]);
-      eq = key == kth;
-    }
-    const uint64_t bal = __ballot(eq);
-    const uint32_t below = static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)));
-    if (lane == 0) wave_cnt[wv] = static_cast<uint32_t>(__popcll(bal));
-    __syncthreads();
-    uint32_t before = s_run;
-    for (int w = 0; w < wv; ++w) before += wave_cnt[w];
-    if (i >= 0) keep[i] = (key > kth || (eq && before + below < want)) ? 1.0f : 0.0f;
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t t = 0u;
-      for (int w = 0; w < (int)(blockDim.x / 64); ++w) t += wave_cnt[w];
-      s_run += t;
-    }
-    __syncthreads();
-  }
+  __syncthreads();
+  for (int64_t p = tid; p < n; p += blockDim.x) keep[I[p]] = p < k ? 1.0f : 0.0f;
 }
 
-__device__ __forceinline__ int wave_sum_i(int x) {
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
-
-// block16: top-k of each 16 x 16 tile, one wave per tile, 4 consecutive
-// elements of a tile row per lane (lane L holds tile positions 4L .. 4L + 3).
-// The k-th largest key comes from a bitwise search over the 32 key bits;
-// equal keys are kept from the highest tile position down.
+// block16: torch.topk(k) of each 16 x 16 tile (row-major positions), one
+// thread per tile running the selection above on its 256 pairs in LDS.
 template <int XD, int OD>
-__global__ void __launch_bounds__(kBlock) tile_topk_kernel(const void* __restrict__ x, int64_t cols, int64_t ib,
-                                                           int64_t nb, int k, bool vec, void* __restrict__ out) {
-  const int lane = threadIdx.x & 63;
-  const int64_t waves = ((int64_t)gridDim.x * blockDim.x) >> 6;
-  for (int64_t b = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6; b < nb; b += waves) {
+__global__ void __launch_bounds__(kSelTileThreads) tile_topk_kernel(const void* __restrict__ x, int64_t cols,
+                                                                    int64_t ib, int64_t nb, int k, bool vec,
+                                                                    void* __restrict__ out) {
+  __shared__ uint32_t keys[256 * kSelTileThreads];
+  __shared__ uint8_t idx[256 * kSelTileThreads];
+  const int t = threadIdx.x;
+  const SelTile st{keys + t, idx + t};
+  for (int64_t b = (int64_t)blockIdx.x * kSelTileThreads + t; b < nb; b += (int64_t)gridDim.x * kSelTileThreads) {
     const int64_t br = b / ib, bc = b - br * ib;
-    const int64_t e0 = (br * 16 + (lane >> 2)) * cols + bc * 16 + 4 * (lane & 3);
-    float xv[4], o[4];
-    load4<XD>(x, e0, 4, vec, xv);
-    uint32_t key[4];
+    const int64_t e0 = br * 16 * cols + bc * 16;
+    for (int r = 0; r < 16; ++r)
+      for (int q = 0; q < 4; ++q) {
+        float xv[4];
+        load4<XD>(x, e0 + r * cols + 4 * q, 4, vec, xv);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) key[j] = ordered_key(xv[j]);
-    uint32_t kth = 0u;
-    for (int bit = 31; bit >= 0; --bit) {
-      const uint32_t cand = kth | (1u << bit);
-      int c = 0;
+        for (int j = 0; j < 4; ++j) st.put(r * 16 + 4 * q + j, (static_cast<uint64_t>(ordered_key(xv[j])) << 32) |
+                                                                    static_cast<uint32_t>(r * 16 + 4 * q + j));
+      }
+    uint32_t kept[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    if (k >= 256) {
+      for (int w = 0; w < 8; ++w) kept[w] = 0xffffffffu;
+    } else if (k > 0) {
+      sel_topk_seq(st, 256, k);
+      for (int p = 0; p < k; ++p) {
+        const int e = static_cast<uint8_t>(st.get(p));
+        kept[e >> 5] |= 1u << (e & 31);
+      }
+    }
+    for (int r = 0; r < 16; ++r)
+      for (int q = 0; q < 4; ++q) {
+        float o[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) c += key[j] >= cand ? 1 : 0;
-      if (wave_sum_i(c) >= k) kth = cand;
-    }
-    int gt = 0, eq = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      gt += key[j] > kth ? 1 : 0;
-      eq += key[j] == kth ? 1 : 0;
-    }
-    const int want = k - wave_sum_i(gt);
-    // equal keys at higher tile positions: lanes above this one, then j' > j inside it
-    int incl = eq;
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += t;
-    }
-    const int total = __shfl(incl, 63, 64);
-    int above = total - incl;
-#pragma unroll
-    for (int j = 3; j >= 0; --j) {
-      const bool e = key[j] == kth;
-      o[j] = (key[j] > kth || (e && above < want)) ? 1.0f : 0.0f;
-      above += e ? 1 : 0;
-    }
-    store4<OD>(out, e0, 4, vec, o);
+        for (int j = 0; j < 4; ++j) {
+          const int e = r * 16 + 4 * q + j;
+          o[j] = ((kept[e >> 5] >> (e & 31)) & 1u) ? 1.0f : 0.0f;
+        }
+        store4<OD>(out, e0 + r * cols + 4 * q, 4, vec, o);
+      }
   }
 }
 
@@ -2484,12 +2711,27 @@ extern "C" int sf_block_stat(const void* x, int x_dtype, int64_t rows, int64_t c
   return launch_status("sf_block_stat");
 }
 
-extern "C" int sf_topk_keep(const float* v, int64_t n, int64_t k, float* keep, void* stream) {
+extern "C" size_t sf_topk_keep_workspace_size(int64_t n) {
+  return n <= 0 ? 0 : static_cast<size_t>(n) * 16 + 256;
+}
+
+extern "C" int sf_topk_keep(const float* v, int64_t n, int64_t k, float* keep, void* workspace,
+                            size_t workspace_bytes, void* stream) {
   SF_CHECK_ARG(n >= 0, "negative length");
   if (n == 0) return SF_OK;
   SF_CHECK_ARG(v && keep, "null tensor");
   SF_CHECK_ARG(n < (1ll << 31), "top-k over more than 2^31 entries");
-  topk_keep_kernel<<<1, kTopkBlock, 0, static_cast<hipStream_t>(stream)>>>(v, n, k, keep);
+  SF_CHECK_ARG(workspace && workspace_bytes >= sf_topk_keep_workspace_size(n) &&
+                   (reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+               "top-k needs a 16-byte aligned workspace of sf_topk_keep_workspace_size(n) bytes");
+  unsigned char* w = static_cast<unsigned char*>(workspace);
+  uint32_t* K = reinterpret_cast<uint32_t*>(w);
+  int32_t* I = reinterpret_cast<int32_t*>(w + 4 * n);
+  int32_t* PL = reinterpret_cast<int32_t*>(w + 8 * n);
+  int32_t* PR = reinterpret_cast<int32_t*>(w + 12 * n);
+  int* status = reinterpret_cast<int*>(w + 16 * n);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  topk_keep_kernel<<<1, kTopkBlock, 0, st>>>(v, n, k, keep, K, I, PL, PR, status);
   return launch_status("sf_topk_keep");
 }
 
@@ -2507,10 +2749,9 @@ extern "C" int sf_tile_topk(const void* x, int x_dtype, int64_t rows, int64_t co
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool vec = vec_ok(cols, {{x, x_dtype}, {out, out_dtype}});
   if (nb > 0) {
-    // k = 0 / 256 need no special case: the search then yields all zeros / all ones
     const int kk = static_cast<int>(k <= 0 ? 0 : (k >= 256 ? 256 : k));
 #define SF_LAUNCH_TILE(XD, OD) \
-  tile_topk_kernel<XD, OD><<<elementwise_grid(nb * 64, kBlock), kBlock, 0, st>>>(x, cols, ib, nb, kk, vec, out)
+  tile_topk_kernel<XD, OD><<<static_cast<unsigned>(ceil_div(nb, kSelTileThreads) < 65536 ? ceil_div(nb, kSelTileThreads) : 65536), kSelTileThreads, 0, st>>>(x, cols, ib, nb, kk, vec, out)
     if (x_dtype == SF_DTYPE_F32 && out_dtype == SF_DTYPE_F32) SF_LAUNCH_TILE(SF_DTYPE_F32, SF_DTYPE_F32);
     else if (x_dtype == SF_DTYPE_F32) SF_LAUNCH_TILE(SF_DTYPE_F32, SF_DTYPE_BF16);
     else if (out_dtype == SF_DTYPE_F32) SF_LAUNCH_TILE(SF_DTYPE_BF16, SF_DTYPE_F32);

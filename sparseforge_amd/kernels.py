@@ -284,12 +284,16 @@ def block_stat(x: torch.Tensor, bs: int, stat: int) -> torch.Tensor:
 
 
 def topk_keep(v: torch.Tensor, k: int) -> torch.Tensor:
-    """f32 flags of the k largest entries of a 1-D f32 tensor (ties: higher index first)."""
+    """f32 flags of the entries torch.topk(v, k) keeps for a 1-D f32 tensor (equal values as torch's
+    CPU selection keeps them)."""
     dev = L.require_device(v)
     if v.dim() != 1 or v.dtype != torch.float32:
         raise ValueError("topk_keep expects a 1-D float32 tensor")
     keep = torch.empty_like(v)
-    L.check(L.lib().sf_topk_keep(L.ptr(v), v.numel(), int(k), L.ptr(keep), L.stream(dev)), "sf_topk_keep")
+    wb = L.lib().sf_topk_keep_workspace_size(v.numel())
+    ws = torch.empty(max(wb, 16), dtype=torch.uint8, device=dev)
+    L.check(L.lib().sf_topk_keep(L.ptr(v), v.numel(), int(k), L.ptr(keep), L.ptr(ws), wb, L.stream(dev)),
+            "sf_topk_keep")
     return keep
 
 

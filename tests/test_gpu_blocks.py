@@ -57,21 +57,35 @@ def test_block_hard_mask_matches_reference(cuda_device, case, dtype):
     assert np.array_equal(got.float().cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("n, k", [(1, 1), (7, 3), (1000, 0), (1000, 1000), (1000, 999), (176128, 88064),
-                                  (300001, 12345)])
-def test_topk_keep_matches_oracle_with_ties(cuda_device, n, k):
+def _torch_keep(v, k):
+    """The entries torch.topk keeps (CPU kernel) as a boolean mask along the last axis."""
+    t = torch.from_numpy(np.ascontiguousarray(v))
+    keep = torch.zeros(t.shape, dtype=torch.bool)
+    if k > 0:
+        keep.scatter_(-1, torch.topk(t, k, dim=-1).indices, True)
+    return keep.numpy()
+
+
+@pytest.mark.parametrize("n, k, nv", [(1, 1, 50), (7, 3, 2), (1000, 0, 50), (1000, 1000, 50), (1000, 999, 50),
+                                      (176128, 88064, 50), (176128, 88064, 3), (44032, 13210, 2), (300001, 12345, 50),
+                                      (300001, 4000, 50), (5000, 70, 4), (256, 1, 3), (9, 9 // 2, 1)])
+def test_topk_keep_matches_torch_with_ties(cuda_device, n, k, nv):
+    """Equal values kept exactly as torch.topk keeps them, on both sides of its partial-sort switch."""
     _, K, _ = _mods()
-    rng = np.random.default_rng(n + k)
-    v = rng.integers(0, 50, size=n).astype(np.float32) / 7.0  # heavy ties
+    rng = np.random.default_rng(n + k + nv)
+    v = rng.integers(0, nv, size=n).astype(np.float32) / 7.0  # heavy ties
     if n > 10:
         v[rng.integers(0, n, size=3)] = np.nan
         v[rng.integers(0, n, size=3)] = -0.0
-    got = K.topk_keep(torch.from_numpy(v).to(cuda_device), k).cpu().numpy()
-    assert np.array_equal(got > 0.5, om.topk_keep_desc(v, k))
+    got = K.topk_keep(torch.from_numpy(v).to(cuda_device), k).cpu().numpy() > 0.5
+    assert np.array_equal(got, om.topk_keep_desc(v, k))
+    if 0 < k < n:
+        assert np.array_equal(got, _torch_keep(v, k))
 
 
 @pytest.mark.parametrize("shape, k", [((64, 96), 128), ((40, 56), 179), ((33, 50), 1), ((48, 48), 255),
-                                      ((32, 32), 0), ((32, 32), 256), ((1024, 4096), 128)])
+                                      ((32, 32), 0), ((32, 32), 256), ((1024, 4096), 128), ((256, 512), 4),
+                                      ((256, 512), 3)])
 def test_tile_topk_matches_oracle_with_ties(cuda_device, shape, k):
     _, K, _ = _mods()
     rng = np.random.default_rng(shape[0] + k)
@@ -80,6 +94,12 @@ def test_tile_topk_matches_oracle_with_ties(cuda_device, shape, k):
     sr = 1.0 - k / 256.0
     assert om.keep_count(1.0 - sr, 256) == k
     assert np.array_equal(got, om.hard_mask_from_soft(x, "block16", sparsity_ratio=sr))
+    if 0 < k < 256:  # against torch.topk along each flattened tile
+        of, inf = shape[0] // 16 * 16, shape[1] // 16 * 16
+        ob, ib = of // 16, inf // 16
+        tiles = x[:of, :inf].reshape(ob, 16, ib, 16).transpose(0, 2, 1, 3).reshape(ob, ib, 256)
+        want = _torch_keep(tiles, k).reshape(ob, ib, 16, 16).transpose(0, 2, 1, 3).reshape(of, inf)
+        assert np.array_equal(got[:of, :inf] > 0.5, want)
 
 
 @pytest.mark.parametrize("bs", [16, 32])
