@@ -584,7 +584,6 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16_t 
   float* ep = reinterpret_cast<float*>(smem) + wave * (64 * kEpiPitch);
   const int64_t wrow0 = m0 + wm * kWaveM, wcol0 = n0 + wn * kWaveN;
   const bool cbf = g.c_dtype == SF_DTYPE_BF16;
-  const bool plain = !g.emask && !g.accumulate;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     __syncthreads();
@@ -639,13 +638,33 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const f32x16_t 
       }
       const int64_t off = row * g.ldc + col;
       const bool vec = g.c_aligned && col + 8 <= g.N && (off & 7) == 0;
-      if (plain && vec) {
-        // result of the matmul in the output dtype, then + bias (rounded again)
+      if (!g.emask && vec) {
+        // result of the matmul in the output dtype, then + bias (rounded again), then + C when
+        // accumulating: the per-element sequence below, 8 outputs at a time
         if (g.bias) {
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
             const float b = load_elem(g.bias, col + q, g.bias_dtype);
             v[q] = cbf ? hround(v[q]) + b : v[q] + b;
+          }
+        }
+        if (g.accumulate) {
+          float c[8];
+          if (cbf) {
+            const uint4 cw = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(g.C) + off);
+            const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c[q] = bf16_to_f32(static_cast<uint16_t>(w4[q >> 1] >> (16 * (q & 1))));
+          } else {
+            const float4 c0 = *reinterpret_cast<const float4*>(static_cast<const float*>(g.C) + off);
+            const float4 c1 = *reinterpret_cast<const float4*>(static_cast<const float*>(g.C) + off + 4);
+            c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w;
+            c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+          }
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float x = cbf ? hround(v[q]) : v[q];  // the product (+ bias) in the output dtype
+            v[q] = c[q] + x;
           }
         }
         if (cbf) {
@@ -1580,7 +1599,6 @@ __global__ void __launch_bounds__(kThreads, 1) bsr_mm_kernel(GemmArgs g) {
 
   DmaLoader dak;
   dak.init(g.A1, g.lda1, m0, g.M, g.K1);
-  using Tail = std::integral_constant<bool, true>;
 
   // fragment offsets: A as the dense kernel's K-contiguous tile; B per wave fragment j (output
   // blocks 8 wn + 2 j, + 1) at reduction block 0 (block r adds r * 512)
@@ -1789,7 +1807,6 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyArgs g) {
   const int64_t s0 = kz * g.split_stages;
   const int64_t s1 = s0 + g.split_stages < nk ? s0 + g.split_stages : nk;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
   // Register stage of one K step.  K layout: 16-byte chunks of rows, stored as they are.
   // MN layout: A' as a 4 (k) x 8 (m) block per thread (k fastest over the threads), B' as
   // a 2 (k) x 8 (n) block; both are transposed in registers, so every LDS write is one

@@ -258,6 +258,13 @@ def _as_values(E: torch.Tensor | None, dt: torch.dtype) -> torch.Tensor | None:
     return E
 
 
+def _cat_k(parts, dim: int):
+    """The operands of one K segment side by side (None when there are none)."""
+    if not parts:
+        return None
+    return parts[0] if len(parts) == 1 else torch.cat(parts, dim).contiguous()
+
+
 def _pad_rank(P: torch.Tensor, S: torch.Tensor):
     """Zero-pad the SLoRB rank to a multiple of the vector width."""
     r = P.shape[0]
@@ -296,7 +303,6 @@ class _MaskedLinearBackward(torch.autograd.Function):
             dx = mm_nn(gy, Wm, A2=dz, B2=P, K2=P.shape[0])
         else:
             dx = mm_nn(gy, Wm)
-        del Wm
         if decay != 0.0:
             dW = mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay)
         else:
@@ -304,64 +310,57 @@ class _MaskedLinearBackward(torch.autograd.Function):
         db = column_sum(gy, W.dtype) if has_bias else None
         dP = mm_tn(dz, x) if has_slorb else None
         dS = mm_tn(gy, z) if has_slorb else None
-        ctx.save_for_backward(gy, x, W, P, S, E, z, dz)
+        # W.E stays for the double backward's d/d gy (gdx (W.E)^T), so that product runs unmasked
+        ctx.save_for_backward(gy, x, W, P, S, E, z, dz, Wm if E is not None else None)
+        del Wm
         ctx.decay = decay
         ctx.has_slorb = has_slorb
         return dx, dW, db, dP, dS
 
     @staticmethod
     def backward(ctx, g_dx, g_dW, g_db, g_dP, g_dS):
-        gy, x, W, P, S, E, z, dz = ctx.saved_tensors
+        gy, x, W, P, S, E, z, dz, Wm = ctx.saved_tensors
         T, out = gy.shape
         dt = gy.dtype
         g_dx, g_dW, g_db, g_dP, g_dS = (_opt(t) for t in (g_dx, g_dW, g_db, g_dP, g_dS))
         if not ctx.has_slorb:
             g_dP = g_dS = None
-        # d/d gy = gdx (W.E)^T + x gdW^T + [gdx P^T + x gdP^T] S^T + z gdS^T + gdb
-        ggy = None
-        if g_dx is not None and g_dW is not None:
-            ggy = mm_nt(g_dx, W, bmask=E, A2=x, B2=g_dW, K2=x.shape[1], bias=g_db)
-        elif g_dx is not None:
-            ggy = mm_nt(g_dx, W, bmask=E, bias=g_db)
-        elif g_dW is not None:
-            ggy = mm_nt(x, g_dW, bias=g_db)
+        # d/d gy = gdx (W.E)^T + x gdW^T + u S^T + z gdS^T + gdb with u = gdx P^T + x gdP^T: the
+        # low-rank terms ride as one second K segment [u | z] . [S | gdS]^T of the first full-size
+        # product; the second full-size product accumulates into its output in the output dtype
+        # (as autograd sums gradient contributions)
         u = None
         if ctx.has_slorb:
-            if g_dx is not None and g_dP is not None:
-                u = mm_nt(g_dx, P, A2=x, B2=g_dP, K2=x.shape[1])
-            elif g_dx is not None:
+            if g_dx is not None:
                 u = mm_nt(g_dx, P)
+                if g_dP is not None:
+                    mm_nt(x, g_dP, out=u, accumulate=True)
             elif g_dP is not None:
                 u = mm_nt(x, g_dP)
-            if u is not None or g_dS is not None:
-                if ggy is None:
-                    ggy = torch.zeros(T, out, dtype=dt, device=gy.device)
-                    if g_db is not None:
-                        ggy += g_db
-                if u is not None and g_dS is not None:
-                    mm_nt(u, S, A2=z, B2=g_dS, K2=z.shape[1], out=ggy, accumulate=True)
-                elif u is not None:
-                    mm_nt(u, S, out=ggy, accumulate=True)
-                else:
-                    mm_nt(z, g_dS, out=ggy, accumulate=True)
+        la = _cat_k([t for t in (u, z if g_dS is not None else None) if t is not None], 1)
+        lb = _cat_k([t for t, a in ((S, u), (g_dS, g_dS)) if a is not None], 1)
+        seg = {"A2": la, "B2": lb, "K2": la.shape[1]} if la is not None else {}
+        ggy = None
+        if g_dx is not None:
+            ggy = mm_nt(g_dx, Wm if Wm is not None else W, bias=g_db, **seg)
+            if g_dW is not None:
+                mm_nt(x, g_dW, out=ggy, accumulate=True)
+        elif g_dW is not None:
+            ggy = mm_nt(x, g_dW, bias=g_db, **seg)
+        elif la is not None:
+            ggy = mm_nt(la, lb, bias=g_db)
         if ggy is None and g_db is not None:
             ggy = g_db.expand(T, out).to(dt).contiguous()
-        # d/dx = gy gdW + (gy gdS) P + dz gdP
+        # d/dx = gy gdW + [w | dz] . [P ; gdP] with w = gy gdS (one GEMM, the low-rank part its
+        # second K segment)
+        w = mm_nn(gy, g_dS) if ctx.has_slorb and g_dS is not None else None
+        ra = _cat_k([t for t in (w, dz if g_dP is not None else None) if t is not None], 1)
+        rb = _cat_k([t for t, a in ((P, w), (g_dP, g_dP)) if a is not None], 0)
         gx = None
         if g_dW is not None:
-            gx = mm_nn(gy, g_dW)
-        if ctx.has_slorb and (g_dS is not None or g_dP is not None):
-            w = mm_nn(gy, g_dS) if g_dS is not None else None
-            if gx is None:
-                gx = torch.zeros_like(x)
-            if w is not None and g_dP is not None:
-                mm_nn(w, P, A2=dz, B2=g_dP, K2=dz.shape[1], out=gx, accumulate=True)
-            elif w is not None:
-                mm_nn(w, P, out=gx, accumulate=True)
-            else:
-                mm_nn(dz, g_dP, out=gx, accumulate=True)
-        else:
-            w = None
+            gx = mm_nn(gy, g_dW, **({"A2": ra, "B2": rb, "K2": ra.shape[1]} if ra is not None else {}))
+        elif ra is not None:
+            gx = mm_nn(ra, rb)
         # d/dW = (gy^T gdx) . E  (+ decay gdW [E < 0.5]: the SR-STE term decay W [E < 0.5] of dW is
         # elementwise in W, legacy/sparse_modeling.py:123-125)
         gW = mm_tn(gy, g_dx, emask=_as_values(E, W.dtype)) if g_dx is not None else None
@@ -370,8 +369,9 @@ class _MaskedLinearBackward(torch.autograd.Function):
         # d/dP = dz^T gdx + (gy gdS)^T x ;  d/dS = gy^T (gdx P^T + x gdP^T)
         gP = gS = None
         if ctx.has_slorb:
-            if g_dx is not None and w is not None:
-                gP = gemm(P.shape[0], P.shape[1], dz, g_dx, T, L.LAYOUT_MN, L.LAYOUT_MN, A2=w, B2=x, K2=T)
+            if g_dx is not None and w is not None:  # two skinny products (K = tokens each)
+                gP = mm_tn(dz, g_dx)
+                mm_tn(w, x, out=gP, accumulate=True)
             elif g_dx is not None:
                 gP = mm_tn(dz, g_dx)
             elif w is not None:
