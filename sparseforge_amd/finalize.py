@@ -182,12 +182,19 @@ class SparseLinear24(torch.nn.Module):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1]).to(torch.bfloat16).contiguous()
         b = None if self.bias is None else self.bias.detach().contiguous()
-        y = gemm_2to4(x2, self.packed, b)
-        if self.x_proj is not None:
+        if self.x_proj is None:
+            y = gemm_2to4(x2, self.packed, b)
+        else:
+            # the SLoRB term as the product's second (dense) K segment: x W^T + z S^T + b rounded once,
+            # as the masked layer rounds it; the rank is zero-padded to the segment's multiple of 8
             P = self.x_proj.to(device=x2.device, dtype=torch.bfloat16).contiguous()
             S = self.slorb_weight.to(device=x2.device, dtype=torch.bfloat16).contiguous()
-            u = LIN.mm_nt(x2, P)
-            y = LIN.mm_nt(u, S, out=y, accumulate=True)
+            z = LIN.mm_nt(x2, P)
+            pad = -z.shape[1] % 8
+            if pad:
+                z = torch.nn.functional.pad(z, (0, pad))
+                S = torch.nn.functional.pad(S, (0, pad))
+            y = LIN.gemm_2to4(x2, self.vals, self.idx, self.out_features, z=z, S=S, bias=b)
         return y.reshape(*shape[:-1], self.out_features)
 
 

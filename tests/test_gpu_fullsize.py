@@ -3,7 +3,9 @@ own float32 GPU results (the float64 CPU oracle would take minutes at these size
 
 * SparseLinear fwd / dX / dW / dP / dS at the q/k/v/o, gate/up and down shapes of a
   LLaMA-2-7B layer (T = 8192) with the hard 2:4 mask and SLoRB rank 64: against torch
-  float32 products of the same bf16 operands, rtol 2e-2 (bf16) relative to the output scale.
+  float32 products of the same bf16 operands, each element within bf16 rounding
+  (2^-7 of its magnitude plus 2^-12 of the output scale, plus one ulp of each term of
+  the bf16 SLoRB intermediates z = X P^T and dz = dY S).
 * the fused mask update over a full [11008, 4096] layer: the new mask stays in [0, 1], its
   hard 2:4 projection keeps exactly two of every four, and the flip count equals the number
   of changed hard-mask entries counted independently.
@@ -14,11 +16,6 @@ import pytest
 import torch
 
 pytestmark = pytest.mark.gpu
-
-
-def rel_err(got, ref):
-    got, ref = got.detach().float(), ref.detach().float()
-    return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
 
 
 def within_bf16_rounding(got, ref, extra=None) -> float:
@@ -62,20 +59,18 @@ def test_sparse_linear_full_shape(cuda_device, in_f, out_f):
     xf, gyf, Pf, Sf = x.detach().float(), gy.float(), P.detach().float(), S.detach().float()
     z = xf @ Pf.t()
     dz = gyf @ Sf
-    assert rel_err(y, xf @ Wm.t() + z @ Sf.t()) < 2e-2
-    assert rel_err(x.grad, gyf @ Wm + dz @ Pf) < 2e-2         # dX = dY (W . M) + (dY S) P
-    assert rel_err(W.grad, gyf.t() @ xf) < 2e-2              # dW = dY^T X (straight-through, unmasked)
-    assert rel_err(P.grad, dz.t() @ xf) < 2e-2               # dP = (dY S)^T X
-    assert rel_err(S.grad, gyf.t() @ z) < 2e-2               # dS = dY^T (X P^T)
-    # elementwise: each bf16 result within rounding of the float32 product, the SLoRB intermediates z and
-    # dz rounded to bf16 first as the bf16 path (and the reference under autocast) stores them
+    # each bf16 result within rounding of the float32 product, the SLoRB intermediates z and dz rounded to
+    # bf16 first as the bf16 path (and the reference under autocast) stores them
     zb, dzb = z.bfloat16().float(), dz.bfloat16().float()
     ulp = 2.0 ** -7
-    checks = ((y, xf @ Wm.t() + zb @ Sf.t(), (zb.abs() @ Sf.abs().t()) * ulp),
-              (x.grad, gyf @ Wm + dzb @ Pf, (dzb.abs() @ Pf.abs()) * ulp),
-              (W.grad, gyf.t() @ xf, None))
-    for got, ref, extra in checks:
-        assert within_bf16_rounding(got, ref, extra) <= 1.0
+    checks = (("y", y, xf @ Wm.t() + zb @ Sf.t(), (zb.abs() @ Sf.abs().t()) * ulp),
+              ("dX", x.grad, gyf @ Wm + dzb @ Pf, (dzb.abs() @ Pf.abs()) * ulp),   # dY (W . M) + (dY S) P
+              ("dW", W.grad, gyf.t() @ xf, None),                                   # dY^T X (unmasked)
+              ("dP", P.grad, dzb.t() @ xf, (dzb.abs().t() @ xf.abs()) * ulp),       # (dY S)^T X
+              ("dS", S.grad, gyf.t() @ zb, (gyf.abs().t() @ zb.abs()) * ulp))       # dY^T (X P^T)
+    for name, got, ref, extra in checks:
+        err = within_bf16_rounding(got, ref, extra)
+        assert err <= 1.0, (name, err)
 
 
 def test_update_mask_full_layer_properties(cuda_device):

@@ -1,14 +1,18 @@
 """GPU parity of the masked linear GEMMs (K1-K5) against a float64 CPU reference.
 
-Bar: f32 within rtol 1e-5 (relative to the output scale), bf16 within rtol
-2e-2; gradients follow the reference's STE semantics (dW unmasked, no weight
-scale in dx, legacy/sparse_modeling.py:96-132).
+Bar (conftest.gemm_err): each bf16 result within 2^-7 of its own magnitude plus
+2^-12 of the output scale of the float64 product of the same operands, the
+operands rounded as the kernels and the reference round them (W.E, then W.E.s,
+in the weight dtype; the SLoRB intermediates z = x P^T and dz = dy S in the
+activation dtype, with one ulp of slack each); float32 results within 1e-5 of
+the output scale.  Gradients follow the reference's STE semantics (dW unmasked,
+no weight scale in dx, legacy/sparse_modeling.py:96-132).
 """
 import numpy as np
 import pytest
 import torch
 
-from conftest import load_golden
+from conftest import BF16_ULP, bias_slack, gemm_err, load_golden
 
 pytestmark = pytest.mark.gpu
 
@@ -26,9 +30,9 @@ def rel_err(got: torch.Tensor, ref: torch.Tensor) -> float:
     return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(256, 512, 384), (300, 136, 72), (1024, 768, 3072), (64, 4096, 8)])
-def test_gemm_layouts(cuda_device, dtype, tol, shape):
+def test_gemm_layouts(cuda_device, dtype, shape):
     L, lin = _lin()
     M, K, N = shape
     g = torch.Generator().manual_seed(M + K + N)
@@ -38,19 +42,19 @@ def test_gemm_layouts(cuda_device, dtype, tol, shape):
     At = A.t().contiguous()
     ref = A.double() @ B.double().t()
     d = lambda t: t.to(cuda_device)
-    assert rel_err(lin.mm_nt(d(A), d(B)), ref) < tol
-    assert rel_err(lin.mm_nn(d(A), d(Bt)), ref) < tol
+    assert gemm_err(lin.mm_nt(d(A), d(B)), ref, dtype) <= 1.0
+    assert gemm_err(lin.mm_nn(d(A), d(Bt)), ref, dtype) <= 1.0
     vec = 8 if dtype == torch.bfloat16 else 4
     if M % vec:
         # an M-contiguous operand needs M to be a multiple of the 16-byte vector: rejected on the host
         with pytest.raises(ValueError, match="multiples"):
             lin.mm_tn(d(At), d(Bt))
     else:
-        assert rel_err(lin.mm_tn(d(At), d(Bt)), ref) < tol
+        assert gemm_err(lin.mm_tn(d(At), d(Bt)), ref, dtype) <= 1.0
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-def test_gemm_mask_scale_bias_and_segment(cuda_device, dtype, tol):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gemm_mask_scale_bias_and_segment(cuda_device, dtype):
     L, lin = _lin()
     g = torch.Generator().manual_seed(1)
     T, IN, OUT, R = 320, 256, 200, 16
@@ -62,16 +66,18 @@ def test_gemm_mask_scale_bias_and_segment(cuda_device, dtype, tol):
     b = torch.randn(OUT, generator=g).to(dtype)
     d = lambda t: t.to(cuda_device)
     got = lin.mm_nt(d(x), d(W), bmask=d(E), bscale=1.5, A2=d(z), B2=d(S), K2=R, bias=d(b))
-    Wm = (W.double() * E.double())
-    ref = x.double() @ (Wm * 1.5).t() + z.double() @ S.double().t() + b.double()
-    assert rel_err(got, ref) < tol
+    # the masked operand as the reference forms it (legacy/sparse_modeling.py:79-81): w = W * E, then
+    # w * scale, each rounded to the weight dtype
+    Wm = W * E
+    prod = x.double() @ (Wm * 1.5).double().t() + z.double() @ S.double().t()
+    assert gemm_err(got, prod + b.double(), dtype, bias_slack(prod, dtype)) <= 1.0
     dx = lin.mm_nn(d(x[:, :OUT].contiguous()), d(W), bmask=d(E))
-    assert rel_err(dx, x[:, :OUT].double() @ Wm) < tol
+    assert gemm_err(dx, x[:, :OUT].double() @ Wm.double(), dtype) <= 1.0
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(256, 512, 384), (300, 136, 72), (1024, 768, 3072)])
-def test_gemm_byte_and_mask(cuda_device, dtype, tol, shape):
+def test_gemm_byte_and_mask(cuda_device, dtype, shape):
     """A uint8 and-mask (0xFF keep / 0x00 prune) equals multiplying by the 0/1 mask, in both B layouts."""
     L, lin = _lin()
     M, K, N = shape
@@ -83,15 +89,15 @@ def test_gemm_byte_and_mask(cuda_device, dtype, tol, shape):
     ref = A.double() @ (B.double() * keep.double()).t()
     d = lambda t: t.to(cuda_device)
     got = lin.mm_nt(d(A), d(B), bmask=d(E8))
-    assert rel_err(got, ref) < tol
+    assert gemm_err(got, ref, dtype) <= 1.0
     # input-grad layout: C = G . (B.E) with B [N, K] read N-contiguous
     G = torch.randn(M, N, generator=g).to(dtype)
     got2 = lin.mm_nn(d(G), d(B), bmask=d(E8))
     ref2 = G.double() @ (B.double() * keep.double())
-    assert rel_err(got2, ref2) < tol
+    assert gemm_err(got2, ref2, dtype) <= 1.0
     # the same with the mask also given K-major ([K, N] here: B's columns are the GEMM's n)
     got3 = lin.mm_nn(d(G), d(B), bmask=d(E8), bmask_t=lin.transpose_u8(d(E8)))
-    assert rel_err(got3, ref2) < tol
+    assert gemm_err(got3, ref2, dtype) <= 1.0
 
 
 @pytest.mark.parametrize("shape", [(64, 64), (3, 5), (130, 67), (4096, 11008), (11008, 4096), (1, 1000)])
@@ -115,9 +121,9 @@ def test_gemm_input_grad_kmajor_mask(cuda_device, M, N, K):
     d = lambda t: t.to(cuda_device)
     got = lin.mm_nn(d(G), d(W), bmask=d(E8), bmask_t=lin.transpose_u8(d(E8)))
     ref = G.double() @ (W.double() * keep.double())
-    assert rel_err(got, ref) < 2e-2
+    assert gemm_err(got, ref, torch.bfloat16) <= 1.0
     plain = lin.mm_nn(d(G), d(W))
-    assert rel_err(plain, G.double() @ W.double()) < 2e-2
+    assert gemm_err(plain, G.double() @ W.double(), torch.bfloat16) <= 1.0
 
 
 @pytest.mark.parametrize("mdt", [torch.float32, torch.bfloat16])
@@ -136,34 +142,37 @@ def test_effective_mask_hard_bytes_bit_exact(cuda_device, mdt, cols):
 
 
 def _dense_reference(x, W, b, E, s, P, S, gy):
-    """float64 CPU restatement of FusedMaskedLinearSTE + SLoRB forward/backward."""
-    x = x.double().requires_grad_(True)
-    Wd, Ed = W.double(), E.double()
-    y = x @ (Wd * Ed * s).t()
-    if b is not None:
-        y = y + b.double()
-    if P is not None:
-        Pd = P.double().requires_grad_(True)
-        Sd = S.double().requires_grad_(True)
-        y = y + (x @ Pd.t()) @ Sd.t()
+    """float64 products of FusedMaskedLinearSTE + SLoRB forward / backward (legacy/sparse_modeling.py:72-132,
+    :790-794) over the operands rounded as the layer rounds them: w = W * E, then w * s, in the weight
+    dtype (:79-81); z = x P^T and dz = dy S stored in the activation dtype.  Returns the references and,
+    for bf16, the elementwise slack of one ulp of z or dz (two float32 sums may round to neighbours)."""
+    dt = x.dtype
+    Wm = W * E
+    Ws = Wm * s if s != 1.0 else Wm
+    xd, gyd, Pd, Sd = x.double(), gy.double(), P.double(), S.double()
+    z = (xd @ Pd.t()).to(dt).double()
+    dz = (gyd @ Sd).to(dt).double()
+    prod = xd @ Ws.double().t() + z @ Sd.t()
+    y = prod + b.double() if b is not None else prod
     # STE: dW = gy^T x (unmasked), dx = gy (W.E) without s
-    gyd = gy.double()
-    dW = gyd.t() @ x.detach()
-    db = gyd.sum(0) if b is not None else None
-    dx = gyd @ (Wd * Ed)
-    out = dict(y=y.detach(), dW=dW, db=db)
-    if P is not None:
-        z = x.detach() @ Pd.detach().t()
-        dz = gyd @ Sd.detach()
-        dx = dx + dz @ Pd.detach()
-        out.update(dP=dz.t() @ x.detach(), dS=gyd.t() @ z)
-    out["dx"] = dx
-    return out
+    ref = dict(y=y, dx=gyd @ Wm.double() + dz @ Pd, dW=gyd.t() @ xd, db=gyd.sum(0), dP=dz.t() @ xd,
+               dS=gyd.t() @ z)
+    u = BF16_ULP if dt == torch.bfloat16 else 0.0
+    # y: the bias is added to the rounded product (as the reference's out + bias)
+    slack = dict(y=u * (z.abs() @ Sd.abs().t()) + (u / 2 * prod.abs() if b is not None else 0.0),
+                 dx=u * (dz.abs() @ Pd.abs()), dP=u * (dz.abs().t() @ xd.abs()), dS=u * (gyd.abs().t() @ z.abs()))
+    return ref, slack
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("mode", ["soft", "mix", "hard", "none"])
-def test_sparse_linear_fwd_bwd(cuda_device, dtype, tol, mode):
+def test_sparse_linear_fwd_bwd(cuda_device, dtype, mode):
+    """SparseLinear (soft / mixed / hard effective mask, SLoRB rank 16, bias, weight scaling) forward and
+    backward against the float64 products of the same rounded operands.  The mixed mask is formed as the
+    reference forms it, hx * M + (1 - hx) * hard(M) with each op rounded to the mask dtype (:759-771),
+    and must equal the layer's own effective mask bit for bit."""
+    from sparseforge_amd import _lib as L
+    from sparseforge_amd import linear as lin
     from sparseforge_amd import sparse_modeling as sm
     from oracle import masks as om
 
@@ -193,21 +202,23 @@ def test_sparse_linear_fwd_bwd(cuda_device, dtype, tol, mode):
     y = layer(xd)
     y.backward(gy.to(cuda_device))
     if mode == "none":
-        E, s = torch.ones(OUT, IN), 1.0
+        E, s = torch.ones(OUT, IN, dtype=dtype), 1.0
     elif mode == "soft":
-        E, s = M.float(), 1.0
+        E, s = M, 1.0
     else:
-        hard = torch.from_numpy(om.hard_mask_from_soft(M.float().numpy(), "nm_2_4"))
-        E = hx * M.float() + (1 - hx) * hard
+        hard = torch.from_numpy(om.hard_mask_from_soft(M.float().numpy(), "nm_2_4")).to(dtype)
+        E = hx * M + (1 - hx) * hard
         s = 1.0 + (1.0 - hx) * (2.0 - 1.0) if cfg.weight_scaling else 1.0
-    ref = _dense_reference(x.reshape(T, IN), W, b, E.to(dtype), s, layer.x_proj.detach().cpu(),
-                           layer.SLoRB_Weight.detach().cpu(), gy.reshape(T, OUT))
-    assert rel_err(y.reshape(T, OUT), ref["y"]) < tol
-    assert rel_err(xd.grad.reshape(T, IN), ref["dx"]) < tol
-    assert rel_err(layer.weight.grad, ref["dW"]) < tol
-    assert rel_err(layer.bias.grad, ref["db"]) < tol
-    assert rel_err(layer.x_proj.grad, ref["dP"]) < tol
-    assert rel_err(layer.SLoRB_Weight.grad, ref["dS"]) < tol
+        if mode == "mix":
+            got_E = lin.effective_mask(layer.mask.detach(), dtype, "mix", hx, L.HARD_NM_TAIL_KEEP, 2).cpu()
+            assert torch.equal(got_E, E)
+    ref, slack = _dense_reference(x.reshape(T, IN), W, b, E, s, layer.x_proj.detach().cpu(),
+                                  layer.SLoRB_Weight.detach().cpu(), gy.reshape(T, OUT))
+    for name, got, extra in (("y", y.reshape(T, OUT), slack["y"]), ("dx", xd.grad.reshape(T, IN), slack["dx"]),
+                             ("dW", layer.weight.grad, None), ("db", layer.bias.grad, None),
+                             ("dP", layer.x_proj.grad, slack["dP"]), ("dS", layer.SLoRB_Weight.grad, slack["dS"])):
+        err = gemm_err(got, ref[name], dtype, extra)
+        assert err <= 1.0, (name, err)
 
 
 def test_sparse_linear_matches_reference_golden(cuda_device):
@@ -270,8 +281,8 @@ def test_cpu_tensor_raises():
         lin.mm_nt(torch.ones(8, 8), torch.ones(8, 8))
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-def test_gemm_split_k_skinny(cuda_device, dtype, tol):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gemm_split_k_skinny(cuda_device, dtype):
     """GEMMs with few output tiles and long K split K over f32 partials; the
     reduce applies bias / accumulation, and the second K segment runs once."""
     L, lin = _lin()
@@ -285,8 +296,8 @@ def test_gemm_split_k_skinny(cuda_device, dtype, tol):
     desc = L.GemmDesc()
     desc.dtype, desc.M, desc.N, desc.K1 = L.dtype_code(x), T, R, IN
     assert L.lib().sf_gemm_workspace_size(L.byref(desc)) > 0  # this shape splits
-    assert rel_err(lin.mm_nt(d(x), d(P)), x.double() @ P.double().t()) < tol
-    assert rel_err(lin.mm_tn(d(dz), d(x)), dz.double().t() @ x.double()) < tol
+    assert gemm_err(lin.mm_nt(d(x), d(P)), x.double() @ P.double().t(), dtype) <= 1.0
+    assert gemm_err(lin.mm_tn(d(dz), d(x)), dz.double().t() @ x.double(), dtype) <= 1.0
     # second segment + bias on the last split, then accumulate into an existing C
     W = torch.randn(OUT, IN, generator=g).to(dtype)
     S = torch.randn(OUT, R, generator=g).to(dtype)
@@ -295,11 +306,13 @@ def test_gemm_split_k_skinny(cuda_device, dtype, tol):
     b = torch.randn(OUT, generator=g).to(dtype)
     ref = xa.double() @ W.double().t() + z.double() @ S.double().t() + b.double()
     got = lin.mm_nt(d(xa), d(W), A2=d(z), B2=d(S), K2=R, bias=d(b))
-    assert rel_err(got, ref) < tol
+    assert gemm_err(got, ref, dtype, bias_slack(ref - b.double(), dtype)) <= 1.0
     base = torch.randn(256, OUT, generator=g).to(dtype)
     acc = d(base.clone())
     lin.mm_nt(d(xa), d(W), out=acc, accumulate=True)
-    assert rel_err(acc, base.double() + xa.double() @ W.double().t()) < tol
+    # C += A B^T into a bf16 C rounds the product to bf16 before the sum (as torch's C += A @ B does)
+    prod = xa.double() @ W.double().t()
+    assert gemm_err(acc, base.double() + prod, dtype, bias_slack(prod, dtype)) <= 1.0
 
 
 def test_gemm_split_k_deterministic(cuda_device):
@@ -340,15 +353,24 @@ def test_fused_masked_linear_ste_apply_decay_matches_reference(cuda_device, tag,
     y = FusedMaskedLinearSTE.apply(x, W, b, mask, decay, scale)
     y.backward(d("gy"))
     ref = lambda k: torch.from_numpy(r[k])  # noqa: E731
-    assert rel_err(y, ref("y")) < tol
-    assert rel_err(x.grad, ref("dx")) < tol
-    assert rel_err(W.grad, ref("dW")) < tol
-    assert rel_err(b.grad, ref("db")) < tol
+    sy = sw = None
+    if tag == "bf16":
+        # both sides round x w^T before adding the bias, and gy^T x and decay * W before adding the decay
+        # term (:84-87, :123-125), each product from its own float32 sum: the rounded products may be
+        # neighbours, one ulp apart
+        term = decay * ref("W").double() * (ref("mask") < 0.5)
+        sy = (ref("y").double() - ref("b").double()).abs() * BF16_ULP
+        sw = (ref("dW").double().abs() + 2 * term.abs()) * BF16_ULP
+    for name, got, extra in (("y", y, sy), ("dx", x.grad, None), ("dW", W.grad, sw), ("db", b.grad, None)):
+        err = gemm_err(got, ref(name), dt, extra)
+        assert err <= 1.0, (name, err)
     Wh = d("W").requires_grad_(True)
     yh = FusedMaskedLinearSTE.apply(d("x"), Wh, d("b"), mask, decay, scale)
     loss = 0.5 * ((yh.float() - d("t").float()) ** 2).sum()
     (g,) = torch.autograd.grad(loss, Wh, create_graph=True)
     (hvp,) = torch.autograd.grad((g * d("v")).sum(), Wh)
+    # a chain of products whose bf16 intermediates (the residual y - t, the gradient) both sides round:
+    # checked against the output scale
     assert rel_err(hvp, ref("hvp")) < (3e-5 if tag == "f32" else tol)
     if tag == "f32":
         # the decay terms themselves: below the bars above (about 1e-4 of dW's scale), so checked
@@ -364,8 +386,8 @@ def test_fused_masked_linear_ste_apply_decay_matches_reference(cuda_device, tag,
         assert (h_resid - decay * v * (M < 0.5)).abs().max() < 2e-5 * ref("hvp").abs().max()
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-def test_decay_epilogue_through_split_k(cuda_device, dtype, tol):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decay_epilogue_through_split_k(cuda_device, dtype):
     """dW = gy^T x + decay W [E < 0.5] when the weight gradient has few output tiles and a long
     token dimension (48 x 64 over 4096 tokens): the products run split K and the ordered reduce
     pass applies the decay term.  Checked against the float64 oracle; the f32 case also checks the
@@ -386,8 +408,9 @@ def test_decay_epilogue_through_split_k(cuda_device, dtype, tol):
     Mw = M.to(dtype).double().numpy()  # the reference casts the mask to the weight dtype
     ref = ol.backward(x.double().numpy(), W.double().numpy(), Mw, gy.double().numpy(), False, decay=decay,
                       dtype=np.float64)
-    assert rel_err(Wd.grad, torch.from_numpy(ref["dW"])) < tol
-    assert rel_err(xd.grad, torch.from_numpy(ref["dx"])) < tol
+    assert gemm_err(Wd.grad, torch.from_numpy(ref["dW"]), dtype) <= 1.0
+    # dx reads w = W * E rounded to the weight dtype, as the reference forms it (:112-113)
+    assert gemm_err(xd.grad, gy.double() @ (W * M.to(dtype)).double(), dtype) <= 1.0
     if dtype == torch.float32:
         st = torch.from_numpy(gy.double().numpy().T @ x.double().numpy())
         term = decay * W.double() * torch.from_numpy(Mw < 0.5)
