@@ -1013,8 +1013,10 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
                 (14 / sustained["update_pattern"] + 6 / sustained["stats_pattern"]) * mask_gbs / 20, 4),
             "score_stats_gbs": round(st_gbs, 2),
             "stage_ms": {k: round(v.total_ms, 3) for k, v in stage_ms.items()},
+            # sixteen statistics per element: bound by VALU issue (about 58 instructions per element)
             "mask_stats": {"kernel": "sf_mask_stats", "GB/s": round(mstats_gbs, 2), "bytes_per_param": 4,
-                           "frac": round(mstats_gbs / PEAK_HBM_GBS, 4), "launches": msk.launches,
+                           "bound": "valu", "frac_of_hbm": round(mstats_gbs / PEAK_HBM_GBS, 4),
+                           "launches": msk.launches,
                            "avg_launch_ms": round(msk.avg_ms, 4)},
         }
     if "hutch" in legs and a.hutch_steps > 0:

@@ -7,9 +7,12 @@
 // conditional sums, m * (1 - m), a NaN scan, a sort of every group of 4) and a
 // host sync per scalar.  Here one HBM pass per mask produces all of them:
 // each thread walks groups of 4 along a row (16-byte loads for f32, 8-byte for
-// bf16), keeps the sums in f64 and the counts in u32 registers (the entropy
-// terms in f32), the workgroup folds them, and a
-// one-workgroup pass adds the per-workgroup partials in a fixed order.  The
+// bf16, the next group's load issued before this one's arithmetic) and keeps
+// the sums in f64 registers (the entropy terms in f32); the eight counts are
+// wave ballots added on the scalar unit.  The workgroup folds the sums, and a
+// one-workgroup pass adds the per-workgroup partials in a fixed order.  With
+// sixteen statistics per element the pass is bound by VALU issue (about 58
+// instructions per element), not by HBM.  The
 // number of workgroups depends only on the shape, so results are bitwise
 // reproducible.  The host composes mid_penalty / sparsity_penalty /
 // nm_2_4_tile_stats / mask_stats from the rows of all layers after one copy.
@@ -21,6 +24,8 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kParts = 1024;  // most workgroups of the partial pass
 constexpr int kSlots = SF_MSTAT_COUNT;
+constexpr double kLn2 = 0.69314718055994530942;
+constexpr float kInvLn2 = 1.44269504088896340736f;
 
 struct StatSpec {
   int64_t cols, groups, gpr, tail_col;
@@ -29,10 +34,11 @@ struct StatSpec {
   bool vec;                    // every group full and vector-aligned
 };
 
+// Round to the mask dtype: v_cvt_pk_bf16_f32 rounds to nearest even, as torch does.
 template <int DT>
 __device__ __forceinline__ float rnd(float x) {
   if constexpr (DT == SF_DTYPE_BF16)
-    return round_bf16(x);
+    return static_cast<float>(static_cast<__bf16>(x));
   else
     return x;
 }
@@ -65,52 +71,80 @@ struct Acc {
   uint32_t n[kSlots];
 };
 
-// The per-element terms of every slot but TOP2 / BOT2.  The entropy term is
-// evaluated in f32 (logf, log1pf) and summed in f64: within a few f32 ulp of
-// the reference's f64 logs per element (the f64 logs would cost more than
-// the memory pass).
+// The summed terms of one element (every f64 slot but TOP2 / BOT2).  The
+// entropy term -(c ln c) - (1 - c) ln(1 - c) is evaluated in f32 and summed in
+// f64, in log2 units (ln 2 multiplies each workgroup's sum once).  The
+// reference takes both logs in f64, where 1 - c is exact; here 1 - c = u + t
+// exactly with u = fl(1 - c) and t its rounding error (Fast2Sum: 1 >= c), so
+// (1 - c) log2(1 - c) = u log2 u + t (log2 u + 1 / ln 2) to within t^2 / u.
+// v_log_f32 is within 1 ulp of log2 over the clamped range [eps, 1] (u is 0
+// or at least 2^-24, never denormal), so every term is within a few f32 ulp
+// of the f64 one; log1pf would cost three times the memory pass.  c == 1
+// gives 0 * -inf = NaN, as in f64.
 template <int DT>
-__device__ __forceinline__ void add_element(const StatSpec& s, float x, bool tail, Acc& a) {
+__device__ __forceinline__ void add_sums(const StatSpec& s, float x, Acc& a) {
   const double d = static_cast<double>(x);
   a.s[SF_MSTAT_SUM] += d;
   a.s[SF_MSTAT_SUM2] += d * d;
   // m.clamp(eps, 1 - eps) in the mask dtype (NaN passes through)
   float c = x < s.lo ? s.lo : (x > s.hi ? s.hi : x);
   c = rnd<DT>(c);
-  const float ent = -(c * logf(c)) - ((1.0f - c) * log1pf(-c));  // c == 1: 0 * -inf = NaN, as in f64
-  a.s[SF_MSTAT_ENTROPY] += static_cast<double>(ent);
-  const bool lt05 = x < 0.5f, gt05 = x > 0.5f;
-  a.n[SF_MSTAT_LT05] += lt05;
-  a.n[SF_MSTAT_LT01] += x < s.t01;
-  a.n[SF_MSTAT_LT001] += x < s.t001;
-  a.n[SF_MSTAT_GT90] += x > s.t90;
-  a.n[SF_MSTAT_GT99] += x > s.t99;
-  a.n[SF_MSTAT_GT05] += gt05;
-  a.s[SF_MSTAT_SUM_LT05] += lt05 ? d : 0.0;
-  a.s[SF_MSTAT_SUM_GT05] += gt05 ? d : 0.0;
+  const float u = 1.0f - c;
+  const float t = -c - (u - 1.0f);
+  const float lu = __builtin_amdgcn_logf(u);
+  const float ent2 = -(c * __builtin_amdgcn_logf(c)) - (u * lu + t * (lu + kInvLn2));
+  a.s[SF_MSTAT_ENTROPY] += static_cast<double>(ent2);
+  a.s[SF_MSTAT_SUM_LT05] += x < 0.5f ? d : 0.0;
+  a.s[SF_MSTAT_SUM_GT05] += x > 0.5f ? d : 0.0;
   // m * (1 - m): both operations rounded to the mask dtype, as torch evaluates them
   const float om = rnd<DT>(1.0f - x);
   a.s[SF_MSTAT_MID] += static_cast<double>(rnd<DT>(x * om));
-  a.n[SF_MSTAT_NONFINITE] += !isfinite(x);
-  a.n[SF_MSTAT_TAIL_LT05] += tail && lt05;
+}
+
+// The counted tests of one element, in the order of kCountSlot.
+constexpr int kNCount = 8;
+constexpr int kCountSlot[kNCount] = {SF_MSTAT_LT05, SF_MSTAT_LT01, SF_MSTAT_LT001,     SF_MSTAT_GT90,
+                                     SF_MSTAT_GT99, SF_MSTAT_GT05, SF_MSTAT_NONFINITE, SF_MSTAT_TAIL_LT05};
+__device__ __forceinline__ void count_tests(const StatSpec& s, float x, bool tail, bool (&b)[kNCount]) {
+  b[0] = x < 0.5f;
+  b[1] = x < s.t01;
+  b[2] = x < s.t001;
+  b[3] = x > s.t90;
+  b[4] = x > s.t99;
+  b[5] = x > 0.5f;
+  b[6] = !isfinite(x);
+  b[7] = tail && b[0];
 }
 
 // TOP2 / BOT2 of a full group: members ranked by the descending sort order
-// (ordered keys: NaN largest, -0 == +0; equal keys by position).
+// (ordered keys: NaN largest, -0 == +0; equal keys by position).  Only which
+// values land in each pair matters for the two sums, so a group without NaN
+// takes them from a min / max network (the two pair sums are exact in f64);
+// a group holding NaN ranks its members by key.
 __device__ __forceinline__ void add_tile(const float v[4], Acc& a) {
-  uint32_t key[4];
+  float top[2], bot[2];
+  if (!(isnan(v[0]) || isnan(v[1]) || isnan(v[2]) || isnan(v[3]))) {
+    const float h0 = fmaxf(v[0], v[1]), l0 = fminf(v[0], v[1]);
+    const float h1 = fmaxf(v[2], v[3]), l1 = fminf(v[2], v[3]);
+    top[0] = fmaxf(h0, h1);
+    bot[0] = fminf(l0, l1);
+    const float mh = fminf(h0, h1), ml = fmaxf(l0, l1);  // the middle two
+    top[1] = fmaxf(mh, ml);
+    bot[1] = fminf(mh, ml);
+  } else {
+    uint32_t key[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) key[i] = ordered_key(v[i]);
-  float top[2] = {0.0f, 0.0f}, bot[2] = {0.0f, 0.0f};
+    for (int i = 0; i < 4; ++i) key[i] = ordered_key(v[i]);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int r = 0;
+    for (int i = 0; i < 4; ++i) {
+      int r = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r += (key[j] > key[i]) || (j < i && key[j] == key[i]);
-    if (r == 0) top[0] = v[i];
-    if (r == 1) top[1] = v[i];
-    if (r == 2) bot[0] = v[i];
-    if (r == 3) bot[1] = v[i];
+      for (int j = 0; j < 4; ++j) r += (key[j] > key[i]) || (j < i && key[j] == key[i]);
+      if (r == 0) top[0] = v[i];
+      if (r == 1) top[1] = v[i];
+      if (r == 2) bot[0] = v[i];
+      if (r == 3) bot[1] = v[i];
+    }
   }
   a.s[SF_MSTAT_TOP2] += static_cast<double>(top[0]) + static_cast<double>(top[1]);
   a.s[SF_MSTAT_BOT2] += static_cast<double>(bot[0]) + static_cast<double>(bot[1]);
@@ -138,6 +172,38 @@ __device__ __forceinline__ double block_fold(double (&a)[kSlots]) {
   return t;
 }
 
+// One group of the walk: its sums into `a`; its counts into the wave-uniform
+// `wc` through ballots when every lane of the wave is live (WAVE), else into
+// each lane's own counts.
+template <int DT, bool VEC, bool WAVE>
+__device__ __forceinline__ void stats_values(const StatSpec& s, const float (&v)[4], const Group& g, Acc& a,
+                                             uint32_t (&wc)[kNCount]) {
+  const int n = VEC ? 4 : g.n;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (VEC || j < n) add_sums<DT>(s, v[j], a);
+    bool b[kNCount];
+    count_tests(s, v[j], g.col + j >= s.tail_col, b);
+#pragma unroll
+    for (int k = 0; k < kNCount; ++k) {
+      const bool hit = (VEC || j < n) && b[k];
+      if constexpr (WAVE)
+        wc[k] += static_cast<uint32_t>(__popcll(__ballot(hit)));
+      else
+        a.n[kCountSlot[k]] += hit;
+    }
+  }
+  if (VEC || n == 4) add_tile(v, a);
+}
+
+template <int DT, bool VEC, bool WAVE>
+__device__ __forceinline__ void stats_group(const StatSpec& s, const void* __restrict__ mask, const Group& g, Acc& a,
+                                            uint32_t (&wc)[kNCount]) {
+  float v[4];
+  load_group<DT>(mask, g.elem, g.n, VEC || (s.vec && g.full), v);
+  stats_values<DT, VEC, WAVE>(s, v, g, a, wc);
+}
+
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(kBlock) mask_stats_partial_kernel(StatSpec s, const void* __restrict__ mask,
                                                                     double* __restrict__ partial) {
@@ -147,44 +213,83 @@ __global__ void __launch_bounds__(kBlock) mask_stats_partial_kernel(StatSpec s, 
     a.s[k] = 0.0;
     a.n[k] = 0u;
   }
-  for (GroupWalk w(s.groups, s.cols, s.gpr); w.live(); w.next()) {
-    const Group g = w.group();
-    float v[4];
-    load_group<DT>(mask, g.elem, g.n, VEC || (s.vec && g.full), v);
-    const int n = VEC ? 4 : g.n;
+  uint32_t wc[kNCount];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (j < n) add_element<DT>(s, v[j], g.col + j >= s.tail_col, a);
-    if (VEC || n == 4) add_tile(v, a);
+  for (int k = 0; k < kNCount; ++k) wc[k] = 0u;
+  GroupWalk w(s.groups, s.cols, s.gpr);
+  // Walk steps in which every lane of the wave is live (the wave's last lane
+  // has its largest group index): the step count is wave-uniform.  The stride
+  // is at least one workgroup, so at most one step with some lanes past the
+  // end remains.
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+  int64_t wave_last = static_cast<int64_t>(blockIdx.x) * kBlock +
+                      static_cast<int64_t>(__builtin_amdgcn_readfirstlane(threadIdx.x) | 63u);
+  if constexpr (VEC) {
+    // software-pipelined: the next step's 16 bytes are requested before this
+    // step's arithmetic (lanes past the end re-read their current group, so the
+    // load stays unconditional and its wait counted)
+    if (wave_last < s.groups) {
+      Group g = w.group();
+      float v[4];
+      load_group<DT>(mask, g.elem, 4, true, v);
+      for (;;) {
+        w.next();
+        wave_last += stride;
+        const Group gn = w.group();
+        float nv[4];
+        load_group<DT>(mask, w.live() ? gn.elem : g.elem, 4, true, nv);
+        stats_values<DT, VEC, true>(s, v, g, a, wc);
+        g = gn;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = nv[j];
+        if (wave_last >= s.groups) break;
+      }
+      if (w.live()) stats_values<DT, VEC, false>(s, v, g, a, wc);
+    } else if (w.live()) {
+      stats_group<DT, VEC, false>(s, mask, w.group(), a, wc);
+    }
+  } else {
+    for (; wave_last < s.groups; wave_last += stride, w.next()) stats_group<DT, VEC, true>(s, mask, w.group(), a, wc);
+    if (w.live()) stats_group<DT, VEC, false>(s, mask, w.group(), a, wc);
+  }
+  // lane 0 is live whenever any lane of its wave is: it carries the wave's counts
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int k = 0; k < kNCount; ++k) a.n[kCountSlot[k]] += wc[k];
   }
   double t[kSlots];
 #pragma unroll
   for (int k = 0; k < kSlots; ++k) t[k] = a.s[k] + static_cast<double>(a.n[k]);  // each slot is a sum or a count
-  const double tot = block_fold(t);
+  double tot = block_fold(t);
+  if (threadIdx.x == SF_MSTAT_ENTROPY) tot *= kLn2;  // the entropy was summed in log2 units
   if (threadIdx.x < kSlots) partial[blockIdx.x * (int64_t)kSlots + threadIdx.x] = tot;
 }
 
-// out[k] = sum over the parts: thread t adds parts t, t + 256, ..., then a
-// fixed tree over the threads (deterministic).
+// out[k] = sum over the parts.  Thread t reads slot t % 16 of parts t / 16,
+// t / 16 + 16, ... (consecutive threads read consecutive doubles), then the
+// 16 partial sums of each slot are added in a fixed order (deterministic).
+static_assert(kSlots == 16 && kBlock == 256, "the final fold maps 16 slots x 16 part strides onto the workgroup");
 __global__ void __launch_bounds__(kBlock) mask_stats_final_kernel(const double* __restrict__ partial, int nparts,
                                                                   double* __restrict__ out) {
-  __shared__ double red[kSlots][kBlock];
-  double t[kSlots];
-#pragma unroll
-  for (int k = 0; k < kSlots; ++k) t[k] = 0.0;
-  for (int p = threadIdx.x; p < nparts; p += kBlock)
-#pragma unroll
-    for (int k = 0; k < kSlots; ++k) t[k] += partial[p * (int64_t)kSlots + k];
-#pragma unroll
-  for (int k = 0; k < kSlots; ++k) red[k][threadIdx.x] = t[k];
-  __syncthreads();
-  for (int h = kBlock / 2; h > 0; h >>= 1) {
-    if (threadIdx.x < h)
-#pragma unroll
-      for (int k = 0; k < kSlots; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + h];
-    __syncthreads();
+  __shared__ double red[kBlock];
+  const int k = threadIdx.x & 15, p0 = threadIdx.x >> 4;
+  double t0 = 0.0, t1 = 0.0, t2 = 0.0, t3 = 0.0;  // four chains: the loads are not serialised by the adds
+  int p = p0;
+  for (; p + 48 < nparts; p += 64) {
+    t0 += partial[p * (int64_t)kSlots + k];
+    t1 += partial[(p + 16) * (int64_t)kSlots + k];
+    t2 += partial[(p + 32) * (int64_t)kSlots + k];
+    t3 += partial[(p + 48) * (int64_t)kSlots + k];
   }
-  if (threadIdx.x < kSlots) out[threadIdx.x] = red[threadIdx.x][0];
+  for (; p < nparts; p += 16) t0 += partial[p * (int64_t)kSlots + k];
+  red[threadIdx.x] = (t0 + t1) + (t2 + t3);
+  __syncthreads();
+  if (threadIdx.x < kSlots) {
+    double tot = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) tot += red[j * 16 + threadIdx.x];
+    out[threadIdx.x] = tot;
+  }
 }
 
 __global__ void __launch_bounds__(kBlock) mask_hist_kernel(const void* __restrict__ mask, int dtype, int64_t n,

@@ -68,6 +68,25 @@ def test_layer_sums_match_oracle(cuda_device, shape, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_entropy_of_nearly_hard_masks(cuda_device, dtype):
+    """Masks within 2e-3 (f32) / 2e-2 (bf16) of 0 and 1, as late in hardening, where fl(1 - c) drops
+    the low bits of a small c and both entropy terms are small: the entropy sum within 1e-6 of the
+    oracle's f64 logs, and every other slot to its usual bar."""
+    g = torch.Generator().manual_seed(17)
+    r = torch.rand(512, 1024, generator=g, dtype=torch.float64)
+    span, gap = (2e-3, 2e-6) if dtype == torch.float32 else (2e-2, 2.0 ** -8)  # gap: below 1 in the dtype
+    near = torch.where(r < 0.5, r * span + 1e-9, 1 - gap - (r - 0.5) * span).float()
+    near.view(-1)[:4] = torch.tensor([3e-8, 1e-7, 2.0 ** -24, 1 - gap])
+    m = near.to(dtype)
+    assert not bool((m == 1).any())
+    dt = "bf16" if dtype == torch.bfloat16 else "f32"
+    got = _dev_rows(m.to(cuda_device), 1024)
+    want = ost.layer_sums(m.float().numpy(), dt, 1024)
+    assert want[ost.ENTROPY] > 0
+    _check_row(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_layer_sums_nan_inf_and_ones(cuda_device, dtype):
     m = torch.rand(16, 22)
     m[0, 1], m[2, 5], m[3, 3], m[5, 21] = float("nan"), float("inf"), 1.0, -float("inf")
