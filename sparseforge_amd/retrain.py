@@ -3,11 +3,14 @@
 Follows legacy/main_llama.py:1996-2211 for one process on one GPU (no
 FSDP/DDP, no GradScaler: bf16 needs none):
 
+  penalty = mid_penalty(student, lambda_mid)                     (:2047-2057)
+          + sparsity_penalty(student, ratio, alpha)[0]           (:2059-2064)
+      (the reference evaluates both in every micro-batch; they read only the
+      frozen masks, so every micro-batch adds the same value)
   for each micro-batch (X, Y):                                   (:1996)
       logits, task, layerwise, kl = Distill_Model(X, Y)          (:2022)
       loss = h_task * task + h_kl * kl (+ h_sq * layerwise)       (:2025-2028)
-      loss += mid_penalty(student, lambda_mid)                   (:2047-2057)
-      loss += sparsity_penalty(student, ratio, alpha)[0]         (:2059-2064)
+      loss += penalty
       loss /= grad_accum                                         (:2067)
       all-finite check, else skip the step                       (:2074-2115)
       last micro-batch: update_hessian_hutchinson(student, loss) (:2111-2112)
@@ -106,6 +109,13 @@ class RetrainStep:
         lam = lambda_mid_at(cfg, iter_num)
         total = 0.0
         t = self._mark(ev, None, None)
+        # The penalties read only the masks (frozen, no gradient), which change after the optimizer
+        # step, not between micro-batches: each micro-batch's loss adds the same value, so it is
+        # computed once per step (the reference recomputes it per micro-batch, :2047-2064).
+        penalty = U.mid_penalty(self.student, lam)
+        if cfg.sparsity_alpha:
+            pen, _cur = U.sparsity_penalty(self.student, target_sparsity=cfg.sparsity_ratio, alpha=cfg.sparsity_alpha)
+            penalty = penalty + pen
         for micro, (X, Y) in enumerate(batches):
             last = micro == cfg.grad_accum - 1
             ctx = (torch.autocast("cuda", dtype=cfg.autocast_dtype) if cfg.autocast_dtype is not None
@@ -118,11 +128,7 @@ class RetrainStep:
                     loss = cfg.hardness_task * task + cfg.hardness_kldiv * kl
                 else:
                     loss = cfg.hardness_task * task + cfg.hardness_squarehead * layerwise + cfg.hardness_kldiv * kl
-                loss = loss + U.mid_penalty(self.student, lam)
-                if cfg.sparsity_alpha:
-                    pen, _cur = U.sparsity_penalty(self.student, target_sparsity=cfg.sparsity_ratio,
-                                                   alpha=cfg.sparsity_alpha)
-                    loss = loss + pen
+                loss = loss + penalty
                 loss = loss / cfg.grad_accum
             del _logits
             if not bool(torch.isfinite(loss.detach()).item()):
