@@ -26,6 +26,7 @@ namespace {
 constexpr int kKlBlock = 256;
 constexpr int kKlFinalBlock = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kKlU = 4;  // slices of a row a thread loads before using them (forward)
 
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
@@ -57,6 +58,9 @@ __device__ __forceinline__ void load8(const void* base, int64_t i, int n, bool v
   }
 }
 
+// Round to nearest even bf16 with the hardware conversion (the stores here never see a NaN).
+__device__ __forceinline__ uint16_t bf16_rne(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
+
 template <int DT>
 __device__ __forceinline__ void store8(void* base, int64_t i, int n, bool vec, const float v[8]) {
   if (DT == SF_DTYPE_F32) {
@@ -76,20 +80,24 @@ __device__ __forceinline__ void store8(void* base, int64_t i, int n, bool vec, c
       uint32_t w[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        w[k] = static_cast<uint32_t>(f32_to_bf16(v[2 * k])) | (static_cast<uint32_t>(f32_to_bf16(v[2 * k + 1])) << 16);
+        w[k] = static_cast<uint32_t>(bf16_rne(v[2 * k])) | (static_cast<uint32_t>(bf16_rne(v[2 * k + 1])) << 16);
       o.x = w[0]; o.y = w[1]; o.z = w[2]; o.w = w[3];
       *reinterpret_cast<uint4*>(p) = o;
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (k < n) p[k] = f32_to_bf16(v[k]);
+        if (k < n) p[k] = bf16_rne(v[k]);
     }
   }
 }
 
-// clamp(x, -100, 100) / T as the reference's clamp_ then mul_(1 / T); a NaN maps to
-// a finite value here and is reported through the row's NaN flag instead.
-__device__ __forceinline__ float scaled(float x, float inv_t) { return fminf(fmaxf(x, -100.0f), 100.0f) * inv_t; }
+// clamp(x, -100, 100) / T as the reference's clamp_ then mul_(1 / T), the clamp as
+// one v_med3 (equal to min(max(x, -100), 100) for every x but NaN).  A NaN logit's
+// value here does not matter: the row's NaN flag drops its chunk from the loss and
+// zeroes the chunk's gradient.
+__device__ __forceinline__ float scaled(float x, float inv_t) {
+  return __builtin_amdgcn_fmed3f(x, -100.0f, 100.0f) * inv_t;
+}
 
 struct KlAcc {
   float ms, zs, mt, zt, a;
@@ -128,50 +136,81 @@ __device__ __forceinline__ KlAcc kl_shfl_xor(const KlAcc& x, int off) {
   return y;
 }
 
-template <int DT>
-__global__ void __launch_bounds__(kKlBlock) kl_rows_kernel(const void* __restrict__ s, const void* __restrict__ t,
-                                                           int64_t vocab, float inv_t, bool vec,
-                                                           double* __restrict__ lse, double* __restrict__ row_kl,
-                                                           int* __restrict__ row_nan) {
-  const int64_t r = blockIdx.x, base = r * vocab;
-  KlAcc acc{-INFINITY, 0.0f, -INFINITY, 0.0f, 0.0f};
-  int nan = 0;
-  for (int64_t j0 = threadIdx.x * 8; j0 < vocab; j0 += 8 * (int64_t)blockDim.x) {
-    const int n = vocab - j0 >= 8 ? 8 : static_cast<int>(vocab - j0);
-    float a[8], b[8];
-    load8<DT>(s, base + j0, n, vec, a);
-    load8<DT>(t, base + j0, n, vec, b);
-    float cs = -INFINITY, ct = -INFINITY;
+// One 8-element slice of a row into a thread's accumulators: the slice maxima,
+// a rescale only when a maximum rises, then the exp sums (n < 8: a partial
+// slice, whose missing elements do not count).
+__device__ __forceinline__ void kl_slice(KlAcc& acc, bool& bad, float (&a)[8], float (&b)[8], int n, float inv_t) {
+  float cs = -INFINITY, ct = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (k < n) {
-        nan |= (a[k] != a[k]) | (b[k] != b[k]);
-        a[k] = scaled(a[k], inv_t);
-        b[k] = scaled(b[k], inv_t);
-        cs = fmaxf(cs, a[k]);
-        ct = fmaxf(ct, b[k]);
-      }
-    }
-    if (cs > acc.ms) {
-      acc.zs *= exp_f(acc.ms - cs);
-      acc.ms = cs;
-    }
-    if (ct > acc.mt) {
-      const float sc = exp_f(acc.mt - ct);
-      acc.zt *= sc;
-      acc.a *= sc;
-      acc.mt = ct;
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (k < n) {
-        acc.zs += exp_f(a[k] - acc.ms);
-        const float e = exp_f(b[k] - acc.mt);
-        acc.zt += e;
-        acc.a = fmaf(e, b[k] - a[k], acc.a);
-      }
+  for (int k = 0; k < 8; ++k) {
+    if (k < n) {
+      bad |= __builtin_isunordered(a[k], b[k]);
+      a[k] = scaled(a[k], inv_t);
+      b[k] = scaled(b[k], inv_t);
+      cs = fmaxf(cs, a[k]);
+      ct = fmaxf(ct, b[k]);
     }
   }
+  if (cs > acc.ms) {
+    acc.zs *= exp_f(acc.ms - cs);
+    acc.ms = cs;
+  }
+  if (ct > acc.mt) {
+    const float sc = exp_f(acc.mt - ct);
+    acc.zt *= sc;
+    acc.a *= sc;
+    acc.mt = ct;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < n) {
+      acc.zs += exp_f(a[k] - acc.ms);
+      const float e = exp_f(b[k] - acc.mt);
+      acc.zt += e;
+      acc.a = fmaf(e, b[k] - a[k], acc.a);
+    }
+  }
+}
+
+// One workgroup per token row; thread t takes slices t, t + 256, ... in order.
+// VEC (vocab % 8 == 0, 16-byte aligned rows): every slice is whole and a
+// thread's next two slices of both rows are loaded before either is used.
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(kKlBlock) kl_rows_kernel(const void* __restrict__ s, const void* __restrict__ t,
+                                                           int64_t vocab, float inv_t, double* __restrict__ lse,
+                                                           double* __restrict__ row_kl, int* __restrict__ row_nan) {
+  const int64_t r = blockIdx.x, base = r * vocab;
+  KlAcc acc{-INFINITY, 0.0f, -INFINITY, 0.0f, 0.0f};
+  bool bad = false;
+  if constexpr (VEC) {
+    const int64_t slices = vocab / 8, step = blockDim.x;
+    int64_t c = threadIdx.x;
+    for (; c + (kKlU - 1) * step < slices; c += kKlU * step) {
+      float a[kKlU][8], b[kKlU][8];
+#pragma unroll
+      for (int u = 0; u < kKlU; ++u) {
+        load8<DT>(s, base + 8 * (c + u * step), 8, true, a[u]);
+        load8<DT>(t, base + 8 * (c + u * step), 8, true, b[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kKlU; ++u) kl_slice(acc, bad, a[u], b[u], 8, inv_t);
+    }
+    for (; c < slices; c += step) {
+      float a0[8], b0[8];
+      load8<DT>(s, base + 8 * c, 8, true, a0);
+      load8<DT>(t, base + 8 * c, 8, true, b0);
+      kl_slice(acc, bad, a0, b0, 8, inv_t);
+    }
+  } else {
+    for (int64_t j0 = threadIdx.x * 8; j0 < vocab; j0 += 8 * (int64_t)blockDim.x) {
+      const int n = vocab - j0 >= 8 ? 8 : static_cast<int>(vocab - j0);
+      float a[8], b[8];
+      load8<DT>(s, base + j0, n, false, a);
+      load8<DT>(t, base + j0, n, false, b);
+      kl_slice(acc, bad, a, b, n, inv_t);
+    }
+  }
+  int nan = bad;
   for (int off = 32; off > 0; off >>= 1) acc = kl_merge(acc, kl_shfl_xor(acc, off));
   for (int off = 32; off > 0; off >>= 1) nan |= __shfl_xor(nan, off, 64);
   __shared__ KlAcc part[kKlBlock / 64];
@@ -260,9 +299,19 @@ __global__ void __launch_bounds__(kKlFinalBlock) kl_final_kernel(const double* _
     for (int64_t i = tid; i < rows; i += blockDim.x) row_scale[i] = 0.0f;
 }
 
-template <int DT>
+// d loss / d student logit: factor (q - p) inside the clamp range, 0 outside it.
+__device__ __forceinline__ float kl_grad1(float a, float b, float inv_t, double ls, double lt, float factor) {
+  const bool in_range = a >= -100.0f && a <= 100.0f;  // clamp passes the gradient inside [min, max]
+  const float q = exp_f(static_cast<float>(static_cast<double>(scaled(a, inv_t)) - ls));
+  const float p = exp_f(static_cast<float>(static_cast<double>(scaled(b, inv_t)) - lt));
+  return in_range ? factor * (q - p) : 0.0f;
+}
+
+// One workgroup per token row, slices as in kl_rows_kernel (VEC: two slices'
+// loads in flight per thread); rows whose chunk was dropped get zeros.
+template <int DT, bool VEC>
 __global__ void __launch_bounds__(kKlBlock) kl_backward_kernel(const void* __restrict__ s, const void* __restrict__ t,
-                                                               int64_t vocab, float inv_t, bool vec,
+                                                               int64_t vocab, float inv_t,
                                                                const double* __restrict__ lse,
                                                                const float* __restrict__ row_scale,
                                                                const void* __restrict__ gout, int gout_dtype,
@@ -270,23 +319,46 @@ __global__ void __launch_bounds__(kKlBlock) kl_backward_kernel(const void* __res
   const int64_t r = blockIdx.x, base = r * vocab;
   const float factor = row_scale[r] * load_as_f32(gout, 0, gout_dtype);
   const double ls = lse[2 * r], lt = lse[2 * r + 1];
-  for (int64_t j0 = threadIdx.x * 8; j0 < vocab; j0 += 8 * (int64_t)blockDim.x) {
-    const int n = vocab - j0 >= 8 ? 8 : static_cast<int>(vocab - j0);
-    float a[8], b[8], g[8];
-    load8<DT>(s, base + j0, n, vec, a);
-    if (factor != 0.0f) load8<DT>(t, base + j0, n, vec, b);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (factor == 0.0f) {
-        g[k] = 0.0f;
-        continue;
-      }
-      const bool in_range = a[k] >= -100.0f && a[k] <= 100.0f;  // clamp passes the gradient inside [min, max]
-      const float q = exp_f(static_cast<float>(static_cast<double>(scaled(a[k], inv_t)) - ls));
-      const float p = exp_f(static_cast<float>(static_cast<double>(scaled(b[k], inv_t)) - lt));
-      g[k] = in_range ? factor * (q - p) : 0.0f;
+  if constexpr (VEC) {
+    const int64_t slices = vocab / 8, step = blockDim.x;
+    if (factor == 0.0f) {
+      const float z[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+      for (int64_t c = threadIdx.x; c < slices; c += step) store8<DT>(gs, base + 8 * c, 8, true, z);
+      return;
     }
-    store8<DT>(gs, base + j0, n, vec, g);
+    int64_t c = threadIdx.x;
+    for (; c + step < slices; c += 2 * step) {
+      float a0[8], b0[8], a1[8], b1[8];
+      load8<DT>(s, base + 8 * c, 8, true, a0);
+      load8<DT>(t, base + 8 * c, 8, true, b0);
+      load8<DT>(s, base + 8 * (c + step), 8, true, a1);
+      load8<DT>(t, base + 8 * (c + step), 8, true, b1);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        a0[k] = kl_grad1(a0[k], b0[k], inv_t, ls, lt, factor);
+        a1[k] = kl_grad1(a1[k], b1[k], inv_t, ls, lt, factor);
+      }
+      store8<DT>(gs, base + 8 * c, 8, true, a0);
+      store8<DT>(gs, base + 8 * (c + step), 8, true, a1);
+    }
+    if (c < slices) {
+      float a0[8], b0[8];
+      load8<DT>(s, base + 8 * c, 8, true, a0);
+      load8<DT>(t, base + 8 * c, 8, true, b0);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a0[k] = kl_grad1(a0[k], b0[k], inv_t, ls, lt, factor);
+      store8<DT>(gs, base + 8 * c, 8, true, a0);
+    }
+  } else {
+    for (int64_t j0 = threadIdx.x * 8; j0 < vocab; j0 += 8 * (int64_t)blockDim.x) {
+      const int n = vocab - j0 >= 8 ? 8 : static_cast<int>(vocab - j0);
+      float a[8], b[8], g[8];
+      load8<DT>(s, base + j0, n, false, a);
+      if (factor != 0.0f) load8<DT>(t, base + j0, n, false, b);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) g[k] = factor == 0.0f ? 0.0f : kl_grad1(a[k], b[k], inv_t, ls, lt, factor);
+      store8<DT>(gs, base + j0, n, false, g);
+    }
   }
 }
 
@@ -328,12 +400,20 @@ extern "C" int sf_kl_forward(const void* student, const void* teacher, int dtype
   const bool vec = kl_vec_ok(vocab, dtype, {student, teacher});
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(rows));
-  if (dtype == SF_DTYPE_F32)
-    kl_rows_kernel<SF_DTYPE_F32><<<grid, kKlBlock, 0, st>>>(student, teacher, vocab, inv_t, vec, row_lse, row_kl,
-                                                            row_nan);
-  else
-    kl_rows_kernel<SF_DTYPE_BF16><<<grid, kKlBlock, 0, st>>>(student, teacher, vocab, inv_t, vec, row_lse, row_kl,
-                                                             row_nan);
+#define SF_KL_ROWS(DT, V) kl_rows_kernel<DT, V><<<grid, kKlBlock, 0, st>>>(student, teacher, vocab, inv_t, row_lse, \
+                                                                          row_kl, row_nan)
+  if (dtype == SF_DTYPE_F32) {
+    if (vec)
+      SF_KL_ROWS(SF_DTYPE_F32, true);
+    else
+      SF_KL_ROWS(SF_DTYPE_F32, false);
+  } else {
+    if (vec)
+      SF_KL_ROWS(SF_DTYPE_BF16, true);
+    else
+      SF_KL_ROWS(SF_DTYPE_BF16, false);
+  }
+#undef SF_KL_ROWS
   const float t_sq = static_cast<float>(static_cast<double>(temperature) * static_cast<double>(temperature));
   kl_final_kernel<<<1, kKlFinalBlock, 0, st>>>(row_kl, row_nan, rows, chunk_rows, temperature, t_sq, row_scale, out,
                                                out_dtype);
@@ -352,11 +432,20 @@ extern "C" int sf_kl_backward(const void* student, const void* teacher, int dtyp
   const bool vec = kl_vec_ok(vocab, dtype, {student, teacher, grad_student});
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(rows));
-  if (dtype == SF_DTYPE_F32)
-    kl_backward_kernel<SF_DTYPE_F32><<<grid, kKlBlock, 0, st>>>(student, teacher, vocab, inv_t, vec, row_lse,
-                                                                row_scale, grad_out, grad_out_dtype, grad_student);
-  else
-    kl_backward_kernel<SF_DTYPE_BF16><<<grid, kKlBlock, 0, st>>>(student, teacher, vocab, inv_t, vec, row_lse,
-                                                                 row_scale, grad_out, grad_out_dtype, grad_student);
+#define SF_KL_BWD(DT, V)                                                                                    \
+  kl_backward_kernel<DT, V><<<grid, kKlBlock, 0, st>>>(student, teacher, vocab, inv_t, row_lse, row_scale, grad_out, \
+                                                       grad_out_dtype, grad_student)
+  if (dtype == SF_DTYPE_F32) {
+    if (vec)
+      SF_KL_BWD(SF_DTYPE_F32, true);
+    else
+      SF_KL_BWD(SF_DTYPE_F32, false);
+  } else {
+    if (vec)
+      SF_KL_BWD(SF_DTYPE_BF16, true);
+    else
+      SF_KL_BWD(SF_DTYPE_BF16, false);
+  }
+#undef SF_KL_BWD
   return launch_status("sf_kl_backward");
 }
