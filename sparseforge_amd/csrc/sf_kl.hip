@@ -58,7 +58,8 @@ __device__ __forceinline__ void load8(const void* base, int64_t i, int n, bool v
   }
 }
 
-// Round to nearest even bf16 with the hardware conversion (the stores here never see a NaN).
+// Round to nearest even bf16 with the hardware conversion (a NaN stays a NaN: only a
+// non-finite upstream gradient can bring one here).
 __device__ __forceinline__ uint16_t bf16_rne(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
 
 template <int DT>
