@@ -112,9 +112,13 @@ def profiled_traffic() -> dict:
     return out
 
 
-def step_flops(tokens: int) -> float:
-    from oracle.linear import flops_fwd_bwd  # closed-form count only
+def flops_fwd_bwd(tokens: int, in_f: int, out_f: int, rank: int = 0) -> int:
+    """Algorithmic FLOPs of one SparseLinear fwd+bwd: y, dX and dW are 2 T in out each, and the four
+    rank-r SLoRB products (z, dz, dP, dS) add 6 T r (in + out)."""
+    return 6 * tokens * in_f * out_f + 6 * tokens * rank * (in_f + out_f)
 
+
+def step_flops(tokens: int) -> float:
     return float(sum(flops_fwd_bwd(tokens, i, o, RANK) for _, i, o in LINEARS))
 
 
@@ -694,8 +698,6 @@ def cpu_parallel_baseline(worker, bytes_per_param: int, budget_s: float, what: s
 # ---------------------------------------------------------------------------
 def per_linear_times(torch, mods, xs, gys, reps: int = 5) -> list:
     """cfg2's per-linear figure: fwd + bwd of each linear alone (device events around each repetition)."""
-    from oracle.linear import flops_fwd_bwd
-
     out = []
     for (name, fin, fout), lin, x, gy in zip(LINEARS, mods, xs, gys):
         for _ in range(2):
