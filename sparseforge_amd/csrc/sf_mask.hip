@@ -2416,7 +2416,7 @@ __global__ void __launch_bounds__(kTopkBlock) topk_keep_kernel(const float* __re
                                                                int32_t* __restrict__ I, int32_t* __restrict__ PL,
                                                                int32_t* __restrict__ PR, int* __restrict__ status) {
   __shared__ int64_t s_first, s_last, s_cut;
-  __shared__ int s_depth, s_end;  // s_end: 0 running, 1 insertion sort due, 2 done
+  __shared__ int s_depth;
   __shared__ int s_scl[kTopkBlock / 64], s_scr[kTopkBlock / 64];
   __shared__ int s_tot[2];
   const int tid = threadIdx.x;
@@ -2438,7 +2438,6 @@ __global__ void __launch_bounds__(kTopkBlock) topk_keep_kernel(const float* __re
       s_first = 0;
       s_last = n;
       s_depth = 2 * floor_log2(n);
-      s_end = 0;
     }
     __syncthreads();
     while (true) {
