@@ -781,8 +781,9 @@ def main(argv=None) -> int:
     ap.add_argument("--tokens", type=int, default=TOKENS)
     ap.add_argument("--mask-layers", type=int, default=LAYERS, help="decoder layers in the mask-update arena")
     ap.add_argument("--mask-steps", type=int, default=10)
-    ap.add_argument("--adamw-steps", type=int, default=5)
-    ap.add_argument("--hutch-steps", type=int, default=5, help="updates of the Hutchinson accumulator leg")
+    ap.add_argument("--adamw-steps", type=int, default=10,
+                    help="steps of the AdamW leg (the first step's host-side table build is not overlapped)")
+    ap.add_argument("--hutch-steps", type=int, default=10, help="updates of the Hutchinson accumulator leg")
     ap.add_argument("--bsr-steps", type=int, default=5, help="steps of the block-sparse leg (0 skips it)")
     ap.add_argument("--kl-steps", type=int, default=10, help="steps of the distillation-KL leg (0 skips it)")
     ap.add_argument("--s24-steps", type=int, default=10,
