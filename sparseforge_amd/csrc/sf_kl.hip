@@ -27,6 +27,7 @@ constexpr int kKlBlock = 256;
 constexpr int kKlFinalBlock = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kKlU = 4;  // slices of a row a thread loads before using them (forward)
+constexpr int kKlBwdU = 4;  // the same for the backward
 
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
@@ -308,8 +309,8 @@ __device__ __forceinline__ float kl_grad1(float a, float b, float inv_t, double 
   return in_range ? factor * (q - p) : 0.0f;
 }
 
-// One workgroup per token row, slices as in kl_rows_kernel (VEC: two slices'
-// loads in flight per thread); rows whose chunk was dropped get zeros.
+// One workgroup per token row, slices as in kl_rows_kernel (VEC: kKlBwdU
+// slices' loads in flight per thread); rows whose chunk was dropped get zeros.
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(kKlBlock) kl_backward_kernel(const void* __restrict__ s, const void* __restrict__ t,
                                                                int64_t vocab, float inv_t,
@@ -328,21 +329,21 @@ __global__ void __launch_bounds__(kKlBlock) kl_backward_kernel(const void* __res
       return;
     }
     int64_t c = threadIdx.x;
-    for (; c + step < slices; c += 2 * step) {
-      float a0[8], b0[8], a1[8], b1[8];
-      load8<DT>(s, base + 8 * c, 8, true, a0);
-      load8<DT>(t, base + 8 * c, 8, true, b0);
-      load8<DT>(s, base + 8 * (c + step), 8, true, a1);
-      load8<DT>(t, base + 8 * (c + step), 8, true, b1);
+    for (; c + (kKlBwdU - 1) * step < slices; c += kKlBwdU * step) {
+      float a[kKlBwdU][8], b[kKlBwdU][8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        a0[k] = kl_grad1(a0[k], b0[k], inv_t, ls, lt, factor);
-        a1[k] = kl_grad1(a1[k], b1[k], inv_t, ls, lt, factor);
+      for (int u = 0; u < kKlBwdU; ++u) {
+        load8<DT>(s, base + 8 * (c + u * step), 8, true, a[u]);
+        load8<DT>(t, base + 8 * (c + u * step), 8, true, b[u]);
       }
-      store8<DT>(gs, base + 8 * c, 8, true, a0);
-      store8<DT>(gs, base + 8 * (c + step), 8, true, a1);
+#pragma unroll
+      for (int u = 0; u < kKlBwdU; ++u) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[u][k] = kl_grad1(a[u][k], b[u][k], inv_t, ls, lt, factor);
+        store8<DT>(gs, base + 8 * (c + u * step), 8, true, a[u]);
+      }
     }
-    if (c < slices) {
+    for (; c < slices; c += step) {
       float a0[8], b0[8];
       load8<DT>(s, base + 8 * c, 8, true, a0);
       load8<DT>(t, base + 8 * c, 8, true, b0);
