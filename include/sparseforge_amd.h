@@ -51,6 +51,8 @@ extern "C" {
 #define SF_METRIC_HESSIAN 3
 #define SF_METRIC_WANDA 4
 #define SF_METRIC_MOVEMENT 5
+#define SF_METRIC_WEIGHT_SQUARED 6 /* W * W in W's dtype: hessian_obd when hessian_diag is a placeholder
+                                      (:1049-1055; legacy/utils.py:506-511) */
 
 /* ---- gate-target forms ------------------------------------------------- */
 #define SF_GATE_UNSTRUCTURED 0 /* sigmoid((z - tau) / (T + 1e-8)), global tau  (:1097-1162) */

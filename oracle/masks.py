@@ -197,6 +197,8 @@ def scores(W, H, aux, metric: str, w_dt: str = F32, h_dt: str = F32, aux_dt: str
         return rnd(np.abs(W) / rnd(np.sqrt(rnd(H + e, h_dt)), h_dt), promote(h_dt, w_dt))
     if metric == "hessian":
         return np.asarray(H, dtype=np.float32)
+    if metric == "weight_squared":  # hessian_obd without a Hessian (:1053-1055)
+        return rnd(W * W, w_dt)
     if metric == "wanda":
         a = np.asarray(aux, dtype=np.float32).reshape(1, -1)
         return rnd(np.abs(W) * rnd(np.sqrt(rnd(a + e, aux_dt)), aux_dt), promote(aux_dt, w_dt))
@@ -477,6 +479,15 @@ def effective_hard_type(c: dict) -> str:
     return c["mask_type"] if h == "match" else h
 
 
+def effective_metric(c: dict, W, H) -> str:
+    """The metric compute_gate_target evaluates: a Hessian metric whose hessian_diag is a placeholder falls
+    back to W * W (hessian_obd) or |W| (hessian_ratio, hessian) (:1049-1068)."""
+    metric = c["mask_metric"]
+    if metric in ("hessian_obd", "hessian_ratio", "hessian") and (H is None or np.shape(H) != np.shape(W)):
+        return "weight_squared" if metric == "hessian_obd" else "magnitude"
+    return metric
+
+
 def layer_gate_target(c: dict, step: int, W, H, mask, frozen, sample_idx, w_dt=F32, h_dt=F32, m_dt=F32, aux=None,
                       aux_dt=F32):
     """SparseLinear.compute_gate_target for mask_type unstructured / structured (non-block hard types).
@@ -486,7 +497,7 @@ def layer_gate_target(c: dict, step: int, W, H, mask, frozen, sample_idx, w_dt=F
     """
     if (not c["change_mask"]) or c["mask_type"] == "none":
         return np.ones_like(np.asarray(mask, dtype=np.float32))
-    metric = c["mask_metric"]
+    metric = effective_metric(c, W, H)
     s = scores(W, H, aux, metric, w_dt, h_dt, aux_dt, temperature=c["temperature"])
     sdt = score_dtype(metric, w_dt, h_dt, aux_dt)
     mu, sigma = score_stats(s)
@@ -512,7 +523,7 @@ def layer_update_mask(c: dict, step: int, W, H, mask, frozen, sample_idx, lambda
     if step % K != 0:
         return None
     G = layer_gate_target(c, step, W, H, mask, frozen, sample_idx, w_dt, h_dt, m_dt, aux, aux_dt)
-    sdt = score_dtype(c["mask_metric"], w_dt, h_dt, aux_dt)
+    sdt = score_dtype(effective_metric(c, W, H), w_dt, h_dt, aux_dt)
     pen_lr = float(c["mask_penalty_lr"]) if c["mask_penalty_lr"] is not None else float(c["mask_lr"])
     lam = float(lambda_mid or 0.0)
     mode = c["mask_penalty_mode"] or "mid"

@@ -24,7 +24,11 @@ every SparseForge-specific piece is one of the pinned oracle functions:
                   (legacy/sparse_modeling.py:1242-1666)
 
 The stock pieces (RMSNorm, rotary embedding, causal softmax attention, SwiGLU,
-cross-entropy) follow sparseforge_amd/llama.py's definitions in float64.
+cross-entropy) restate HuggingFace's LlamaForCausalLM, the model the reference
+retrains (legacy/model_llama.py:39-55), in float64 except where that model
+itself computes in float32 whatever its dtype (the rotary tables, RMSNorm's
+normalisation, the attention softmax); tests/test_llama_reference_model.py
+pins this forward against transformers' own LlamaForCausalLM in float64.
 """
 from __future__ import annotations
 
@@ -59,14 +63,19 @@ class _STE(torch.autograd.Function):
 
 
 def rmsnorm(x, w, eps):
-    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+    """LlamaRMSNorm: the normalisation in float32 whatever the activations' dtype, then the weight."""
+    xf = x.to(torch.float32)
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * xf.to(x.dtype)
 
 
 def rope(seq, d, theta):
-    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=F64) / d))
-    ang = torch.arange(seq, dtype=F64)[:, None] * inv[None, :]
+    """cos, sin of HuggingFace's LlamaRotaryEmbedding (the reference's model): inverse frequencies,
+    angles, cos and sin in float32, then widened (the module casts them to the activations' dtype)."""
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    ang = torch.arange(seq, dtype=torch.float32)[:, None] * inv[None, :]
     ang = torch.cat([ang, ang], dim=-1)
-    return ang.cos(), ang.sin()
+    return ang.cos().to(F64), ang.sin().to(F64)
 
 
 def _rot(x, cos, sin):
@@ -75,11 +84,12 @@ def _rot(x, cos, sin):
 
 
 def attention(q, k, v, cos, sin):
+    """Eager attention: scores (q k^T) * D^-0.5, causal mask, softmax in float32 cast back, p v."""
     B, S, H, D = q.shape
     q, k, v = (_rot(q.transpose(1, 2), cos, sin), _rot(k.transpose(1, 2), cos, sin), v.transpose(1, 2))
-    s = (q @ k.transpose(-2, -1)) / math.sqrt(D)
+    s = (q @ k.transpose(-2, -1)) * (D ** -0.5)
     s = s.masked_fill(torch.ones(S, S, dtype=torch.bool).triu(1), float("-inf"))
-    return (torch.softmax(s, -1) @ v).transpose(1, 2).reshape(B, S, H * D)
+    return (torch.softmax(s, -1, dtype=torch.float32).to(q.dtype) @ v).transpose(1, 2).reshape(B, S, H * D)
 
 
 def kl_loss(s, t, T=2.0):

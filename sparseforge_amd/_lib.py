@@ -39,6 +39,7 @@ METRIC = {
     "hessian": 3,
     "wanda": 4,
     "movement": 5,
+    "weight_squared": 6,  # hessian_obd's score when hessian_diag is a placeholder: W * W
 }
 
 GATE_UNSTRUCTURED = 0

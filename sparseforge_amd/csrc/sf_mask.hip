@@ -152,6 +152,8 @@ __device__ __forceinline__ float score_of(const ScoreSpec& s, float w, float h, 
     }
     case SF_METRIC_HESSIAN:
       return h;
+    case SF_METRIC_WEIGHT_SQUARED:  // W * W (hessian_obd without a Hessian)
+      return rndc<WD>(w * w);
     case SF_METRIC_WANDA: {  // |W| * sqrt(scaler + eps)
       float sp = rnd(a + s.eps, s.aux_dtype);
       float sq = rnd(sqrtf(sp), s.aux_dtype);
@@ -213,6 +215,7 @@ __device__ __forceinline__ void scores_of_ops(const ScoreSpec& s, const GroupOps
     SF_SCORES_CASE(SF_METRIC_HESSIAN)
     SF_SCORES_CASE(SF_METRIC_WANDA)
     SF_SCORES_CASE(SF_METRIC_MOVEMENT)
+    SF_SCORES_CASE(SF_METRIC_WEIGHT_SQUARED)
 #undef SF_SCORES_CASE
     default:
 #pragma unroll
@@ -1258,7 +1261,8 @@ bool vec_ok(int64_t cols, std::initializer_list<std::pair<const void*, int>> ops
 int check_common(const sf_mask_params* p) {
   SF_CHECK_ARG(p != nullptr, "null sf_mask_params");
   SF_CHECK_ARG(p->rows >= 0 && p->cols >= 0, "negative shape [%lld, %lld]", (long long)p->rows, (long long)p->cols);
-  SF_CHECK_ARG(p->metric >= SF_METRIC_MAGNITUDE && p->metric <= SF_METRIC_MOVEMENT, "bad metric %d", p->metric);
+  SF_CHECK_ARG(p->metric >= SF_METRIC_MAGNITUDE && p->metric <= SF_METRIC_WEIGHT_SQUARED, "bad metric %d",
+               p->metric);
   SF_CHECK_ARG(dtype_ok(p->score_dtype), "bad score dtype %d", p->score_dtype);
   return SF_OK;
 }

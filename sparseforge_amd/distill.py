@@ -56,7 +56,8 @@ class _KLGrad(torch.autograd.Function):
     so the vector-Jacobian product with u = ggs * m is
         s_bar_j = m_j (g c_r / T) q_j (u_j - sum_i u_i q_i),
     and d gs / d g = c_r m (q - p) gives g_bar = sum ggs * c_r * m * (q - p).  These run as float32
-    device elementwise ops and row sums (they are needed once per Hutchinson probe)."""
+    device elementwise ops and row sums (they are needed once per Hutchinson probe).  Rows of a dropped
+    chunk (c_r = 0) give exact zeros even where their logits are NaN."""
 
     @staticmethod
     def forward(ctx, s2, t2, lse, scale, g, temperature: float):
@@ -79,15 +80,18 @@ class _KLGrad(torch.autograd.Function):
         s2, t2, lse, scale, g = ctx.saved_tensors
         T = ctx.temperature
         s = s2.float()
-        inside = (s >= -100.0) & (s <= 100.0)
-        q = torch.exp(s.clamp(-100.0, 100.0) / T - lse[:, 0:1].float())
-        u = ggs.float() * inside
+        # live: inside the clamp range in a chunk the forward kept (row scale > 0).  A dropped chunk may hold
+        # NaN logits (that is why it was dropped), and the reference takes it out of the graph, so every
+        # term there is selected to 0 rather than multiplied by 0 (0 * NaN would be NaN).
+        live = (s >= -100.0) & (s <= 100.0) & (scale > 0)[:, None]
+        q = torch.where(live, torch.exp(s.clamp(-100.0, 100.0) / T - lse[:, 0:1].float()), 0.0)
+        u = torch.where(live, ggs.float(), 0.0)
         dot = (u * q).sum(dim=1, keepdim=True)
         coef = (g.float() * scale / T)[:, None]
-        s_bar = (coef * q * (u - dot) * inside).to(s2.dtype)
+        s_bar = torch.where(live, coef * q * (u - dot), 0.0).to(s2.dtype)
         g_bar = None
         if ctx.needs_input_grad[4]:
-            p = torch.exp(t2.float().clamp(-100.0, 100.0) / T - lse[:, 1:2].float())
+            p = torch.where(live, torch.exp(t2.float().clamp(-100.0, 100.0) / T - lse[:, 1:2].float()), 0.0)
             g_bar = (u * (q - p) * scale[:, None]).sum().to(g.dtype).reshape(g.shape)
         return s_bar, None, None, None, g_bar, None
 

@@ -104,8 +104,6 @@ def glu_joint_update(gate_module, up_module, step, lambda_mid, sample_idx=None):
         return
     ops_g, ops_u = gate_module._mask_operands(), up_module._mask_operands()
     code_g, code_u = gate_module._metric_code(ops_g), up_module._metric_code(ops_u)
-    if code_g == -1 or code_u == -1:  # hessian_obd without H: scores = W * W
-        raise NotImplementedError("hessian_obd without a hessian_diag tensor")
     pg = gate_module._mask_params(step, ops_g, code_g) if gate_module.mask_type in ("unstructured", "structured") \
         else None
     pu = up_module._mask_params(step, ops_u, code_u) if up_module.mask_type in ("unstructured", "structured") \

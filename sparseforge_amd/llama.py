@@ -16,11 +16,16 @@ projections and plain nn.Linear for the dense teacher:
 * RMSNorm: x * rsqrt(mean(x^2) + eps) in float32, scaled by a learned
   weight after the cast back to the input dtype.
 * Rotary embedding: the half-split form (pairs (i, i + d/2) rotate by
-  position * theta^(-2i/d)).
+  position * theta^(-2i/d)); the tables are computed in float32 and cast to
+  the activations' dtype, as HuggingFace's LlamaRotaryEmbedding does.
 * Attention: causal softmax attention written with differentiable torch ops
-  in float32 (the Hessian-vector product differentiates it twice; float32
-  batched products with contiguous operands also stay clear of bf16 batched
-  products on transposed operands).
+  (the Hessian-vector product differentiates it twice).  bf16 activations
+  follow HuggingFace's eager attention operation for operation: rotation in
+  bf16, bf16 products q k^T and p v (float32 accumulation), the 1/sqrt(D)
+  scale, the causal mask, the softmax in float32 cast back to bf16.  float32
+  activations run the same sequence in float32.  Every batched product goes
+  through _BMM, whose operands (in the forward and in every derivative) are
+  made contiguous first: no batched bf16 product sees a transposed view.
 * forward(idx, targets) returns (logits, loss, None) like the reference's
   LlamaSparse.forward (legacy/model_llama.py:59-85): loss is the
   cross-entropy of the logits against already shifted targets,
@@ -83,33 +88,65 @@ def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tens
     return x * cos + swapped * sin
 
 
+class _BMM(torch.autograd.Function):
+    """torch.bmm(a, b) differentiable any number of times, with contiguous operands in every product.
+
+    The derivatives are products of the same kind (grad_a = g b^T, grad_b = a^T g), so the forward,
+    the backward and the Hutchinson double backward all multiply contiguous tensors."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        return torch.bmm(a.contiguous(), b.contiguous())
+
+    @staticmethod
+    def backward(ctx, g):
+        a, b = ctx.saved_tensors
+        g = g.to(a.dtype)
+        ga = _BMM.apply(g, b.transpose(1, 2)) if ctx.needs_input_grad[0] else None
+        gb = _BMM.apply(a.transpose(1, 2), g) if ctx.needs_input_grad[1] else None
+        return ga, gb
+
+
 _CAUSAL_BIAS: dict = {}
 
 
-def causal_bias(S: int, device) -> torch.Tensor:
-    """[1, S, S] float32: 0 on and below the diagonal, -inf above (cached per size and device)."""
-    key = (S, str(device))
+def causal_bias(S: int, device, dtype=torch.float32) -> torch.Tensor:
+    """[1, S, S]: 0 on and below the diagonal, -inf above (cached per size, device and dtype)."""
+    key = (S, str(device), dtype)
     if key not in _CAUSAL_BIAS:
-        _CAUSAL_BIAS[key] = torch.full((S, S), float("-inf"), device=device).triu_(1)[None]
+        _CAUSAL_BIAS[key] = torch.full((S, S), float("-inf"), device=device, dtype=dtype).triu_(1)[None]
     return _CAUSAL_BIAS[key]
 
 
 def causal_attention(q, k, v, cos, sin) -> torch.Tensor:
-    """q, k, v [B, S, H, D] -> [B, S, H * D] in q's dtype; float32 arithmetic, causal mask.
+    """q, k, v [B, S, H, D] -> [B, S, H * D] in q's dtype, causal.
 
-    The 1/sqrt(D) scale goes into q and the causal mask into the product's bias
-    (one baddbmm writes the masked scores), so the [B H, S, S] scores make one
-    write, one softmax pass and one read."""
+    The operation sequence of HuggingFace's eager attention, which the reference retrains with
+    (legacy/model_llama.py:39-55, eager_attention_forward): rotary tables cast to q's dtype and the
+    rotation in it; s = (q k^T) * D^-0.5; s + causal mask; softmax in float32, cast to q's dtype;
+    p v.  When D^-0.5 is a power of two (D = 64, 256, ...) the scale goes into q before the product,
+    which gives the same bits ((2^e q) k^T = 2^e (q k^T) exactly); otherwise the scores are scaled after
+    it.  The masked positions get -inf where the reference adds the dtype's lowest value: either way
+    their probability is exactly 0."""
     B, S, H, D = q.shape
-    # autocast would recast these float32 products to bf16: keep it off for the attention math
+    dt = q.dtype
     with torch.autocast(q.device.type, enabled=False):
-        qf = _rotate(q.float().transpose(1, 2), cos, sin) * (1.0 / math.sqrt(D))   # [B, H, S, D]
-        kf = _rotate(k.float().transpose(1, 2), cos, sin)
-        vf = v.float().transpose(1, 2).reshape(B * H, S, D).contiguous()
-        kt = kf.transpose(-2, -1).reshape(B * H, D, S).contiguous()
-        scores = torch.baddbmm(causal_bias(S, q.device).to(qf.dtype), qf.reshape(B * H, S, D).contiguous(), kt)
-        out = torch.bmm(torch.softmax(scores, dim=-1), vf)                          # [B H, S, D]
-    return out.view(B, H, S, D).transpose(1, 2).reshape(B, S, H * D).to(q.dtype)
+        c, s_ = cos.to(dt), sin.to(dt)
+        qh = _rotate(q.transpose(1, 2), c, s_)                                   # [B, H, S, D]
+        kh = _rotate(k.transpose(1, 2), c, s_)
+        scale = D ** -0.5
+        exact = math.frexp(scale)[0] == 0.5                                       # a power of two
+        if exact:
+            qh = qh * scale
+        qh = qh.reshape(B * H, S, D)
+        kt = kh.transpose(-2, -1).reshape(B * H, D, S)
+        scores = _BMM.apply(qh, kt)                                               # [B H, S, S]
+        if not exact:
+            scores = scores * scale
+        p = torch.softmax(scores + causal_bias(S, q.device, dt), dim=-1, dtype=torch.float32).to(dt)
+        out = _BMM.apply(p, v.transpose(1, 2).reshape(B * H, S, D))              # [B H, S, D]
+    return out.view(B, H, S, D).transpose(1, 2).reshape(B, S, H * D)
 
 
 class DecoderLayer(nn.Module):

@@ -169,19 +169,19 @@ def calculate_model_mask(model, step=0, lambda_mid: float = 0.0):
         key = (ops.device(), tuple(ops.dt(t) if t is not None else -1
                                    for t in (ops.weight, ops.hessian, ops.aux, ops.mask, ops.frozen)),
                bytes(shape_free), q)
-        batches.setdefault(key, []).append((m, ops, p))
+        # the tau sample, drawn here so every layer (staged or batched) draws in module order, as one
+        # update_mask per layer does
+        idx = m._sample_indices(ops.weight.numel(), ops.device()) if p.gate == L.GATE_UNSTRUCTURED else None
+        batches.setdefault(key, []).append((m, ops, p, idx))
     for (dev, _dts, _pb, q), items in batches.items():
         n = len(items)
         stats = torch.empty((n, 2), dtype=torch.float32, device=dev)
         tau = torch.empty(n, dtype=torch.float32, device=dev)
         flips = torch.zeros(n, dtype=torch.int64, device=dev)
-        jobs = []
-        for i, (m, ops, p) in enumerate(items):
-            # the tau sample of each layer, drawn in layer order as update_mask draws it
-            idx = m._sample_indices(ops.weight.numel(), dev) if p.gate == L.GATE_UNSTRUCTURED else None
-            jobs.append(K.MaskJob(ops, idx, stats[i], tau[i:i + 1], flips[i:i + 1]))
+        jobs = [K.MaskJob(ops, idx, stats[i], tau[i:i + 1], flips[i:i + 1])
+                for i, (m, ops, p, idx) in enumerate(items)]
         K.update_mask_multi(items[0][2], q, jobs)
-        for i, (m, _ops, _p) in enumerate(items):
+        for i, (m, _ops, _p, _idx) in enumerate(items):
             m._finish_update(step, flips[i:i + 1])
     if pipe:
         pipe.join()
@@ -202,9 +202,7 @@ def _compute_importance_scores(module):
     from .glu import _score_only_params
 
     ops = module._mask_operands()
-    code = module._metric_code(ops)
-    if code == -1:  # hessian_obd without H: the reference takes W * W
-        raise NotImplementedError("hessian_obd without a hessian_diag tensor")
+    code = module._metric_code(ops)  # hessian_obd without H: W * W, as :506-511
     p = _score_only_params(module, ops, code)
     dt = torch.bfloat16 if p.score_dtype == L.DT_BF16 else torch.float32
     return K.importance_scores(p, ops, dt)

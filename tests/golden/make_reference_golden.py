@@ -20,6 +20,9 @@ never travels with them.  Functions covered (reference file:line):
   stats_*     mid_penalty, sparsity_penalty,       legacy/utils.py:876-1234, :2069-2280
               nm_2_4_tile_stats, mask_stats
   harden_*    harden_fraction                      legacy/utils.py:1236-1276
+  slorb_init_* init_SLoRB (projection P, weight S)  legacy/sparse_modeling.py:830-872
+  *_obd_noH_* hessian_obd scores without a Hessian  legacy/sparse_modeling.py:1049-1055
+              (compute_gate_target, update_mask)
 
 The reference module imports wandb at top level without using it
 (legacy/sparse_modeling.py:20); an empty module object is registered under
@@ -31,7 +34,7 @@ mask_stats samples torch.randint indices per layer; the draws are replayed
 after the same torch.manual_seed and stored with the fixture.
 
 Run:  python tests/golden/make_reference_golden.py [group ...]   (needs /root/reference;
-      groups: gate update glu adamw hutch linear ste kl bsr block stats harden, default all)
+      groups: gate update glu adamw hutch linear ste kl bsr block stats harden slorb, default all)
 """
 from __future__ import annotations
 
@@ -60,9 +63,9 @@ def np32(t: torch.Tensor) -> np.ndarray:
     return t.detach().float().cpu().numpy().astype(np.float32)
 
 
-def make_layer(ref_sm, out_f, in_f, dtype, seed, **cfg_kw):
+def make_layer(ref_sm, out_f, in_f, dtype, seed, no_hessian=False, **cfg_kw):
     cfg = ref_sm.SparseLinearConfig(**cfg_kw)
-    if cfg_kw.get("mask_metric", "") in ("hessian_ratio", "hessian_obd", "hessian"):
+    if cfg_kw.get("mask_metric", "") in ("hessian_ratio", "hessian_obd", "hessian") and not no_hessian:
         cfg.enable_hutchinson = True
     torch.manual_seed(seed)
     layer = ref_sm.SparseLinear(in_f, out_f, sparselinear_config=cfg, bias=False).to(dtype)
@@ -97,12 +100,19 @@ def gate_cases(ref_sm, out):
         "gate_struct_bf16": dict(dtype=torch.bfloat16, mask_type="structured", hard_mask_type="match",
                                  mask_metric="hessian_obd", step=12, beta_structural_start=0,
                                  beta_structural_end=20),
+        # hessian_diag left a placeholder: the score falls back to W * W (:1053-1055)
+        "gate_obd_noH_f32": dict(dtype=torch.float32, mask_type="unstructured", hard_mask_type="nm_2_4",
+                                 mask_metric="hessian_obd", tau_sample_size=512, sparsity_warmup_steps=0,
+                                 step=9, no_hessian=True),
+        "gate_obd_noH_bf16": dict(dtype=torch.bfloat16, mask_type="structured", hard_mask_type="match",
+                                  mask_metric="hessian_obd", step=4, no_hessian=True),
     }
     for i, (name, kw) in enumerate(cases.items()):
         kw = dict(kw)
         dtype = kw.pop("dtype")
         step = kw.pop("step")
         layer, cfg = make_layer(ref_sm, 32, 64, dtype, 100 + i, **kw)
+        kw.pop("no_hessian", None)
         seed = 1000 + i
         torch.manual_seed(seed)
         G = layer.compute_gate_target(step)
@@ -140,6 +150,10 @@ def update_cases(ref_sm, out):
                                   mask_metric="hessian_ratio", tau_sample_size=512, sparsity_warmup_steps=0,
                                   mask_update_period=1, mask_penalty_mode="nm_2_4", mask_penalty_lr=0.1,
                                   mask_lr=0.1, lam=0.1),
+        "update_obd_noH_f32": dict(dtype=torch.float32, mask_type="unstructured", hard_mask_type="nm_2_4",
+                                   mask_metric="hessian_obd", tau_sample_size=512, sparsity_warmup_steps=0,
+                                   mask_update_period=1, mask_penalty_mode="nm_2_4", mask_penalty_lr=0.1,
+                                   mask_lr=0.1, lam=0.1, steps=(1, 2, 3), no_hessian=True),
     }
     for i, (name, kw) in enumerate(cases.items()):
         kw = dict(kw)
@@ -148,9 +162,10 @@ def update_cases(ref_sm, out):
         steps = kw.pop("steps", (1, 2, 3, 4, 5))
         # 32 x 66: a 2-column tail after 16 full groups (nm_2_4 keeps the tail)
         cols = 64 if kw["mask_type"] == "structured" else 66
+        kw_rec = {k: v for k, v in kw.items() if k != "no_hessian"}
         layer, cfg = make_layer(ref_sm, 32, cols, dtype, 200 + i, **kw)
         rec = dict(W=np32(layer.weight), H=np32(layer.hessian_diag), init_mask=np32(layer.mask),
-                   init_frozen=np32(layer.frozen_mask_flags), dtype=np.array(str(dtype)), cfg=np.array(repr(kw)),
+                   init_frozen=np32(layer.frozen_mask_flags), dtype=np.array(str(dtype)), cfg=np.array(repr(kw_rec)),
                    lam=np.float64(lam), steps=np.array(steps, dtype=np.int64))
         n = layer.weight.numel()
         m = int(cfg.tau_sample_size)
@@ -281,6 +296,25 @@ def linear_case(ref_sm, out):
         rec[f"dS{j}"] = np32(layer.SLoRB_Weight.grad)
         layer.zero_grad(set_to_none=True)
     out["linear_slorb_f32"] = rec
+
+
+def slorb_init_cases(ref_sm, out):
+    """init_SLoRB on a layer with a random soft mask: the block-sum projection P and the SLoRB weight S
+    (the sum or mean of the pruned part W (1 - mask) over each block of k inputs)."""
+    for name, (out_f, in_f, k, init, dtype) in {"slorb_init_sum_f32": (20, 32, 8, "sum", torch.float32),
+                                                  "slorb_init_mean_f32": (24, 48, 16, "mean", torch.float32),
+                                                  "slorb_init_mean_bf16": (16, 64, 8, "mean", torch.bfloat16)}.items():
+        kw = dict(mask_type="unstructured", hard_mask_type="nm_2_4", mask_metric="magnitude", SLoRB=True,
+                  SLoRB_k=k, SLoRB_init_type=init, trainable_projection=True)
+        cfg = ref_sm.SparseLinearConfig(**kw)
+        torch.manual_seed(750 + k)
+        layer = ref_sm.SparseLinear(in_f, out_f, sparselinear_config=cfg, bias=False).to(dtype)
+        with torch.no_grad():
+            layer.weight.copy_((torch.randn(out_f, in_f) * 0.02).to(dtype))
+            layer.mask.copy_(torch.rand(out_f, in_f).to(dtype))
+        layer.init_SLoRB()
+        out[name] = dict(W=np32(layer.weight), mask=np32(layer.mask), P=np32(layer.x_proj),
+                         S=np32(layer.SLoRB_Weight), dtype=np.array(str(dtype)), cfg=np.array(repr(kw)))
 
 
 def ste_cases(ref_sm, out):
@@ -522,7 +556,8 @@ def harden_case(ref_sm, ref_utils, out):
     out["harden_f32"] = rec
 
 
-GROUPS = ("gate", "update", "glu", "adamw", "hutch", "linear", "ste", "kl", "bsr", "block", "stats", "harden")
+GROUPS = ("gate", "update", "glu", "adamw", "hutch", "linear", "ste", "kl", "bsr", "block", "stats", "harden",
+          "slorb")
 
 
 def main():
@@ -557,6 +592,8 @@ def main():
         stats_cases(ref_sm, ref_utils, out)
     if "harden" in groups:
         harden_case(ref_sm, ref_utils, out)
+    if "slorb" in groups:
+        slorb_init_cases(ref_sm, out)
     for name, rec in out.items():
         path = os.path.join(OUT, f"ref_{name}.npz")
         np.savez_compressed(path, torch_version=np.array(torch.__version__), **rec)

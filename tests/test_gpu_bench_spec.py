@@ -1,0 +1,100 @@
+"""The batched mask update at the exact specification bench.py's mask-update leg times, against the oracle.
+
+bench.py updates a LLaMA-2-7B arena through sf_update_mask_multi with bf16 W, f32
+hessian_diag and an f32 soft mask, hessian_ratio scores, the unstructured gate
+(tau = the 0.5-quantile of a 262144-element z sample), the nm_2_4 hard type for the
+flip count, no penalty, mask_lr 0.1 and a temperature going from 1.0 down to 0.01
+(legacy/sparse_modeling.py:932-942, :987-1015, :1018-1239, :1242-1666).  Those
+parameters select the kernel's compile-time specialisation for that spec (the
+nm_2_4 penalty selects its sibling), so this runs the very instance the bench
+measures, on one full decoder layer (q/k/v/o 4096x4096, gate/up 11008x4096, down
+4096x11008), at T = 1.0, 0.1 and 0.01 -- where the sigmoid's argument reaches
+~10^3 -- and with and without the nm_2_4 penalty.
+
+Bar: every layer's soft mask within 1e-6 of oracle.masks.layer_update_mask
+(float32, bf16 W emulated); the device's own hard 2:4 projection of its mask
+equal bit for bit to the oracle's projection of the same mask; against the
+oracle's own mask only genuine near-ties may decide differently, and the flip
+count moves by at most four per such group.
+"""
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import masks as om
+from oracle.numerics import BF16, F32
+from test_gpu_masks import _hard_parity
+
+pytestmark = pytest.mark.gpu
+
+LAYER = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
+         ("gate", 4096, 11008), ("up", 4096, 11008), ("down", 11008, 4096)]  # (name, in, out)
+MASK_LR, PEN_LR, LAMBDA = 0.1, 0.1, 0.05
+
+
+def _params(L, temperature: float, penalty: str):
+    """The MaskParams bench.py's mask-update leg passes, with the penalty switched on for 'nm_2_4'."""
+    p = L.MaskParams()
+    p.metric = L.METRIC["hessian_ratio"]
+    p.gate = L.GATE_UNSTRUCTURED
+    p.n_keep, p.m_group = 2, 4
+    p.hard_kind, p.hard_n, p.hard_m = L.HARD_NM_TAIL_KEEP, 2, 4
+    p.penalty = L.PENALTY_NONE if penalty == "none" else L.PENALTY_NM_2_4
+    p.penalty_coef = 0.0 if penalty == "none" else PEN_LR * LAMBDA
+    p.score_dtype = L.DT_F32
+    p.temperature = temperature
+    p.eps_metric = 1e-8
+    p.movement_temp = 1.0
+    p.mask_lr = MASK_LR
+    return p
+
+
+def _oracle_layer(args):
+    W, H, M0, idx, T, penalty = args
+    c = om.full_config(mask_type="unstructured", hard_mask_type="nm_2_4", mask_metric="hessian_ratio",
+                       sparsity_warmup_steps=0, mask_update_period=1, mask_lr=MASK_LR, mask_penalty_lr=PEN_LR,
+                       mask_penalty_mode="nm_2_4", temp_init=T, temp_decay=1.0, temp_min=0.0)
+    new, _fr, flips, _hx = om.layer_update_mask(c, 1, W, H, M0, None, idx, LAMBDA if penalty != "none" else 0.0,
+                                                BF16, F32, F32)
+    return new, flips
+
+
+@pytest.mark.parametrize("penalty", ["none", "nm_2_4"])
+@pytest.mark.parametrize("temperature", [1.0, 0.1, 0.01])
+def test_bench_mask_update_instance_matches_oracle(cuda_device, temperature, penalty):
+    from sparseforge_amd import _lib as L
+    from sparseforge_amd import kernels as K
+
+    print(f"[bench-spec] update_mask_multi, 7B layer, T={temperature}, penalty={penalty}", flush=True)
+    g = torch.Generator(device=cuda_device).manual_seed(11)
+    layers = []
+    for _name, fin, fout in LAYER:
+        W = (torch.randn(fout, fin, generator=g, device=cuda_device) * 0.02).to(torch.bfloat16)
+        H = torch.rand(fout, fin, generator=g, device=cuda_device) * 1e-3 + 1e-6
+        M = torch.rand(fout, fin, generator=g, device=cuda_device)
+        idx = torch.randint(0, W.numel(), (262144,), generator=g, device=cuda_device)
+        layers.append((W, H, M, idx))
+    host_in = [(W.float().cpu().numpy(), H.cpu().numpy(), M.cpu().numpy(), idx.cpu().numpy()) for W, H, M, idx in
+               layers]
+    n = len(layers)
+    stats = torch.empty((n, 2), dtype=torch.float32, device=cuda_device)
+    tau = torch.empty(n, dtype=torch.float32, device=cuda_device)
+    flips = torch.zeros(n, dtype=torch.int64, device=cuda_device)
+    jobs = [K.MaskJob(K.MaskOperands(weight=W, mask=M, hessian=H), idx, stats[i], tau[i:i + 1], flips[i:i + 1])
+            for i, (W, H, M, idx) in enumerate(layers)]
+    K.update_mask_multi(_params(L, temperature, penalty), 0.5, jobs, L.MULTI_ALL, K.multi_workspace(jobs, cuda_device))
+    torch.cuda.synchronize()
+    got = [M.cpu().numpy() for _W, _H, M, _i in layers]
+    gpu_flips = flips.cpu().tolist()
+    hard_dev = [K.hard_mask(M, L.HARD_NM_TAIL_KEEP, 2, 4).cpu().numpy() for _W, _H, M, _i in layers]
+    with ThreadPoolExecutor(max_workers=n) as ex:  # numpy releases the GIL: the seven layers in parallel
+        ref = list(ex.map(_oracle_layer, [(W, H, M0, idx, temperature, penalty) for W, H, M0, idx in host_in]))
+    near = 0
+    for (name, _fin, _fout), m_got, hd, (m_ref, f_ref), f_got in zip(LAYER, got, hard_dev, ref, gpu_flips):
+        d = float(np.abs(m_got - m_ref).max())
+        assert d <= 1e-6, (name, temperature, penalty, d)
+        assert np.array_equal(hd, om.hard_mask_from_soft(m_got, "nm_2_4")), (name, "device projection")
+        near += _hard_parity(m_got, m_ref, 1e-6, int(f_got), int(f_ref), f"{name} T={temperature} {penalty}")
+    print(f"[bench-spec] T={temperature} {penalty}: all seven layers within 1e-6, {near} near-tie groups", flush=True)

@@ -144,3 +144,35 @@ def test_kl_second_derivative_matches_float64_autograd(cuda_device, dtype, tol):
     terms = gs64.detach() / w.double() * d.double()
     ref_w = float(terms.sum())
     assert abs(hw.item() - ref_w) <= tol * float(terms.abs().sum())
+
+
+def test_kl_second_derivative_zero_on_dropped_nan_chunk(cuda_device):
+    """A chunk the forward drops for a NaN logit (student or teacher) takes no part in the double backward
+    either: the Hessian-vector product is finite, exactly 0 on the dropped chunk, and equals the float64
+    double backward of the reference formula elsewhere; d/dw of the weighted loss stays finite."""
+    from oracle import retrain as orc
+    from sparseforge_amd.distill import chunked_kl_loss
+
+    g = torch.Generator().manual_seed(29)
+    s = torch.randn(6000, 64, generator=g) * 3
+    t = torch.randn(6000, 64, generator=g) * 3
+    s[2100, 7] = float("nan")   # drops rows [2048, 4096)
+    t[4500, 3] = float("nan")   # drops rows [4096, 6000)
+    d = torch.randn(6000, 64, generator=g)
+    w = torch.tensor(1.3)
+    sd = s.to(cuda_device).requires_grad_(True)
+    wd = w.to(cuda_device).requires_grad_(True)
+    kl = chunked_kl_loss(sd, t.to(cuda_device), 2) * wd
+    (gs,) = torch.autograd.grad(kl, sd, create_graph=True)
+    hv, hw = torch.autograd.grad((gs * d.to(cuda_device)).sum(), (sd, wd))
+    hv = hv.cpu()
+    assert torch.isfinite(hv).all() and torch.isfinite(hw).all()
+    assert (hv[2048:] == 0).all()
+    s64 = s[:2048].double().requires_grad_(True)
+    # rows [0, 2048) are the only kept chunk: the reference's loss is their KL times 2048 / 6000
+    (gs64,) = torch.autograd.grad(orc.kl_loss(s64, t[:2048].double()) * (2048 / 6000) * w.double(), s64,
+                                  create_graph=True)
+    (h64,) = torch.autograd.grad((gs64 * d[:2048].double()).sum(), s64)
+    assert float((hv[:2048].double() - h64).abs().max() / h64.abs().max()) < 1e-5
+    ref_w = float((gs64.detach() / w.double() * d[:2048].double()).sum())
+    assert abs(hw.item() - ref_w) <= 1e-5 * float((gs64.detach() / w.double() * d[:2048].double()).abs().sum())

@@ -183,6 +183,26 @@ def test_compute_importance_scores_bit_exact(cuda_device, metric, tdt):
     np.testing.assert_array_equal(S.float().cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("tdt", [torch.float32, torch.bfloat16])
+def test_compute_importance_scores_obd_without_hessian(cuda_device, tdt):
+    """hessian_obd with hessian_diag left a placeholder scores W * W in W's dtype (legacy/utils.py:506-511),
+    bit for bit (a product of two representable values rounds once)."""
+    from sparseforge_amd import utils as U
+
+    sm = _sm()
+    cfg = sm.SparseLinearConfig(mask_metric="hessian_obd")
+    layer = sm.SparseLinear(70, 40, sparselinear_config=cfg, bias=False).to(tdt).to(cuda_device)
+    assert layer._is_placeholder("hessian_diag")
+    g = torch.Generator().manual_seed(2)
+    with torch.no_grad():
+        layer.weight.copy_((torch.randn(40, 70, generator=g) * 0.02).to(tdt))
+    S = U._compute_importance_scores(layer)
+    assert S.dtype == tdt
+    W = layer.weight.detach().float().cpu().numpy()
+    np.testing.assert_array_equal(S.float().cpu().numpy(), om.scores(W, None, None, "weight_squared",
+                                                                      F32 if tdt == torch.float32 else BF16))
+
+
 @pytest.mark.parametrize("kw", [dict(mask_type="unstructured"), dict(mask_type="structured"),
                                 dict(mask_type="unstructured", beta_structural_start=0, beta_structural_end=10)])
 @pytest.mark.parametrize("tdt", [torch.float32, torch.bfloat16])

@@ -123,8 +123,8 @@ def _dt(name):
 def _layer_from_golden(r, cfg_kw, tdt, dev, cols=None):
     sm = _sm()
     cfg = sm.SparseLinearConfig(**cfg_kw)
-    if cfg_kw.get("mask_metric", "") in ("hessian_ratio", "hessian_obd", "hessian"):
-        cfg.enable_hutchinson = True
+    if cfg_kw.get("mask_metric", "") in ("hessian_ratio", "hessian_obd", "hessian") and r["H"].shape == r["W"].shape:
+        cfg.enable_hutchinson = True  # the *_noH_* fixtures keep hessian_diag a placeholder
     W = r["W"]
     layer = sm.SparseLinear(W.shape[1], W.shape[0], sparselinear_config=cfg, bias=False).to(tdt).to(dev)
     layer.weight.mask = layer.mask
@@ -137,7 +137,7 @@ def _layer_from_golden(r, cfg_kw, tdt, dev, cols=None):
 
 @pytest.mark.parametrize("case", ["gate_unstr_ratio_f32", "gate_unstr_beta_f32", "gate_unstr_frozen_f32",
                                   "gate_struct_f32", "gate_struct_exact_f32", "gate_unstr_ratio_bf16",
-                                  "gate_struct_bf16"])
+                                  "gate_struct_bf16", "gate_obd_noH_f32", "gate_obd_noH_bf16"])
 def test_gate_target_matches_reference(cuda_device, case):
     r = load_golden(case)
     kw = ast.literal_eval(str(r["cfg"]))
@@ -155,7 +155,7 @@ def test_gate_target_matches_reference(cuda_device, case):
 
 
 @pytest.mark.parametrize("case", ["update_paper_f32", "update_mid_bin_f32", "update_struct_topn_f32",
-                                  "update_freeze_f32", "update_paper_bf16"])
+                                  "update_freeze_f32", "update_paper_bf16", "update_obd_noH_f32"])
 def test_update_mask_matches_reference(cuda_device, case):
     r = load_golden(case)
     kw = ast.literal_eval(str(r["cfg"]))
@@ -282,3 +282,29 @@ def test_tau_quantile_radix_select_large(cuda_device, case):
             assert got != got and ref != ref
         else:
             assert got == ref, (case, q, got, ref)
+
+
+@pytest.mark.parametrize("N,M", [(2, 8), (4, 8), (1, 2)])
+def test_structured_group_size_other_than_4_is_rejected(cuda_device, N, M):
+    """The device kernels build N:M groups of 4 only (the reference's structured mask takes any M,
+    legacy/sparse_modeling.py:720-735, :1164-1185, :1531-1565).  Every entry point that would need another
+    group size raises NotImplementedError instead of projecting groups of 4: the hard projection, the
+    forward during hardening, the gate target and update_mask."""
+    sm = _sm()
+    cfg = sm.SparseLinearConfig(mask_type="structured", N=N, M=M, hard_mask_type="match", mask_metric="magnitude",
+                                sparsity_warmup_steps=0, mask_update_period=1)
+    layer = sm.SparseLinear(64, 16, sparselinear_config=cfg, bias=False).to(cuda_device)
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(16, 64) * 0.02)
+        layer.mask.copy_(torch.rand(16, 64))
+    before = layer.mask.detach().clone()
+    with pytest.raises(NotImplementedError):
+        layer._hard_mask_from_soft(layer.mask)
+    layer.hardening_x = 0.5
+    with pytest.raises(NotImplementedError):
+        layer(torch.randn(8, 64, device=cuda_device))
+    with pytest.raises(NotImplementedError):
+        layer.compute_gate_target(1)
+    with pytest.raises(NotImplementedError):
+        layer.update_mask(1)
+    assert torch.equal(layer.mask, before)  # nothing was written

@@ -112,7 +112,7 @@ def _cfg(rec):
 
 @pytest.mark.parametrize("case", ["gate_unstr_ratio_f32", "gate_unstr_beta_f32", "gate_unstr_frozen_f32",
                                   "gate_struct_f32", "gate_struct_exact_f32", "gate_unstr_ratio_bf16",
-                                  "gate_struct_bf16"])
+                                  "gate_struct_bf16", "gate_obd_noH_f32", "gate_obd_noH_bf16"])
 def test_gate_target_matches_reference_golden(case):
     r = load_golden(case)
     c = _cfg(r)
@@ -127,7 +127,7 @@ def test_gate_target_matches_reference_golden(case):
 
 
 @pytest.mark.parametrize("case", ["update_paper_f32", "update_mid_bin_f32", "update_struct_topn_f32",
-                                  "update_freeze_f32", "update_paper_bf16"])
+                                  "update_freeze_f32", "update_paper_bf16", "update_obd_noH_f32"])
 def test_update_mask_matches_reference_golden(case):
     r = load_golden(case)
     c = _cfg(r)
