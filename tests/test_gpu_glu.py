@@ -186,11 +186,13 @@ def test_compute_importance_scores_bit_exact(cuda_device, metric, tdt):
 @pytest.mark.parametrize("tdt", [torch.float32, torch.bfloat16])
 def test_compute_importance_scores_obd_without_hessian(cuda_device, tdt):
     """hessian_obd with hessian_diag left a placeholder scores W * W in W's dtype (legacy/utils.py:506-511),
-    bit for bit (a product of two representable values rounds once)."""
+    bit for bit (a product of two representable values rounds once).  A hessian_obd layer holds a full
+    hessian_diag unless change_mask is off (legacy/sparse_modeling.py:318-334), so that is how the
+    placeholder arises."""
     from sparseforge_amd import utils as U
 
     sm = _sm()
-    cfg = sm.SparseLinearConfig(mask_metric="hessian_obd")
+    cfg = sm.SparseLinearConfig(mask_metric="hessian_obd", change_mask=False)
     layer = sm.SparseLinear(70, 40, sparselinear_config=cfg, bias=False).to(tdt).to(cuda_device)
     assert layer._is_placeholder("hessian_diag")
     g = torch.Generator().manual_seed(2)
