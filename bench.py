@@ -915,6 +915,7 @@ def linear_leg(torch, sm, prof, dev, a) -> dict:
              for n, s in ks.items()}
     per_linear = per_linear_times(torch, mods, xs, gys)
     log("per linear: " + ", ".join(f"{r['linear']} {r['ms']:.3f} ms" for r in per_linear))
+    mixed = mixed_phase_leg(torch, prof, mods, xs, gys, a.steps, flops)
     hvp = hvp_layer_leg(torch, mods, xs)
     del mods, xs, gys
     torch.cuda.empty_cache()
@@ -946,9 +947,41 @@ def linear_leg(torch, sm, prof, dev, a) -> dict:
             "unit": "TFLOP/s dense-equivalent", "peak": PEAK_BF16_SPARSE_TFLOPS,
             "frac": round(s24.rate / 1e12 / PEAK_BF16_SPARSE_TFLOPS, 4)},
         "per_linear": per_linear,
+        "mixed_phase": mixed,
         "hutchinson_probe_layer": hvp,
         "kernels": other,
     }
+
+
+def mixed_phase_leg(torch, prof, mods, xs, gys, steps: int, flops: float) -> dict:
+    """The same layer step in the hardening phase (0 < hardening_x < 1, most of a training run: the
+    paper's schedule spends steps 2000..17000 there): E = hx * soft + (1 - hx) * hard(soft) in bf16, the
+    forward on the dense kernel over the masked weight one elementwise pass writes."""
+    hx0 = [m.hardening_x for m in mods]
+    for m in mods:
+        m.hardening_x = 0.5
+    for _ in range(2):
+        linear_step(mods, xs, gys)
+    with prof.kernel_timer() as kt:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            linear_step(mods, xs, gys)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+    for m, h in zip(mods, hx0):
+        m.hardening_x = h
+    ks = kt.summary()
+    g = ks["sf_gemm"]
+    res = {"hardening_x": 0.5, "ms_per_step": round(el * 1e3 / steps, 4),
+           "TFLOP/s": round(flops * steps / el / 1e12, 3),
+           "sf_gemm": {"launches": g.launches, "avg_ms": round(g.avg_ms, 4), "TFLOP/s": round(g.rate / 1e12, 3),
+                       "frac": round(g.rate / 1e12 / PEAK_BF16_TFLOPS, 4)},
+           "kernels": {n: {"launches": k.launches, "avg_ms": round(k.avg_ms, 4), "total_ms": round(k.total_ms, 3)}
+                       for n, k in ks.items()}}
+    log(f"mixed phase (hardening_x = 0.5): {res['ms_per_step']:.2f} ms/step, {res['TFLOP/s']:.1f} TFLOP/s; "
+        f"sf_gemm {g.rate / 1e12:.1f} TFLOP/s")
+    return res
 
 
 def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:

@@ -142,7 +142,7 @@ def optimize_sparse_model_for_inference(model, use_slorb: bool = False):
                 module.weight.data.copy_(LIN.apply_mask(module.weight.data.contiguous(), hard.contiguous()))
                 module.mode = "dense_forward"
             else:
-                module.mask.data.copy_(hard)
+                module.mask.detach().copy_(hard)  # (bumps the mask's version: a cached projection is rebuilt)
             module._inference_optimized = True
         optimized += 1
     if total:

@@ -116,7 +116,7 @@ def glu_joint_update(gate_module, up_module, step, lambda_mid, sample_idx=None):
     S = K.joint_scores(pg, ops_g, pu, ops_u, s_dtype)
 
     rows, cols = S.shape
-    mask_g, mask_u = gate_module.mask.data, up_module.mask.data
+    mask_g, mask_u = gate_module.mask.detach(), up_module.mask.detach()
     frozen = ops_g.frozen
     p = _joint_params(gate_module, step, rows, cols, mask_g.dtype, frozen is not None, lambda_mid)
     ops_s = K.MaskOperands(weight=S, mask=S, hessian=S)

@@ -16,6 +16,14 @@ from . import _lib as L
 from . import profiling as _prof
 
 
+def _written(*ts) -> None:
+    """Bump the version counter of tensors a kernel wrote in place, as a torch in-place op would: caches
+    keyed on a mask's version (the forward's effective mask) then see the write."""
+    for t in ts:
+        if t is not None:
+            torch.autograd.graph.increment_version(t)
+
+
 def _ws(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
@@ -192,6 +200,7 @@ def update_mask(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, tau: to
                                    L.ptr(tau), L.ptr(flips), L.stream(dev)),
             "sf_update_mask",
         )
+    _written(ops.mask, ops.frozen)
 
 
 @dataclass
@@ -263,6 +272,9 @@ def update_mask_multi(p: L.MaskParams, q: float, jobs: list[MaskJob], stages: in
                                          ws.numel(), L.stream(dev)),
             "sf_update_mask_multi",
         )
+    if stages & L.MULTI_UPDATE:
+        for j in jobs:
+            _written(j.ops.mask, j.ops.frozen)
 
 
 # ---------------------------------------------------------------------------
@@ -328,6 +340,7 @@ def block_fill(bvals: torch.Tensor | None, out: torch.Tensor, bs: int, tau: torc
                                   L.dtype_code(ov_src) if ov_src is not None else L.DT_F32, L.ptr(ov_flags),
                                   L.dtype_code(ov_flags) if ov_flags is not None else L.DT_F32, L.stream(dev)),
             "sf_block_fill")
+    _written(out)
     return out
 
 
@@ -343,6 +356,7 @@ def apply_gate(p: L.MaskParams, G: torch.Tensor, target: torch.Tensor | None, ma
                                       L.dtype_code(mask), L.ptr(frozen),
                                       L.dtype_code(frozen) if frozen is not None else L.DT_F32, int(do_freeze),
                                       L.stream(dev)), "sf_apply_gate")
+    _written(mask, frozen)
 
 
 def freeze_mask(p: L.MaskParams, mask: torch.Tensor, frozen: torch.Tensor | None) -> None:
@@ -350,6 +364,7 @@ def freeze_mask(p: L.MaskParams, mask: torch.Tensor, frozen: torch.Tensor | None
     L.check(L.lib().sf_freeze_mask(ctypes.byref(p), L.ptr(mask), L.dtype_code(mask), L.ptr(frozen),
                                    L.dtype_code(frozen) if frozen is not None else L.DT_F32, L.stream(dev)),
             "sf_freeze_mask")
+    _written(mask, frozen)
 
 
 # ---------------------------------------------------------------------------
@@ -410,6 +425,7 @@ def glu_update_masks(p: L.MaskParams, S: torch.Tensor, gate_mask: torch.Tensor, 
                                             L.ptr(stats), L.ptr(tau), up_hard_kind, up_hard_n, L.ptr(gate_flips),
                                             L.ptr(up_flips), L.stream(dev)),
                 "sf_glu_update_masks")
+    _written(gate_mask, up_mask, gate_frozen)
 
 
 # ---------------------------------------------------------------------------

@@ -427,13 +427,18 @@ def _compute_dtype(x: torch.Tensor, W: torch.Tensor) -> torch.dtype:
 
 
 def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale, P=None, S=None, decay=0.0,
-                  eff=None, hard=None, hard_m=4):
+                  eff=None, hard=None, hard_m=4, cache=None):
     """y = x (W.E.s)^T + (x P^T) S^T + b with STE gradients.
 
     mask_mode: 'none' (E = 1), 'soft' (E = mask) or 'mix' (E = hx*mask + (1-hx)*hard(mask)).
     eff: a precomputed E in the compute dtype (skips the mask pass).
     hard: a precomputed hard(mask) (block hard types); else hard_kind / hard_n / hard_m project
     per group of hard_m along the input dimension.
+    cache: a dict owned by the caller (one per layer) that keeps the mixed-mode E between calls.
+    The soft mask changes only when the mask update writes it, while the reference rebuilds
+    hard(mask) on every forward (legacy/sparse_modeling.py:759-771); E is reused while the mask's
+    storage, its version counter (bumped by every in-place write: torch ops, and the library's mask
+    kernels explicitly) and the projection parameters are unchanged.
     Strided inputs are accepted (made contiguous before the kernels, as F.linear accepts them).
     """
     L.require_device_only(x, weight, bias, mask, P, S, eff, hard)
@@ -450,6 +455,14 @@ def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale
     mask = _opt(mask)
     hard = _opt(hard)
     own_hard_bytes = eff is None and hard is None and mask_mode == "mix" and hx <= 0.0 and scale == 1.0
+    key = None
+    if eff is None and cache is not None and mask_mode == "mix" and hard is None:
+        key = (mask.data_ptr(), mask._version, tuple(mask.shape), mask.dtype, float(hx), float(scale), hard_kind,
+               hard_n, hard_m, dt)
+        if cache.get("key") == key:
+            eff = cache["eff"]
+        else:
+            cache.clear()
     if eff is None and mask_mode != "none":
         if mask_mode == "mix" and hx <= 0.0 and scale == 1.0:
             # E = hard(mask) exactly: staged as a byte and-mask (W * 1 = W, W * 0 = 0)
@@ -459,6 +472,8 @@ def masked_linear(x, weight, bias, mask, mask_mode, hx, hard_kind, hard_n, scale
             eff = effective_mask_given(mask, hard, dt, mask_mode, hx)
         else:
             eff = effective_mask(mask, dt, mask_mode, hx, hard_kind, hard_n, hard_m)
+        if key is not None:
+            cache["key"], cache["eff"] = key, eff
     if mask_mode == "none":
         eff = None
     eff = _opt(eff)
