@@ -81,15 +81,22 @@ __device__ __forceinline__ void adam_element(const AdamArgs& a, float& p, float 
   }
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
 // 4 consecutive elements as f32: one 16-byte (f32) or 8-byte (bf16) access
-// when `vec`, element by element (cnt of them) otherwise.
+// when `vec`, element by element (cnt of them) otherwise.  NT: non-temporal
+// vector accesses (the multi-tensor step streams the whole optimizer arena once).
+template <bool NT = false>
 __device__ __forceinline__ void ld4(const void* b, int64_t i0, int dt, bool vec, int cnt, float o[4]) {
   if (vec) {
     if (dt == SF_DTYPE_F32) {
-      const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(b) + i0);
+      const f32x4_t* q = reinterpret_cast<const f32x4_t*>(static_cast<const float*>(b) + i0);
+      const f32x4_t x = NT ? __builtin_nontemporal_load(q) : *q;
       o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
     } else {
-      const uint2 x = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(b) + i0);
+      const u32x2_t* q = reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(b) + i0);
+      const u32x2_t x = NT ? __builtin_nontemporal_load(q) : *q;
       o[0] = bf16_to_f32(x.x & 0xffffu); o[1] = bf16_to_f32(x.x >> 16);
       o[2] = bf16_to_f32(x.y & 0xffffu); o[3] = bf16_to_f32(x.y >> 16);
     }
@@ -99,15 +106,25 @@ __device__ __forceinline__ void ld4(const void* b, int64_t i0, int dt, bool vec,
   for (int j = 0; j < 4; ++j) o[j] = j < cnt ? load_as_f32(b, i0 + j, dt) : 0.0f;
 }
 
+template <bool NT = false>
 __device__ __forceinline__ void st4(void* b, int64_t i0, int dt, bool vec, int cnt, const float v[4]) {
   if (vec) {
     if (dt == SF_DTYPE_F32) {
-      *reinterpret_cast<float4*>(static_cast<float*>(b) + i0) = make_float4(v[0], v[1], v[2], v[3]);
+      f32x4_t* q = reinterpret_cast<f32x4_t*>(static_cast<float*>(b) + i0);
+      const f32x4_t x{v[0], v[1], v[2], v[3]};
+      if constexpr (NT)
+        __builtin_nontemporal_store(x, q);
+      else
+        *q = x;
     } else {
-      uint2 x;
+      u32x2_t x;
       x.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
       x.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
-      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(b) + i0) = x;
+      u32x2_t* q = reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(b) + i0);
+      if constexpr (NT)
+        __builtin_nontemporal_store(x, q);
+      else
+        *q = x;
     }
     return;
   }
@@ -202,19 +219,19 @@ __global__ void __launch_bounds__(kBlock) adamw_multi_kernel(MultiArgs ma) {
   const int cnt = t.n - i0 >= 4 ? 4 : static_cast<int>(t.n - i0);
   const bool vec = t.aligned && cnt == 4;
   float p[4], g[4], m[4], v[4], x[4] = {0, 0, 0, 0}, mk[4] = {0, 0, 0, 0};
-  ld4(t.p, i0, PD, vec, cnt, p);
-  ld4(t.g, i0, t.g_dt, vec, cnt, g);
-  ld4(t.m, i0, SD, vec, cnt, m);
-  ld4(t.v, i0, SD, vec, cnt, v);
-  if (a.amsgrad) ld4(t.vmax, i0, SD, vec, cnt, x);
-  if (has_mask) ld4(t.mask, i0, t.m_dt, vec, cnt, mk);
+  ld4<true>(t.p, i0, PD, vec, cnt, p);
+  ld4<true>(t.g, i0, t.g_dt, vec, cnt, g);
+  ld4<true>(t.m, i0, SD, vec, cnt, m);
+  ld4<true>(t.v, i0, SD, vec, cnt, v);
+  if (a.amsgrad) ld4<true>(t.vmax, i0, SD, vec, cnt, x);
+  if (has_mask) ld4<true>(t.mask, i0, t.m_dt, vec, cnt, mk);
 #pragma unroll
   for (int j = 0; j < 4; ++j) adam_element<PD, SD>(a, p[j], g[j], m[j], v[j], x[j], mk[j], has_mask);
-  st4(t.p, i0, PD, vec, cnt, p);
-  st4(t.m, i0, SD, vec, cnt, m);
-  st4(t.v, i0, SD, vec, cnt, v);
-  if (a.amsgrad) st4(t.vmax, i0, SD, vec, cnt, x);
-  if (t.pcopy) st4(t.pcopy, i0, SF_DTYPE_BF16, vec, cnt, p);
+  st4<true>(t.p, i0, PD, vec, cnt, p);
+  st4<true>(t.m, i0, SD, vec, cnt, m);
+  st4<true>(t.v, i0, SD, vec, cnt, v);
+  if (a.amsgrad) st4<true>(t.vmax, i0, SD, vec, cnt, x);
+  if (t.pcopy) st4<true>(t.pcopy, i0, SF_DTYPE_BF16, vec, cnt, p);
 }
 
 // Shared scalars of one step from the host hyper-parameters (the reference's Python doubles,

@@ -101,6 +101,32 @@ __device__ __forceinline__ void ld4v(const void* p, int64_t i, int dt, float o[4
   }
 }
 
+// ld4v / the 4-element store as non-temporal accesses (the multi-tensor update streams the whole
+// accumulator arena once; nothing re-reads it before it is evicted).
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void ld4v_nt(const void* p, int64_t i, int dt, float o[4]) {
+  if (dt == SF_DTYPE_F32) {
+    const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(static_cast<const float*>(p) + i));
+    o[0] = x.x; o[1] = x.y; o[2] = x.z; o[3] = x.w;
+  } else {
+    const u32x2_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(static_cast<const uint16_t*>(p) + i));
+    o[0] = bf16_to_f32(x.x & 0xffffu); o[1] = bf16_to_f32(x.x >> 16);
+    o[2] = bf16_to_f32(x.y & 0xffffu); o[3] = bf16_to_f32(x.y >> 16);
+  }
+}
+template <int HD>
+__device__ __forceinline__ void st4v_nt(void* p, int64_t i, const float v[4]) {
+  if (HD == SF_DTYPE_F32) {
+    __builtin_nontemporal_store(f32x4_t{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4_t*>(static_cast<float*>(p) + i));
+  } else {
+    u32x2_t o;
+    o.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+    o.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p) + i));
+  }
+}
+
 template <int HD>
 __global__ void __launch_bounds__(kBlock) hutch_update_vec_kernel(void* __restrict__ H, const void* __restrict__ hvp,
                                                                   int hvp_dtype, int est_dtype, int64_t n4,
@@ -174,28 +200,35 @@ __global__ void __launch_bounds__(kBlock) hutch_update_multi_kernel(HutchArgs a)
   const HutchEntry& e = a.t[i];
   const int64_t nblk = a.first[i + 1] - a.first[i];
   const int64_t stride = nblk * kBlock;
-  for (int64_t j = (b - a.first[i]) * (int64_t)kBlock + threadIdx.x; j < e.n4; j += stride) {
-    float h[4], x[4];
-    ld4v<float>(e.H, 4 * j, HD, h);
-    ld4v<float>(e.hvp, 4 * j, a.hvp_dtype, x);
-    const int64_t i0 = 4 * j;
-    const uint64_t word = counter_hash(e.seed, static_cast<uint64_t>(i0) >> 6);
-    float out[4];
+  // two vectors per iteration, both loaded before either is used
+  constexpr int kU = 2;
+  for (int64_t j = (b - a.first[i]) * (int64_t)kBlock + threadIdx.x; j < e.n4; j += kU * stride) {
+    float h[kU][4], x[kU][4];
+    bool live[kU];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float v = ((word >> ((i0 + q) & 63)) & 1ull) ? 1.0f : -1.0f;
-      float est = rnd(x[q] * v, a.est_dtype);
-      est = est < 0.0f ? 0.0f : est;
-      const float hb = rnd(h[q] * e.beta, HD);
-      out[q] = rnd(fmaf(est, e.omb, hb), HD);
+    for (int u = 0; u < kU; ++u) {
+      const int64_t jj = j + u * stride;
+      live[u] = jj < e.n4;
+      if (live[u]) {
+        ld4v_nt(e.H, 4 * jj, HD, h[u]);
+        ld4v_nt(e.hvp, 4 * jj, a.hvp_dtype, x[u]);
+      }
     }
-    if (HD == SF_DTYPE_F32) {
-      *reinterpret_cast<float4*>(static_cast<float*>(e.H) + i0) = make_float4(out[0], out[1], out[2], out[3]);
-    } else {
-      uint2 o;
-      o.x = static_cast<uint32_t>(f32_to_bf16(out[0])) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
-      o.y = static_cast<uint32_t>(f32_to_bf16(out[2])) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
-      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(e.H) + i0) = o;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (!live[u]) continue;
+      const int64_t i0 = 4 * (j + u * stride);
+      const uint64_t word = counter_hash(e.seed, static_cast<uint64_t>(i0) >> 6);
+      float out[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float v = ((word >> ((i0 + q) & 63)) & 1ull) ? 1.0f : -1.0f;
+        float est = rnd(x[u][q] * v, a.est_dtype);
+        est = est < 0.0f ? 0.0f : est;
+        const float hb = rnd(h[u][q] * e.beta, HD);
+        out[q] = rnd(fmaf(est, e.omb, hb), HD);
+      }
+      st4v_nt<HD>(e.H, i0, out);
     }
   }
 }

@@ -39,14 +39,22 @@ __device__ __forceinline__ float sigmoidf_(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
 // Load up to 4 consecutive elements [i, i + n) as f32; vector path when the
-// group is full and aligned.
-template <int DT>
+// group is full and aligned.  NT: a non-temporal load (the batched arena
+// passes stream gigabytes that nothing re-reads before they are evicted).
+template <int DT, bool NT = false>
 __device__ __forceinline__ void load4(const void* base, int64_t i, int n, bool vec, float out[4]) {
   if (DT == SF_DTYPE_F32) {
     const float* p = static_cast<const float*>(base) + i;
     if (vec) {
-      float4 v = *reinterpret_cast<const float4*>(p);
+      f32x4_t v;
+      if constexpr (NT)
+        v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+      else
+        v = *reinterpret_cast<const f32x4_t*>(p);
       out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
     } else {
 #pragma unroll
@@ -55,7 +63,11 @@ __device__ __forceinline__ void load4(const void* base, int64_t i, int n, bool v
   } else {
     const uint16_t* p = static_cast<const uint16_t*>(base) + i;
     if (vec) {
-      uint2 v = *reinterpret_cast<const uint2*>(p);
+      u32x2_t v;
+      if constexpr (NT)
+        v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+      else
+        v = *reinterpret_cast<const u32x2_t*>(p);
       out[0] = bf16_to_f32(v.x & 0xffff); out[1] = bf16_to_f32(v.x >> 16);
       out[2] = bf16_to_f32(v.y & 0xffff); out[3] = bf16_to_f32(v.y >> 16);
     } else {
@@ -65,12 +77,16 @@ __device__ __forceinline__ void load4(const void* base, int64_t i, int n, bool v
   }
 }
 
-template <int DT>
+template <int DT, bool NT = false>
 __device__ __forceinline__ void store4(void* base, int64_t i, int n, bool vec, const float v[4]) {
   if (DT == SF_DTYPE_F32) {
     float* p = static_cast<float*>(base) + i;
     if (vec) {
-      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+      const f32x4_t o{v[0], v[1], v[2], v[3]};
+      if constexpr (NT)
+        __builtin_nontemporal_store(o, reinterpret_cast<f32x4_t*>(p));
+      else
+        *reinterpret_cast<f32x4_t*>(p) = o;
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -79,10 +95,13 @@ __device__ __forceinline__ void store4(void* base, int64_t i, int n, bool vec, c
   } else {
     uint16_t* p = static_cast<uint16_t*>(base) + i;
     if (vec) {
-      uint2 o;
+      u32x2_t o;
       o.x = static_cast<uint32_t>(f32_to_bf16(v[0])) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
       o.y = static_cast<uint32_t>(f32_to_bf16(v[2])) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
-      *reinterpret_cast<uint2*>(p) = o;
+      if constexpr (NT)
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x2_t*>(p));
+      else
+        *reinterpret_cast<u32x2_t*>(p) = o;
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -182,13 +201,13 @@ struct GroupOps {
   float w[4], h[4], a[4];
 };
 
-template <int WD, int HD>
+template <int WD, int HD, bool NT = false>
 __device__ __forceinline__ void load_group_ops(const ScoreSpec& s, const void* W, const void* H, const void* aux,
                                                const Group& g, bool vec, GroupOps& o) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) o.h[j] = o.a[j] = 0.0f;
-  load4<WD>(W, g.elem, g.n, vec, o.w);
-  if (H) load4<HD>(H, g.elem, g.n, vec, o.h);
+  load4<WD, NT>(W, g.elem, g.n, vec, o.w);
+  if (H) load4<HD, NT>(H, g.elem, g.n, vec, o.h);
   if (aux) {
     if (s.metric == SF_METRIC_WANDA)
       load4_any(aux, s.aux_dtype, g.col, g.n, vec, o.a);  // scaler_row [cols]
@@ -387,7 +406,8 @@ __device__ __forceinline__ void block_sum2_f64(double a, double b, double* out_a
 // Partial sums of workgroup `blk` of the kStatsGrid-workgroup grid over one
 // layer.  VEC: every group full and vector-loadable (as in update_mask_kernel).
 // RATIO: the metric is hessian_ratio (|W| / sqrt(H + eps), no aux operand), fixed at compile time.
-template <int WD, int HD, bool VEC, bool RATIO = false>
+// NT: W and H through non-temporal loads (the batched arena pass).
+template <int WD, int HD, bool VEC, bool RATIO = false, bool NT = false>
 __device__ __forceinline__ void stats_partial_block(const ScoreSpec& s_in, const void* __restrict__ W,
                                                     const void* __restrict__ H, const void* __restrict__ aux_in,
                                                     int64_t cols, int64_t groups, int64_t gpr, bool vec,
@@ -427,8 +447,8 @@ __device__ __forceinline__ void stats_partial_block(const ScoreSpec& s_in, const
         w.next();
       }
       GroupOps o0, o1;
-      load_group_ops<WD, HD>(s, W, H, aux, g0, true, o0);
-      if (two) load_group_ops<WD, HD>(s, W, H, aux, g1, true, o1);
+      load_group_ops<WD, HD, NT>(s, W, H, aux, g0, true, o0);
+      if (two) load_group_ops<WD, HD, NT>(s, W, H, aux, g1, true, o1);
       add(g0, o0);
       if (two) add(g1, o1);
     }
@@ -971,7 +991,8 @@ int fast_kind(const UpdateSpec& us) {
 // VEC: cols % 4 == 0 and every operand 16-byte aligned, so every group is a
 // full, vector-loadable group of 4 (known at compile time: no tail branches).
 // Workgroup `blk` of a grid of `nblk` over one layer.
-template <int WD, int HD, int MD, int SD, bool VEC, int FAST = kFastNone>
+// NT: W, H and the mask through non-temporal loads and stores (the batched arena pass).
+template <int WD, int HD, int MD, int SD, bool VEC, int FAST = kFastNone, bool NT = false>
 __device__ __forceinline__ void update_mask_block(const UpdateSpec& us_in, const void* __restrict__ W,
                                                   const void* __restrict__ H, const void* __restrict__ aux,
                                                   void* __restrict__ mask, void* __restrict__ frozen,
@@ -984,8 +1005,8 @@ __device__ __forceinline__ void update_mask_block(const UpdateSpec& us_in, const
   const float tau = tau_p ? *tau_p : 0.0f;
   int64_t cnt = 0;
   auto load = [&](const Group& g, bool v, GroupOps& o, float mp[4], float fz[4]) {
-    load_group_ops<WD, HD>(gs.s, W, H, aux, g, v, o);
-    load4<MD>(mask, g.elem, g.n, v, mp);
+    load_group_ops<WD, HD, NT>(gs.s, W, H, aux, g, v, o);
+    load4<MD, NT>(mask, g.elem, g.n, v, mp);
 #pragma unroll
     for (int j = 0; j < 4; ++j) fz[j] = 0.0f;
     if (gs.has_frozen) load4_any(frozen, gs.frozen_dtype, g.elem, g.n, v, fz);
@@ -997,7 +1018,7 @@ __device__ __forceinline__ void update_mask_block(const UpdateSpec& us_in, const
     pull_and_push<MD, SD>(us, g, mp, G);
     ema_of<MD>(us, mp, G, mn);
     if (us.apply_freeze) freeze_group(us, g, v, mn, fz, frozen);
-    store4<MD>(mask, g.elem, g.n, v, mn);
+    store4<MD, NT>(mask, g.elem, g.n, v, mn);
     if (flips) cnt += flips_of(mp, mn, g, us.hard_kind, us.hard_n);
   };
   GroupWalk w(groups, cols, gpr, blk, nblk);
@@ -1112,7 +1133,7 @@ __global__ void __launch_bounds__(kBlock) stats_partial_multi_kernel(MultiArgs a
   const int l = b / kStatsGrid, blk = b - l * kStatsGrid;
   const MultiLayer& L = a.l[l];
   const int64_t gpr = ceil_div(L.cols, 4);
-  stats_partial_block<WD, HD, VEC, RATIO>(a.us.gs.s, L.W, L.H, L.aux, L.cols, L.rows * gpr, gpr, L.vec != 0,
+  stats_partial_block<WD, HD, VEC, RATIO, true>(a.us.gs.s, L.W, L.H, L.aux, L.cols, L.rows * gpr, gpr, L.vec != 0,
                                           partial + (int64_t)l * 2 * kStatsGrid, blk);
 }
 
@@ -1155,7 +1176,7 @@ __global__ void __launch_bounds__(kBlock) update_mask_multi_kernel(MultiArgs a) 
   const int l = multi_layer_of(a, blockIdx.x);
   const MultiLayer& L = a.l[l];
   const int64_t gpr = ceil_div(L.cols, 4);
-  update_mask_block<WD, HD, MD, SD, VEC, FAST>(a.us, L.W, L.H, L.aux, L.mask, L.frozen, L.stats, L.tau, L.cols,
+  update_mask_block<WD, HD, MD, SD, VEC, FAST, true>(a.us, L.W, L.H, L.aux, L.mask, L.frozen, L.stats, L.tau, L.cols,
                                                L.rows * gpr, gpr, L.vec != 0, L.flips, blockIdx.x - a.first[l],
                                                L.nblk);
 }
