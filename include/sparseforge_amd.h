@@ -529,6 +529,14 @@ int sf_bsr_fill(const void* W, int w_dtype, const void* mask, int mask_dtype, in
 int sf_bsr_block_map(const int32_t* row_ptr, const int32_t* col_idx, int64_t nbr, int64_t nbc, int32_t* block_map,
                      void* stream);
 
+/* The transposed block-sparse matrix, for the input gradient x_grad = dy . (W . M)
+ * (the reference's BlockSparseLinear is forward-only, legacy/triton_block_sparse.py:290-470;
+ * its CSR layout is :86-101): blocks_t[b] = blocks[b]^T for b < nblocks (same order,
+ * so the indices stay valid) and block_map_t [nbc][nbr] = block_map^T.  The
+ * block-sparse GEMM then multiplies by W^T with the forward's kernel. */
+int sf_bsr_transpose(const void* blocks, int dtype, int64_t nblocks, const int32_t* block_map, int64_t nbr,
+                     int64_t nbc, void* blocks_t, int32_t* block_map_t, void* stream);
+
 /* ---- mask-aware AdamW (AdamW.step, legacy/adamw.py:65-176) ------------- */
 typedef struct sf_adamw_params {
   double lr, weight_decay, beta1, beta2, eps;

@@ -274,6 +274,7 @@ SIGNATURES = {
     "sf_bsr_scan": (_I, [_P, _I64, _P, _P]),
     "sf_bsr_fill": (_I, [_P, _I, _P, _I, _I64, _I64, _I, _P, _P, _P, _P, _I, _P, _P]),
     "sf_bsr_block_map": (_I, [_P, _P, _I64, _I64, _P, _P]),
+    "sf_bsr_transpose": (_I, [_P, _I, _I64, _P, _I64, _I64, _P, _P, _P]),
     "sf_rademacher": (_I, [_P, _I, _I64, ctypes.c_uint64, _P]),
     "sf_rademacher_dot_workspace_size": (_SZ, []),
     "sf_rademacher_dot": (_I, [_P, _I, _P, _I, _I64, ctypes.c_uint64, _P, _P, _SZ, _P]),

@@ -94,13 +94,33 @@ def get_sparsity_info(block_row_indices: torch.Tensor, num_block_cols: int) -> d
 # ---------------------------------------------------------------------------
 # products
 # ---------------------------------------------------------------------------
+def bsr_transpose(blocks: torch.Tensor, bmap: torch.Tensor):
+    """(blocks_t, bmap_t) of W^T: every block transposed (same order, so the indices stay valid) and the
+    map transposed to [nbc, nbr]."""
+    dev = L.require_device(blocks, bmap)
+    nbr, nbc = bmap.shape
+    bt = torch.empty_like(blocks)
+    mt = torch.empty(nbc, nbr, dtype=torch.int32, device=dev)
+    with _prof.region("sf_bsr_transpose", 2 * blocks.numel() * blocks.element_size() + 8 * bmap.numel(), "B", dev):
+        L.check(L.lib().sf_bsr_transpose(L.ptr(blocks), L.dtype_code(blocks), blocks.shape[0], L.ptr(bmap), nbr, nbc,
+                                         L.ptr(bt), L.ptr(mt), L.stream(dev)), "sf_bsr_transpose")
+    return bt, mt
+
+
 def _bsr_gemm(A: torch.Tensor, blocks: torch.Tensor, bmap: torch.Tensor, n_out: int, transposed: bool,
               out_dtype: torch.dtype) -> torch.Tensor:
-    """A [M, K] . B^T with B = W (transposed=False, W [n_out, K]) or B = W^T (True, W [K, n_out])."""
+    """A [M, K] . B^T with B = W (transposed=False, W [n_out, K]) or B = W^T (True, W [K, n_out]).
+
+    bf16 products whose K is a multiple of 64 run the exact-skip kernel; the input gradient
+    (transposed) then multiplies by the transposed block matrix (sf_bsr_transpose) with it."""
     dev = L.require_device(A, blocks, bmap)
     if blocks.dtype != A.dtype:
         raise TypeError(f"bsr: blocks dtype {blocks.dtype} != activation dtype {A.dtype}")
     M, K = A.shape
+    if transposed and A.dtype == torch.bfloat16 and out_dtype == torch.bfloat16 and K % 64 == 0 and \
+            tuple(bmap.shape) == (K // BLOCK, n_out // BLOCK):
+        bt, mt = bsr_transpose(blocks, bmap)
+        return _bsr_gemm(A, bt, mt, n_out, False, out_dtype)
     C = torch.empty(M, n_out, dtype=out_dtype, device=dev)
     d = L.GemmDesc()
     d.dtype = L.dtype_code(A)

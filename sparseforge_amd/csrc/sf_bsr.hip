@@ -16,6 +16,7 @@
 //   sf_bsr_scan    row_ptr = exclusive scan of the counts  (one workgroup)
 //   sf_bsr_fill    col_idx, blocks, block_map              (grid: block rows)
 //   sf_bsr_block_map  block_map from any row_ptr / col_idx
+//   sf_bsr_transpose  the transposed matrix: every block transposed, map [nbc, nbr]
 
 #include "sf_common.hpp"
 
@@ -149,6 +150,31 @@ __global__ void __launch_bounds__(kBlock) bsr_map_fill_kernel(const int32_t* row
 
 bool dt_ok(int d) { return d == SF_DTYPE_F32 || d == SF_DTYPE_BF16; }
 
+// Every block transposed in place order: out[b][c][r] = in[b][r][c] (element size es bytes).
+__global__ void __launch_bounds__(kBlock) bsr_transpose_blocks_kernel(const unsigned char* __restrict__ in,
+                                                                      unsigned char* __restrict__ out, int64_t n,
+                                                                      int es) {
+  for (int64_t e = blockIdx.x * (int64_t)kBlock + threadIdx.x; e < n * 256; e += (int64_t)gridDim.x * kBlock) {
+    const int64_t b = e >> 8;
+    const int w = static_cast<int>(e & 255), r = w >> 4, c = w & 15;
+    const unsigned char* src = in + (b * 256 + r * 16 + c) * es;
+    unsigned char* dst = out + (b * 256 + c * 16 + r) * es;
+    if (es == 2)
+      *reinterpret_cast<uint16_t*>(dst) = *reinterpret_cast<const uint16_t*>(src);
+    else
+      *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
+  }
+}
+
+// map_t[c][r] = map[r][c].
+__global__ void __launch_bounds__(kBlock) bsr_transpose_map_kernel(const int32_t* __restrict__ map, int64_t nbr,
+                                                                   int64_t nbc, int32_t* __restrict__ map_t) {
+  for (int64_t e = blockIdx.x * (int64_t)kBlock + threadIdx.x; e < nbr * nbc; e += (int64_t)gridDim.x * kBlock) {
+    const int64_t r = e / nbc, c = e - r * nbc;
+    map_t[c * nbr + r] = map[e];
+  }
+}
+
 }  // namespace
 }  // namespace sf
 
@@ -198,4 +224,22 @@ extern "C" int sf_bsr_block_map(const int32_t* row_ptr, const int32_t* col_idx, 
   bsr_map_clear_kernel<<<elementwise_grid(nbr * nbc, kBlock), kBlock, 0, st>>>(block_map, nbr * nbc);
   bsr_map_fill_kernel<<<static_cast<unsigned>(nbr), kBlock, 0, st>>>(row_ptr, col_idx, nbr, nbc, block_map);
   return launch_status("sf_bsr_block_map");
+}
+
+extern "C" int sf_bsr_transpose(const void* blocks, int dtype, int64_t nblocks, const int32_t* block_map, int64_t nbr,
+                                int64_t nbc, void* blocks_t, int32_t* block_map_t, void* stream) {
+  SF_CHECK_ARG(nblocks >= 0 && nbr >= 0 && nbc >= 0, "bad shape");
+  SF_CHECK_ARG(dtype == SF_DTYPE_F32 || dtype == SF_DTYPE_BF16, "bad dtype %d", dtype);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (nblocks > 0) {
+    SF_CHECK_ARG(blocks && blocks_t, "null tensor");
+    bsr_transpose_blocks_kernel<<<elementwise_grid(nblocks * 256, kBlock), kBlock, 0, st>>>(
+        static_cast<const unsigned char*>(blocks), static_cast<unsigned char*>(blocks_t), nblocks,
+        dtype == SF_DTYPE_F32 ? 4 : 2);
+  }
+  if (nbr > 0 && nbc > 0) {
+    SF_CHECK_ARG(block_map && block_map_t, "null tensor");
+    bsr_transpose_map_kernel<<<elementwise_grid(nbr * nbc, kBlock), kBlock, 0, st>>>(block_map, nbr, nbc, block_map_t);
+  }
+  return launch_status("sf_bsr_transpose");
 }

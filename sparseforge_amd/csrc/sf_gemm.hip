@@ -1772,6 +1772,251 @@ int launch_bsr_kernel(K kern, bool& attr, const GemmArgs& g, hipStream_t st, con
 }
 
 // ---------------------------------------------------------------------------
+// Block-sparse-16 product with exact block skipping (bf16 operands and output):
+//   C[T, R] = X[T, K] . S^T,   S [R, K] held as 16 x 16 blocks
+// S's blocks come from `blocks` ([n][16][16], row-major) through `map`
+// ([R / 16][K / 16]: block index, negative for an absent block).  The forward
+// passes W (R = out, K = in) with the index convert_to_block_sparse builds;
+// the input gradient passes the transposed matrix (sf_bsr_transpose: every
+// block transposed, the map transposed), so one kernel serves both.
+//
+// v_mfma_f32_16x16x32_bf16 multiplies one block row (16 rows of S) by 16
+// tokens over 32 k, i.e. two adjacent k-blocks; it is skipped when both are
+// absent (a pair with one absent block multiplies zeros for that half).  Its
+// S operand (lane l: row l % 16, k 8 (l / 16) .. + 8, so lanes 0-31 read the
+// pair's first block and lanes 32-63 its second) is 16 contiguous bytes of a
+// stored block row, loaded straight from the blocks array into registers:
+// one instruction reads two whole 512-byte blocks, an absent block reads
+// zeros through an out-of-range offset.  Only X goes through LDS: stages of
+// 128 tokens x 64 k (4 k-blocks), double buffered, staged through registers
+// (every load is a compiler-tracked one, so its waits are exact), shared by
+// the 4 waves of the workgroup.  Wave w owns rows [128 w, 128 w + 128) of
+// the workgroup's 512 (8 block rows) and all 128 tokens: 8 x 8 accumulator
+// blocks of 16 x 16 (256 AGPRs).  The block map is read with scalar loads,
+// one 16-byte row segment per block row and stage; the stage's S fragments
+// are loaded one stage ahead.
+// ---------------------------------------------------------------------------
+constexpr int kBsWaveRows = 128;                   // rows of S per wave (8 block rows)
+constexpr int kBsRows = 4 * kBsWaveRows;           // rows of S per workgroup
+constexpr int kBsTok = 128;                        // tokens per workgroup (8 column blocks of 16)
+constexpr int kBsStageK = 64;                      // k per stage: 4 k-blocks, 2 MFMA k-steps
+constexpr uint32_t kBsXBuf = kBsTok * 128u;        // one X stage: 128 token rows x 128 B, chunk-swizzled
+constexpr int kBsEpiPitch = kBsWaveRows * 2 + 16;  // bytes per token row of a wave's bf16 output staging
+
+struct Bs16Args {
+  const uint16_t* X;
+  int64_t ldx, T, K;
+  const uint16_t* blocks;
+  const int32_t* map;
+  int64_t nrb, nkb;
+  uint16_t* C;
+  int64_t ldc, R;
+  int64_t tiles_t, tiles_r;
+};
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int bs_swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+__global__ void __launch_bounds__(kThreads, 1) bsr16_kernel(Bs16Args g) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  int64_t tt, tr;
+  tile_coords(blockIdx.x, g.tiles_t, g.tiles_r, tt, tr);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t t0 = tt * kBsTok;
+  const int64_t rb0 = (tr * kBsRows + wave * kBsWaveRows) / 16;  // the wave's first block row
+  const int64_t nk = g.K / kBsStageK;
+  const Rsrc rx = make_rsrc(g.X, g.T * g.ldx * 2);
+  const Rsrc rbk = make_rsrc(g.blocks, g.nrb * g.nkb * 512);
+
+  // X copy: thread t moves 16-byte chunk t % 8 of token rows 32 i + t / 8, i = 0..3
+  const int crow = threadIdx.x >> 3, cch = threadIdx.x & 7;
+  uint32_t xoff[4], xlds[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 32 * i + crow;
+    xoff[i] = t0 + row < g.T ? (uint32_t)(((t0 + row) * g.ldx + cch * 8) * 2) : kOob;
+    xlds[i] = (uint32_t)(row * 128 + ((cch ^ bs_swz(row)) << 4));
+  }
+  // X fragment of k-step p, column block t: token row 16 t + lane % 16, chunk 4 p + lane / 16
+  uint32_t boff[2][8];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int row = 16 * t + (lane & 15);
+      boff[p][t] = (uint32_t)(row * 128 + (((4 * p + (lane >> 4)) ^ bs_swz(row)) << 4));
+    }
+  // S fragment: row lane % 16 of the block, 16-byte half (lane / 16) % 2; lanes >= 32 take the second block
+  const uint32_t aoff = (uint32_t)((lane & 15) * 32 + ((lane >> 4) & 1) * 16);
+  const bool second = lane >= 32;
+
+  f32x4_t acc[8][8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[j][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Pipeline (every load compiler-tracked): at the start of stage s the X rows of stage s + 2, the
+  // S fragments of stage s + 1 (from the block indices read a stage earlier) and the block indices
+  // of stage s + 2 are loaded; the stage's MFMAs follow; at its end the X rows of stage s + 1
+  // (loaded two stages earlier) are written to the other LDS buffer, and one barrier publishes them.
+  // Lane l reads, per block row j and k-step p, the index of the block its half of the fragment
+  // covers (block 2 p + (l >= 32) of the stage), so the skip test is a ballot.
+  V4 xr[2][4];           // X rows of stage k in xr[k % 2]
+  int32_t mv[2];         // block indices of stage k in mv[k % 2]: lane 4 j + kb holds block row j's
+                         // entry kb of the stage (lanes 32-63 unused)
+  bf16x8_t af[2][8][2];  // S fragments of stage k in af[k % 2]
+  uint32_t live[2][8];   // per stage set and block row: bit p set when k-step p has a block
+  const int mj = (lane >> 2) & 7, mk = lane & 3;
+  auto load_map = [&](auto set_c, int64_t s) {
+    constexpr int set = decltype(set_c)::value;
+    const int64_t r = rb0 + mj;
+    mv[set] = (lane < 32 && r < g.nrb) ? g.map[r * g.nkb + s * 4 + mk] : -1;
+  };
+  auto load_a = [&](auto set_c) {  // the fragments of the stage whose indices mv[set] holds
+    constexpr int set = decltype(set_c)::value;
+    const int32_t m = mv[set];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e0 = __builtin_amdgcn_readlane(m, 4 * j), e1 = __builtin_amdgcn_readlane(m, 4 * j + 1);
+      const int e2 = __builtin_amdgcn_readlane(m, 4 * j + 2), e3 = __builtin_amdgcn_readlane(m, 4 * j + 3);
+      live[set][j] = ((e0 >= 0 || e1 >= 0) ? 1u : 0u) | ((e2 >= 0 || e3 >= 0) ? 2u : 0u);
+      const int b0 = second ? e1 : e0, b1 = second ? e3 : e2;
+      af[set][j][0] = __builtin_bit_cast(bf16x8_t, bload(rbk, b0 >= 0 ? (uint32_t)b0 * 512u + aoff : kOob, 0));
+      af[set][j][1] = __builtin_bit_cast(bf16x8_t, bload(rbk, b1 >= 0 ? (uint32_t)b1 * 512u + aoff : kOob, 0));
+    }
+  };
+  auto load_x = [&](auto set_c, int64_t s) {
+    constexpr int set = decltype(set_c)::value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xr[set][i] = bload(rx, xoff[i], (uint32_t)(s * kBsStageK * 2));
+  };
+  auto store_x = [&](auto set_c, int buf) {
+    constexpr int set = decltype(set_c)::value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint4 v;
+      v.x = xr[set][i].w[0];
+      v.y = xr[set][i].w[1];
+      v.z = xr[set][i].w[2];
+      v.w = xr[set][i].w[3];
+      *reinterpret_cast<uint4*>(smem + buf * kBsXBuf + xlds[i]) = v;
+    }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  // stage s with set = s % 2 (compile time)
+  auto stage = [&](auto set_c, int64_t s) {
+    constexpr int set = decltype(set_c)::value;
+    using Other = std::integral_constant<int, set ^ 1>;
+    // Unconditional (past the last stage they re-read it): the compiler's wait counts then stay exact.
+    // The fragments of stage s + 1 first (their indices, mv[(s + 1) % 2], were read two stages ago),
+    // then X of stage s + 2, then the indices of stage s + 3 into the slot just consumed.
+    const int64_t s2 = s + 2 < nk ? s + 2 : nk - 1, s3 = s + 3 < nk ? s + 3 : nk - 1;
+    load_a(Other{});
+    load_x(set_c, s2);
+    load_map(Other{}, s3);
+    const unsigned char* xb = smem + set * kBsXBuf;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      bf16x8_t bf[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) bf[t] = *reinterpret_cast<const bf16x8_t*>(xb + boff[p][t]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (live[set][j] & (1u << p)) {
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[set][j][p], bf[t], acc[j][t], 0, 0, 0);
+        }
+      }
+    }
+    store_x(Other{}, set ^ 1);  // X rows of stage s + 1, loaded at the start of stage s - 1 (past the end: unread)
+    __syncthreads();
+  };
+  // prologue: stage 0's rows in LDS and fragments in registers, stage 1's rows and indices loading
+  load_map(S0{}, 0);
+  load_x(S0{}, 0);
+  load_a(S0{});
+  store_x(S0{}, 0);
+  load_map(S1{}, nk > 1 ? 1 : 0);
+  load_x(S1{}, nk > 1 ? 1 : 0);
+  load_map(S0{}, nk > 2 ? 2 : nk - 1);
+  __syncthreads();
+  int64_t s = 0;
+  for (; s + 1 < nk; s += 2) {
+    stage(S0{}, s);
+    stage(S1{}, s + 1);
+  }
+  if (s < nk) stage(S0{}, s);
+
+  // Epilogue: lane l holds rows 16 j + 4 (l / 16) + e of token 16 t + l % 16.  Each wave stages its
+  // 128 x 128 bf16 result token-major in LDS (the X buffers are free: the last stage ended in a
+  // barrier), then writes 16 bytes (8 rows of one token) per lane.
+  unsigned char* ep = smem + wave * (kBsTok * kBsEpiPitch);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int tok = 16 * t + (lane & 15), row = 16 * j + 4 * (lane >> 4);
+      uint2 v;
+      v.x = pack2(acc[j][t][0], acc[j][t][1]);
+      v.y = pack2(acc[j][t][2], acc[j][t][3]);
+      *reinterpret_cast<uint2*>(ep + tok * kBsEpiPitch + row * 2) = v;
+    }
+  __syncthreads();
+  const int64_t r0 = tr * kBsRows + wave * kBsWaveRows;
+#pragma unroll 4
+  for (int it = 0; it < kBsTok * 16 / 64; ++it) {
+    const int id = it * 64 + lane, tok = id >> 4, cc = id & 15;
+    const int64_t trow = t0 + tok, col = r0 + cc * 8;
+    if (trow < g.T && col < g.R)
+      *reinterpret_cast<uint4*>(g.C + trow * g.ldc + col) =
+          *reinterpret_cast<const uint4*>(ep + tok * kBsEpiPitch + cc * 16);
+  }
+}
+
+constexpr size_t smem_bytes_bs16() {
+  constexpr size_t ops = 2ull * kBsXBuf, epi = 4ull * kBsTok * kBsEpiPitch;
+  return ops > epi ? ops : epi;
+}
+
+// The block-sparse products bsr16_kernel takes: bf16 in and out, K a multiple of 64 (whole stages, the
+// map's row segments 16-byte aligned), C 16-byte aligned rows, no epilogue operand.
+bool bs16_ok(const GemmArgs& g) {
+  return g.K1 % kBsStageK == 0 && g.c_dtype == SF_DTYPE_BF16 && !g.bias && !g.emask && !g.dw && !g.accumulate &&
+         !g.c_blocks && g.c_aligned && g.ldc % 8 == 0 && g.N % 16 == 0 && g.b_map_rows * 16 == g.N &&
+         g.b_map_cols * 16 == g.K1 && (reinterpret_cast<uintptr_t>(g.b_map) & 15u) == 0 && g.A2 == nullptr;
+}
+
+int launch_bs16(const GemmArgs& g, hipStream_t st) {
+  static bool attr = false;
+  const size_t smem = smem_bytes_bs16();
+  if (int rc = set_smem(bsr16_kernel, smem, attr)) return rc;
+  Bs16Args a;
+  a.X = static_cast<const uint16_t*>(g.A1);
+  a.ldx = g.lda1;
+  a.T = g.M;
+  a.K = g.K1;
+  a.blocks = static_cast<const uint16_t*>(g.B1);
+  a.map = g.b_map;
+  a.nrb = g.b_map_rows;
+  a.nkb = g.b_map_cols;
+  a.C = static_cast<uint16_t*>(g.C);
+  a.ldc = g.ldc;
+  a.R = g.N;
+  a.tiles_t = ceil_div(g.M, kBsTok);
+  a.tiles_r = ceil_div(g.N, kBsRows);
+  const int64_t tiles = a.tiles_t * a.tiles_r;
+  if (tiles == 0) return SF_OK;
+  SF_CHECK_ARG(tiles < (1ll << 31), "GEMM grid too large");
+  hipLaunchKernelGGL(bsr16_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), smem, st, a);
+  return launch_status("sf_gemm (block-sparse, exact skip)");
+}
+
+// ---------------------------------------------------------------------------
 // Skinny products: one side of C at most 64 wide (the SLoRB terms z = x P^T,
 // dz = dy S, dP = dz^T x, dS = dy^T z at rank 64).  On the 256 x 256 tile
 // three quarters of every MFMA would multiply padding, so these run on a
@@ -2035,6 +2280,7 @@ int dispatch_layouts(const sf_gemm_desc* d, const GemmArgs& g, hipStream_t st) {
   if constexpr (MASK == kMaskNone) {
     if constexpr (sizeof(T) == 2) {
       if (d->b_format == SF_BFMT_BSR16 && g.splits == 1) {
+        if (d->b_layout == SF_LAYOUT_K && bs16_ok(g)) return launch_bs16(g, st);
         static bool attr_f = false, attr_t = false;
         return d->b_layout == SF_LAYOUT_K
                    ? launch_bsr_kernel(bsr_mm_kernel<0>, attr_f, g, st, "sf_gemm (block-sparse)")

@@ -175,3 +175,27 @@ def test_rejects_bad_operands(cuda_device):
         bs.convert_to_block_sparse(torch.ones(30, 32, device=cuda_device), torch.ones(30, 32, device=cuda_device))
     with pytest.raises(ValueError):
         bs.BlockSparseLinear(blocks[:1], rp, ci, 32, 32)  # fewer blocks than the index lists
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_bsr_transpose(cuda_device, dtype):
+    """sf_bsr_transpose: every block transposed in place order and the map transposed, so the pair is the
+    block-sparse form of (W . M)^T (the input gradient's operand)."""
+    bs = _bs()
+    g = torch.Generator().manual_seed(11)
+    out_f, in_f = 160, 96
+    W = torch.randn(out_f, in_f, generator=g).to(dtype)
+    M = _block_mask(g, out_f, in_f, 0.4).to(dtype)
+    blocks, rp, ci, bmap = bs.convert_to_block_sparse(W.to(cuda_device), M.to(cuda_device), return_block_map=True)
+    bt, mt = bs.bsr_transpose(blocks, bmap)
+    assert torch.equal(mt, bmap.t().contiguous())
+    assert torch.equal(bt, blocks.transpose(1, 2).contiguous())
+    Wt, Mt = (W * M).t().contiguous(), M.t().contiguous()
+    b2, _rp2, _ci2, m2 = bs.convert_to_block_sparse(Wt.to(cuda_device), Mt.to(cuda_device), return_block_map=True)
+    # the transposed pair describes the same matrix as converting (W . M)^T directly
+    dense = torch.zeros(in_f // 16, out_f // 16, 16, 16, dtype=dtype, device=cuda_device)
+    dense2 = torch.zeros_like(dense)
+    kept = mt >= 0
+    dense[kept] = bt[mt[kept].long()]
+    dense2[m2 >= 0] = b2[m2[m2 >= 0].long()]
+    assert torch.equal(dense, dense2)
