@@ -89,23 +89,39 @@ def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tens
 
 
 class _BMM(torch.autograd.Function):
-    """torch.bmm(a, b) differentiable any number of times, with contiguous operands in every product.
+    """torch.bmm(a, b) (+ a constant bias, broadcast over the batch) differentiable any number of times,
+    with contiguous operands in every product.
 
-    The derivatives are products of the same kind (grad_a = g b^T, grad_b = a^T g), so the forward,
-    the backward and the Hutchinson double backward all multiply contiguous tensors."""
+    The derivatives are products of the same kind, so the forward, the backward and the Hutchinson
+    double backward all multiply contiguous tensors.  Each derivative takes the form whose transposed
+    copies are smaller: grad_a = g b^T copies b^T, (b g^T)^T copies g^T and the result; grad_b = a^T g
+    copies a^T, (g^T a)^T copies g^T and the result.  For p v (p [S, S], v [S, D]) that keeps the
+    value gradient from transposing the S x S probabilities."""
 
     @staticmethod
-    def forward(ctx, a, b):
+    def forward(ctx, a, b, bias=None):
         ctx.save_for_backward(a, b)
+        if bias is not None:
+            return torch.baddbmm(bias, a.contiguous(), b.contiguous())
         return torch.bmm(a.contiguous(), b.contiguous())
 
     @staticmethod
     def backward(ctx, g):
         a, b = ctx.saved_tensors
         g = g.to(a.dtype)
-        ga = _BMM.apply(g, b.transpose(1, 2)) if ctx.needs_input_grad[0] else None
-        gb = _BMM.apply(a.transpose(1, 2), g) if ctx.needs_input_grad[1] else None
-        return ga, gb
+        n = lambda t: t.shape[1] * t.shape[2]  # noqa: E731
+        ga = gb = None
+        if ctx.needs_input_grad[0]:
+            if n(b) <= n(g) + n(a):
+                ga = _BMM.apply(g, b.transpose(1, 2))
+            else:
+                ga = _BMM.apply(b, g.transpose(1, 2)).transpose(1, 2)
+        if ctx.needs_input_grad[1]:
+            if n(a) <= n(g) + n(b):
+                gb = _BMM.apply(a.transpose(1, 2), g)
+            else:
+                gb = _BMM.apply(g.transpose(1, 2), a).transpose(1, 2)
+        return ga, gb, None
 
 
 _CAUSAL_BIAS: dict = {}
@@ -141,10 +157,13 @@ def causal_attention(q, k, v, cos, sin) -> torch.Tensor:
             qh = qh * scale
         qh = qh.reshape(B * H, S, D)
         kt = kh.transpose(-2, -1).reshape(B * H, D, S)
-        scores = _BMM.apply(qh, kt)                                               # [B H, S, S]
-        if not exact:
-            scores = scores * scale
-        p = torch.softmax(scores + causal_bias(S, q.device, dt), dim=-1, dtype=torch.float32).to(dt)
+        if exact:
+            # the mask rides in the product: rnd(qk + 0) = rnd(qk) and qk + -inf = -inf, the bits of the
+            # product followed by the masked add
+            scores = _BMM.apply(qh, kt, causal_bias(S, q.device, dt))              # [B H, S, S]
+        else:
+            scores = _BMM.apply(qh, kt) * scale + causal_bias(S, q.device, dt)
+        p = torch.softmax(scores, dim=-1, dtype=torch.float32).to(dt)
         out = _BMM.apply(p, v.transpose(1, 2).reshape(B * H, S, D))              # [B H, S, D]
     return out.view(B, H, S, D).transpose(1, 2).reshape(B, S, H * D)
 
