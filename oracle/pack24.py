@@ -12,6 +12,9 @@ column order (groups keeping fewer are padded with zeros at their lowest
 unused columns); idx u32 [out / 32][in / 64][2][32]: word (rb, q, h, r) holds
 the 2-bit in-group columns of the 8 kept values of row rb * 32 + r, columns
 [64 q + 16 h, +16) in bits 0..15 and [64 q + 32 + 16 h, +16) in bits 16..31.
+pack() / unpack() keep vals in that row order; the device stores the same
+values in the sparse MFMA's fragment order, tile_vals() (pinned by the
+round trip through the device pack and unpack).
 """
 from __future__ import annotations
 
@@ -69,3 +72,22 @@ def unpack(vals: np.ndarray, idx: np.ndarray, out_f: int, in_f: int) -> np.ndarr
             rows = np.repeat(np.arange(out_f)[:, None], in_f // 64, axis=1)
             np.add.at(W, (rows, col), v[:, np.arange(in_f // 64) * 4 + sub, j])
     return W
+
+
+def tile_vals(vals: np.ndarray) -> np.ndarray:
+    """vals [out, in / 2] in row order -> the device order (same shape, flattened): the 8 values of
+    16-column chunk 4 q + 2 kk + h of row 32 rb + r at [rb][q][kk][h * 32 + r][8]."""
+    vals = np.asarray(vals)
+    out_f, half = vals.shape
+    nk = half // 32
+    v = vals.reshape(out_f // 32, 32, nk, 2, 2, 8)  # rb, r, q, kk, h, value
+    return np.ascontiguousarray(v.transpose(0, 2, 3, 4, 1, 5)).reshape(out_f, half)
+
+
+def untile_vals(tiled: np.ndarray) -> np.ndarray:
+    """The inverse of tile_vals."""
+    tiled = np.asarray(tiled)
+    out_f, half = tiled.shape
+    nk = half // 32
+    v = tiled.reshape(out_f // 32, nk, 2, 2, 32, 8)  # rb, q, kk, h, r, value
+    return np.ascontiguousarray(v.transpose(0, 4, 1, 2, 3, 5)).reshape(out_f, half)

@@ -2501,16 +2501,19 @@ extern "C" int sf_column_sum(const void* A, int a_dtype, int64_t rows, int64_t c
 // them into the weights; legacy/eval_wiki_ppl.py:548-651 then runs the plain
 // forward).  A hardened 2:4 weight W [M = out, K = in] keeps two of every four
 // consecutive k; it is stored as
-//   vals [M, K / 2] bf16: the kept values of each group in column order;
+//   vals bf16 (M * K / 2 values): the two kept values of each group in column
+//        order, 8 per 16-column chunk; chunk 4 q + 2 kk + h of row
+//        rb * 32 + r sits at [rb][q][kk][h * 32 + r][8] (vals_off);
 //   idx  u32 [M / 32][K / 64][2][32]: for row block rb, 64-column chunk q, half
 //        h and row rb * 32 + r, word (bits 2j + 1 : 2j = column in its group
 //        of the j-th kept value, j = 0..7) for columns [q * 64 + 16 h, +16) in
 //        the low 16 bits and [q * 64 + 32 + 16 h, +16) in the high 16 bits.
-// That is the operand layout of v_smfmac_f32_32x32x32_bf16 (A sparse, lane l:
+// Both are the operand layout of v_smfmac_f32_32x32x32_bf16 (A sparse, lane l:
 // row l % 32, dense k [16 (l / 32), +16) as 8 values + 16 index bits, the
-// index register's half picked by abid = the k-step), so the kernel moves
-// vals and idx straight from HBM to LDS and into the instruction.  The MFMA
-// computes y^T tiles (out x tokens); the epilogue writes them transposed.
+// index register's half picked by abid = the k-step), one 1 KiB (values) or
+// 256-byte (indices) run per row block, stage and k-step, so the kernel loads
+// its A fragments straight from memory into registers, fully coalesced.  The
+// MFMA computes y^T tiles (out x tokens); the epilogue writes them transposed.
 // ---------------------------------------------------------------------------
 namespace sf {
 namespace {
@@ -2520,7 +2523,7 @@ typedef __bf16 bf16x16_t __attribute__((ext_vector_type(16)));
 struct Gemm24Args {
   const void* x;       // [N = tokens, K] bf16, row pitch ldx
   int64_t ldx;
-  const void* vals;    // [M, K / 2] bf16
+  const void* vals;    // M * K / 2 bf16, fragment order (vals_off)
   const void* idx;     // u32 [M / 32][K / 64][2][32]
   int64_t M, N, K;
   const void* bias;    // [M] or null
@@ -2537,16 +2540,7 @@ struct Gemm24Args {
 };
 
 constexpr int kEpi24Pitch = 68;  // f32 pitch of the transposed staging: 128 token rows x 64 out columns per wave
-constexpr uint32_t k24ABuf = 256u * 64;   // compressed W: 256 rows x 64 B (32 kept values of a 64-k stage)
-constexpr uint32_t k24IBuf = 8u * 64 * 4; // indices: 8 row blocks x 2 halves x 32 rows x u32
-constexpr uint32_t k24BBuf = 256u * kRowSw;
-constexpr uint32_t k24Stage = k24ABuf + k24IBuf + k24BBuf;
-
-// One 4-byte-per-lane copy global -> LDS: lane l's word lands at lds + 4 l.
-__device__ __forceinline__ void dma4(Rsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
-}
+constexpr uint32_t k24XBuf = 256u * kRowSw;  // one x stage: 256 token rows x 128 B
 
 __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -2562,113 +2556,127 @@ __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
 #pragma unroll
   for (int i = 0; i < kFragM * kFragN; ++i) acc[i] = f32x16_t{};
 
-  // fragment offsets inside a stage buffer
-  uint32_t aoff[2][kFragM], ioff[kFragM], boff[4][kFragN];
-#pragma unroll
-  for (int i = 0; i < kFragM; ++i) {
-    const int r = wm * kWaveM + i * 32 + (lane & 31), h = lane >> 5;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) aoff[kk][i] = (uint32_t)(r * 64 + (((kk * 2 + h) ^ ((r >> 2) & 3)) << 4));
-    ioff[i] = k24ABuf + (uint32_t)((((wm * 4 + i) * 2 + h) * 32 + (lane & 31)) * 4);
-  }
+  // x stages (256 tokens x 64 k, swizzled rows of 128 B) double-buffered in LDS; the sparse A
+  // operand (values + index words) loaded straight into registers.  Every load is compiler-tracked
+  // and unconditional (past the last stage the clamped index re-reads it), so the compiler's wait
+  // counts are exact: at the start of stage s the A fragments of stage s + 1 and the x rows of
+  // stage s + 2 are issued; the x rows of stage s + 1 (loaded at the start of stage s - 1) are
+  // written to the other buffer after the stage's MFMAs, and one barrier a stage publishes them.
+  uint32_t boff[4][kFragN];
 #pragma unroll
   for (int j = 0; j < kFragN; ++j) {
     const uint32_t b = frag_base<true>(wn * kWaveN + j * 32 + (lane & 31));
 #pragma unroll
-    for (int q = 0; q < 4; ++q) boff[q][j] = k24ABuf + k24IBuf + frag_at<true>(b, q);
+    for (int q = 0; q < 4; ++q) boff[q][j] = frag_at<true>(b, q);
   }
-
-  // copies: compressed W rows (64-byte rows), index words (row blocks of 256 B), x rows
-  DmaMaskLoader da;
-  da.init(g.vals, g.K, m0, g.M, g.K);  // K bytes per row: K / 2 bf16
-  DmaLoader db;
-  db.init(g.x, g.ldx, n0, g.N, g.K);
+  // x copy: thread t moves 16-byte chunk t % 8 of token rows 32 i + t / 8, i = 0..7
+  const Rsrc rx = make_rsrc(g.x, g.N * g.ldx * 2);
+  const int crow = threadIdx.x >> 3, cch = threadIdx.x & 7;
+  uint32_t xoff[8], xlds[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 32 * i + crow;
+    xoff[i] = n0 + row < g.N ? (uint32_t)(((n0 + row) * g.ldx + cch * 8) * 2) : kOob;
+    xlds[i] = (uint32_t)(row * kRowSw + ((cch ^ ((row ^ (row >> 3)) & 7)) << 4));
+  }
+  // A fragments: row block rb = m0 / 32 + 4 wm + i, lane's 16 bytes of k-step kk at
+  // vals + ((rb nk + s) 2 + kk) 1 KiB + 16 lane; its index word at idx + ((rb nk + s) 64 + lane) 4
+  const Rsrc rv = make_rsrc(g.vals, g.M * g.K);
   const Rsrc ri = make_rsrc(g.idx, (g.M / 32) * nk * 256);
-  // wave w copies row blocks 2 w, 2 w + 1 of the tile: 256 contiguous bytes each per stage
-  uint32_t ivo[2];
+  uint32_t voff[kFragM], wioff[kFragM];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int64_t rb = m0 / 32 + wave * 2 + q;
-    ivo[q] = rb < g.M / 32 ? (uint32_t)((rb * nk * 64 + lane) * 4) : kOob;
+  for (int i = 0; i < kFragM; ++i) {
+    const int64_t rb = m0 / 32 + wm * 4 + i;
+    voff[i] = rb < g.M / 32 ? (uint32_t)((rb * nk * 2 * 64 + lane) * 16) : kOob;
+    wioff[i] = rb < g.M / 32 ? (uint32_t)((rb * nk * 64 + lane) * 4) : kOob;
   }
-  auto issue = [&](int buf, int64_t s) {
-    const uint32_t st = base_l + (uint32_t)buf * k24Stage;
-    da.issue<false>(st, s * 64);
+  bf16x8_t fa[2][kFragM][2];  // [stage set][fragment][k-step]
+  uint32_t fi[2][kFragM];
+  V4 xr[2][8];
+  auto load_a = [&](auto set_c, int64_t st) {
+    constexpr int set = decltype(set_c)::value;
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
-      dma4(ri, st + k24ABuf + (uint32_t)((wave * 2 + q) * 256), ivo[q] >= kOob ? kOob : ivo[q], (uint32_t)(s * 256));
-    db.issue<false>(st + k24ABuf + k24IBuf, s * 64);
-  };
-
-  bf16x8_t fa[2][kFragM];
-  bf16x16_t fb[2][kFragN];
-  uint32_t fi[kFragM];
-  auto read_frags = [&](int slot, int buf, int kk) {
-    const unsigned char* st = smem + buf * k24Stage;
+    for (int i = 0; i < kFragM; ++i) {
 #pragma unroll
-    for (int i = 0; i < kFragM; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8_t*>(st + aoff[kk][i]);
-    if (kk == 0) {
-#pragma unroll
-      for (int i = 0; i < kFragM; ++i) fi[i] = *reinterpret_cast<const uint32_t*>(st + ioff[i]);
+      for (int kk = 0; kk < 2; ++kk)
+        fa[set][i][kk] = __builtin_bit_cast(bf16x8_t, bload(rv, voff[i], (uint32_t)((st * 2 + kk) * 1024)));
+      fi[set][i] = __builtin_amdgcn_raw_buffer_load_b32(ri, (int)wioff[i], (int)(st * 256), 0);
     }
+  };
+  auto load_x = [&](auto set_c, int64_t st) {
+    constexpr int set = decltype(set_c)::value;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xr[set][i] = bload(rx, xoff[i], (uint32_t)(st * 128));
+  };
+  auto store_x = [&](auto set_c, int buf) {
+    constexpr int set = decltype(set_c)::value;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint4 v;
+      v.x = xr[set][i].w[0];
+      v.y = xr[set][i].w[1];
+      v.z = xr[set][i].w[2];
+      v.w = xr[set][i].w[3];
+      *reinterpret_cast<uint4*>(smem + buf * k24XBuf + xlds[i]) = v;
+    }
+  };
+  // B fragments: fb[kk] holds k-step kk of the current stage.  Stage s: fragments of k-step 1 read
+  // during the k-step 0 MFMAs; x of stage s + 1 written to the other buffer; the barrier; the next
+  // stage's k-step 0 fragments read during the k-step 1 MFMAs.
+  bf16x16_t fb[2][kFragN];
+  auto read_b = [&](int slot, int buf, int kk) {
+    const unsigned char* xb = smem + buf * k24XBuf;
 #pragma unroll
     for (int j = 0; j < kFragN; ++j) {
-      const bf16x8_t lo = *reinterpret_cast<const bf16x8_t*>(st + boff[2 * kk][j]);
-      const bf16x8_t hi = *reinterpret_cast<const bf16x8_t*>(st + boff[2 * kk + 1][j]);
+      const bf16x8_t lo = *reinterpret_cast<const bf16x8_t*>(xb + boff[2 * kk][j]);
+      const bf16x8_t hi = *reinterpret_cast<const bf16x8_t*>(xb + boff[2 * kk + 1][j]);
       fb[slot][j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
     }
   };
-  // k-step 0 takes the low index half (abid 0), k-step 1 the high half (abid 1)
-  auto mfmas0 = [&](int slot) {
+  auto mfmas = [&](auto set_c, auto kk_c) {
+    constexpr int set = decltype(set_c)::value, kk = decltype(kk_c)::value;
 #pragma unroll
     for (int j = 0; j < kFragN; ++j)
 #pragma unroll
       for (int i = 0; i < kFragM; ++i)
-        acc[i * kFragN + j] =
-            __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], (int)fi[i], 0, 0);
+        acc[i * kFragN + j] = __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[set][i][kk], fb[kk][j], acc[i * kFragN + j],
+                                                                       (int)fi[set][i], 0, kk);
   };
-  auto mfmas1 = [&](int slot, const uint32_t (&ix)[kFragM]) {
-#pragma unroll
-    for (int j = 0; j < kFragN; ++j)
-#pragma unroll
-      for (int i = 0; i < kFragM; ++i)
-        acc[i * kFragN + j] =
-            __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[slot][i], fb[slot][j], acc[i * kFragN + j], (int)ix[i], 0, 1);
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  auto stage = [&](auto set_c, int64_t st) {
+    constexpr int set = decltype(set_c)::value;
+    using Other = std::integral_constant<int, set ^ 1>;
+    const int64_t s1 = st + 1 < nk ? st + 1 : nk - 1, s2 = st + 2 < nk ? st + 2 : nk - 1;
+    load_a(Other{}, s1);
+    load_x(set_c, s2);
+    // scheduling barriers keep the phases in this order (the MFMAs touch no memory, so the compiler
+    // would otherwise hoist them next to the reads they wait for)
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(1, set, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(set_c, S0{});
+    __builtin_amdgcn_sched_barrier(0);
+    store_x(Other{}, set ^ 1);  // x of stage s + 1 (past the end: written, never read)
+    __syncthreads();
+    read_b(0, set ^ 1, 0);      // the next stage's k-step 0 (past the end: unused)
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(set_c, S1{});
+    __builtin_amdgcn_sched_barrier(0);
   };
-
-  // Three-buffer ring, stage s in buffer s % 3.  One barrier a stage (between its k-steps):
-  // before it, this wave's copies of stage s + 1 have landed (the copies of stage s + 2,
-  // issued a stage later, may still be in flight: 14 copy instructions a stage per wave);
-  // after it, every wave holds stage s's last fragments in registers, so buffer s % 3 takes
-  // the copies of stage s + 3, which then have two stages' products to land.
-  if (nk > 0) issue(0, 0);
-  if (nk > 1) issue(1, 1);
-  if (nk > 2) issue(2, 2);
-  if (nk > 2)
-    asm volatile("s_waitcnt vmcnt(28)" ::: "memory");
-  else if (nk > 1)
-    asm volatile("s_waitcnt vmcnt(14)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (nk > 0) read_frags(0, 0, 0);
-  for (int64_t s = 0; s < nk; ++s) {
-    const int b = static_cast<int>(s % 3);
-    uint32_t ix[kFragM];
-#pragma unroll
-    for (int i = 0; i < kFragM; ++i) ix[i] = fi[i];
-    read_frags(1, b, 1);
-    mfmas0(0);
-    if (s + 1 < nk) {
-      if (s + 2 < nk)
-        asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)" ::: "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (s + 3 < nk) issue(b, s + 3);
-      read_frags(0, b == 2 ? 0 : b + 1, 0);
+  if (nk > 0) {
+    load_a(S0{}, 0);
+    load_x(S0{}, 0);
+    store_x(S0{}, 0);
+    load_x(S1{}, nk > 1 ? 1 : 0);
+    __syncthreads();
+    read_b(0, 0, 0);
+    int64_t s = 0;
+    for (; s + 1 < nk; s += 2) {
+      stage(S0{}, s);
+      stage(S1{}, s + 1);
     }
-    mfmas1(1, ix);
+    if (s < nk) stage(S0{}, s);
   }
 
   // Segment 2 (dense, 64 k a stage through the first 64 KB of LDS): the low-rank term
@@ -2777,8 +2785,16 @@ __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
 }
 
 constexpr size_t smem24_bytes() {
-  constexpr size_t ops = 3ull * k24Stage, epi = 4ull * 128 * kEpi24Pitch * sizeof(float);
+  constexpr size_t ops = 2ull * k24XBuf, epi = 4ull * 128 * kEpi24Pitch * sizeof(float);
   return ops > epi ? ops : epi;
+}
+
+// Element offset in `vals` of the 8 kept values of row `row`, 16-column chunk c16 (K / 64
+// stages of 4 chunks): chunk c16 = 4 q + 2 kk + h of row block rb = row / 32 lands in the
+// 2 KiB run (rb, q) at [kk][h * 32 + row % 32][8], the order of the sparse MFMA's A fragments.
+__device__ __forceinline__ int64_t vals_off(int64_t row, int64_t c16, int64_t nk) {
+  const int64_t q = c16 >> 2, sub = c16 & 3;
+  return ((((row >> 5) * nk + q) * 2 + (sub >> 1)) * 64 + (sub & 1) * 32 + (row & 31)) * 8;
 }
 
 // Pack: one thread per (row, 16 columns): 4 groups -> 8 kept values (16 bytes)
@@ -2827,7 +2843,7 @@ __global__ void __launch_bounds__(256) pack24_kernel(const void* __restrict__ W,
       bits |= (uint32_t)pos[0] << (4 * grp);
       bits |= (uint32_t)pos[1] << (4 * grp + 2);
     }
-    uint16_t* vp = vals + row * (K / 2) + c16 * 8;
+    uint16_t* vp = vals + vals_off(row, c16, nk);
 #pragma unroll
     for (int q = 0; q < 8; ++q) vp[q] = out[q];
     const int64_t q64 = c16 >> 2, sub = c16 & 3;  // 16-column block inside its 64-column chunk
@@ -2892,7 +2908,7 @@ __global__ void __launch_bounds__(256) apply_pack24_kernel(const uint16_t* __res
     }
     *reinterpret_cast<uint4*>(Wm + e0) = make_uint4(om[0], om[1], om[2], om[3]);
     *reinterpret_cast<uint4*>(Wm + e0 + 8) = make_uint4(om[4], om[5], om[6], om[7]);
-    *reinterpret_cast<uint4*>(vals + row * (K / 2) + c16 * 8) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+    *reinterpret_cast<uint4*>(vals + vals_off(row, c16, nk)) = make_uint4(ov[0], ov[1], ov[2], ov[3]);
     const int64_t q64 = c16 >> 2, sub = c16 & 3;
     const int64_t word = (((row >> 5) * nk + q64) * 2 + (sub & 1)) * 32 + (row & 31);
     idx[word * 2 + (sub >> 1)] = static_cast<uint16_t>(bits);
@@ -2914,7 +2930,7 @@ __global__ void __launch_bounds__(256) unpack24_kernel(const uint16_t* __restric
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int p = (bits >> (2 * j)) & 3;
-      d[(j >> 1) * 4 + p] += bf16_to_f32(vals[row * (K / 2) + c16 * 8 + j]);
+      d[(j >> 1) * 4 + p] += bf16_to_f32(vals[vals_off(row, c16, nk) + j]);
     }
 #pragma unroll
     for (int q = 0; q < 16; ++q) store_from_f32(W, row * K + c16 * 16 + q, w_dtype, d[q]);

@@ -31,12 +31,18 @@ constexpr int kKlBwdU = 4;  // the same for the backward
 
 __device__ __forceinline__ float exp_f(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 8 consecutive logits as f32.  The vector paths load non-temporally: the logits (gigabytes) stream
+// through once per pass, and nothing re-reads them before they are evicted.
 template <int DT>
 __device__ __forceinline__ void load8(const void* base, int64_t i, int n, bool vec, float v[8]) {
   if (DT == SF_DTYPE_F32) {
     const float* p = static_cast<const float*>(base) + i;
     if (vec) {
-      const float4 x = *reinterpret_cast<const float4*>(p), y = *reinterpret_cast<const float4*>(p + 4);
+      const f32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+      const f32x4_t y = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p + 4));
       v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w; v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
     } else {
 #pragma unroll
@@ -45,7 +51,7 @@ __device__ __forceinline__ void load8(const void* base, int64_t i, int n, bool v
   } else {
     const uint16_t* p = static_cast<const uint16_t*>(base) + i;
     if (vec) {
-      const uint4 x = *reinterpret_cast<const uint4*>(p);
+      const u32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
       const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -68,8 +74,8 @@ __device__ __forceinline__ void store8(void* base, int64_t i, int n, bool vec, c
   if (DT == SF_DTYPE_F32) {
     float* p = static_cast<float*>(base) + i;
     if (vec) {
-      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-      *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      __builtin_nontemporal_store(f32x4_t{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4_t*>(p));
+      __builtin_nontemporal_store(f32x4_t{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4_t*>(p + 4));
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
@@ -78,13 +84,11 @@ __device__ __forceinline__ void store8(void* base, int64_t i, int n, bool vec, c
   } else {
     uint16_t* p = static_cast<uint16_t*>(base) + i;
     if (vec) {
-      uint4 o;
       uint32_t w[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k)
         w[k] = static_cast<uint32_t>(bf16_rne(v[2 * k])) | (static_cast<uint32_t>(bf16_rne(v[2 * k + 1])) << 16);
-      o.x = w[0]; o.y = w[1]; o.z = w[2]; o.w = w[3];
-      *reinterpret_cast<uint4*>(p) = o;
+      __builtin_nontemporal_store(u32x4_t{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4_t*>(p));
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k)

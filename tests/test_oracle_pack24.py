@@ -48,3 +48,19 @@ def test_index_word_layout_direct_decode():
         for grp in range(4):
             kept = [c for c in range(4) if M[r, sub * 16 + grp * 4 + c]]
             assert [(bits >> (4 * grp)) & 3, (bits >> (4 * grp + 2)) & 3] == kept
+
+
+def test_tile_vals_round_trip_and_order():
+    """tile_vals is a permutation (untile_vals inverts it) and puts chunk (q, kk, h) of row 32 rb + r at
+    the 1 KiB run (rb, q, kk), lane h * 32 + r."""
+    out_f, in_f = 64, 128
+    vals = np.arange(out_f * in_f // 2, dtype=np.float32).reshape(out_f, in_f // 2)
+    t = op.tile_vals(vals)
+    assert np.array_equal(op.untile_vals(t), vals)
+    flat = t.ravel()
+    nk = in_f // 64
+    for row, c16 in [(0, 0), (5, 3), (33, 6), (63, 7)]:
+        rb, r, q, sub = row // 32, row % 32, c16 // 4, c16 % 4
+        kk, h = sub // 2, sub % 2
+        off = (((rb * nk + q) * 2 + kk) * 64 + h * 32 + r) * 8
+        assert np.array_equal(flat[off:off + 8], vals[row, c16 * 8:c16 * 8 + 8])
