@@ -431,6 +431,38 @@ int sf_kl_backward(const void* student, const void* teacher, int dtype, int64_t 
 int sf_apply_mask(const void* W, int w_dtype, const void* E, int e_dtype, float scale, void* out, int64_t rows,
                   int64_t cols, void* stream);
 
+/* ---- attention softmax of the retraining model (cfg5; legacy/model_llama.py:39-55 eager attention,
+ *      legacy/main_llama.py:194 autocast; differentiated twice by the Hutchinson HVP, legacy/utils.py:714-869) */
+
+/*
+ * p = softmax(x, dim=-1, dtype=float32).to(x dtype) over rows of `cols`
+ * columns (x, p: [rows, cols], dtype f32 or bf16).  causal: row r keeps columns
+ * 0 .. r % cols (the rows of [batches, S, S] attention scores whose masked
+ * entries are -inf), the rest of the row gets probability 0 and is not read.
+ * y is computed in f32 and rounded to nearest even.  cols <= 4096.
+ */
+int sf_softmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int causal, void* p, void* stream);
+
+/*
+ * The backward of that softmax and cast from the scores x (y recomputed, bit
+ * for bit the forward's): grad_x = (y (g - sum(g y))).to(x dtype), g =
+ * grad_p in f32 (torch's _softmax_backward_data after ToCopyBackward).
+ */
+int sf_softmax_rows_backward(const void* x, const void* grad_p, int dtype, int64_t rows, int64_t cols, int causal,
+                             void* grad_x, void* stream);
+
+/*
+ * The backward of sf_softmax_rows_backward with respect to grad_p and x, given
+ * the gradient grad_grad_x of its output: with y, g as above, h = grad_grad_x
+ * in f32, c = sum g y, d = sum h y, u = g h - c h - d g, e = sum u y:
+ *   grad_grad_p = (y (h - d)).to(dtype), grad2_x = (y (u - e)).to(dtype)
+ * (torch's SoftmaxBackwardDataBackward0 with its softmax_double_backward, and
+ * the softmax backward that carries u to the scores).
+ */
+int sf_softmax_rows_double_backward(const void* x, const void* grad_p, const void* grad_grad_x, int dtype,
+                                    int64_t rows, int64_t cols, int causal, void* grad_grad_p, void* grad2_x,
+                                    void* stream);
+
 /* ---- GEMM engine (FusedMaskedLinearSTE, :56-132, and the SLoRB F.linear pair, :790-794) */
 #define SF_LAYOUT_K 0  /* operand stored K-contiguous: X[row * ld + k]                        */
 #define SF_LAYOUT_MN 1 /* operand stored M/N-contiguous: X[k * ld + row] (a transposed view)  */

@@ -41,6 +41,8 @@ import torch
 import torch.nn as nn
 from torch.nn import functional as F
 
+from . import _lib as L
+from . import profiling as _prof
 from .sparse_modeling import SparseLinear, SparseLinearConfig
 
 
@@ -124,6 +126,70 @@ class _BMM(torch.autograd.Function):
         return ga, gb, None
 
 
+def _softmax_launch(name: str, fn, nbytes: int, dev, *args) -> None:
+    with _prof.region(name, nbytes, "B", dev):
+        L.check(fn(*args, L.stream(dev)), name)
+
+
+class _CausalSoftmax(torch.autograd.Function):
+    """p = softmax(scores, dim=-1, dtype=float32).to(scores.dtype) of causal [B H, S, S] scores (the masked
+    entries -inf, their probability 0) on the device (sf_softmax_rows).  Its backward is a Function of its
+    own (_CausalSoftmaxGrad), so the Hutchinson Hessian-vector product differentiates it once more, as it
+    differentiates the reference's torch ops.  Only the scores are kept: each pass recomputes y from them."""
+
+    @staticmethod
+    def forward(ctx, x):
+        dev = L.require_device(x)
+        rows, cols = x.numel() // x.shape[-1], x.shape[-1]
+        p = torch.empty_like(x)
+        _softmax_launch("sf_softmax_rows", L.lib().sf_softmax_rows, x.numel() * x.element_size(), dev,
+                        L.ptr(x), L.dtype_code(x), rows, cols, 1, L.ptr(p))
+        ctx.save_for_backward(x)
+        return p
+
+    @staticmethod
+    def backward(ctx, gp):
+        x, = ctx.saved_tensors
+        return _CausalSoftmaxGrad.apply(gp.to(x.dtype).contiguous(), x)
+
+
+class _CausalSoftmaxGrad(torch.autograd.Function):
+    """grad_x = (y (g - sum(g y))).to(x dtype), g = grad_p in float32 (sf_softmax_rows_backward), and its
+    backward with respect to grad_p and the scores (sf_softmax_rows_double_backward)."""
+
+    @staticmethod
+    def forward(ctx, gp, x):
+        dev = L.require_device(gp, x)
+        rows, cols = x.numel() // x.shape[-1], x.shape[-1]
+        gx = torch.empty_like(x)
+        _softmax_launch("sf_softmax_rows_backward", L.lib().sf_softmax_rows_backward,
+                        x.numel() * x.element_size(), dev, L.ptr(x), L.ptr(gp), L.dtype_code(x), rows, cols, 1,
+                        L.ptr(gx))
+        ctx.save_for_backward(gp, x)
+        return gx
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggx):
+        gp, x = ctx.saved_tensors
+        dev = x.device
+        ggx = ggx.to(x.dtype).contiguous()
+        rows, cols = x.numel() // x.shape[-1], x.shape[-1]
+        ggp, gx2 = torch.empty_like(x), torch.empty_like(x)
+        _softmax_launch("sf_softmax_rows_double_backward", L.lib().sf_softmax_rows_double_backward,
+                        x.numel() * x.element_size(), dev, L.ptr(x), L.ptr(gp), L.ptr(ggx), L.dtype_code(x), rows,
+                        cols, 1, L.ptr(ggp), L.ptr(gx2))
+        return ggp, gx2
+
+
+def causal_softmax(scores: torch.Tensor) -> torch.Tensor:
+    """softmax(scores, dim=-1, dtype=float32).to(scores.dtype) of causal scores [.., S, S] whose masked entries
+    are -inf: the device kernels on a GPU (S <= 4096), torch's ops on the CPU."""
+    if scores.is_cuda:
+        return _CausalSoftmax.apply(scores.contiguous())
+    return torch.softmax(scores, dim=-1, dtype=torch.float32).to(scores.dtype)
+
+
 _CAUSAL_BIAS: dict = {}
 
 
@@ -163,7 +229,7 @@ def causal_attention(q, k, v, cos, sin) -> torch.Tensor:
             scores = _BMM.apply(qh, kt, causal_bias(S, q.device, dt))              # [B H, S, S]
         else:
             scores = _BMM.apply(qh, kt) * scale + causal_bias(S, q.device, dt)
-        p = torch.softmax(scores, dim=-1, dtype=torch.float32).to(dt)
+        p = causal_softmax(scores)
         out = _BMM.apply(p, v.transpose(1, 2).reshape(B * H, S, D))              # [B H, S, D]
     return out.view(B, H, S, D).transpose(1, 2).reshape(B, S, H * D)
 
