@@ -85,9 +85,12 @@ def rotary_tables(seq: int, head_dim: int, theta: float, device) -> tuple[torch.
 
 
 def _rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x * cos + rotate_half(x) * sin with rotate_half(x) = cat(-x2, x1) (the half-split rotation), written as
+    roll(x, half) * cat(-sin1, sin2): (-a) * s and a * (-s) round to the same value, so the result is bit for bit
+    the cat form's, and the derivatives are a roll and products instead of zero-filled slice gradients."""
     half = x.shape[-1] // 2
-    swapped = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
-    return x * cos + swapped * sin
+    signed_sin = torch.cat([-sin[..., :half], sin[..., half:]], dim=-1)
+    return x * cos + torch.roll(x, shifts=half, dims=-1) * signed_sin
 
 
 class _BMM(torch.autograd.Function):
