@@ -2856,7 +2856,10 @@ __global__ void __launch_bounds__(256) pack24_kernel(const void* __restrict__ W,
 // The hx = 0 training forward's weight pass: Wm = round(W * E) for a byte and-mask E (W
 // bf16; the elementwise product of sf_apply_mask, kept for the input gradient) and, from
 // the same loads, the packed 2:4 form of Wm (the kept bf16 values exactly, the index bits
-// of pack24_kernel).  One thread per (row, 16 columns).
+// of pack24_kernel).  One thread per (row, 16 columns), 128 consecutive threads per (32-row block,
+// 64 columns): thread w of the run takes row 32 rb + w % 32 and 16-column chunk 4 q + w / 32, so
+// the run writes whole lines of every output (the 2 KiB value run and the index words of (rb, q),
+// each row's 128 bytes of W . E) and reads whole 128-byte lines of W.
 __global__ void __launch_bounds__(256) apply_pack24_kernel(const uint16_t* __restrict__ W, const uint8_t* __restrict__ E,
                                                            int64_t M, int64_t K, uint16_t* __restrict__ Wm,
                                                            uint16_t* __restrict__ vals, uint16_t* __restrict__ idx,
@@ -2864,7 +2867,9 @@ __global__ void __launch_bounds__(256) apply_pack24_kernel(const uint16_t* __res
   const int64_t per_row = K / 16, total = M * per_row, nk = K / 64;
   unsigned long long nbad = 0;
   for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = t / per_row, c16 = t - row * per_row;
+    const int64_t run = t >> 7, rb = run / nk, q = run - rb * nk;
+    const int w = static_cast<int>(t & 127);
+    const int64_t row = rb * 32 + (w & 31), c16 = q * 4 + (w >> 5);
     const int64_t e0 = row * K + c16 * 16;
     const uint4 wa = *reinterpret_cast<const uint4*>(W + e0), wb = *reinterpret_cast<const uint4*>(W + e0 + 8);
     const uint4 mb = *reinterpret_cast<const uint4*>(E + e0);
