@@ -2650,18 +2650,31 @@ __global__ void __launch_bounds__(kThreads, 1) gemm24_kernel(Gemm24Args g) {
     const int64_t s1 = st + 1 < nk ? st + 1 : nk - 1, s2 = st + 2 < nk ? st + 2 : nk - 1;
     load_a(Other{}, s1);
     load_x(set_c, s2);
-    // scheduling barriers keep the phases in this order (the MFMAs touch no memory, so the compiler
-    // would otherwise hoist them next to the reads they wait for)
-    __builtin_amdgcn_sched_barrier(0);
     read_b(1, set, 1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(set_c, S0{});
-    __builtin_amdgcn_sched_barrier(0);
     store_x(Other{}, set ^ 1);  // x of stage s + 1 (past the end: written, never read)
+    mfmas(set_c, S0{});
+    // With one wave per SIMD nothing else feeds the MFMA pipe while a wave issues memory
+    // instructions, so they go between the MFMAs (scheduling groups, in this order): k-step 0's 16
+    // MFMAs each followed by one of 12 loads and by a fragment read (MFMAs 0-7) or a copy write
+    // (8-15); after the barrier, k-step 1's MFMAs with the next stage's fragment reads (0-7) and
+    // the remaining 8 loads (8-15).  Group sync ids 0 / 1 keep the two phases apart.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (i < 12) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+      if (i >= 8) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+    }
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     read_b(0, set ^ 1, 0);      // the next stage's k-step 0 (past the end: unused)
-    __builtin_amdgcn_sched_barrier(0);
     mfmas(set_c, S1{});
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      if (i >= 8) __builtin_amdgcn_sched_group_barrier(0x020, 1, 1);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   if (nk > 0) {
