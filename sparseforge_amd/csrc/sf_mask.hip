@@ -17,6 +17,7 @@
 #include <utility>
 
 #include <mutex>
+#include <vector>
 
 #include "sf_common.hpp"
 #include "sf_rng.hpp"
@@ -1732,14 +1733,61 @@ void for_each_batch(const sf_mask_layer* layers, int count, F&& f) {
     f(first, i, keys);
   }
 }
+
+// Workspace of sf_update_mask_multi.  Serial layout: [stats partials | select states | radix partials x 2 |
+// keys].  The pipelined schedule (below) appends a second stats-partials region and a second keys region,
+// so that batch b + 1's statistics and tau gather never write what batch b's selection still reads.  It is
+// offered only while a batch's sample keys stay below kOverlapMaxKeys (a tau sample over every element of
+// large layers would double a workspace of gigabytes).
+constexpr int64_t kOverlapMaxKeys = int64_t(1) << 25;
+struct MultiSizes {
+  int64_t keys = 0;  // largest batch's sample keys
+  int batches = 0;
+  size_t serial_bytes = 0, overlap_bytes = 0, keys1_off = 0, partial1_off = 0;
+};
+MultiSizes multi_sizes(const sf_mask_layer* layers, int count) {
+  MultiSizes z;
+  if (layers && count > 0)
+    for_each_batch(layers, count, [&](int, int, int64_t k) {
+      z.keys = k > z.keys ? k : z.keys;
+      ++z.batches;
+    });
+  const size_t kb = sizeof(uint32_t) * static_cast<size_t>(z.keys);
+  z.serial_bytes = multi_keys_off() + kb;
+  z.partial1_off = align256(z.serial_bytes);
+  z.keys1_off = z.partial1_off + multi_partial_bytes();
+  z.overlap_bytes = z.keys1_off + kb;
+  return z;
+}
+
+// Second stream of the pipelined multi-layer update, one per GPU, and its events (two per batch), created
+// on first use with that GPU current and held until the process ends.  The lock is held while a call
+// enqueues its work, so calls from several host threads never share an event in flight.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  std::vector<hipEvent_t> ev;
+};
+std::mutex g_side_lock;
+SideStream g_side[64];
+
+int side_stream(int device, size_t events, SideStream** out) {
+  SF_CHECK_ARG(device >= 0 && device < 64, "device ordinal %d out of range", device);
+  SideStream& ss = g_side[device];
+  if (!ss.stream) SF_CHECK_HIP(hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking));
+  while (ss.ev.size() < events) {
+    hipEvent_t e;
+    SF_CHECK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    ss.ev.push_back(e);
+  }
+  *out = &ss;
+  return SF_OK;
+}
 }  // namespace
 }  // namespace sf
 
 extern "C" size_t sf_update_mask_multi_workspace_size(const sf_mask_layer* layers, int count) {
-  int64_t keys = 0;
-  if (layers && count > 0)
-    for_each_batch(layers, count, [&](int, int, int64_t k) { keys = k > keys ? k : keys; });
-  return multi_keys_off() + sizeof(uint32_t) * static_cast<size_t>(keys);
+  const MultiSizes z = multi_sizes(layers, count);
+  return z.batches > 1 && z.keys <= kOverlapMaxKeys ? z.overlap_bytes : z.serial_bytes;
 }
 
 extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_mask_layer* layers, int count,
@@ -1787,20 +1835,31 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
     have_spec = true;
   }
   if (!have_spec) return SF_OK;
-  SF_CHECK_ARG(workspace && workspace_bytes >= sf_update_mask_multi_workspace_size(layers, count),
-               "workspace too small");
+  const MultiSizes z = multi_sizes(layers, count);
+  SF_CHECK_ARG(workspace && workspace_bytes >= z.serial_bytes, "workspace too small");
   char* ws = static_cast<char*>(workspace);
-  double* partial = reinterpret_cast<double*>(ws);
   SelState* states = reinterpret_cast<SelState*>(ws + multi_partial_bytes());
   uint32_t* parts0 = reinterpret_cast<uint32_t*>(ws + multi_partial_bytes() + multi_states_bytes());
   uint32_t* parts1 = reinterpret_cast<uint32_t*>(ws + multi_partial_bytes() + multi_states_bytes() + multi_hist_bytes());
-  uint32_t* keys = reinterpret_cast<uint32_t*>(ws + multi_keys_off());
+  // statistics partials and tau keys: region 0, and region 1 for odd batches of the pipelined schedule
+  double* partial_r[2] = {reinterpret_cast<double*>(ws), reinterpret_cast<double*>(ws + z.partial1_off)};
+  uint32_t* keys_r[2] = {reinterpret_cast<uint32_t*>(ws + multi_keys_off()),
+                         reinterpret_cast<uint32_t*>(ws + z.keys1_off)};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool sf32 = p->score_dtype == SF_DTYPE_F32;
-  int rc_all = SF_OK;
-  for_each_batch(layers, count, [&](int first, int end, int64_t) {
-    if (rc_all != SF_OK) return;
+
+  // the batches' layer tables and launch shapes
+  struct Batch {
     MultiArgs a;
+    int n, total, gather_grid;
+    bool all_vec;
+  };
+  std::vector<Batch> batches;
+  batches.reserve(static_cast<size_t>(z.batches));
+  for_each_batch(layers, count, [&](int first, int end, int64_t) {
+    batches.emplace_back();
+    Batch& bt = batches.back();
+    MultiArgs& a = bt.a;
     memset(&a, 0, sizeof(a));
     a.us = us;
     int n = 0, gather_grid = 1;
@@ -1842,35 +1901,41 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
       ++n;
     }
     a.count = n;
-    const int total = a.first[n];
-    // statistics
-    const bool want_tau = unstructured && (stages & SF_MULTI_TAU);
-    // the tau gather rides in the statistics launch when both stages run
-    const bool fused_gather = want_tau && (stages & SF_MULTI_STATS);
-    if (stages & SF_MULTI_STATS) {
-      const int g = fused_gather ? gather_grid : 0;
-      const int grid = n * g + n * kStatsGrid;
-      if (all_vec && p->metric == SF_METRIC_HESSIAN_RATIO)
-        SF_DISPATCH_WH(w_dtype, h_dtype,
-                       stats_partial_multi_kernel<WD_, HD_, true, true><<<grid, kBlock, 0, st>>>(a, partial, g, keys));
-      else if (all_vec)
-        SF_DISPATCH_WH(w_dtype, h_dtype,
-                       stats_partial_multi_kernel<WD_, HD_, true, false><<<grid, kBlock, 0, st>>>(a, partial, g, keys));
-      else
-        SF_DISPATCH_WH(w_dtype, h_dtype,
-                       stats_partial_multi_kernel<WD_, HD_, false, false><<<grid, kBlock, 0, st>>>(a, partial, g,
-                                                                                                   keys));
-      stats_final_multi_kernel<<<n, kBlock, 0, st>>>(a, partial);
-    }
-    // tau
-    if (want_tau) {
-      if (!fused_gather) tau_gather_multi_kernel<<<dim3(gather_grid, n), kBlock, 0, st>>>(a, keys);
-      for (int pass = 0; pass < 4; ++pass)
-        tau_pass_multi_kernel<<<dim3(kSelGrid, n), kBlock, 0, st>>>(a, keys, pass, q, states, parts0, parts1);
-      tau_final_multi_kernel<<<n, kBlock, 0, st>>>(a, q, states, parts1);
-    }
-    // update
-    if (stages & SF_MULTI_UPDATE) {
+    bt.n = n;
+    bt.total = a.first[n];
+    bt.gather_grid = gather_grid;
+    bt.all_vec = all_vec;
+  });
+
+  const bool want_tau = unstructured && (stages & SF_MULTI_TAU);
+  // the tau gather rides in the statistics launch when both stages run
+  const bool fused_gather = want_tau && (stages & SF_MULTI_STATS);
+  auto launch_stats = [&](const Batch& bt, double* partial, uint32_t* keys) {
+    const MultiArgs& a = bt.a;
+    const int g = fused_gather ? bt.gather_grid : 0;
+    const int grid = bt.n * g + bt.n * kStatsGrid;
+    if (bt.all_vec && p->metric == SF_METRIC_HESSIAN_RATIO)
+      SF_DISPATCH_WH(w_dtype, h_dtype,
+                     stats_partial_multi_kernel<WD_, HD_, true, true><<<grid, kBlock, 0, st>>>(a, partial, g, keys));
+    else if (bt.all_vec)
+      SF_DISPATCH_WH(w_dtype, h_dtype,
+                     stats_partial_multi_kernel<WD_, HD_, true, false><<<grid, kBlock, 0, st>>>(a, partial, g, keys));
+    else
+      SF_DISPATCH_WH(w_dtype, h_dtype,
+                     stats_partial_multi_kernel<WD_, HD_, false, false><<<grid, kBlock, 0, st>>>(a, partial, g,
+                                                                                                 keys));
+  };
+  auto launch_tau = [&](const Batch& bt, uint32_t* keys, hipStream_t s) {
+    const MultiArgs& a = bt.a;
+    if (!fused_gather) tau_gather_multi_kernel<<<dim3(bt.gather_grid, bt.n), kBlock, 0, s>>>(a, keys);
+    for (int pass = 0; pass < 4; ++pass)
+      tau_pass_multi_kernel<<<dim3(kSelGrid, bt.n), kBlock, 0, s>>>(a, keys, pass, q, states, parts0, parts1);
+    tau_final_multi_kernel<<<bt.n, kBlock, 0, s>>>(a, q, states, parts1);
+  };
+  auto launch_update = [&](const Batch& bt) {
+    const MultiArgs& a = bt.a;
+    const int total = bt.total;
+    const bool all_vec = bt.all_vec;
 #define SF_LAUNCH_UPDM_V(MDT, SDT, VEC, FAST) \
   SF_DISPATCH_WH(w_dtype, h_dtype, update_mask_multi_kernel<WD_, HD_, MDT, SDT, VEC, FAST><<<total, kBlock, 0, st>>>(a))
 #define SF_LAUNCH_UPDM(MDT, SDT)                            \
@@ -1880,32 +1945,80 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
     else                                                    \
       SF_LAUNCH_UPDM_V(MDT, SDT, false, kFastNone);         \
   } while (0)
-      const int fk = all_vec ? fast_kind(us) : kFastNone;
-      if (mask_dtype == SF_DTYPE_F32) {
-        if (sf32 && fk == kFastPlain)
-          SF_LAUNCH_UPDM_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastPlain);
-        else if (sf32 && fk == kFastNm24)
-          SF_LAUNCH_UPDM_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastNm24);
-        else if (sf32)
-          SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_F32);
-        else
-          SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_BF16);
-      } else {
-        if (sf32)
-          SF_LAUNCH_UPDM(SF_DTYPE_BF16, SF_DTYPE_F32);
-        else
-          SF_LAUNCH_UPDM(SF_DTYPE_BF16, SF_DTYPE_BF16);
-      }
+    const int fk = all_vec ? fast_kind(us) : kFastNone;
+    if (mask_dtype == SF_DTYPE_F32) {
+      if (sf32 && fk == kFastPlain)
+        SF_LAUNCH_UPDM_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastPlain);
+      else if (sf32 && fk == kFastNm24)
+        SF_LAUNCH_UPDM_V(SF_DTYPE_F32, SF_DTYPE_F32, true, kFastNm24);
+      else if (sf32)
+        SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_F32);
+      else
+        SF_LAUNCH_UPDM(SF_DTYPE_F32, SF_DTYPE_BF16);
+    } else {
+      if (sf32)
+        SF_LAUNCH_UPDM(SF_DTYPE_BF16, SF_DTYPE_F32);
+      else
+        SF_LAUNCH_UPDM(SF_DTYPE_BF16, SF_DTYPE_BF16);
+    }
 #undef SF_LAUNCH_UPDM
 #undef SF_LAUNCH_UPDM_V
-    }
+  };
+  auto launched = [&]() {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
       set_error("sf_update_mask_multi: launch failed: %s", hipGetErrorString(e));
-      rc_all = SF_ERR_HIP;
+      return SF_ERR_HIP;
     }
-  });
-  if (rc_all != SF_OK) return rc_all;
+    return SF_OK;
+  };
+
+  const int nb = static_cast<int>(batches.size());
+  const bool pipelined = stages == SF_MULTI_ALL && unstructured && nb > 1 && z.keys <= kOverlapMaxKeys &&
+                         workspace_bytes >= z.overlap_bytes;
+  if (!pipelined) {
+    // serial: each batch's statistics, tau selection and update in turn, on the caller's stream
+    for (const Batch& bt : batches) {
+      if (stages & SF_MULTI_STATS) {
+        launch_stats(bt, partial_r[0], keys_r[0]);
+        stats_final_multi_kernel<<<bt.n, kBlock, 0, st>>>(bt.a, partial_r[0]);
+      }
+      if (want_tau) launch_tau(bt, keys_r[0], st);
+      if (stages & SF_MULTI_UPDATE) launch_update(bt);
+      if (int rc = launched()) return rc;
+    }
+    return launch_status("sf_update_mask_multi");
+  }
+
+  // Pipelined: the statistics (with the tau gather) and the updates run in order on the caller's stream,
+  // S0 S1 U0 S2 U1 ... S(n-1) U(n-2) U(n-1); batch b's statistics fold and radix selection (a few small
+  // launches) run on the side stream once S(b) is done, beside S(b + 1), and U(b) waits for them.
+  // S(b + 2) reuses batch b's regions only after U(b), hence after batch b's selection.  The same
+  // kernels as the serial schedule, on the same data, so every output is identical.
+  int device = -1;
+  SF_CHECK_HIP(hipGetDevice(&device));
+  std::lock_guard<std::mutex> guard(g_side_lock);
+  SideStream* side = nullptr;
+  if (int rc = side_stream(device, 2 * static_cast<size_t>(nb), &side)) return rc;
+  hipStream_t ss = side->stream;
+  for (int b = 0; b <= nb; ++b) {
+    if (b < nb) {
+      const Batch& bt = batches[b];
+      double* partial = partial_r[b & 1];
+      uint32_t* keys = keys_r[b & 1];
+      launch_stats(bt, partial, keys);
+      SF_CHECK_HIP(hipEventRecord(side->ev[2 * b], st));
+      SF_CHECK_HIP(hipStreamWaitEvent(ss, side->ev[2 * b], 0));
+      stats_final_multi_kernel<<<bt.n, kBlock, 0, ss>>>(bt.a, partial);
+      launch_tau(bt, keys, ss);
+      SF_CHECK_HIP(hipEventRecord(side->ev[2 * b + 1], ss));
+    }
+    if (b >= 1) {
+      SF_CHECK_HIP(hipStreamWaitEvent(st, side->ev[2 * (b - 1) + 1], 0));
+      launch_update(batches[b - 1]);
+    }
+    if (int rc = launched()) return rc;
+  }
   return launch_status("sf_update_mask_multi");
 }
 

@@ -147,6 +147,54 @@ def test_multi_stages_one_call_at_a_time(cuda_device):
         assert torch.equal(la[2], lb[2])
 
 
+def test_multi_pipelined_schedule_equals_serial(cuda_device):
+    """Four batches (100 layers, sampled and full tau samples): with the full workspace the batches' tau
+    selections run on the side stream beside the next batch's statistics, and batch b + 2 reuses batch b's
+    regions; with the serial minimum the stages run batch after batch.  Both equal the single-layer calls,
+    over two updates in a row (the second starts from the first's masks)."""
+    L, K = _lib()
+    p0 = _params(L, "unstructured")
+    layers = _layers("unstructured", cuda_device, n=100, seed=11)
+    a, b, c = _clone(layers), _clone(layers), _clone(layers)
+    n = len(layers)
+    jobs_of = lambda ls, st, ta, fl: [K.MaskJob(K.MaskOperands(weight=W, mask=M, hessian=H, frozen=F), idx, st[i],
+                                                ta[i:i + 1], fl[i:i + 1]) for i, (W, H, M, F, idx) in enumerate(ls)]
+    outs = []
+    for ls, small in ((b, False), (c, True)):
+        st = torch.full((n, 2), float("nan"), device=cuda_device)
+        ta = torch.full((n,), float("nan"), device=cuda_device)
+        fl = torch.zeros(n, dtype=torch.int64, device=cuda_device)
+        jobs = jobs_of(ls, st, ta, fl)
+        table = K._layer_table(jobs)
+        full = L.lib().sf_update_mask_multi_workspace_size(table, n)
+        ws = K.multi_workspace(jobs, cuda_device)
+        assert ws.numel() == full
+        if small:  # the serial layout's size: below what the pipelined schedule needs
+            ws = ws[:full - 4096 * 4]
+        for step in range(2):
+            p = L.MaskParams.from_buffer_copy(p0)
+            p.temperature = 0.3 if step == 0 else 0.05
+            K.update_mask_multi(p, 0.37, jobs, L.MULTI_ALL, ws)
+        outs.append((st, ta, fl))
+    want = []
+    for step in range(2):
+        p = L.MaskParams.from_buffer_copy(p0)
+        p.temperature = 0.3 if step == 0 else 0.05
+        want.append(_single(L, K, p, 0.37, a))
+    torch.cuda.synchronize()
+    s_stats, s_tau, _ = want[1]
+    for st, ta, fl in outs:
+        for i, ((W, _, M, _, _), (_, _, M2, _, _), (_, _, M3, _, _)) in enumerate(zip(a, b, c)):
+            if W.numel() == 0:
+                continue
+            assert torch.equal(st[i], s_stats[i]), i
+            assert torch.equal(ta[i:i + 1], s_tau[i]), i
+            total_flips = int(want[0][2][i]) + int(want[1][2][i])
+            assert int(fl[i]) == total_flips, i
+    for (W, _, M, _, _), (_, _, M2, _, _), (_, _, M3, _, _) in zip(a, b, c):
+        assert torch.equal(M2, M) and torch.equal(M3, M)
+
+
 def test_multi_rejects_bad_calls(cuda_device):
     L, K = _lib()
     p0 = _params(L, "unstructured")
