@@ -991,11 +991,25 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
     n_params = sum(W.numel() for W, _, _ in arena)
     traffic = profiled_traffic()
     if "mask" in legs:
+        # the tau samples: sorted draws (sf_sample_indices_sorted, what update_mask and calculate_model_mask
+        # draw), one per layer shape, reused by every layer and update as a fixed input
         sample_idx = {}
         for W, _, _ in arena:
             key = tuple(W.shape)
             if key not in sample_idx:
-                sample_idx[key] = K.sample_indices(262144, W.numel(), 1234 + len(sample_idx), dev)
+                sample_idx[key] = K.sample_indices_sorted(262144, [W.numel()], [1234 + len(sample_idx)], dev)[0]
+        # what drawing a fresh sample for every layer costs (calculate_model_mask's draws: one call per sample
+        # size, the layers' lists in launches of 64)
+        numels = [W.numel() for W, _, _ in arena]
+        K.sample_indices_sorted(262144, numels, list(range(len(numels))), dev)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        K.sample_indices_sorted(262144, numels, list(range(len(numels))), dev)
+        e1.record()
+        torch.cuda.synchronize()
+        sampler_ms = e0.elapsed_time(e1)
+        log(f"sorted tau samples for all {len(numels)} layers: {sampler_ms:.3f} ms")
         jobs, mws = mask_jobs(torch, K, arena, sample_idx)
         mask_step(L, K, jobs, mws, 0)  # warmup
         torch.cuda.synchronize()
@@ -1048,6 +1062,7 @@ def arena_legs(torch, L, K, prof, dev, a, legs, out) -> None:
             "arena_frac_of_sustained": round(
                 (14 / sustained["update_pattern"] + 6 / sustained["stats_pattern"]) * mask_gbs / 20, 4),
             "score_stats_gbs": round(st_gbs, 2),
+            "sampler_ms_all_layers": round(sampler_ms, 3),
             "stage_ms": {k: round(v.total_ms, 3) for k, v in stage_ms.items()},
             # sixteen statistics per element: bound by VALU issue (about 58 instructions per element)
             "mask_stats": {"kernel": "sf_mask_stats", "GB/s": round(mstats_gbs, 2), "bytes_per_param": 4,

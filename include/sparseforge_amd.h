@@ -165,6 +165,21 @@ int sf_tau_quantile_noalloc(const sf_mask_params* p, const void* W, int w_dtype,
 int sf_sample_indices(int64_t* idx, int64_t sample_size, int64_t n, uint64_t seed, void* stream);
 
 /*
+ * Sorted sample indices for the tau quantile: `count` independent lists of
+ * sample_size indices, list c (at idx + c * sample_size) distributed as
+ * sample_size independent uniform draws from [0, n[c]) -- torch.randint's
+ * law at :993 -- and delivered in non-decreasing order (the quantile of a
+ * sample does not depend on its order).  seeds[c] seeds list c's counter
+ * generator; n and seeds are host arrays.  sf_update_mask_multi reads a
+ * sorted sample's keys from its statistics pass instead of gathering them.
+ * workspace: sf_sample_indices_sorted_workspace_size(sample_size, count)
+ * bytes.  sample_size < 2^28.
+ */
+size_t sf_sample_indices_sorted_workspace_size(int64_t sample_size, int count);
+int sf_sample_indices_sorted(int64_t* idx, int64_t sample_size, const int64_t* n, const uint64_t* seeds,
+                             int count, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Gate target G (compute_gate_target, legacy/sparse_modeling.py:1018-1239):
  * scores -> z-norm -> gate form -> beta structural mix -> frozen override.
  * G: [rows, cols] in g_dtype.  stats / tau: device scalars from the calls above

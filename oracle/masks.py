@@ -269,6 +269,26 @@ def hardening_x(step, start, duration) -> float:
     return max(0.0, min(1.0, 1.0 - progress))
 
 
+def sorted_sample_indices(m: int, n: int, seed: int) -> np.ndarray:
+    """The sorted tau sample the device draws (sf_sample_indices_sorted): m uniform draws from [0, n)
+    in non-decreasing order, int64.  The reference draws torch.randint(0, n, (m,)) (:993); the
+    quantile of a sample does not depend on its order.  E_j = -log((r_j + 1) 2^-53), r_j the top 53
+    bits of splitmix64(seed, j), j = 0..m, held as round(E_j 2^32); S_k = E_0 + ... + E_k (exact
+    integers); index k = floor(S_k / S_m * n), clamped below n.  (S_0 / S_m, ..., S_(m-1) / S_m) has
+    the law of the order statistics of m independent U(0, 1) (Devroye 1986, ch. V.2).
+    Pinned in tests/test_oracle_sampling.py by that law's closed-form moments, by the frequencies of
+    numpy's own uniform integers and by exhaustive counts on tiny n."""
+    from .hutchinson import splitmix64
+
+    j = np.arange(m + 1, dtype=np.uint64)
+    r = splitmix64(seed, j) >> np.uint64(11)
+    u = (r.astype(np.float64) + 1.0) * 2.0 ** -53
+    e = np.floor(-np.log(u) * 2.0 ** 32 + 0.5).astype(np.uint64)
+    s = np.cumsum(e, dtype=np.uint64)
+    idx = np.floor(s[:m].astype(np.float64) / float(s[m]) * float(n)).astype(np.int64)
+    return np.minimum(idx, n - 1)
+
+
 def quantile_linear(sample, q: float) -> np.float32:
     """torch.quantile(sample.float(), q) with linear interpolation (f32 ranks, torch lerp)."""
     v = np.sort(np.asarray(sample, dtype=np.float32).ravel())  # NaN sorts last

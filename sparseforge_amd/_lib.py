@@ -242,6 +242,8 @@ SIGNATURES = {
     "sf_tau_quantile": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _P, _I64, _F, _P, _P, _SZ, _P]),
     "sf_tau_quantile_noalloc": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _P, _I64, _F, _P, _P]),
     "sf_sample_indices": (_I, [_P, _I64, _I64, ctypes.c_uint64, _P]),
+    "sf_sample_indices_sorted_workspace_size": (_SZ, [_I64, _I]),
+    "sf_sample_indices_sorted": (_I, [_P, _I64, _P, _P, _I, _P, _SZ, _P]),
     "sf_gate_target": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P]),
     "sf_update_mask": (_I, [_MP, _P, _I, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P, _P]),
     "sf_update_mask_multi_workspace_size": (_SZ, [ctypes.POINTER(MaskLayer), _I]),

@@ -749,6 +749,117 @@ __global__ void __launch_bounds__(kBlock) sample_indices_kernel(int64_t* idx, in
 }
 
 // ---------------------------------------------------------------------------
+// Sorted tau samples: m indices distributed as m independent uniform draws
+// from [0, n) (torch.randint's law), delivered in non-decreasing order.  With
+// E_0..E_m independent Exp(1) and S_k = E_0 + ... + E_k, the vector
+// (S_0 / S_m, ..., S_(m-1) / S_m) has the law of the order statistics of m
+// independent U(0, 1) (L. Devroye, "Non-Uniform Random Variate Generation",
+// 1986, ch. V.2), and floor(U n) maps U(0, 1) to the uniform integers of
+// [0, n).  E_j = -log(U_j), U_j = (r_j + 1) 2^-53 from the top 53 bits of
+// counter_hash(seed, j); each E_j is held as the integer round(E_j 2^32), so
+// every partial sum is exact whatever the summation order (the chunks and the
+// workgroup scan below) and S_k is non-decreasing in k; the index is
+// floor(double(S_k) / double(S_m) n), a composition of non-decreasing
+// roundings, so the list is sorted by construction.
+// Pass 1 writes round(E_j 2^32) over the index list (j < m) and each chunk's
+// sum to the workspace; pass 2 turns the list into indices in place.
+// ---------------------------------------------------------------------------
+constexpr int kSortedPer = 16;                        // positions per thread
+constexpr int kSortedChunk = kBlock * kSortedPer;     // positions per workgroup
+constexpr int kSortedLists = 64;                      // lists per launch (kernel-argument table)
+
+struct SortedSampleArgs {
+  int64_t* idx;  // lists of m indices, list c at idx + c m
+  int64_t m;
+  int64_t chunks;  // workgroups per list: ceil((m + 1) / kSortedChunk)
+  uint64_t seed[kSortedLists];
+  int64_t n[kSortedLists];
+};
+
+__device__ __forceinline__ uint64_t exp_fixed(uint64_t seed, uint64_t j) {
+  const uint64_t r = counter_hash(seed, j) >> 11;
+  const double u = static_cast<double>(r + 1) * 0x1p-53;  // (0, 1]
+  const double e = -log(u);                              // [0, 36.8]
+  return static_cast<uint64_t>(e * 0x1p32 + 0.5);
+}
+
+// Exact sum of one value per thread (uint64, so any order gives the same total).
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v) {
+  __shared__ uint64_t part[kBlock / 64];
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kBlock / 64; ++w) t += part[w];
+  __syncthreads();
+  return t;
+}
+
+__global__ void __launch_bounds__(kBlock) sorted_sample_exp_kernel(SortedSampleArgs a, uint64_t* chunk_sums) {
+  const int c = blockIdx.y;
+  const int64_t j0 = (int64_t)blockIdx.x * kSortedChunk + (int64_t)threadIdx.x * kSortedPer;
+  uint64_t* out = reinterpret_cast<uint64_t*>(a.idx + c * a.m);
+  uint64_t s = 0;
+#pragma unroll
+  for (int k = 0; k < kSortedPer; ++k) {
+    const int64_t j = j0 + k;
+    if (j <= a.m) {
+      const uint64_t e = exp_fixed(a.seed[c], static_cast<uint64_t>(j));
+      s += e;
+      if (j < a.m) out[j] = e;
+    }
+  }
+  const uint64_t tot = block_sum_u64(s);
+  if (threadIdx.x == 0) chunk_sums[c * a.chunks + blockIdx.x] = tot;
+}
+
+__global__ void __launch_bounds__(kBlock) sorted_sample_idx_kernel(SortedSampleArgs a, const uint64_t* chunk_sums) {
+  const int c = blockIdx.y;
+  const uint64_t* cs = chunk_sums + c * a.chunks;
+  // sum of the chunks before this one, and of all (S_m)
+  uint64_t before = 0, all = 0;
+  for (int64_t h = threadIdx.x; h < a.chunks; h += kBlock) {
+    const uint64_t v = cs[h];
+    all += v;
+    if (h < (int64_t)blockIdx.x) before += v;
+  }
+  before = block_sum_u64(before);
+  all = block_sum_u64(all);
+  // this thread's positions, their sum, and the exclusive scan of the thread sums
+  const int64_t j0 = (int64_t)blockIdx.x * kSortedChunk + (int64_t)threadIdx.x * kSortedPer;
+  uint64_t* e = reinterpret_cast<uint64_t*>(a.idx + c * a.m);
+  uint64_t v[kSortedPer];
+  uint64_t s = 0;
+#pragma unroll
+  for (int k = 0; k < kSortedPer; ++k) {
+    v[k] = j0 + k < a.m ? e[j0 + k] : 0;
+    s += v[k];
+  }
+  __shared__ uint64_t scan[kBlock];
+  scan[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 1; o < kBlock; o <<= 1) {  // inclusive Hillis-Steele scan (exact: integers)
+    const uint64_t add = threadIdx.x >= o ? scan[threadIdx.x - o] : 0;
+    __syncthreads();
+    scan[threadIdx.x] += add;
+    __syncthreads();
+  }
+  uint64_t run = before + scan[threadIdx.x] - s;
+  const double total = static_cast<double>(all);
+  const int64_t n = a.n[c];
+  const double dn = static_cast<double>(n);
+#pragma unroll
+  for (int k = 0; k < kSortedPer; ++k) {
+    if (j0 + k < a.m) {
+      run += v[k];
+      int64_t i = static_cast<int64_t>(static_cast<double>(run) / total * dn);
+      a.idx[c * a.m + j0 + k] = i < n ? i : n - 1;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // K7 / K8: gate target of one group, and the fused update.
 // ---------------------------------------------------------------------------
 struct GateSpec {
@@ -1097,7 +1208,7 @@ struct MultiLayer {
   int32_t nblk;        // workgroups of the layer's update grid
   int32_t vec;         // vector-loadable groups
   int32_t nsel;        // workgroups of the layer's radix passes
-  int32_t pad;
+  int32_t win_off;     // first window start of the layer in the window-start buffer (statistics fold)
 };
 
 struct MultiArgs {
@@ -1136,6 +1247,190 @@ __global__ void __launch_bounds__(kBlock) stats_partial_multi_kernel(MultiArgs a
   const int64_t gpr = ceil_div(L.cols, 4);
   stats_partial_block<WD, HD, VEC, RATIO, true>(a.us.gs.s, L.W, L.H, L.aux, L.cols, L.rows * gpr, gpr, L.vec != 0,
                                           partial + (int64_t)l * 2 * kStatsGrid, blk);
+}
+
+// ---------------------------------------------------------------------------
+// Statistics with the tau sample folded in (batched update, every layer's
+// groups vector-loadable).  Round r of statistics workgroup b covers the
+// 1024 elements [1024 (b + r kStatsGrid), +1024), each wave a 256-element
+// sub-window of them (64 lanes x one group), so every element is scored
+// exactly once per pass.  When a layer's sample is in non-decreasing index
+// order, the samples that fall in sub-window v are the positions
+// [wstart[v], wstart[v + 1]) of the list: the wave stages its sub-window's
+// scores in LDS and those samples take their keys from there, instead of a
+// separate gather reading W and H at random positions (at a 262 144 sample
+// over a 4096 x 4096 layer that gather touches about 63 % of W's 128-byte
+// lines and 39 % of H's).  Each wave works alone (no workgroup barrier: LDS
+// accesses of one wave are performed in order), a round's samples are
+// resolved one iteration later, so their index loads have a whole iteration
+// to arrive, and only sampled scores are turned into keys: the pass is
+// bound by its score arithmetic, and every instruction added per element
+// shows.  The keys land where the gather puts them (key i for sample i), so
+// the selection and tau are unchanged.  A layer whose sample is not sorted
+// gets empty sub-window ranges and is gathered at random by
+// sample_windows_multi_kernel instead.
+// ---------------------------------------------------------------------------
+constexpr int kWinShift = 8;  // log2 of a sub-window: one wave's 64 groups of 4
+constexpr int kWinGrid = 64;  // workgroups per layer of the order check: one flag per lane of a wave
+
+__device__ __forceinline__ int64_t clamp_index(int64_t e, int64_t n) { return e < 0 ? 0 : (e >= n ? n - 1 : e); }
+
+// ok[l][b] = 1 when the (clamped) sample indices workgroup b checked are in non-decreasing order.
+__global__ void __launch_bounds__(kBlock) sample_order_multi_kernel(MultiArgs a, int32_t* ok) {
+  const int l = blockIdx.y;
+  const MultiLayer& L = a.l[l];
+  if (!L.idx) return;  // uniform: the whole workgroup
+  const int64_t n = L.rows * L.cols;
+  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x, nth = (int64_t)kWinGrid * kBlock;
+  bool bad = false;
+  for (int64_t i = tid + 1; i < L.m; i += nth) bad = bad || clamp_index(L.idx[i - 1], n) > clamp_index(L.idx[i], n);
+  const int any = __syncthreads_or(bad ? 1 : 0);
+  if (threadIdx.x == 0) ok[l * kWinGrid + blockIdx.x] = any ? 0 : 1;
+}
+
+// Sub-window starts: wstart[v] = the first sample position whose (clamped) index is at least 256 v,
+// v = 0..nsub (nsub = the layer's sub-windows; wstart[nsub] = m), written by the samples that open them
+// (sample i writes the sub-windows after its predecessor's, up to its own: nsub + 1 writes in all).  A
+// layer whose sample is not sorted gets wstart = 0 everywhere (empty ranges), and its sample's keys are
+// gathered here at random positions instead.
+__global__ void __launch_bounds__(kBlock) sample_windows_multi_kernel(MultiArgs a, const int32_t* ok,
+                                                                      int32_t* wstart, uint32_t* keys) {
+  const int l = blockIdx.y;
+  const MultiLayer& L = a.l[l];
+  if (!L.idx) return;
+  const int64_t n = L.rows * L.cols, m = L.m;
+  const int64_t nsub = (n + (1 << kWinShift) - 1) >> kWinShift;
+  int32_t* ws = wstart + L.win_off;
+  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x, nth = (int64_t)gridDim.x * kBlock;
+  const bool sorted = __all(ok[l * kWinGrid + (threadIdx.x & 63)] != 0);
+  if (!sorted) {  // empty ranges for the statistics pass; the sample is gathered here, at random
+    for (int64_t v = tid; v <= nsub; v += nth) ws[v] = 0;
+    tau_gather_block(a.us.gs.s, L.W, L.H, L.aux, L.rows, L.cols, L.idx, m, keys + L.keys_off, blockIdx.x,
+                     gridDim.x);
+    return;
+  }
+  for (int64_t i = tid; i < m; i += nth) {
+    const int64_t v = clamp_index(L.idx[i], n) >> kWinShift;
+    const int64_t from = i == 0 ? 0 : (clamp_index(L.idx[i - 1], n) >> kWinShift) + 1;
+    for (int64_t u = from; u <= v; ++u) ws[u] = static_cast<int32_t>(i);
+    if (i == m - 1)
+      for (int64_t u = v + 1; u <= nsub; ++u) ws[u] = static_cast<int32_t>(m);
+  }
+}
+
+// The statistics of one workgroup with the sample's keys folded in; hessian_ratio scores (|W| / sqrt(H + eps),
+// no aux operand: the paper's metric), so the walk is a plain group index (element = 4 x group).
+template <int WD, int HD>
+__device__ __forceinline__ void stats_fold_block(const ScoreSpec& s_in, const MultiLayer& L,
+                                                 const int32_t* __restrict__ wstart, uint32_t* __restrict__ keys,
+                                                 double* partial, int blk) {
+  ScoreSpec s = s_in;
+  s.metric = SF_METRIC_HESSIAN_RATIO;
+  const int64_t groups = L.rows * (L.cols >> 2), n = L.rows * L.cols;
+  const int64_t* idx = L.idx;
+  uint32_t* kout = keys + L.keys_off;
+  const int32_t* ws = wstart + L.win_off;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // raw scores of the wave's two sub-windows of an iteration, double-buffered: [wave][parity][round][element]
+  __shared__ __align__(16) float win[kBlock / 64][2][2][256];
+  float(*mine)[2][256] = win[wave];
+  const int64_t stride = (int64_t)kStatsGrid * kBlock;
+  double sum = 0.0, sq = 0.0;
+  // The previous iteration's samples, resolved in one pass: lane l serves sample (l % 32) of sub-window
+  // l / 32 (rounds 0 and 1), so its range, element base and first index are this lane's.
+  const int h = lane >> 5, j = lane & 31;
+  int32_t ps = 0, pe = 0;  // the lane's sub-window: sample positions [ps, pe)
+  int64_t pb = 0;          // its first element
+  int64_t pv = 0;          // index of sample ps + j
+  int par = 0;
+  auto resolve = [&](int pp) {
+    for (int32_t i = ps + j; i < pe; i += 32) {
+      const int64_t e = i == ps + j ? pv : idx[i];
+      int64_t off = e - pb;  // clamp_index(e, n) - pb: the clamped ends lie in the first / last sub-window
+      off = off < 0 ? 0 : off;
+      off = off > n - 1 - pb ? n - 1 - pb : off;
+      kout[i] = ordered_key(mine[pp][h][off]);
+    }
+  };
+  auto load_group = [&](int64_t g, GroupOps& o) {
+    Group G;
+    G.row = 0;
+    G.col = 0;
+    G.elem = 4 * g;
+    G.n = 4;
+    G.full = true;
+    load_group_ops<WD, HD, true>(s, L.W, L.H, nullptr, G, true, o);
+  };
+  auto score_ops = [&](const GroupOps& o, float sc[4]) {
+    Group G;
+    G.n = 4;
+    scores_of_ops<WD, HD>(s, o, G, sc);
+  };
+  // two rounds per iteration, both loaded before either is used (a lane past the layer loads group 0 and
+  // discards it, so the loads are unconditional); the loop bound is wave-uniform and each thread adds its
+  // groups in the order of stats_partial_block
+  for (int64_t base = (int64_t)blk * kBlock + 64 * wave; base < groups; base += 2 * stride, par ^= 1) {
+    const bool two = base + stride < groups;
+    const int64_t g0 = base + lane, g1 = base + stride + lane;
+    const bool live0 = g0 < groups, live1 = g1 < groups;
+    GroupOps o0, o1;
+    load_group(live0 ? g0 : 0, o0);
+    load_group(live1 ? g1 : 0, o1);
+    const int64_t v0 = base >> (kWinShift - 2), v1 = (base + stride) >> (kWinShift - 2);
+    int32_t s0 = 0, e0 = 0, s1 = 0, e1 = 0;
+    if (idx) {
+      s0 = ws[v0];
+      e0 = ws[v0 + 1];
+      if (two) {
+        s1 = ws[v1];
+        e1 = ws[v1 + 1];
+      }
+      resolve(par ^ 1);  // the previous iteration's samples, from the other buffer
+    }
+    float sc0[4], sc1[4];
+    score_ops(o0, sc0);
+    score_ops(o1, sc1);
+    if (live0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const double d = sc0[k];
+        sum += d;
+        sq += d * d;
+      }
+    }
+    if (live1) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const double d = sc1[k];
+        sum += d;
+        sq += d * d;
+      }
+    }
+    if (!idx) {  // the sample is every element, in element order (4-byte stores: keys_off may be odd)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (live0) kout[4 * g0 + k] = ordered_key(sc0[k]);
+        if (live1) kout[4 * g1 + k] = ordered_key(sc1[k]);
+      }
+      continue;
+    }
+    if (e0 > s0 && live0) *reinterpret_cast<float4*>(&mine[par][0][4 * lane]) = make_float4(sc0[0], sc0[1], sc0[2], sc0[3]);
+    if (e1 > s1 && live1) *reinterpret_cast<float4*>(&mine[par][1][4 * lane]) = make_float4(sc1[0], sc1[1], sc1[2], sc1[3]);
+    // this iteration's samples: the lane's first index loads now, the rest after the next iteration's loads
+    ps = h ? s1 : s0;
+    pe = h ? e1 : e0;
+    pb = (h ? v1 : v0) << kWinShift;
+    pv = ps + j < pe ? idx[ps + j] : 0;
+  }
+  if (idx) resolve(par ^ 1);
+  block_sum2_f64(sum, sq, &partial[2 * blk], &partial[2 * blk + 1]);
+}
+
+template <int WD, int HD>
+__global__ void __launch_bounds__(kBlock) stats_fold_multi_kernel(MultiArgs a, double* partial, uint32_t* keys,
+                                                                  const int32_t* wstart) {
+  const int l = blockIdx.x / kStatsGrid, blk = blockIdx.x - l * kStatsGrid;
+  stats_fold_block<WD, HD>(a.us.gs.s, a.l[l], wstart, keys, partial + (int64_t)l * 2 * kStatsGrid, blk);
 }
 
 __global__ void __launch_bounds__(kBlock) stats_final_multi_kernel(MultiArgs a, const double* partial) {
@@ -1433,6 +1728,43 @@ extern "C" int sf_sample_indices(int64_t* idx, int64_t sample_size, int64_t n, u
   return launch_status("sf_sample_indices");
 }
 
+extern "C" size_t sf_sample_indices_sorted_workspace_size(int64_t sample_size, int count) {
+  if (sample_size < 0 || count <= 0) return 0;
+  return sizeof(uint64_t) * static_cast<size_t>(count) * static_cast<size_t>(ceil_div(sample_size + 1, kSortedChunk));
+}
+
+extern "C" int sf_sample_indices_sorted(int64_t* idx, int64_t sample_size, const int64_t* n, const uint64_t* seeds,
+                                        int count, void* workspace, size_t workspace_bytes, void* stream) {
+  SF_CHECK_ARG(sample_size >= 0 && count >= 0, "bad sample size %lld / count %d", (long long)sample_size, count);
+  // the fixed-point sums stay below 2^64: S_m is about (m + 1) 2^32 and one term is at most 37 2^32
+  SF_CHECK_ARG(sample_size < (int64_t(1) << 30), "sample size %lld above 2^30", (long long)sample_size);
+  if (sample_size == 0 || count == 0) return SF_OK;
+  SF_CHECK_ARG(idx && n && seeds, "null argument");
+  for (int c = 0; c < count; ++c) SF_CHECK_ARG(n[c] > 0, "list %d: n = %lld", c, (long long)n[c]);
+  SF_CHECK_ARG(workspace && workspace_bytes >= sf_sample_indices_sorted_workspace_size(sample_size, count),
+               "workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t chunks = ceil_div(sample_size + 1, kSortedChunk);
+  SF_CHECK_ARG(chunks < 65536, "sample size %lld needs too many chunks", (long long)sample_size);
+  uint64_t* sums = static_cast<uint64_t*>(workspace);
+  for (int c0 = 0; c0 < count; c0 += kSortedLists) {
+    const int k = count - c0 < kSortedLists ? count - c0 : kSortedLists;
+    SortedSampleArgs a;
+    memset(&a, 0, sizeof(a));
+    a.idx = idx + static_cast<int64_t>(c0) * sample_size;
+    a.m = sample_size;
+    a.chunks = chunks;
+    for (int c = 0; c < k; ++c) {
+      a.seed[c] = seeds[c0 + c];
+      a.n[c] = n[c0 + c];
+    }
+    const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(k));
+    sorted_sample_exp_kernel<<<grid, kBlock, 0, st>>>(a, sums + static_cast<int64_t>(c0) * chunks);
+    sorted_sample_idx_kernel<<<grid, kBlock, 0, st>>>(a, sums + static_cast<int64_t>(c0) * chunks);
+  }
+  return launch_status("sf_sample_indices_sorted");
+}
+
 namespace sf {
 namespace {
 // Argument checks and launches of the tau selection, over a scratch region `ws`
@@ -1709,6 +2041,11 @@ size_t multi_partial_bytes() { return align256(sizeof(double) * 2 * kStatsGrid *
 size_t multi_states_bytes() { return align256(sizeof(SelState) * 2 * kMultiLayers); }
 size_t multi_hist_bytes() { return align256(sizeof(uint32_t) * kSelStride * kSelGrid * kMultiLayers); }
 size_t multi_keys_off() { return multi_partial_bytes() + multi_states_bytes() + 2 * multi_hist_bytes(); }
+size_t multi_ok_bytes() { return align256(sizeof(int32_t) * kWinGrid * kMultiLayers); }
+// window starts of a layer's sample for the statistics fold (windows + 1 entries)
+int64_t layer_window_starts(const sf_mask_layer& l) {
+  return ((l.rows * l.cols + (1 << kWinShift) - 1) >> kWinShift) + 1;
+}
 
 bool layer_empty(const sf_mask_layer& l) { return l.rows == 0 || l.cols == 0; }
 
@@ -1735,25 +2072,33 @@ void for_each_batch(const sf_mask_layer* layers, int count, F&& f) {
 }
 
 // Workspace of sf_update_mask_multi.  Serial layout: [stats partials | select states | radix partials x 2 |
-// keys].  The pipelined schedule (below) appends a second stats-partials region and a second keys region,
+// keys | sample window starts | sample order flags].  The pipelined schedule (below) appends a second
+// stats-partials region and a second keys region,
 // so that batch b + 1's statistics and tau gather never write what batch b's selection still reads.  It is
 // offered only while a batch's sample keys stay below kOverlapMaxKeys (a tau sample over every element of
 // large layers would double a workspace of gigabytes).
 constexpr int64_t kOverlapMaxKeys = int64_t(1) << 25;
 struct MultiSizes {
   int64_t keys = 0;  // largest batch's sample keys
+  int64_t wins = 0;  // largest batch's window starts (layers with sample indices)
   int batches = 0;
-  size_t serial_bytes = 0, overlap_bytes = 0, keys1_off = 0, partial1_off = 0;
+  size_t serial_bytes = 0, overlap_bytes = 0, keys1_off = 0, partial1_off = 0, wins_off = 0, ok_off = 0;
 };
 MultiSizes multi_sizes(const sf_mask_layer* layers, int count) {
   MultiSizes z;
   if (layers && count > 0)
-    for_each_batch(layers, count, [&](int, int, int64_t k) {
+    for_each_batch(layers, count, [&](int first, int end, int64_t k) {
       z.keys = k > z.keys ? k : z.keys;
+      int64_t wn = 0;
+      for (int i = first; i < end; ++i)
+        if (!layer_empty(layers[i]) && layers[i].sample_idx) wn += layer_window_starts(layers[i]);
+      z.wins = wn > z.wins ? wn : z.wins;
       ++z.batches;
     });
   const size_t kb = sizeof(uint32_t) * static_cast<size_t>(z.keys);
-  z.serial_bytes = multi_keys_off() + kb;
+  z.wins_off = align256(multi_keys_off() + kb);
+  z.ok_off = z.wins_off + align256(sizeof(int32_t) * static_cast<size_t>(z.wins));
+  z.serial_bytes = z.ok_off + multi_ok_bytes();
   z.partial1_off = align256(z.serial_bytes);
   z.keys1_off = z.partial1_off + multi_partial_bytes();
   z.overlap_bytes = z.keys1_off + kb;
@@ -1852,7 +2197,7 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
   struct Batch {
     MultiArgs a;
     int n, total, gather_grid;
-    bool all_vec;
+    bool all_vec, any_idx, fold;
   };
   std::vector<Batch> batches;
   batches.reserve(static_cast<size_t>(z.batches));
@@ -1863,8 +2208,8 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
     memset(&a, 0, sizeof(a));
     a.us = us;
     int n = 0, gather_grid = 1;
-    bool all_vec = true;
-    int64_t koff = 0;
+    bool all_vec = true, any_idx = false, fold_ok = true;
+    int64_t koff = 0, woff = 0;
     a.first[0] = 0;
     for (int i = first; i < end; ++i) {
       const sf_mask_layer& l = layers[i];
@@ -1896,6 +2241,13 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
         koff += l.sample_size;
         const int gg = elementwise_grid(l.sample_size, kBlock);
         gather_grid = gg > gather_grid ? gg : gather_grid;
+        // the fold keeps sample positions and window starts in int32
+        fold_ok = fold_ok && l.sample_size <= INT32_MAX;
+        if (l.sample_idx) {
+          any_idx = true;
+          L.win_off = static_cast<int32_t>(woff);
+          woff += layer_window_starts(l);
+        }
       }
       a.first[n + 1] = a.first[n] + L.nblk;
       ++n;
@@ -1905,13 +2257,27 @@ extern "C" int sf_update_mask_multi(const sf_mask_params* p, float q, const sf_m
     bt.total = a.first[n];
     bt.gather_grid = gather_grid;
     bt.all_vec = all_vec;
+    bt.any_idx = any_idx;
+    bt.fold = all_vec && fold_ok && woff <= INT32_MAX && p->metric == SF_METRIC_HESSIAN_RATIO;
   });
 
   const bool want_tau = unstructured && (stages & SF_MULTI_TAU);
   // the tau gather rides in the statistics launch when both stages run
   const bool fused_gather = want_tau && (stages & SF_MULTI_STATS);
+  int32_t* wins = reinterpret_cast<int32_t*>(ws + z.wins_off);
+  int32_t* okf = reinterpret_cast<int32_t*>(ws + z.ok_off);
   auto launch_stats = [&](const Batch& bt, double* partial, uint32_t* keys) {
     const MultiArgs& a = bt.a;
+    if (fused_gather && bt.fold) {
+      // the tau sample's keys from the statistics pass itself (sorted samples; others gathered beside it)
+      if (bt.any_idx) {
+        sample_order_multi_kernel<<<dim3(kWinGrid, bt.n), kBlock, 0, st>>>(a, okf);
+        sample_windows_multi_kernel<<<dim3(kWinGrid, bt.n), kBlock, 0, st>>>(a, okf, wins, keys);
+      }
+      SF_DISPATCH_WH(w_dtype, h_dtype,
+                     stats_fold_multi_kernel<WD_, HD_><<<bt.n * kStatsGrid, kBlock, 0, st>>>(a, partial, keys, wins));
+      return;
+    }
     const int g = fused_gather ? bt.gather_grid : 0;
     const int grid = bt.n * g + bt.n * kStatsGrid;
     if (bt.all_vec && p->metric == SF_METRIC_HESSIAN_RATIO)

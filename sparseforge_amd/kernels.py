@@ -120,6 +120,25 @@ def sample_indices(sample_size: int, n: int, seed: int, device: torch.device) ->
     return idx
 
 
+def sample_indices_sorted(sample_size: int, ns, seeds, device: torch.device) -> torch.Tensor:
+    """[len(ns), sample_size] int64: row c holds sample_size uniform draws from [0, ns[c]) in
+    non-decreasing order (sf_sample_indices_sorted), from the counter generator seeded by seeds[c]."""
+    ns, seeds = [int(v) for v in ns], [int(v) & ((1 << 64) - 1) for v in seeds]
+    if len(ns) != len(seeds):
+        raise ValueError("one seed per list")
+    count = len(ns)
+    idx = torch.empty((count, sample_size), dtype=torch.int64, device=device)
+    if count == 0 or sample_size == 0:
+        return idx
+    ws = _ws(L.lib().sf_sample_indices_sorted_workspace_size(sample_size, count), device)
+    n_arr = (ctypes.c_int64 * count)(*ns)
+    s_arr = (ctypes.c_uint64 * count)(*seeds)
+    L.check(L.lib().sf_sample_indices_sorted(L.ptr(idx), sample_size, n_arr, s_arr, count, L.ptr(ws), ws.numel(),
+                                             L.stream(device)),
+            "sf_sample_indices_sorted")
+    return idx
+
+
 def tau_quantile(p: L.MaskParams, ops: MaskOperands, stats: torch.Tensor, q: float,
                  sample_idx: torch.Tensor | None) -> torch.Tensor:
     dev = ops.device()

@@ -149,6 +149,8 @@ def calculate_model_mask(model, step=0, lambda_mid: float = 0.0):
     # (sf_update_mask_multi: a few launches per 28 layers, results equal to one update_mask per
     # layer); the block hard types and block penalty modes keep their multi-pass update.
     batches: dict = {}
+    draws: dict = {}    # (device, sample size) -> [(size, numel, seed)] of the batched layers
+    samples: dict = {}  # id of a draw -> its sorted sample
     for name, m in mods.items():
         if name in handled:
             continue
@@ -169,11 +171,21 @@ def calculate_model_mask(model, step=0, lambda_mid: float = 0.0):
         key = (ops.device(), tuple(ops.dt(t) if t is not None else -1
                                    for t in (ops.weight, ops.hessian, ops.aux, ops.mask, ops.frozen)),
                bytes(shape_free), q)
-        # the tau sample, drawn here so every layer (staged or batched) draws in module order, as one
-        # update_mask per layer does
-        idx = m._sample_indices(ops.weight.numel(), ops.device()) if p.gate == L.GATE_UNSTRUCTURED else None
-        batches.setdefault(key, []).append((m, ops, p, idx))
+        # the tau sample's seed, drawn here so every layer (staged or batched) draws in module order, as one
+        # update_mask per layer does; the samples themselves are generated below, several lists per launch
+        seed = m._sample_seed(ops.weight.numel()) if p.gate == L.GATE_UNSTRUCTURED else None
+        idx = None
+        if seed is not None:
+            idx = (m._sample_size(ops.weight.numel()), ops.weight.numel(), seed)
+            draws.setdefault((ops.device(), idx[0]), []).append(idx)
+        batches.setdefault(key, []).append([m, ops, p, idx])
+    for (dev, size), lists in draws.items():
+        rows = K.sample_indices_sorted(size, [n for _, n, _ in lists], [s for _, _, s in lists], dev)
+        for r, spec in enumerate(lists):
+            samples[id(spec)] = rows[r]
     for (dev, _dts, _pb, q), items in batches.items():
+        for it in items:
+            it[3] = samples[id(it[3])] if it[3] is not None else None
         n = len(items)
         stats = torch.empty((n, 2), dtype=torch.float32, device=dev)
         tau = torch.empty(n, dtype=torch.float32, device=dev)

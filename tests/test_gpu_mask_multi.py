@@ -281,3 +281,76 @@ def test_calculate_model_mask_mixed_paths_draw_in_module_order(cuda_device):
     for k, (ma, mb) in enumerate(zip(a, b)):
         assert torch.equal(ma.mask, mb.mask), (k, ma.weight.shape)
         assert int(ma.weight.flipped_mask) == int(mb.weight.flipped_mask), k
+
+
+# shapes whose groups are all vector-loadable, so the batched update reads the tau sample's keys from its
+# statistics pass: windows of 1024 elements, partial last windows, one-window and sub-window layers
+VEC_SHAPES = [(64, 256), (96, 1020), (33, 68), (128, 4096), (40, 4), (256, 512), (1, 1024), (3, 8), (130, 96)]
+
+
+def _vec_layers(K, dev, n, seed, sampling):
+    """sampling(i, numel, g) -> the layer's sample indices (or None for every element)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    out = []
+    for i in range(n):
+        rows, cols = VEC_SHAPES[i % len(VEC_SHAPES)]
+        W = (torch.randn(rows, cols, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        H = torch.rand(rows, cols, generator=g, device=dev) * 1e-3 + 1e-6
+        M = torch.rand(rows, cols, generator=g, device=dev)
+        out.append((W, H, M, None, sampling(i, rows * cols, g)))
+    return out
+
+
+def _sorted_sampling(K, dev):
+    def f(i, numel, g):
+        kind = i % 5
+        if kind == 0:
+            return None  # every element
+        if kind == 1:  # the library's sorted sampler
+            return K.sample_indices_sorted(4099, [numel], [77 + i], dev)[0]
+        if kind == 2:  # sorted torch.randint draws (duplicates), with out-of-range ends that clamp
+            v = torch.sort(torch.randint(0, numel, (3001,), generator=g, device=dev)).values
+            return torch.cat([torch.tensor([-3], device=dev), v, torch.tensor([numel + 5], device=dev)])
+        if kind == 3:  # unsorted: gathered by the statistics workgroups
+            return torch.randint(0, numel, (2048,), generator=g, device=dev)
+        # sorted, denser than one sample per element (many samples per window)
+        return K.sample_indices_sorted(3 * numel, [numel], [5 + i], dev)[0]
+    return f
+
+
+@pytest.mark.parametrize("n_layers", [9, 61])
+def test_multi_fold_equals_single_layer_calls(cuda_device, n_layers):
+    """Every layer vector-loadable: the statistics pass writes the keys of sorted samples from its own
+    windows, unsorted samples are gathered by the same workgroups, full samples are written in element
+    order.  Stats, tau, masks and flip counts equal the single-layer calls (whose tau gathers every sample
+    at random) bit for bit; 61 layers run three batches on the pipelined schedule."""
+    L, K = _lib()
+    p0 = _params(L, "unstructured")
+    layers = _vec_layers(K, cuda_device, n_layers, 21, _sorted_sampling(K, cuda_device))
+    a, b = _clone(layers), _clone(layers)
+    for q in (0.37, 0.81):
+        s_stats, s_tau, s_flips = _single(L, K, p0, q, a)
+        m_stats, m_tau, m_flips = _multi(L, K, p0, q, b)
+        torch.cuda.synchronize()
+        for i, ((W, _, M, _, idx), (_, _, M2, _, _)) in enumerate(zip(a, b)):
+            assert torch.equal(m_stats[i], s_stats[i]), (q, i, W.shape)
+            assert torch.equal(m_tau[i:i + 1], s_tau[i]), (q, i, W.shape, None if idx is None else idx.numel())
+            assert torch.equal(M2, M), (q, i, W.shape)
+            assert int(m_flips[i]) == int(s_flips[i]), (q, i)
+
+
+def test_multi_fold_nan_scores(cuda_device):
+    """A NaN weight makes its score NaN: the folded keys carry it, and tau is NaN as with the gather."""
+    L, K = _lib()
+    p0 = _params(L, "unstructured")
+    layers = _vec_layers(K, cuda_device, 4, 5, lambda i, numel, g: K.sample_indices_sorted(
+        max(numel // 2, 1), [numel], [i], cuda_device)[0])
+    W = layers[0][0]
+    W.view(-1)[layers[0][4][7]] = float("nan")
+    a, b = _clone(layers), _clone(layers)
+    _s, s_tau, _f = _single(L, K, p0, 0.5, a)
+    _s2, m_tau, _f2 = _multi(L, K, p0, 0.5, b)
+    torch.cuda.synchronize()
+    assert torch.isnan(m_tau[0]) and torch.isnan(s_tau[0])
+    for i in range(1, 4):
+        assert torch.equal(m_tau[i:i + 1], s_tau[i]), i
