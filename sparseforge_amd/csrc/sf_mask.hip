@@ -156,6 +156,28 @@ __device__ __forceinline__ float sqrt_rn(float x) {
   return odd ? alt : r;
 }
 
+// sqrt_rn of the four values of a group with one range test and one branch: x is in [2^-96, 2^127)
+// exactly when its bit pattern minus that of 2^-96 is below the width of the range (as unsigned: negative
+// values, zeros, subnormals, inf and NaN all fall outside).  Both paths round correctly, so a group with
+// one value outside the range may recompute all four with sqrtf and give the same results.
+__device__ __forceinline__ void sqrt_rn4(const float x[4], float r[4]) {
+  constexpr uint32_t lo = 0x0F800000u, width = 0x7F000000u - 0x0F800000u;  // 2^-96, 2^127
+  uint32_t u = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t d = __float_as_uint(x[j]) - lo;
+    u = d > u ? d : u;
+    const float y = __builtin_amdgcn_sqrtf(x[j]);
+    const float dn = __int_as_float(__float_as_int(y) - 1), up = __int_as_float(__float_as_int(y) + 1);
+    float t = fmaf(-dn, y, x[j]) <= 0.0f ? dn : y;
+    r[j] = fmaf(-up, y, x[j]) > 0.0f ? up : t;
+  }
+  if (__builtin_expect(u >= width, 0)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = sqrtf(x[j]);
+  }
+}
+
 template <int WD, int HD>
 __device__ __forceinline__ float score_of(const ScoreSpec& s, float w, float h, float a) {
   constexpr int PWH = (WD == SF_DTYPE_F32 || HD == SF_DTYPE_F32) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
@@ -221,6 +243,16 @@ __device__ __forceinline__ void load_group_ops(const ScoreSpec& s, const void* W
 template <int WD, int HD>
 __device__ __forceinline__ void scores_of_ops(const ScoreSpec& s, const GroupOps& o, const Group& g, float sc[4]) {
   const float *w = o.w, *h = o.h, *a = o.a;
+  if (s.metric == SF_METRIC_HESSIAN_RATIO && g.n == 4) {  // |W| / sqrt(H + eps), the sqrt range test per group
+    constexpr int PWH = (WD == SF_DTYPE_F32 || HD == SF_DTYPE_F32) ? SF_DTYPE_F32 : SF_DTYPE_BF16;
+    float hp[4], sq[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hp[j] = rndc<HD>(h[j] + s.eps);
+    sqrt_rn4(hp, sq);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = rndc<PWH>(fabsf(w[j]) / rndc<HD>(sq[j]));
+    return;
+  }
   // one switch per group, the element loop inside each case
   switch (s.metric) {
 #define SF_SCORES_CASE(M)                                                                            \
