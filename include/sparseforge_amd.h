@@ -478,6 +478,26 @@ int sf_softmax_rows_double_backward(const void* x, const void* grad_p, const voi
                                     int64_t rows, int64_t cols, int causal, void* grad_grad_p, void* grad2_x,
                                     void* stream);
 
+/*
+ * Per-head operands of the retraining model's attention (HuggingFace eager
+ * LlamaAttention, legacy/model_llama.py:39-55: q/k/v views [B, S, H, D]
+ * transposed to [B, H, S, D], apply_rotary_pos_emb on q and k).  x is
+ * [B, S, H * D] (the projections' rows); y is [B * H, S, D], or [B * H, D, S]
+ * when `transposed` (the key operand of q k^T).
+ *   sf_to_heads:   y = scale * rot(x), or scale * x without `rotate`
+ *   sf_from_heads: its adjoint, x_grad [B, S, H * D] = rot^T(scale * g)
+ * rot(x)[d] = x[d] c[d] + x[(d + D/2) % D] ss[d] with c = cos, ss = -sin on
+ * the first half and sin on the second (cos, sin: f32 tables [S, D], rounded
+ * to the dtype), each product rounded to the dtype, then their sum; the
+ * adjoint rounds the same way, so the pair equals torch's ops and their
+ * derivatives bit for bit.  dtype f32 or bf16, D a multiple of 16 up to 128,
+ * 16-byte aligned tensors, scale 1 or a power of two.
+ */
+int sf_to_heads(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, const float* cos,
+                const float* sin, int rotate, int transposed, float scale, void* y, void* stream);
+int sf_from_heads(const void* g, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, const float* cos,
+                  const float* sin, int rotate, int transposed, float scale, void* x_grad, void* stream);
+
 /* ---- GEMM engine (FusedMaskedLinearSTE, :56-132, and the SLoRB F.linear pair, :790-794) */
 #define SF_LAYOUT_K 0  /* operand stored K-contiguous: X[row * ld + k]                        */
 #define SF_LAYOUT_MN 1 /* operand stored M/N-contiguous: X[k * ld + row] (a transposed view)  */

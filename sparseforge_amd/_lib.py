@@ -266,6 +266,8 @@ SIGNATURES = {
     "sf_kl_workspace_size": (ctypes.c_size_t, [_I64]),
     "sf_kl_forward": (_I, [_P, _P, _I, _I64, _I64, _F, _I64, _P, _I, _P, _P, _P, ctypes.c_size_t, _P]),
     "sf_kl_backward": (_I, [_P, _P, _I, _I64, _I64, _F, _P, _P, _P, _I, _P, _P]),
+    "sf_to_heads": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _I, _F, _P, _P]),
+    "sf_from_heads": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _I, _F, _P, _P]),
     "sf_softmax_rows": (_I, [_P, _I, _I64, _I64, _I, _P, _P]),
     "sf_softmax_rows_backward": (_I, [_P, _P, _I, _I64, _I64, _I, _P, _P]),
     "sf_softmax_rows_double_backward": (_I, [_P, _P, _P, _I, _I64, _I64, _I, _P, _P, _P]),

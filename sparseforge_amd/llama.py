@@ -193,6 +193,67 @@ def causal_softmax(scores: torch.Tensor) -> torch.Tensor:
     return torch.softmax(scores, dim=-1, dtype=torch.float32).to(scores.dtype)
 
 
+def _heads_launch(name: str, fn, src: torch.Tensor, dst: torch.Tensor, B: int, S: int, H: int, D: int,
+                  cos: torch.Tensor, sin: torch.Tensor, rotate: bool, transposed: bool, scale: float) -> None:
+    dev = L.require_device(src, dst)
+    with _prof.region(name, 2 * src.numel() * src.element_size(), "B", dev):
+        L.check(fn(L.ptr(src), L.dtype_code(src), B, S, H, D, L.ptr(cos), L.ptr(sin), int(rotate), int(transposed),
+                   float(scale), L.ptr(dst), L.stream(dev)), name)
+
+
+def _head_major(g: torch.Tensor, transposed: bool) -> tuple[torch.Tensor, bool]:
+    """A head-major gradient as the kernels read it: contiguous in the expected layout, or the transposed view of
+    a contiguous tensor of the other layout (the flag flips, no copy); otherwise a contiguous copy."""
+    if g.is_contiguous():
+        return g, transposed
+    if g.transpose(1, 2).is_contiguous():
+        return g.transpose(1, 2), not transposed
+    return g.contiguous(), transposed
+
+
+class _ToHeads(torch.autograd.Function):
+    """x [B, S, H, D] (a projection's rows) -> scale * rot(x) (or scale * x) as [B H, S, D], or [B H, D, S] when
+    transposed (sf_to_heads): the transpose to per-head operands and the rotary embedding of HuggingFace's eager
+    attention in one pass.  Its backward is _FromHeads (the adjoint), whose backward is this map again."""
+
+    @staticmethod
+    def forward(ctx, x, cos, sin, rotate: bool, transposed: bool, scale: float):
+        B, S, H, D = x.shape
+        x = x.contiguous()
+        y = torch.empty((B * H, D, S) if transposed else (B * H, S, D), dtype=x.dtype, device=x.device)
+        _heads_launch("sf_to_heads", L.lib().sf_to_heads, x, y, B, S, H, D, cos, sin, rotate, transposed, scale)
+        ctx.cfg = (B, S, H, D, rotate, transposed, scale)
+        ctx.save_for_backward(cos, sin)
+        return y
+
+    @staticmethod
+    def backward(ctx, g):
+        cos, sin = ctx.saved_tensors
+        B, S, H, D, rotate, transposed, scale = ctx.cfg
+        return _FromHeads.apply(g, cos, sin, (B, S, H, D), rotate, transposed, scale), None, None, None, None, None
+
+
+class _FromHeads(torch.autograd.Function):
+    """The adjoint of _ToHeads (sf_from_heads): g [B H, S, D] (or [B H, D, S] when transposed) ->
+    rot^T(scale * g) as [B, S, H, D]; without rotation and scale it is the per-head output's way back to rows."""
+
+    @staticmethod
+    def forward(ctx, g, cos, sin, shape, rotate: bool, transposed: bool, scale: float):
+        B, S, H, D = shape
+        src, tr = _head_major(g, transposed)
+        x = torch.empty((B, S, H, D), dtype=g.dtype, device=g.device)
+        _heads_launch("sf_from_heads", L.lib().sf_from_heads, src, x, B, S, H, D, cos, sin, rotate, tr, scale)
+        ctx.cfg = (rotate, transposed, scale)
+        ctx.save_for_backward(cos, sin)
+        return x
+
+    @staticmethod
+    def backward(ctx, gx):
+        cos, sin = ctx.saved_tensors
+        rotate, transposed, scale = ctx.cfg
+        return _ToHeads.apply(gx, cos, sin, rotate, transposed, scale), None, None, None, None, None, None
+
+
 _CAUSAL_BIAS: dict = {}
 
 
@@ -214,6 +275,14 @@ def causal_attention(q, k, v, cos, sin) -> torch.Tensor:
     which gives the same bits ((2^e q) k^T = 2^e (q k^T) exactly); otherwise the scores are scaled after
     it.  The masked positions get -inf where the reference adds the dtype's lowest value: either way
     their probability is exactly 0."""
+    if q.is_cuda:
+        return _causal_attention_device(q, k, v, cos, sin)
+    return _causal_attention_torch(q, k, v, cos, sin)
+
+
+def _causal_attention_torch(q, k, v, cos, sin) -> torch.Tensor:
+    """causal_attention with torch's layout ops (the CPU path; on the GPU the reference form the device path is
+    checked against)."""
     B, S, H, D = q.shape
     dt = q.dtype
     with torch.autocast(q.device.type, enabled=False):
@@ -235,6 +304,27 @@ def causal_attention(q, k, v, cos, sin) -> torch.Tensor:
         p = causal_softmax(scores)
         out = _BMM.apply(p, v.transpose(1, 2).reshape(B * H, S, D))              # [B H, S, D]
     return out.view(B, H, S, D).transpose(1, 2).reshape(B, S, H * D)
+
+
+def _causal_attention_device(q, k, v, cos, sin) -> torch.Tensor:
+    """causal_attention on the GPU: the same operations, with the transposes to per-head operands, the rotary
+    embedding and the way back to rows in sf_to_heads / sf_from_heads passes (no strided copies)."""
+    B, S, H, D = q.shape
+    dt = q.dtype
+    with torch.autocast(q.device.type, enabled=False):
+        scale = D ** -0.5
+        exact = math.frexp(scale)[0] == 0.5  # a power of two: it rides in q, bit for bit the scaled product
+        cos, sin = cos.float().contiguous(), sin.float().contiguous()
+        qh = _ToHeads.apply(q, cos, sin, True, False, scale if exact else 1.0)   # [B H, S, D]
+        kt = _ToHeads.apply(k, cos, sin, True, True, 1.0)                        # [B H, D, S]
+        if exact:
+            scores = _BMM.apply(qh, kt, causal_bias(S, q.device, dt))
+        else:
+            scores = _BMM.apply(qh, kt) * scale + causal_bias(S, q.device, dt)
+        p = causal_softmax(scores)
+        vh = _ToHeads.apply(v, cos, sin, False, False, 1.0)                      # [B H, S, D]
+        out = _BMM.apply(p, vh)                                                  # [B H, S, D]
+        return _FromHeads.apply(out, cos, sin, (B, S, H, D), False, False, 1.0).view(B, S, H * D)
 
 
 class DecoderLayer(nn.Module):
