@@ -498,6 +498,15 @@ int sf_to_heads(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64
 int sf_from_heads(const void* g, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, const float* cos,
                   const float* sin, int rotate, int transposed, float scale, void* x_grad, void* stream);
 
+/*
+ * dst[b] = src[b]^T for `batch` row-major [rows, cols] matrices of 2- or
+ * 4-byte elements (dst: [batch, cols, rows]): the contiguous transposed
+ * operands of the attention products' derivatives (torch.bmm gets contiguous
+ * operands only).  16-byte aligned, not aliased.
+ */
+int sf_transpose_batched(const void* src, int elem_bytes, int64_t batch, int64_t rows, int64_t cols, void* dst,
+                         void* stream);
+
 /* ---- GEMM engine (FusedMaskedLinearSTE, :56-132, and the SLoRB F.linear pair, :790-794) */
 #define SF_LAYOUT_K 0  /* operand stored K-contiguous: X[row * ld + k]                        */
 #define SF_LAYOUT_MN 1 /* operand stored M/N-contiguous: X[k * ld + row] (a transposed view)  */

@@ -268,6 +268,7 @@ SIGNATURES = {
     "sf_kl_backward": (_I, [_P, _P, _I, _I64, _I64, _F, _P, _P, _P, _I, _P, _P]),
     "sf_to_heads": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _I, _F, _P, _P]),
     "sf_from_heads": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I, _I, _F, _P, _P]),
+    "sf_transpose_batched": (_I, [_P, _I, _I64, _I64, _I64, _P, _P]),
     "sf_softmax_rows": (_I, [_P, _I, _I64, _I64, _I, _P, _P]),
     "sf_softmax_rows_backward": (_I, [_P, _P, _I, _I64, _I64, _I, _P, _P]),
     "sf_softmax_rows_double_backward": (_I, [_P, _P, _P, _I, _I64, _I64, _I, _P, _P, _P]),

@@ -248,10 +248,74 @@ int heads_call(const char* what, bool adj, const void* in, int dtype, int64_t B,
   return launch_status(what);
 }
 
+// dst[b][c][r] = src[b][r][c] for [batch, rows, cols] matrices of 2- or 4-byte elements: one workgroup
+// per 64 x 64 tile, read as rows of 16-byte chunks into LDS, written as rows of the transpose.
+template <typename E>
+__global__ void __launch_bounds__(kHdThreads) transpose_batched_kernel(const E* __restrict__ src, E* __restrict__ dst,
+                                                                      int64_t rows, int64_t cols) {
+  constexpr int kV = 16 / sizeof(E);  // elements per 16-byte chunk
+  __shared__ E tile[64][64 + kV];
+  const int64_t b = blockIdx.z, r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const E* s = src + b * rows * cols;
+  E* d = dst + b * rows * cols;
+  const int t = threadIdx.x;
+  const bool vec = (cols % kV) == 0 && (rows % kV) == 0 && r0 + 64 <= rows && c0 + 64 <= cols;
+  constexpr int per_row = 64 / kV;
+  for (int i = t; i < 64 * per_row; i += kHdThreads) {
+    const int r = i / per_row, c = (i - r * per_row) * kV;
+    if (vec) {
+      const uint4 q = *reinterpret_cast<const uint4*>(s + (r0 + r) * cols + c0 + c);
+      const E* e = reinterpret_cast<const E*>(&q);
+#pragma unroll
+      for (int k = 0; k < kV; ++k) tile[r][c + k] = e[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < kV; ++k)
+        if (r0 + r < rows && c0 + c + k < cols) tile[r][c + k] = s[(r0 + r) * cols + c0 + c + k];
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < 64 * per_row; i += kHdThreads) {
+    const int c = i / per_row, r = (i - c * per_row) * kV;  // output row c (a source column), positions r ..
+    if (vec) {
+      uint4 q;
+      E* e = reinterpret_cast<E*>(&q);
+#pragma unroll
+      for (int k = 0; k < kV; ++k) e[k] = tile[r + k][c];
+      *reinterpret_cast<uint4*>(d + (c0 + c) * rows + r0 + r) = q;
+    } else {
+#pragma unroll
+      for (int k = 0; k < kV; ++k)
+        if (c0 + c < cols && r0 + r + k < rows) d[(c0 + c) * rows + r0 + r + k] = tile[r + k][c];
+    }
+  }
+}
+
 }  // namespace
 }  // namespace sf
 
 using namespace sf;
+
+extern "C" int sf_transpose_batched(const void* src, int elem_bytes, int64_t batch, int64_t rows, int64_t cols,
+                                    void* dst, void* stream) {
+  SF_CHECK_ARG(elem_bytes == 2 || elem_bytes == 4, "sf_transpose_batched: element size %d", elem_bytes);
+  SF_CHECK_ARG(batch >= 0 && rows >= 0 && cols >= 0, "sf_transpose_batched: negative shape");
+  if (batch == 0 || rows == 0 || cols == 0) return SF_OK;
+  SF_CHECK_ARG(src && dst && src != dst, "sf_transpose_batched: null or aliased tensors");
+  SF_CHECK_ARG((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 == 0,
+               "sf_transpose_batched: tensors must be 16-byte aligned");
+  SF_CHECK_ARG(batch < 65536 && ceil_div(rows, 64) < 65536, "sf_transpose_batched: grid too large");
+  const dim3 grid(static_cast<unsigned>(ceil_div(cols, 64)), static_cast<unsigned>(ceil_div(rows, 64)),
+                  static_cast<unsigned>(batch));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (elem_bytes == 2)
+    transpose_batched_kernel<uint16_t><<<grid, kHdThreads, 0, st>>>(static_cast<const uint16_t*>(src),
+                                                                    static_cast<uint16_t*>(dst), rows, cols);
+  else
+    transpose_batched_kernel<uint32_t><<<grid, kHdThreads, 0, st>>>(static_cast<const uint32_t*>(src),
+                                                                    static_cast<uint32_t*>(dst), rows, cols);
+  return launch_status("sf_transpose_batched");
+}
 
 extern "C" int sf_to_heads(const void* x, int dtype, int64_t B, int64_t S, int64_t H, int64_t D, const float* cos,
                            const float* sin, int rotate, int transposed, float scale, void* y, void* stream) {

@@ -98,3 +98,16 @@ def test_heads_reject_bad_calls(cuda_device):
     assert lib.sf_to_heads(L.ptr(x), L.DT_F32, 2, 8, 2, 64, None, None, 1, 0, 1.0, L.ptr(y), st) == L.SF_ERR_INVALID
     assert lib.sf_from_heads(L.ptr(y), 9, 2, 8, 2, 64, L.ptr(cos), L.ptr(sin), 0, 0, 1.0, L.ptr(x), st) \
         == L.SF_ERR_INVALID
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(3, 128, 192), (2, 100, 72), (1, 7, 130), (4, 64, 64)])
+def test_transpose_batched(cuda_device, dtype, shape):
+    """The derivatives' transposed operands (llama._contig3 -> sf_transpose_batched): exactly torch's
+    contiguous copy of the transposed view, whole and partial 64 x 64 tiles, rows / cols not multiples of 8."""
+    from sparseforge_amd import llama
+
+    g = torch.Generator(device=cuda_device).manual_seed(sum(shape))
+    x = torch.randn(shape, generator=g, device=cuda_device).to(dtype)
+    got = llama._contig3(x.transpose(1, 2))
+    assert got.is_contiguous() and torch.equal(got, x.transpose(1, 2).contiguous())
