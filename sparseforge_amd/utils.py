@@ -29,7 +29,7 @@ import contextlib
 from . import _lib as L
 from . import kernels as K
 from . import profiling as _prof
-from .sparse_modeling import SparseLinear
+from .sparse_modeling import SparseLinear, draw_samples
 
 _nullctx = contextlib.nullcontext
 
@@ -180,7 +180,7 @@ def calculate_model_mask(model, step=0, lambda_mid: float = 0.0):
             draws.setdefault((ops.device(), idx[0]), []).append(idx)
         batches.setdefault(key, []).append([m, ops, p, idx])
     for (dev, size), lists in draws.items():
-        rows = K.sample_indices_sorted(size, [n for _, n, _ in lists], [s for _, _, s in lists], dev)
+        rows = draw_samples(size, [n for _, n, _ in lists], [s for _, _, s in lists], dev)
         for r, spec in enumerate(lists):
             samples[id(spec)] = rows[r]
     for (dev, _dts, _pb, q), items in batches.items():

@@ -354,3 +354,27 @@ def test_multi_fold_nan_scores(cuda_device):
     assert torch.isnan(m_tau[0]) and torch.isnan(s_tau[0])
     for i in range(1, 4):
         assert torch.equal(m_tau[i:i + 1], s_tau[i]), i
+
+
+def test_calculate_model_mask_large_sample_fallback(cuda_device, monkeypatch):
+    """Samples at or above the sorted sampler's bound come from a seeded torch.randint (unsorted); the
+    batched update gathers them, and calculate_model_mask still equals update_mask layer by layer.  The
+    bound is lowered below the models' 5000-element sample to take that path on small layers."""
+    from sparseforge_amd import sparse_modeling as sm
+    from sparseforge_amd import utils as U
+
+    monkeypatch.setattr(sm, "SORTED_SAMPLE_MAX", 1000)
+    rows = sm.draw_samples(5000, [7000, 9000], [3, 4], cuda_device)
+    assert rows.shape == (2, 5000) and int(rows[0].max()) < 7000 and int(rows[1].max()) < 9000
+    assert not bool((rows[0][1:] >= rows[0][:-1]).all())  # unsorted: the gather path
+    assert torch.equal(rows, sm.draw_samples(5000, [7000, 9000], [3, 4], cuda_device))  # seeded
+    a, b = _model(cuda_device, 2), _model(cuda_device, 2)
+    torch.manual_seed(99)
+    U.calculate_model_mask(a, step=5, lambda_mid=0.05)
+    torch.manual_seed(99)
+    for m in b:
+        m.update_mask(5, lambda_mid=0.05)
+    torch.cuda.synchronize()
+    for ma, mb in zip(a, b):
+        assert torch.equal(ma.mask, mb.mask), ma.weight.shape
+        assert int(ma.weight.flipped_mask) == int(mb.weight.flipped_mask)
