@@ -442,7 +442,20 @@ def e2e_leg(torch, dev, steps: int, warmup: int, micro: int, layers: int = 22) -
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     tokens = E2E_BATCH * E2E_SEQ * steps
+    # Model FLOPs of a step (the usual convention: 2 per multiply-add of a matrix product, the Hutchinson
+    # probe's extra forward / double backward not counted): the student's forward + backward (3x its
+    # forward) over every linear (projections, SLoRB factors, lm_head) and the attention products (q k^T
+    # and p v over the full S x S square, as eager attention computes them), the teacher's forward.
+    h, f_, v_, L_ = shape.hidden_size, shape.intermediate_size, shape.vocab_size, shape.num_hidden_layers
+    proj = 4 * h * h + 3 * h * f_
+    slorb = RANK * (4 * (h + h) + 3 * (h + f_))
+    attn = 2 * 2 * E2E_SEQ * h  # q k^T and p v per token and layer
+    per_token_fwd_student = 2 * (L_ * (proj + slorb) + h * v_) + L_ * attn
+    per_token_fwd_teacher = 2 * (L_ * proj + h * v_) + L_ * attn
+    model_flops = (3 * per_token_fwd_student + per_token_fwd_teacher) * E2E_BATCH * E2E_SEQ
     res = {"value": round(tokens / el, 1), "unit": "tokens/s", "steps": steps, "warmup": warmup,
+           "model_tflop_per_step": round(model_flops / 1e12, 2),
+           "mfu": round(model_flops * steps / el / (PEAK_BF16_TFLOPS * 1e12), 4),
            "ms_per_step": round(el * 1e3 / steps, 2), "batch": E2E_BATCH, "seq_len": E2E_SEQ, "micro_batch": micro,
            "grad_accum": rc.grad_accum, "layers": shape.num_hidden_layers, "trainable_params": n_student,
            "sparse_params": n_sparse, "first_iter": E2E_START, "hardening_x": round(hx, 4),
@@ -451,7 +464,8 @@ def e2e_leg(torch, dev, steps: int, warmup: int, micro: int, layers: int = 22) -
            "peak_mem_gib": round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 1),
            "loss_first_last": [round(losses[0], 4), round(losses[-1], 4)],
            "data": "synthetic token ids uniform over the vocabulary; random-init student and teacher"}
-    log(f"e2e: {res['ms_per_step']:.0f} ms/step, {res['value']:.0f} tokens/s; phases {res['phase_ms_per_step']}; "
+    log(f"e2e: {res['ms_per_step']:.0f} ms/step, {res['value']:.0f} tokens/s, MFU {res['mfu']:.3f} "
+        f"({res['model_tflop_per_step']} TFLOP of model work a step); phases {res['phase_ms_per_step']}; "
         f"peak {res['peak_mem_gib']} GiB")
     del step, opt, student, teacher, data
     return res
