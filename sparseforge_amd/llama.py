@@ -328,17 +328,18 @@ def _causal_attention_device(q, k, v, cos, sin) -> torch.Tensor:
     """causal_attention on the GPU: the same operations, with the transposes to per-head operands, the rotary
     embedding and the way back to rows in sf_to_heads / sf_from_heads passes (no strided copies)."""
     B, S, H, D = q.shape
-    dt = q.dtype
     with torch.autocast(q.device.type, enabled=False):
         scale = D ** -0.5
         exact = math.frexp(scale)[0] == 0.5  # a power of two: it rides in q, bit for bit the scaled product
         cos, sin = cos.float().contiguous(), sin.float().contiguous()
         qh = _ToHeads.apply(q, cos, sin, True, False, scale if exact else 1.0)   # [B H, S, D]
         kt = _ToHeads.apply(k, cos, sin, True, True, 1.0)                        # [B H, D, S]
-        if exact:
-            scores = _BMM.apply(qh, kt, causal_bias(S, q.device, dt))
-        else:
-            scores = _BMM.apply(qh, kt) * scale + causal_bias(S, q.device, dt)
+        # No mask tensor: the causal softmax kernels read only columns 0..i of row i and give the rest
+        # probability 0 (zero gradient), which is what adding -inf there does; on the kept entries the
+        # mask adds 0, so the scores' bits there are the product's either way.
+        scores = _BMM.apply(qh, kt)
+        if not exact:
+            scores = scores * scale
         p = causal_softmax(scores)
         vh = _ToHeads.apply(v, cos, sin, False, False, 1.0)                      # [B H, S, D]
         out = _BMM.apply(p, vh)                                                  # [B H, S, D]
