@@ -1768,8 +1768,9 @@ extern "C" size_t sf_sample_indices_sorted_workspace_size(int64_t sample_size, i
 extern "C" int sf_sample_indices_sorted(int64_t* idx, int64_t sample_size, const int64_t* n, const uint64_t* seeds,
                                         int count, void* workspace, size_t workspace_bytes, void* stream) {
   SF_CHECK_ARG(sample_size >= 0 && count >= 0, "bad sample size %lld / count %d", (long long)sample_size, count);
-  // the fixed-point sums stay below 2^64: S_m is about (m + 1) 2^32 and one term is at most 37 2^32
-  SF_CHECK_ARG(sample_size < (int64_t(1) << 30), "sample size %lld above 2^30", (long long)sample_size);
+  // below 2^28: the fixed-point sums stay far below 2^64 (S_m is about (m + 1) 2^32, one term at most
+  // 37 2^32), and a list has at most 2^16 chunks, whose sums every workgroup of the index pass reads
+  SF_CHECK_ARG(sample_size < (int64_t(1) << 28), "sample size %lld not below 2^28", (long long)sample_size);
   if (sample_size == 0 || count == 0) return SF_OK;
   SF_CHECK_ARG(idx && n && seeds, "null argument");
   for (int c = 0; c < count; ++c) SF_CHECK_ARG(n[c] > 0, "list %d: n = %lld", c, (long long)n[c]);
@@ -1777,7 +1778,6 @@ extern "C" int sf_sample_indices_sorted(int64_t* idx, int64_t sample_size, const
                "workspace too small");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t chunks = ceil_div(sample_size + 1, kSortedChunk);
-  SF_CHECK_ARG(chunks < 65536, "sample size %lld needs too many chunks", (long long)sample_size);
   uint64_t* sums = static_cast<uint64_t*>(workspace);
   for (int c0 = 0; c0 < count; c0 += kSortedLists) {
     const int k = count - c0 < kSortedLists ? count - c0 : kSortedLists;

@@ -54,3 +54,26 @@ def test_sorted_sampler_rejects_bad_calls(cuda_device):
         K.sample_indices_sorted(10, [5, 6], [1], cuda_device)
     assert K.sample_indices_sorted(0, [5], [1], cuda_device).shape == (1, 0)
     assert K.sample_indices_sorted(5, [], [], cuda_device).shape == (0, 5)
+
+
+def test_sorted_sampler_size_bound(cuda_device):
+    """The largest sample the sorted path takes (2^28 - 1: 2^16 chunks of 4096 positions) is drawn sorted and
+    in range; 2^28 is refused (the retraining code draws such samples with torch.randint instead)."""
+    from sparseforge_amd import _lib as L
+    from sparseforge_amd import kernels as K
+    from sparseforge_amd import sparse_modeling as sm
+
+    m, n = sm.SORTED_SAMPLE_MAX - 1, 45088768
+    print(f"[sampling] size bound m={m}", flush=True)
+    idx = K.sample_indices_sorted(m, [n], [11], cuda_device)[0]
+    assert int(idx.min()) >= 0 and int(idx.max()) < n
+    assert bool((idx[1:] >= idx[:-1]).all())
+    # the mean of m uniform draws from [0, n) is (n - 1) / 2 within a few standard errors
+    mean = float(idx.double().mean())
+    assert abs(mean - (n - 1) / 2) < 6 * n / (12 * m) ** 0.5
+    del idx
+    big = torch.empty(1, dtype=torch.int64, device=cuda_device)
+    ns = (L.ctypes.c_int64 * 1)(n)
+    ss = (L.ctypes.c_uint64 * 1)(11)
+    assert L.lib().sf_sample_indices_sorted(L.ptr(big), sm.SORTED_SAMPLE_MAX, ns, ss, 1, L.ptr(big), 1 << 20,
+                                            L.stream(cuda_device)) == L.SF_ERR_INVALID
