@@ -478,6 +478,42 @@ int sf_softmax_rows_double_backward(const void* x, const void* grad_p, const voi
                                     int64_t rows, int64_t cols, int causal, void* grad_grad_p, void* grad2_x,
                                     void* stream);
 
+/* ---- RMSNorm of the retraining model (cfg5; HuggingFace LlamaRMSNorm of the LlamaForCausalLM the reference
+ *      retrains, legacy/model_llama.py:18-57; differentiated twice by the Hutchinson HVP, legacy/utils.py:714-869) */
+
+/*
+ * y = weight * (x32 * rsqrt(mean(x32^2, -1) + eps)).to(dtype), x32 = x in f32,
+ * over rows of `cols` columns (x, y: [rows, cols]; weight: [cols]; one dtype,
+ * f32 or bf16).  rstd: f32[rows] receives 1 / sqrt(mean + eps), which the two
+ * backward passes take.  cols: a multiple of 8, at most 4096; every pointer
+ * 16-byte aligned.  The row sums run in another order than torch's.
+ */
+int sf_rmsnorm_forward(const void* x, const void* weight, int dtype, int64_t rows, int64_t cols, float eps, void* y,
+                       float* rstd, void* stream);
+
+/* f32 scratch of the weight-gradient column sums of the two calls below. */
+size_t sf_rmsnorm_workspace_size(int64_t rows, int64_t cols);
+
+/*
+ * The backward of sf_rmsnorm_forward (torch's op sequence: the DT-rounded
+ * grad_y * weight, the rsqrt / mean / pow chain in f32, the cast back):
+ * grad_x [rows, cols] and grad_weight [cols] (the column sums of the rounded
+ * grad_y * n, added in f32 in a fixed order).
+ */
+int sf_rmsnorm_backward(const void* x, const void* weight, const void* grad_y, const float* rstd, int dtype,
+                        int64_t rows, int64_t cols, void* grad_x, void* grad_weight, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
+ * The backward of sf_rmsnorm_backward with respect to grad_y, x and weight,
+ * given the gradients grad_grad_x / grad_grad_weight (null: zero) of its
+ * outputs: the closed-form derivatives evaluated in f32, cast to the dtype.
+ */
+int sf_rmsnorm_double_backward(const void* x, const void* weight, const void* grad_y, const float* rstd,
+                               const void* grad_grad_x, const void* grad_grad_weight, int dtype, int64_t rows,
+                               int64_t cols, void* grad_grad_y, void* grad2_x, void* grad2_weight, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /*
  * Per-head operands of the retraining model's attention (HuggingFace eager
  * LlamaAttention, legacy/model_llama.py:39-55: q/k/v views [B, S, H, D]

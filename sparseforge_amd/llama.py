@@ -65,15 +65,101 @@ class LlamaShape:
 
 
 class RMSNorm(nn.Module):
+    """HuggingFace's LlamaRMSNorm: weight * (x32 * rsqrt(mean(x32^2) + eps)).to(x dtype).  On the GPU (x and
+    weight of one dtype, bf16 or f32, rows of at most 4096 columns, a multiple of 8) each pass is one device
+    kernel (sf_rmsnorm_*): forward, backward and the backward's own backward that the Hutchinson probe takes;
+    elsewhere torch's ops."""
+
     def __init__(self, dim: int, eps: float, device=None, dtype=None):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(dim, device=device, dtype=dtype))
         self.eps = eps
 
     def forward(self, x):
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return self.weight * xf.to(x.dtype)
+        if _norm_on_device(x, self.weight):
+            x2 = x.reshape(-1, x.shape[-1]).contiguous()
+            if x2.data_ptr() % 16 == 0:  # the kernels' vector accesses
+                return _RMSNorm.apply(x2, self.weight, self.eps).view(x.shape)
+        return rms_norm_torch(x, self.weight, self.eps)
+
+
+def rms_norm_torch(x, weight, eps):
+    """The torch form (the CPU path; on the GPU the form the device passes are checked against)."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * xf.to(x.dtype)
+
+
+def _norm_on_device(x: torch.Tensor, w: torch.Tensor) -> bool:
+    D = x.shape[-1]
+    return (x.is_cuda and x.dtype in (torch.bfloat16, torch.float32) and w.dtype == x.dtype and w.dim() == 1
+            and w.shape[0] == D and D % 8 == 0 and D <= 4096 and w.is_contiguous() and w.data_ptr() % 16 == 0)
+
+
+def _norm_ws(rows: int, cols: int, dev) -> torch.Tensor:
+    return torch.empty(max(int(L.lib().sf_rmsnorm_workspace_size(rows, cols)), 16), dtype=torch.uint8, device=dev)
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """A gradient made contiguous at a 16-byte aligned address (a fresh copy when a view starts elsewhere)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+class _RMSNorm(torch.autograd.Function):
+    """RMSNorm over the rows of x2 [rows, D] (sf_rmsnorm_forward); its backward is _RMSNormGrad, whose backward
+    (sf_rmsnorm_double_backward) is what the Hutchinson Hessian-vector product differentiates."""
+
+    @staticmethod
+    def forward(ctx, x2, w, eps):  # x2: contiguous, 16-byte aligned (saved as the graph's own input)
+        dev = L.require_device(x2, w)
+        rows, D = x2.shape
+        y = torch.empty_like(x2)
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+        with _prof.region("sf_rmsnorm_forward", 2 * x2.numel() * x2.element_size(), "B", dev):
+            L.check(L.lib().sf_rmsnorm_forward(L.ptr(x2), L.ptr(w), L.dtype_code(x2), rows, D, float(eps), L.ptr(y),
+                                               L.ptr(rstd), L.stream(dev)), "sf_rmsnorm_forward")
+        ctx.save_for_backward(x2, w, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2, w, rstd = ctx.saved_tensors
+        gx, gw = _RMSNormGrad.apply(gy.to(x2.dtype), x2, w, rstd)
+        return gx, gw, None
+
+
+class _RMSNormGrad(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gy, x2, w, rstd):
+        dev = L.require_device(gy, x2, w, rstd)
+        gy = _aligned(gy)
+        rows, D = x2.shape
+        gx, gw = torch.empty_like(x2), torch.empty_like(w)
+        ws = _norm_ws(rows, D, dev)
+        with _prof.region("sf_rmsnorm_backward", 3 * x2.numel() * x2.element_size(), "B", dev):
+            L.check(L.lib().sf_rmsnorm_backward(L.ptr(x2), L.ptr(w), L.ptr(gy), L.ptr(rstd), L.dtype_code(x2), rows,
+                                                D, L.ptr(gx), L.ptr(gw), L.ptr(ws), ws.numel(), L.stream(dev)),
+                    "sf_rmsnorm_backward")
+        ctx.save_for_backward(gy, x2, w, rstd)
+        return gx, gw
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggx, ggw):
+        gy, x2, w, rstd = ctx.saved_tensors
+        dev = x2.device
+        rows, D = x2.shape
+        ggx = _aligned(ggx.to(x2.dtype)) if ggx is not None else torch.zeros_like(x2)
+        ggw = _aligned(ggw.to(w.dtype)) if ggw is not None else None
+        ggy, gx2, gw2 = torch.empty_like(x2), torch.empty_like(x2), torch.empty_like(w)
+        ws = _norm_ws(rows, D, dev)
+        with _prof.region("sf_rmsnorm_double_backward", 5 * x2.numel() * x2.element_size(), "B", dev):
+            L.check(L.lib().sf_rmsnorm_double_backward(L.ptr(x2), L.ptr(w), L.ptr(gy), L.ptr(rstd), L.ptr(ggx),
+                                                       L.ptr(ggw) if ggw is not None else None, L.dtype_code(x2),
+                                                       rows, D, L.ptr(ggy), L.ptr(gx2), L.ptr(gw2), L.ptr(ws),
+                                                       ws.numel(), L.stream(dev)), "sf_rmsnorm_double_backward")
+        return ggy, gx2, gw2, None
 
 
 def rotary_tables(seq: int, head_dim: int, theta: float, device) -> tuple[torch.Tensor, torch.Tensor]:
