@@ -514,6 +514,32 @@ int sf_rmsnorm_double_backward(const void* x, const void* weight, const void* gr
                                int64_t cols, void* grad_grad_y, void* grad2_x, void* grad2_weight, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* ---- gated MLP product of the retraining model (cfg5; HuggingFace LlamaMLP's silu(gate) * up, the
+ *      LlamaForCausalLM of legacy/model_llama.py:18-57; differentiated twice by the Hutchinson HVP) */
+
+/*
+ * y = silu(g).to(dtype) * u over n elements (g, u, y: one dtype, f32 or bf16;
+ * n a multiple of 8; 16-byte aligned), torch's silu and mul in f32 with the
+ * cast to the dtype after each.
+ */
+int sf_swiglu_forward(const void* g, const void* u, int dtype, int64_t n, void* y, void* stream);
+
+/*
+ * Its backward: grad_g = silu_backward((grad_y * u).to(dtype), g), grad_u =
+ * grad_y * silu(g).to(dtype), each cast to the dtype.
+ */
+int sf_swiglu_backward(const void* g, const void* u, const void* grad_y, int dtype, int64_t n, void* grad_g,
+                       void* grad_u, void* stream);
+
+/*
+ * The backward of sf_swiglu_backward with respect to grad_y, g and u, given
+ * the gradients grad_grad_g / grad_grad_u (null: zero) of its outputs: the
+ * closed-form derivatives (silu's first and second) in f32, cast to the dtype.
+ */
+int sf_swiglu_double_backward(const void* g, const void* u, const void* grad_y, const void* grad_grad_g,
+                              const void* grad_grad_u, int dtype, int64_t n, void* grad_grad_y, void* grad2_g,
+                              void* grad2_u, void* stream);
+
 /*
  * Per-head operands of the retraining model's attention (HuggingFace eager
  * LlamaAttention, legacy/model_llama.py:39-55: q/k/v views [B, S, H, D]

@@ -272,6 +272,9 @@ SIGNATURES = {
     "sf_softmax_rows": (_I, [_P, _I, _I64, _I64, _I, _P, _P]),
     "sf_softmax_rows_backward": (_I, [_P, _P, _I, _I64, _I64, _I, _P, _P]),
     "sf_softmax_rows_double_backward": (_I, [_P, _P, _P, _I, _I64, _I64, _I, _P, _P, _P]),
+    "sf_swiglu_forward": (_I, [_P, _P, _I, _I64, _P, _P]),
+    "sf_swiglu_backward": (_I, [_P, _P, _P, _I, _I64, _P, _P, _P]),
+    "sf_swiglu_double_backward": (_I, [_P, _P, _P, _P, _P, _I, _I64, _P, _P, _P, _P]),
     "sf_rmsnorm_workspace_size": (_SZ, [_I64, _I64]),
     "sf_rmsnorm_forward": (_I, [_P, _P, _I, _I64, _I64, _F, _P, _P, _P]),
     "sf_rmsnorm_backward": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _P, _P, _P, _SZ, _P]),

@@ -432,6 +432,63 @@ def _causal_attention_device(q, k, v, cos, sin) -> torch.Tensor:
         return _FromHeads.apply(out, cos, sin, (B, S, H, D), False, False, 1.0).view(B, S, H * D)
 
 
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """silu(g) * u, HuggingFace LlamaMLP's gate: one device pass each way on the GPU (g and u of one dtype, bf16 or
+    f32, same shape, contiguous, 16-byte aligned, a multiple of 8 elements), torch's ops elsewhere."""
+    if (g.is_cuda and g.dtype in (torch.bfloat16, torch.float32) and u.dtype == g.dtype and u.shape == g.shape
+            and g.is_contiguous() and u.is_contiguous() and g.numel() % 8 == 0 and g.data_ptr() % 16 == 0
+            and u.data_ptr() % 16 == 0):
+        return _SwiGLU.apply(g, u)
+    return F.silu(g) * u
+
+
+def _sg_launch(name: str, nbytes: int, dev, *args) -> None:
+    with _prof.region(name, nbytes, "B", dev):
+        L.check(getattr(L.lib(), name)(*args, L.stream(dev)), name)
+
+
+class _SwiGLU(torch.autograd.Function):
+    """silu(g) * u (sf_swiglu_forward); its backward is _SwiGLUGrad, whose backward (sf_swiglu_double_backward)
+    the Hutchinson Hessian-vector product takes."""
+
+    @staticmethod
+    def forward(ctx, g, u):
+        dev = L.require_device(g, u)
+        y = torch.empty_like(g)
+        _sg_launch("sf_swiglu_forward", 3 * g.numel() * g.element_size(), dev, L.ptr(g), L.ptr(u), L.dtype_code(g),
+                   g.numel(), L.ptr(y))
+        ctx.save_for_backward(g, u)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        g, u = ctx.saved_tensors
+        return _SwiGLUGrad.apply(_aligned(gy.to(g.dtype)), g, u)
+
+
+class _SwiGLUGrad(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gy, g, u):
+        dev = L.require_device(gy, g, u)
+        gg, gu = torch.empty_like(g), torch.empty_like(g)
+        _sg_launch("sf_swiglu_backward", 5 * g.numel() * g.element_size(), dev, L.ptr(g), L.ptr(u), L.ptr(gy),
+                   L.dtype_code(g), g.numel(), L.ptr(gg), L.ptr(gu))
+        ctx.save_for_backward(gy, g, u)
+        return gg, gu
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggg, ggu):
+        gy, g, u = ctx.saved_tensors
+        dev = g.device
+        ggg = _aligned(ggg.to(g.dtype)) if ggg is not None else None
+        ggu = _aligned(ggu.to(g.dtype)) if ggu is not None else None
+        dgy, dg, du = torch.empty_like(g), torch.empty_like(g), torch.empty_like(g)
+        _sg_launch("sf_swiglu_double_backward", 8 * g.numel() * g.element_size(), dev, L.ptr(g), L.ptr(u),
+                   L.ptr(gy), L.ptr(ggg), L.ptr(ggu), L.dtype_code(g), g.numel(), L.ptr(dgy), L.ptr(dg), L.ptr(du))
+        return dgy, dg, du
+
+
 class DecoderLayer(nn.Module):
     def __init__(self, shape: LlamaShape, make_linear, device=None, dtype=None):
         super().__init__()
@@ -457,7 +514,7 @@ class DecoderLayer(nn.Module):
         x = x + a.o_proj(causal_attention(q, k, v, cos, sin))
         n = self.post_attention_layernorm(x)
         m = self.mlp
-        return x + m.down_proj(F.silu(m.gate_proj(n)) * m.up_proj(n))
+        return x + m.down_proj(swiglu(m.gate_proj(n), m.up_proj(n)))
 
 
 class LlamaDecoder(nn.Module):
