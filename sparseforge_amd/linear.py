@@ -283,6 +283,27 @@ def _opt(t):
     return t.contiguous() if t is not None else None
 
 
+_SIDE: dict = {}
+_CUS: dict = {}
+
+
+def _side_stream(t: torch.Tensor):
+    """A second stream for the weight-gradient products when the two big backward products (dx [T, in] and
+    dW [out, in], 256 x 256 tiles) would each leave compute units idle: running dW beside dx fills them.
+    None when both fill the GPU by themselves (the LLaMA-7B layer shapes) or off the GPU."""
+    if not t.is_cuda:
+        return None
+    dev = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    if dev not in _SIDE:
+        _SIDE[dev] = torch.cuda.Stream(device=dev)  # default priority
+        _CUS[dev] = torch.cuda.get_device_properties(dev).multi_processor_count
+    return _SIDE[dev]
+
+
+def _fills(rows: int, cols: int, dev: int) -> bool:
+    return ((rows + 255) // 256) * ((cols + 255) // 256) >= _CUS[dev]
+
+
 # ---------------------------------------------------------------------------
 # autograd
 # ---------------------------------------------------------------------------
@@ -299,17 +320,38 @@ class _MaskedLinearBackward(torch.autograd.Function):
         # dx = gy (W.E): the forward's masked weight when it kept one (no weight-scaling factor),
         # else rebuilt with one elementwise pass
         Wm = wm_fwd if wm_fwd is not None else (apply_mask(W, E) if E is not None else W)
+        T, out, inn = gy.shape[0], gy.shape[1], x.shape[1]
+        side = _side_stream(gy)
+        if side is not None:
+            di = gy.device.index if gy.device.index is not None else torch.cuda.current_device()
+            if _fills(T, inn, di) and _fills(out, inn, di):
+                side = None
+        dW = torch.empty(out, inn, dtype=gy.dtype, device=gy.device)  # allocated on the calling stream
+        dS = torch.empty(out, P.shape[0], dtype=gy.dtype, device=gy.device) if has_slorb else None
+        main = torch.cuda.current_stream(gy.device) if side is not None else None
+
+        def weight_grads():
+            if decay != 0.0:
+                mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay, out=dW)
+            else:
+                mm_tn(gy, x, out=dW)
+            if has_slorb:
+                mm_tn(gy, z, out=dS)
+
+        if side is not None:  # dW and dS beside dz, dx and dP; joined before returning
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                weight_grads()
         if has_slorb:
             dx = mm_nn(gy, Wm, A2=dz, B2=P, K2=P.shape[0])
         else:
             dx = mm_nn(gy, Wm)
-        if decay != 0.0:
-            dW = mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay)
-        else:
-            dW = mm_tn(gy, x)
+        if side is None:
+            weight_grads()
         db = column_sum(gy, W.dtype) if has_bias else None
         dP = mm_tn(dz, x) if has_slorb else None
-        dS = mm_tn(gy, z) if has_slorb else None
+        if side is not None:
+            main.wait_stream(side)
         # W.E stays for the double backward's d/d gy (gdx (W.E)^T), so that product runs unmasked
         ctx.save_for_backward(gy, x, W, P, S, E, z, dz, Wm if E is not None else None)
         del Wm
@@ -340,6 +382,28 @@ class _MaskedLinearBackward(torch.autograd.Function):
         la = _cat_k([t for t in (u, z if g_dS is not None else None) if t is not None], 1)
         lb = _cat_k([t for t, a in ((S, u), (g_dS, g_dS)) if a is not None], 1)
         seg = {"A2": la, "B2": lb, "K2": la.shape[1]} if la is not None else {}
+        # d/dW = (gy^T gdx) . E  (+ decay gdW [E < 0.5]: the SR-STE term decay W [E < 0.5] of dW is
+        # elementwise in W, legacy/sparse_modeling.py:123-125), beside the two products below when
+        # they leave compute units idle (as in forward())
+        gW = None
+        side = _side_stream(gy) if g_dx is not None else None
+        if side is not None:
+            di = gy.device.index if gy.device.index is not None else torch.cuda.current_device()
+            if _fills(T, x.shape[1], di) and _fills(out, x.shape[1], di):
+                side = None
+        if g_dx is not None:
+            gW = torch.empty(out, x.shape[1], dtype=gy.dtype, device=gy.device)
+        main = torch.cuda.current_stream(gy.device) if side is not None else None
+
+        def weight_grad():
+            if g_dx is not None:
+                mm_tn(gy, g_dx, emask=_as_values(E, W.dtype), out=gW)
+            return decay_term(g_dW, E, ctx.decay, out=gW) if ctx.decay != 0.0 and g_dW is not None else gW
+
+        if side is not None:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                weight_grad()
         ggy = None
         if g_dx is not None:
             ggy = mm_nt(g_dx, Wm if Wm is not None else W, bias=g_db, **seg)
@@ -361,11 +425,10 @@ class _MaskedLinearBackward(torch.autograd.Function):
             gx = mm_nn(gy, g_dW, **({"A2": ra, "B2": rb, "K2": ra.shape[1]} if ra is not None else {}))
         elif ra is not None:
             gx = mm_nn(ra, rb)
-        # d/dW = (gy^T gdx) . E  (+ decay gdW [E < 0.5]: the SR-STE term decay W [E < 0.5] of dW is
-        # elementwise in W, legacy/sparse_modeling.py:123-125)
-        gW = mm_tn(gy, g_dx, emask=_as_values(E, W.dtype)) if g_dx is not None else None
-        if ctx.decay != 0.0 and g_dW is not None:
-            gW = decay_term(g_dW, E, ctx.decay, out=gW)
+        if side is None:
+            gW = weight_grad()
+        else:
+            main.wait_stream(side)
         # d/dP = dz^T gdx + (gy gdS)^T x ;  d/dS = gy^T (gdx P^T + x gdP^T)
         gP = gS = None
         if ctx.has_slorb:
