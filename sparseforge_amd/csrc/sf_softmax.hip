@@ -41,17 +41,21 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ uint16_t to_bf16_rne(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
 
+typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
+
 // 8 elements of a row from column e0 (VEC: one 16- or 32-byte load; else
 // element by element, columns at or past n read as `fill`).
 template <int DT, bool VEC>
 __device__ __forceinline__ void ld8(const void* row, int64_t e0, int64_t n, float fill, float (&v)[8]) {
   if constexpr (VEC) {
     if constexpr (DT == SF_DTYPE_F32) {
-      const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + e0);
-      const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(row) + e0 + 4);
+      const f32x4_nt a = __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt*>(static_cast<const float*>(row) + e0));
+      const f32x4_nt b =
+          __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt*>(static_cast<const float*>(row) + e0 + 4));
       v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
-      const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(row) + e0);
+      const u32x4_nt q = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(static_cast<const uint16_t*>(row) + e0));
       const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -69,14 +73,15 @@ template <int DT, bool VEC>
 __device__ __forceinline__ void st8(void* row, int64_t e0, int64_t n, const float (&v)[8]) {
   if constexpr (VEC) {
     if constexpr (DT == SF_DTYPE_F32) {
-      *reinterpret_cast<float4*>(static_cast<float*>(row) + e0) = make_float4(v[0], v[1], v[2], v[3]);
-      *reinterpret_cast<float4*>(static_cast<float*>(row) + e0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      __builtin_nontemporal_store(f32x4_nt{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4_nt*>(static_cast<float*>(row) + e0));
+      __builtin_nontemporal_store(f32x4_nt{v[4], v[5], v[6], v[7]},
+                                  reinterpret_cast<f32x4_nt*>(static_cast<float*>(row) + e0 + 4));
     } else {
       uint32_t w[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k)
         w[k] = static_cast<uint32_t>(to_bf16_rne(v[2 * k])) | (static_cast<uint32_t>(to_bf16_rne(v[2 * k + 1])) << 16);
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(row) + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+      __builtin_nontemporal_store(u32x4_nt{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4_nt*>(static_cast<uint16_t*>(row) + e0));
     }
   } else {
 #pragma unroll
