@@ -112,10 +112,12 @@ class RetrainStep:
         # The penalties read only the masks (frozen, no gradient), which change after the optimizer
         # step, not between micro-batches: each micro-batch's loss adds the same value, so it is
         # computed once per step (the reference recomputes it per micro-batch, :2047-2064).
-        penalty = U.mid_penalty(self.student, lam)
-        if cfg.sparsity_alpha:
-            pen, _cur = U.sparsity_penalty(self.student, target_sparsity=cfg.sparsity_ratio, alpha=cfg.sparsity_alpha)
-            penalty = penalty + pen
+        with U.shared_mask_rows():  # both read every mask's statistics: one pass over the masks
+            penalty = U.mid_penalty(self.student, lam)
+            if cfg.sparsity_alpha:
+                pen, _cur = U.sparsity_penalty(self.student, target_sparsity=cfg.sparsity_ratio,
+                                               alpha=cfg.sparsity_alpha)
+                penalty = penalty + pen
         for micro, (X, Y) in enumerate(batches):
             last = micro == cfg.grad_accum - 1
             ctx = (torch.autocast("cuda", dtype=cfg.autocast_dtype) if cfg.autocast_dtype is not None

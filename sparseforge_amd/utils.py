@@ -19,12 +19,11 @@ single-GPU path and is left out.
 """
 from __future__ import annotations
 
+import contextlib
 import itertools
 import re
 
 import torch
-
-import contextlib
 
 from . import _lib as L
 from . import kernels as K
@@ -426,13 +425,38 @@ def _dist_sum(*tensors):
         pass
 
 
+_ROWS_MEMO: dict | None = None
+
+
+@contextlib.contextmanager
+def shared_mask_rows():
+    """Within the block, statistics rows of a mask list are computed once: a second request for the same
+    masks (same storage, version, shape, dtype and tail) gets the first one's rows.  The retraining step
+    wraps mid_penalty and sparsity_penalty in it (both read every mask of the model, unchanged between
+    them)."""
+    global _ROWS_MEMO
+    prev, _ROWS_MEMO = _ROWS_MEMO, {}
+    try:
+        yield
+    finally:
+        _ROWS_MEMO = prev
+
+
 def _mask_rows(masks, tails=None, eps: float = 1e-8):
     """[len(masks), MSTAT_COUNT] float64 on the masks' device: sf_mask_stats of each mask."""
+    key = None
+    if _ROWS_MEMO is not None:
+        key = (eps,) + tuple((m.data_ptr(), m._version, tuple(m.shape), m.dtype, 0 if tails is None else int(tails[i]))
+                             for i, m in enumerate(masks))
+        if key in _ROWS_MEMO:
+            return _ROWS_MEMO[key]
     dev = masks[0].device
     rows = torch.empty((len(masks), L.MSTAT_COUNT), dtype=torch.float64, device=dev)
     ws = K.mask_stats_workspace(dev)
     for i, m in enumerate(masks):
         K.mask_stats(m.contiguous(), rows[i], 0 if tails is None else int(tails[i]), eps, ws)
+    if key is not None:
+        _ROWS_MEMO[key] = rows
     return rows
 
 

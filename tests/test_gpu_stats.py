@@ -232,3 +232,20 @@ def test_harden_fraction_matches_reference(cuda_device):
     for li, layer in enumerate(model.children()):
         assert (layer.mask.detach().cpu().numpy() == g[f"mask_out{li}"]).all()
         assert (layer.frozen_mask_flags.detach().float().cpu().numpy() == g[f"frozen_out{li}"]).all()
+
+
+def test_shared_mask_rows_reuses_and_invalidates(cuda_device):
+    """Inside utils.shared_mask_rows a repeated request for the same masks returns the first rows; an in-place
+    change of a mask (its version moves) makes the next request compute them again."""
+    _, _, _, U = _mods()
+    g = torch.Generator(device=cuda_device).manual_seed(4)
+    masks = [torch.rand(64, 96, generator=g, device=cuda_device) for _ in range(2)]
+    with U.shared_mask_rows():
+        r1 = U._mask_rows(masks)
+        assert U._mask_rows(masks) is r1
+        masks[0].mul_(0.5)
+        r3 = U._mask_rows(masks)
+        assert r3 is not r1
+        assert not torch.equal(r3[0], r1[0]) and torch.equal(r3[1], r1[1])
+    r4 = U._mask_rows(masks)
+    assert r4 is not r3 and torch.equal(r4, r3)
