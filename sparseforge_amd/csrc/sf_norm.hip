@@ -24,7 +24,7 @@
 // 8-column chunks l, l + 64, ...).  The weight gradients are column sums over
 // the rows: each workgroup folds its rows' terms per column and its four waves
 // in a fixed order into one partial row, and a column pass adds the partial
-// rows in index order (the number of workgroups depends only on the shape, so
+// rows in a fixed order (the number of workgroups depends only on the shape, so
 // the sums are reproducible).
 #include <initializer_list>
 #include <type_traits>
@@ -36,7 +36,8 @@ namespace {
 
 constexpr int kNrWaves = 4;        // rows in flight per workgroup, one wave each
 constexpr int kNrMaxCols = 4096;   // row length bound: 8 chunks of 8 per lane
-constexpr int kNrColGroups = 256;  // most workgroups of the passes with weight gradients
+constexpr int kNrColGroups = 1024;  // most workgroups of the passes with weight gradients (a row per wave
+                                    // up to 4096 rows)
 
 __device__ __forceinline__ float nr_wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -283,22 +284,29 @@ __global__ void __launch_bounds__(64 * kNrWaves) rms_dbwd_kernel(NormArgs a) {
   fold_columns<NJ>(a, acc);
 }
 
-// out[c] = sum over the partial rows p of part[p][c] in index order (four interleaved
-// chains, added in a fixed order), cast to the weight's dtype.
+// out[c] = sum over the partial rows of part[p][c], cast to the weight's dtype: a workgroup takes 64
+// columns, its thread group q (0..3) the rows p = q, q + 4, ... in increasing order (16 loads in
+// flight per thread), and the four group sums are added in q order (a fixed order: reproducible).
 __global__ void __launch_bounds__(256) rms_colsum_kernel(const float* __restrict__ part, int64_t nparts, int64_t D,
                                                          void* out, int dt) {
-  const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (c >= D) return;
-  float t0 = 0.0f, t1 = 0.0f, t2 = 0.0f, t3 = 0.0f;
-  int64_t p = 0;
-  for (; p + 3 < nparts; p += 4) {
-    t0 += part[p * D + c];
-    t1 += part[(p + 1) * D + c];
-    t2 += part[(p + 2) * D + c];
-    t3 += part[(p + 3) * D + c];
+  __shared__ float red[4][64];
+  const int l = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + l;
+  float acc = 0.0f;
+  if (c < D) {
+    int64_t p = q;
+    for (; p + 4 * 15 < nparts; p += 4 * 16) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = part[(p + 4 * j) * D + c];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc += v[j];
+    }
+    for (; p < nparts; p += 4) acc += part[p * D + c];
   }
-  for (; p < nparts; ++p) t0 += part[p * D + c];
-  store_from_f32(out, c, dt, (t0 + t1) + (t2 + t3));
+  red[q][l] = acc;
+  __syncthreads();
+  if (q == 0 && c < D) store_from_f32(out, c, dt, ((red[0][l] + red[1][l]) + red[2][l]) + red[3][l]);
 }
 
 int nr_chunks(int64_t D) {  // 8-column chunks per lane
@@ -371,7 +379,7 @@ struct DbwdNQ {
 };
 
 int nr_colsum(const float* part, unsigned nparts, int64_t D, void* out, int dt, hipStream_t st) {
-  hipLaunchKernelGGL(rms_colsum_kernel, dim3(static_cast<unsigned>(ceil_div(D, 256))), dim3(256), 0, st, part,
+  hipLaunchKernelGGL(rms_colsum_kernel, dim3(static_cast<unsigned>(ceil_div(D, 64))), dim3(256), 0, st, part,
                      static_cast<int64_t>(nparts), D, out, dt);
   return launch_status("sf_rmsnorm (weight-gradient column sums)");
 }
