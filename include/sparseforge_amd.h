@@ -600,7 +600,8 @@ typedef struct sf_gemm_desc {
                       are kept or zeroed; requires bscale == 1                          */
   void* workspace; /* optional scratch of sf_gemm_workspace_size(desc) bytes, 16-byte
                       aligned: lets a GEMM with few output tiles split K (f32 partial
-                      sums reduced in a fixed order); NULL runs it unsplit             */
+                      sums reduced in a fixed order); NULL runs it unsplit; a smaller
+                      workspace limits the splits to the M x N f32 partials it holds  */
   size_t workspace_bytes;
   /* Block-sparse-16 operands (the compressed layout of convert_to_block_sparse,
      legacy/triton_block_sparse.py:46-103, plus its block map from sf_bsr_*): */

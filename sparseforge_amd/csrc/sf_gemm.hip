@@ -2438,8 +2438,12 @@ extern "C" int sf_gemm(const sf_gemm_desc* d, void* stream) {
   g.split_stages = ceil_div(d->K1, d->dtype == SF_DTYPE_BF16 ? Tr<uint16_t>::BK : Tr<float>::BK);
   g.partial = nullptr;
   {
-    const int sp = choose_splits(d);
-    const size_t need = static_cast<size_t>(sp) * d->M * d->N * sizeof(float);
+    // as many of the chosen K splits as the workspace holds partials for (a caller running the product
+    // beside another one can ask for fewer with a smaller workspace)
+    int sp = choose_splits(d);
+    const size_t per = static_cast<size_t>(d->M) * d->N * sizeof(float);
+    if (d->workspace && sp > 1 && d->workspace_bytes < sp * per) sp = static_cast<int>(d->workspace_bytes / per);
+    const size_t need = static_cast<size_t>(sp) * per;
     if (sp > 1 && !d->c_blocks && d->workspace && d->workspace_bytes >= need && al16(d->workspace)) {
       g.splits = sp;
       g.split_stages = ceil_div(g.split_stages, sp);

@@ -33,7 +33,8 @@ def _vec(dtype: torch.dtype) -> int:
 
 
 def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=None, bscale=1.0, bias=None,
-         emask=None, dw=None, decay=0.0, out=None, out_dtype=None, accumulate=False, bmask_t=None) -> torch.Tensor:
+         emask=None, dw=None, decay=0.0, out=None, out_dtype=None, accumulate=False, bmask_t=None,
+         max_splits=None) -> torch.Tensor:
     """C[M, N] = A1 . B1'^T (+ A2 . B2^T) on the device.
 
     a_layout: L.LAYOUT_K (A1 is [M, K]) or L.LAYOUT_MN (A1 is [K, M]);
@@ -99,6 +100,8 @@ def gemm(M, N, A1, B1, K1, a_layout, b_layout, *, A2=None, B2=None, K2=0, bmask=
     d.emask, d.dw, d.decay = L.ptr(emask), L.ptr(dw), float(decay)
     d.accumulate = int(bool(accumulate))
     ws_bytes = L.lib().sf_gemm_workspace_size(L.byref(d))
+    if max_splits is not None and ws_bytes > max_splits * M * N * 4:  # fewer K splits (the big products only)
+        ws_bytes = max_splits * M * N * 4 if max_splits > 1 else 0
     ws = None
     if ws_bytes:  # split-K scratch from torch's caching allocator; the library never allocates
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
@@ -330,11 +333,14 @@ class _MaskedLinearBackward(torch.autograd.Function):
         dS = torch.empty(out, P.shape[0], dtype=gy.dtype, device=gy.device) if has_slorb else None
         main = torch.cuda.current_stream(gy.device) if side is not None else None
 
+        # beside dx a product needs fewer K splits to fill the compute units dx leaves idle
+        ms = 2 if side is not None else None
+
         def weight_grads():
             if decay != 0.0:
-                mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay, out=dW)
+                mm_tn(gy, x, emask=_as_values(E, W.dtype), dw=W, decay=decay, out=dW, max_splits=ms)
             else:
-                mm_tn(gy, x, out=dW)
+                mm_tn(gy, x, out=dW, max_splits=ms)
             if has_slorb:
                 mm_tn(gy, z, out=dS)
 
@@ -397,7 +403,7 @@ class _MaskedLinearBackward(torch.autograd.Function):
 
         def weight_grad():
             if g_dx is not None:
-                mm_tn(gy, g_dx, emask=_as_values(E, W.dtype), out=gW)
+                mm_tn(gy, g_dx, emask=_as_values(E, W.dtype), out=gW, max_splits=2 if side is not None else None)
             return decay_term(g_dW, E, ctx.decay, out=gW) if ctx.decay != 0.0 and g_dW is not None else gW
 
         if side is not None:
