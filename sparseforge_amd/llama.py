@@ -233,6 +233,77 @@ class _BMM(torch.autograd.Function):
         return ga, gb, None
 
 
+# Causal structure of the attention's S x S operands: OUT_LOWER (only the product's lower triangle is ever read:
+# the scores, the gradient of p), A_LOWER / B_LOWER (that operand is zero above its diagonal: p, the scores'
+# gradient).  Products of these kinds skip the blocks the triangle leaves out.
+OUT_LOWER, A_LOWER, B_LOWER = 1, 2, 3
+CAUSAL_BLOCKS = 4  # row (or column) blocks of a causal product; S below 512 runs as one full product
+
+
+def _causal_blocks(S: int):
+    nb = CAUSAL_BLOCKS if S >= 512 else 1
+    step = (S + nb - 1) // nb
+    return [(i, min(i + step, S)) for i in range(0, S, step)]
+
+
+def _causal_product(a: torch.Tensor, b: torch.Tensor, mode: int) -> torch.Tensor:
+    """a @ b ([BH, M, K] x [BH, K, N]) with one S x S side lower-triangular, as row / column blocks of
+    torch.bmm on views (each block's product covers the triangle up to the block's end):
+    OUT_LOWER: c[r0:r1, :r1] = a[r0:r1] b[:, :r1]  (c's entries above the blocks stay unwritten: never read)
+    A_LOWER:   c[r0:r1] = a[r0:r1, :r1] b[:r1]      (a is zero past column r1 in those rows)
+    B_LOWER:   c[:, c0:c1] = a[:, c0:] b[c0:, c0:c1] (b is zero above row c0 in those columns)."""
+    a, b = _contig3(a), _contig3(b)
+    BH, M, K = a.shape
+    N = b.shape[2]
+    c = torch.empty(BH, M, N, dtype=a.dtype, device=a.device)
+    if mode == OUT_LOWER:
+        for r0, r1 in _causal_blocks(M):
+            torch.bmm(a[:, r0:r1], b[:, :, :r1], out=c[:, r0:r1, :r1])
+    elif mode == A_LOWER:
+        for r0, r1 in _causal_blocks(M):
+            torch.bmm(a[:, r0:r1, :r1], b[:, :r1], out=c[:, r0:r1])
+    else:
+        for c0, c1 in _causal_blocks(N):
+            torch.bmm(a[:, :, c0:], b[:, c0:, c0:c1], out=c[:, :, c0:c1])
+    return c
+
+
+class _CBMM(torch.autograd.Function):
+    """A causal product (_causal_product) differentiable any number of times: the derivatives of each kind
+    are products of the kinds again (the S x S operand always untransposed), e.g. for OUT_LOWER the gradient
+    g is zero above its diagonal (it comes from the causal softmax passes), so grad_a = g b^T is A_LOWER and
+    grad_b = a^T g is B_LOWER."""
+
+    @staticmethod
+    def forward(ctx, a, b, mode: int):
+        ctx.save_for_backward(a, b)
+        ctx.mode = mode
+        return _causal_product(a, b, mode)
+
+    @staticmethod
+    def backward(ctx, g):
+        a, b = ctx.saved_tensors
+        mode = ctx.mode
+        g = g.to(a.dtype)
+        ga = gb = None
+        if mode == OUT_LOWER:
+            if ctx.needs_input_grad[0]:
+                ga = _CBMM.apply(g, b.transpose(1, 2), A_LOWER)
+            if ctx.needs_input_grad[1]:
+                gb = _CBMM.apply(a.transpose(1, 2), g, B_LOWER)
+        elif mode == A_LOWER:
+            if ctx.needs_input_grad[0]:
+                ga = _CBMM.apply(g, b.transpose(1, 2), OUT_LOWER)
+            if ctx.needs_input_grad[1]:
+                gb = _CBMM.apply(g.transpose(1, 2), a, B_LOWER).transpose(1, 2)
+        else:
+            if ctx.needs_input_grad[0]:
+                ga = _CBMM.apply(b, g.transpose(1, 2), A_LOWER).transpose(1, 2)
+            if ctx.needs_input_grad[1]:
+                gb = _CBMM.apply(a.transpose(1, 2), g, OUT_LOWER)
+        return ga, gb, None
+
+
 def _softmax_launch(name: str, fn, nbytes: int, dev, *args) -> None:
     with _prof.region(name, nbytes, "B", dev):
         L.check(fn(*args, L.stream(dev)), name)
@@ -423,12 +494,12 @@ def _causal_attention_device(q, k, v, cos, sin) -> torch.Tensor:
         # No mask tensor: the causal softmax kernels read only columns 0..i of row i and give the rest
         # probability 0 (zero gradient), which is what adding -inf there does; on the kept entries the
         # mask adds 0, so the scores' bits there are the product's either way.
-        scores = _BMM.apply(qh, kt)
+        scores = _CBMM.apply(qh, kt, OUT_LOWER)
         if not exact:
             scores = scores * scale
         p = causal_softmax(scores)
         vh = _ToHeads.apply(v, cos, sin, False, False, 1.0)                      # [B H, S, D]
-        out = _BMM.apply(p, vh)                                                  # [B H, S, D]
+        out = _CBMM.apply(p, vh, A_LOWER)                                        # [B H, S, D]
         return _FromHeads.apply(out, cos, sin, (B, S, H, D), False, False, 1.0).view(B, S, H * D)
 
 

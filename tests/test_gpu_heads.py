@@ -114,3 +114,34 @@ def test_transpose_batched(cuda_device, dtype, shape):
     x = torch.randn(shape, generator=g, device=cuda_device).to(dtype)
     got = llama._contig3(x.transpose(1, 2))
     assert got.is_contiguous() and torch.equal(got, x.transpose(1, 2).contiguous())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_device_attention_causal_blocks(cuda_device, dtype):
+    """At S >= 512 the device path's attention products run as causal blocks (llama._CBMM: only the blocks
+    the lower triangle touches); forward, backward and the Hutchinson double backward against the torch
+    form's full products: f32 within 1e-4, bf16 within 2e-2 (norm-wise relative; the blocks accumulate in
+    another order than the full products, and bf16 rounds each operand)."""
+    from sparseforge_amd import llama
+
+    B, S, H, D = 1, 1024, 4, 64
+    g = torch.Generator(device=cuda_device).manual_seed(11)
+    mk = lambda: (torch.randn(B, S, H, D, generator=g, device=cuda_device) * 0.5).to(dtype)  # noqa: E731
+    q0, k0, v0 = mk(), mk(), mk()
+    w = torch.randn(B, S, H * D, generator=g, device=cuda_device).to(dtype)
+    probes = [torch.randn(B, S, H, D, generator=g, device=cuda_device).to(dtype) for _ in range(3)]
+    cos, sin = _tables(S, D, cuda_device)
+    outs = []
+    for fn in (llama._causal_attention_device, llama._causal_attention_torch):
+        q, k, v = (t.clone().requires_grad_(True) for t in (q0, k0, v0))
+        y = fn(q, k, v, cos, sin)
+        loss = (y.float() * w.float()).sum()
+        grads = torch.autograd.grad(loss, (q, k, v), create_graph=True)
+        dot = sum((gr.float() * p.float()).sum() for gr, p in zip(grads, probes))
+        hv = torch.autograd.grad(dot, (q, k, v))
+        outs.append([y.detach()] + [gr.detach() for gr in grads] + list(hv))
+    bar = 1e-4 if dtype == torch.float32 else 2e-2
+    for a, b in zip(*outs):
+        assert torch.isfinite(a).all()
+        err = float((a.double() - b.double()).norm() / b.double().norm())
+        assert err < bar, err
